@@ -1,0 +1,233 @@
+"""Benchmark of the MI355X quantized matrix-multiply path (one GPU).
+
+Headline workload: Q4_K dequant-GEMV, W 17408 x 5120 (N(0, 0.02), seed 2,
+quantized by this repo's quantizer), x one row of 5120 fp32 (N(0, 1), seed 1002), y fp32.
+One step = one GEMV over one weight copy. The weights rotate over enough copies (>= 512 MB)
+that the 256 MB MALL cannot serve repeated reads; inputs are resident in HBM before timing.
+
+`value` = algorithmic bytes per step (stored W + 4 M K + 4 M N) / time per step, in GB/s.
+Also reported on the same line: the Q6_K GEMVs (config 3), the fused gate/up Q4_K GEMM at
+M = 512 (config 4) in TFLOP/s, the roofline of the headline kernel, and the CPU oracle
+(a port of the reference's cpu::matmul) timed on the host cores on the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 512 << 20
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def make_weights(hl, t, rows, cols, seed, outliers=0.0):
+    w = hl.fill_normal(seed, rows * cols, 0.0, 0.02).reshape(rows, cols)
+    if outliers:
+        k = max(1, int(round(cols * outliers)))
+        w[:, np.random.default_rng(seed + 7).choice(cols, size=k, replace=False)] *= 8.0
+    return hl.quantize(t, w.reshape(-1))
+
+
+def device_copies(hl, torch, t, wq, rows, cols, min_bytes=MALL_BYTES):
+    """SLAB images on the device, enough copies to exceed `min_bytes` in total."""
+    one = torch.empty(hl.slab_bytes(t, rows, cols), dtype=torch.uint8, device="cuda")
+    src = torch.from_numpy(wq).to("cuda")
+    hl.repack_slab(t, src, rows, cols, one)
+    del src
+    n = max(2, math.ceil(min_bytes / one.numel()) + 1)
+    copies = [one] + [one.clone() for _ in range(n - 1)]
+    torch.cuda.synchronize()
+    return copies
+
+
+def time_graph(torch, launch, n_copies, steps, warmup):
+    """Capture one pass over the weight copies into a HIP graph, replay it; returns
+    (ms per step from events around the whole timed region, total steps run)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n_copies):  # eager warm-up (also loads the code objects)
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_copies):
+            launch(i)
+    reps_w = max(1, math.ceil(warmup / n_copies))
+    reps = max(1, math.ceil(steps / n_copies))
+    for _ in range(reps_w):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * n_copies), reps * n_copies
+
+
+def time_per_launch(torch, launch, n_copies, iters):
+    """Events around each single eager launch (the kernel's own duration plus event overhead)."""
+    cur = torch.cuda.current_stream()
+    pairs = []
+    for k in range(iters):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        launch(k % n_copies)
+        b.record(cur)
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in pairs)
+    return ts[len(ts) // 2], sum(ts) / len(ts)
+
+
+def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0):
+    wq = make_weights(hl, t, rows, cols, seed, outliers)
+    copies = device_copies(hl, torch, t, wq, rows, cols)
+    x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
+    y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+
+    def launch(i):
+        hl.gemv(t, copies[i], x, y, rows, cols, m)
+
+    ms, n = time_graph(torch, launch, len(copies), steps, warmup)
+    med, mean = time_per_launch(torch, launch, len(copies), 200)
+    algo = len(wq) + 4 * m * cols + 4 * m * rows
+    del copies
+    torch.cuda.empty_cache()
+    return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9,
+            "event_median_us": med * 1e3, "event_mean_us": mean * 1e3, "wq": wq, "x": x.cpu().numpy()}
+
+
+def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
+    wg = make_weights(hl, t, rows, cols, seed)
+    wu = make_weights(hl, t, rows, cols, seed + 40)
+    cg = device_copies(hl, torch, t, wg, rows, cols, MALL_BYTES // 2)
+    cu = device_copies(hl, torch, t, wu, rows, cols, MALL_BYTES // 2)
+    n = min(len(cg), len(cu))
+    x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
+    out = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+
+    def launch(i):
+        hl.gate_up_swiglu(t, cg[i], cu[i], x, out, rows, cols, m)
+
+    ms, nsteps = time_graph(torch, launch, n, steps, warmup)
+    med, mean = time_per_launch(torch, launch, n, 50)
+    flops = 4.0 * m * rows * cols
+    del cg, cu
+    torch.cuda.empty_cache()
+    return {"flops": flops, "ms": ms, "steps": nsteps, "tflops": flops / (ms * 1e-3) / 1e12,
+            "event_median_us": med * 1e3, "event_mean_us": mean * 1e3}
+
+
+def cpu_baseline(t, wq, rows, cols, x, seconds):
+    """The oracle (a C port of the reference's cpu::matmul) on all host cores, best of N
+    after one warm-up, for about `seconds` of CPU time."""
+    from oracle import oracle as orc
+
+    threads = orc.default_threads()
+    orc.matmul(t, wq, rows, cols, x, threads=threads)
+    best, spent, runs = float("inf"), 0.0, 0
+    while spent < seconds and runs < 1000:
+        t0 = time.perf_counter()
+        orc.matmul(t, wq, rows, cols, x, threads=threads)
+        dt = time.perf_counter() - t0
+        best, spent, runs = min(best, dt), spent + dt, runs + 1
+    algo = len(wq) + 4 * x.size + 4 * x.shape[0] * rows
+    return {"value": round(algo / best / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full Q4_K {rows}x{cols} M={x.shape[0]} GEMV, best of {runs} runs after 1 warm-up "
+                      f"({spent:.1f} s total), oracle/oracle.c built -O2 -ffp-contract=off",
+            "ms_per_call": round(best * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import halo_amd as hl
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    hl.lib()
+    Q4_K, Q6_K = int(hl.DType.Q4_K), int(hl.DType.Q6_K)
+
+    log("config 2: Q4_K GEMV 17408x5120 M=1")
+    head = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps, args.warmup)
+    kernel_us = head["event_median_us"]
+    achieved = head["bytes"] / (kernel_us * 1e-6) / 1e9
+    extra = {}
+    if not args.no_extra:
+        log("config 2: Q4_K GEMV M=4")
+        r = gemv_case(hl, torch, Q4_K, 17408, 5120, 4, 2, args.steps // 2, args.warmup)
+        extra["q4k_gemv_17408x5120_m4"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}
+        for m in (1, 4):
+            log(f"config 3: Q6_K GEMV 5120x17408 M={m}")
+            r = gemv_case(hl, torch, Q6_K, 5120, 17408, m, 3, args.steps // 2, args.warmup)
+            extra[f"q6k_gemv_5120x17408_m{m}"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                                  "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("config 3: Q6_K GEMV 151936x5120 M=1 (1% outlier columns)")
+        r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
+        extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        for m in (2, 8, 64, 512):
+            log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
+            r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, max(20, args.steps // 20), 5)
+            extra[f"q4k_gate_up_swiglu_m{m}"] = {"TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 2),
+                                                 "frac_bf16_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)}
+    log("cpu baseline")
+    cpu = cpu_baseline(Q4_K, head["wq"], 17408, 5120, head["x"], args.cpu_seconds)
+
+    line = {
+        "metric": "Q4_K GEMV GB/s at M=1 (17408x5120, BASELINE config 2)",
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": head["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: N(0,0.02) weights quantized to Q4_K by this repo's quantizer, N(0,1) x",
+        "config": {"workload": "Q4_K dequant-GEMV 17408x5120 M=1 (config 2), SLAB layout, "
+                               f"{math.ceil(MALL_BYTES / (17408 * 2880)) + 1}+ rotating weight copies"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_us": round(kernel_us, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,248 @@
+"""ctypes bindings of libhalo_mi355x.so (the C ABI in include/halo_mi355x.h).
+
+Pointer arguments are plain integers (device addresses, e.g. ``tensor.data_ptr()``) and
+``stream`` is a hipStream_t as an integer (0 = null stream). Functions taking torch tensors
+validate dtype/device and pass ``torch.cuda.current_stream()`` unless a stream is given.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import functools
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+_LIB_PATH = _PKG / "libhalo_mi355x.so"
+
+SLAB_ROWS = 64
+
+
+class DType(enum.IntEnum):
+    """ggml type ids (include/halo/tensor/dtype.h:18-49 of the reference)."""
+
+    F32 = 0
+    Q4_0 = 2
+    Q8_0 = 8
+    Q4_K = 12
+    Q6_K = 14
+
+
+class Layout(enum.IntEnum):
+    GGUF = 0
+    SLAB = 1
+
+
+class Variant(enum.IntEnum):
+    DEFAULT = 0
+    GGUF_REF = 1
+    SLAB_GEMV = 2
+    SLAB_GEMM_BF16 = 3
+    SLAB_AUTO = 4
+
+
+class ErrorCode(enum.IntEnum):
+    """Status codes; names follow halo::ErrorCode (include/halo/core/error.h:13-24)."""
+
+    Ok = 0
+    Kernel = 1
+    Unsupported = 2
+    Config = 3
+    Memory = 4
+    Device = 5
+
+
+class HaloError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        self.code = ErrorCode(code)
+        super().__init__(f"{self.code.name.upper()}_ERROR: {message}")
+
+
+_BLOCK = {DType.F32: (1, 4), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q4_K: (256, 144), DType.Q6_K: (256, 210)}
+
+
+def block_elems(t: int) -> int:
+    """Weights per block; 0 for a type this backend does not handle."""
+    return _BLOCK.get(int(t), (0, 0))[0]
+
+
+def block_bytes(t: int) -> int:
+    return _BLOCK.get(int(t), (0, 0))[1]
+
+
+class _GemvParams(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("layout", ctypes.c_uint32),
+        ("w", ctypes.c_void_p),
+        ("w_stride", ctypes.c_uint64),
+        ("x", ctypes.c_void_p),
+        ("x_stride", ctypes.c_uint64),
+        ("y", ctypes.c_void_p),
+        ("y_stride", ctypes.c_uint64),
+        ("rows", ctypes.c_uint32),
+        ("cols", ctypes.c_uint32),
+        ("n_vec", ctypes.c_uint32),
+        ("variant", ctypes.c_uint32),
+    ]
+
+
+class _GateUpParams(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("layout", ctypes.c_uint32),
+        ("w_gate", ctypes.c_void_p),
+        ("w_up", ctypes.c_void_p),
+        ("x", ctypes.c_void_p),
+        ("x_stride", ctypes.c_uint64),
+        ("out", ctypes.c_void_p),
+        ("out_stride", ctypes.c_uint64),
+        ("rows", ctypes.c_uint32),
+        ("cols", ctypes.c_uint32),
+        ("n_vec", ctypes.c_uint32),
+        ("variant", ctypes.c_uint32),
+    ]
+
+
+# Every symbol include/halo_mi355x.h declares, with its ctypes signature.
+_U32, _U64, _VP, _INT = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
+SIGNATURES = {
+    "halo_mi_last_error": (ctypes.c_char_p, []),
+    "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
+    "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
+    "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
+    "halo_mi_row_bytes": (_U64, [_U32, _U32]),
+    "halo_mi_slab_bytes": (_U64, [_U32, _U32, _U32]),
+    "halo_mi_repack_slab": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP, _VP]),
+    "halo_mi_unpack_slab": (_INT, [_U32, _VP, _U32, _U32, _VP, _U64, _VP]),
+    "halo_mi_repack_slab_host": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP]),
+    "halo_mi_unpack_slab_host": (_INT, [_U32, _VP, _U32, _U32, _VP, _U64]),
+    "halo_mi_upload_slab": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP, _U64, _VP]),
+    "halo_mi_fill_normal": (None, [_U64, _VP, _U64, ctypes.c_float, ctypes.c_float]),
+    "halo_mi_quantize": (_INT, [_U32, _VP, _U64, _VP, _U32]),
+}
+
+
+@functools.lru_cache(maxsize=None)
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises (never falls back) when it has not been built."""
+    if not _LIB_PATH.exists():
+        raise RuntimeError(f"{_LIB_PATH} is missing: build it with `python -m halo_amd.build` (hipcc, gfx950)")
+    so = ctypes.CDLL(str(_LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(so, name)
+        fn.restype = res
+        fn.argtypes = args
+    return so
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise HaloError(rc, lib().halo_mi_last_error().decode())
+
+
+def _ptr(t) -> int:
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is not None:
+        return int(stream)
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---- geometry ---------------------------------------------------------------------------
+
+
+def row_bytes(t: int, cols: int) -> int:
+    return int(lib().halo_mi_row_bytes(int(t), int(cols)))
+
+
+def slab_bytes(t: int, rows: int, cols: int) -> int:
+    return int(lib().halo_mi_slab_bytes(int(t), int(rows), int(cols)))
+
+
+# ---- host utilities ---------------------------------------------------------------------
+
+
+def fill_normal(seed: int, n: int, mean: float = 0.0, std: float = 1.0):
+    """SplitMix64 + Box-Muller normal fill (portable, seed-determined), as a float32 numpy array."""
+    import numpy as np
+
+    out = np.empty(int(n), dtype=np.float32)
+    lib().halo_mi_fill_normal(int(seed), out.ctypes.data, int(n), float(mean), float(std))
+    return out
+
+
+def quantize(t: int, src, threads: int = 0):
+    """fp32 numpy array (size a multiple of the block) -> GGUF block bytes (numpy uint8)."""
+    import numpy as np
+
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    be, bb = block_elems(t), block_bytes(t)
+    out = np.empty(src.size // be * bb if be and src.size % be == 0 else 1, dtype=np.uint8)
+    _check(lib().halo_mi_quantize(int(t), src.ctypes.data, src.size, out.ctypes.data, int(threads)))
+    return out
+
+
+def repack_slab_host(t: int, src, rows: int, cols: int, src_stride: int = 0):
+    import numpy as np
+
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(slab_bytes(t, rows, cols), dtype=np.uint8)
+    _check(lib().halo_mi_repack_slab_host(int(t), src.ctypes.data, int(src_stride), int(rows), int(cols), out.ctypes.data))
+    return out
+
+
+def unpack_slab_host(t: int, src, rows: int, cols: int):
+    import numpy as np
+
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    out = np.empty(rows * row_bytes(t, cols), dtype=np.uint8)
+    _check(lib().halo_mi_unpack_slab_host(int(t), src.ctypes.data, int(rows), int(cols), out.ctypes.data, 0))
+    return out
+
+
+# ---- device entry points (torch tensors or raw device addresses) -------------------------
+
+
+def gemv(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB, w_stride: int = 0,
+         x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+    p = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(y), int(y_stride),
+                    int(rows), int(cols), int(n_vec), int(variant))
+    _check(lib().halo_mi_gemv(ctypes.byref(p), _stream(stream)))
+
+
+def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB,
+                   x_stride: int = 0, out_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+    p = _GateUpParams(int(t), int(layout), _ptr(w_gate), _ptr(w_up), _ptr(x), int(x_stride), _ptr(out), int(out_stride),
+                      int(rows), int(cols), int(n_vec), int(variant))
+    _check(lib().halo_mi_gate_up_swiglu(ctypes.byref(p), _stream(stream)))
+
+
+def dequant_rows(t: int, layout: int, w, rows: int, cols: int, out, *, first_row: int = 0, n_rows: int | None = None,
+                 w_stride: int = 0, out_stride: int = 0, stream=None) -> None:
+    n = rows - first_row if n_rows is None else n_rows
+    _check(lib().halo_mi_dequant_rows(int(t), int(layout), _ptr(w), int(w_stride), int(rows), int(cols), int(first_row),
+                                      int(n), _ptr(out), int(out_stride), _stream(stream)))
+
+
+def repack_slab(t: int, src, rows: int, cols: int, dst, *, src_stride: int = 0, stream=None) -> None:
+    _check(lib().halo_mi_repack_slab(int(t), _ptr(src), int(src_stride), int(rows), int(cols), _ptr(dst), _stream(stream)))
+
+
+def unpack_slab(t: int, src, rows: int, cols: int, dst, *, dst_stride: int = 0, stream=None) -> None:
+    _check(lib().halo_mi_unpack_slab(int(t), _ptr(src), int(rows), int(cols), _ptr(dst), int(dst_stride), _stream(stream)))
+
+
+def upload_slab(t: int, host_src, rows: int, cols: int, dst, *, src_stride: int = 0, chunk_bytes: int = 0,
+                stream=None) -> None:
+    """host_src: a numpy uint8 array (e.g. a memmap of the GGUF tensor) or a host address."""
+    addr = host_src if isinstance(host_src, int) else host_src.ctypes.data
+    _check(lib().halo_mi_upload_slab(int(t), addr, int(src_stride), int(rows), int(cols), _ptr(dst), int(chunk_bytes),
+                                     _stream(stream)))

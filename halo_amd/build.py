@@ -1,0 +1,63 @@
+"""Build the halo_mi355x shared library (gfx950) and the CPU oracle in-tree.
+
+The library is compiled with hipcc for gfx950 only. Flags:
+  -fno-gpu-flush-denormals-to-zero   fp16/fp32 subnormal scales must survive (bit-exact dequant)
+  -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+LIB = PKG / "libhalo_mi355x.so"
+SOURCES = [PKG / "csrc" / "kernels.hip", PKG / "csrc" / "host_utils.cpp"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_FLAGS = [
+    "-O3",
+    "--offload-arch=gfx950",
+    "-std=c++20",
+    "-fPIC",
+    "-shared",
+    "-pthread",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: not an error.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build failed ({' '.join(cmd)}):\n{err}\n{proc.stdout}")
+    if err.strip():
+        sys.stderr.write(err + "\n")
+
+
+def build_library() -> Path:
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-o", str(tmp), *map(str, SOURCES)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-B", "-C", str(ROOT / "oracle")])
+    return ROOT / "oracle" / "liboracle.so"
+
+
+def build_all() -> None:
+    build_oracle()
+    build_library()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(LIB)

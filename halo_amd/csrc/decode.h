@@ -1,0 +1,122 @@
+// Device-side unpacking of GGUF blocks and SLAB slot records. Every weight value these
+// helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:79-90,
+// :143-151, :236-269, :302-327): all products in those expressions are exact in fp32, and the
+// one rounding step (Q4_K's `- dmin * m`) is evaluated in the same order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "slab_layout.h"
+
+namespace halo_mi::dev {
+
+// fp16 -> fp32 with v_cvt_f32_f16 (exact, fp16 denormals kept: the library is built without
+// denormal flushing; a test forces a subnormal scale in every row).
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+// ---- Q4_K 6-bit scale/min of sub-block j from the 12 packed bytes (held as 3 dwords) -------
+// s0 = bytes 0..3, s1 = bytes 4..7, s2 = bytes 8..11 of the scales field.
+// j < 4: sc = b[j] & 63, m = b[j+4] & 63; j >= 4: sc = (b[j+4] & 15) | (b[j-4] >> 6) << 4,
+// m = (b[j+4] >> 4) | (b[j] >> 6) << 4 (ggml get_scale_min_k4, quant.cpp:236-244).
+__device__ __forceinline__ void q4k_sc_m(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j, uint32_t& sc,
+                                         uint32_t& m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63u;
+        m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const uint32_t jj = j - 4;
+        const uint32_t b8 = (s2 >> (8 * jj)) & 0xFFu;
+        sc = (b8 & 15u) | (((s0 >> (8 * jj + 6)) & 3u) << 4);
+        m = (b8 >> 4) | (((s1 >> (8 * jj + 6)) & 3u) << 4);
+    }
+}
+
+// d1 = d * sc and m1 = dmin * m for sub-block j of a Q4_K header (16 B as uint4).
+__device__ __forceinline__ void q4k_scales(const uint4& hdr, uint32_t j, float& d1, float& m1) {
+    uint32_t sc, m;
+    q4k_sc_m(hdr.y, hdr.z, hdr.w, j, sc, m);
+    d1 = h2f(hdr.x & 0xFFFFu) * (float)sc;
+    m1 = h2f(hdr.x >> 16) * (float)m;
+}
+
+// ---- Q6_K slot record -> 6-bit unsigned quants, 4 per dword (byte lanes) --------------------
+// ql: the 16-byte low-nibble record; qh: the 8-byte top-bit record (see q6_qh_byte).
+// Output dword i (0..3) holds elements 4i..4i+3 (lo[i]) and 16+4i..16+4i+3 (hi[i]).
+__device__ __forceinline__ void q6_slot_bytes(const uint4& ql, const uint2& qh, uint32_t lo[4], uint32_t hi[4]) {
+    const uint32_t L[4] = {ql.x, ql.y, ql.z, ql.w};
+    const uint32_t H[2] = {qh.x, qh.y};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t a = L[2 * w], b = L[2 * w + 1], h = H[w];
+        lo[2 * w] = (a & 0x0F0F0F0Fu) | (h & 0x30303030u);
+        hi[2 * w] = ((a >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+        lo[2 * w + 1] = (b & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+        hi[2 * w + 1] = ((b >> 4) & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+    }
+}
+
+// ---- per-element decode of a GGUF row (the reference variant; byte loads) -------------------
+// Same expressions as quant.cpp; contraction is off in every caller.
+__device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, uint32_t i) {
+#pragma clang fp contract(off)
+    switch (type) {
+        case kF32: {
+            uint32_t u = (uint32_t)row[4 * i] | ((uint32_t)row[4 * i + 1] << 8) | ((uint32_t)row[4 * i + 2] << 16) |
+                         ((uint32_t)row[4 * i + 3] << 24);
+            return __uint_as_float(u);
+        }
+        case kQ4_0: {
+            const uint8_t* blk = row + (i / 32) * 18;
+            const uint32_t e = i % 32;
+            const float d = h2f(ld_u16(blk));
+            const uint8_t b = blk[2 + (e & 15)];
+            const int q = (int)(e < 16 ? (b & 15) : (b >> 4)) - 8;
+            return (float)q * d;
+        }
+        case kQ8_0: {
+            const uint8_t* blk = row + (i / 32) * 34;
+            const float d = h2f(ld_u16(blk));
+            return (float)(int8_t)blk[2 + i % 32] * d;
+        }
+        case kQ4_K: {
+            const uint8_t* blk = row + (i / 256) * 144;
+            const uint32_t e = i % 256, g = e / 64, hi = (e % 64) / 32, l = e % 32;
+            const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+            const uint8_t* s = blk + 4;
+            const uint32_t j = 2 * g + hi;
+            uint32_t sc, m;
+            if (j < 4) {
+                sc = s[j] & 63;
+                m = s[j + 4] & 63;
+            } else {
+                sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+            }
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            const uint8_t qb = blk[16 + 32 * g + l];
+            const uint32_t q = hi ? (qb >> 4) : (qb & 15);
+            return d1 * (float)q - m1;
+        }
+        case kQ6_K: {
+            const uint8_t* blk = row + (i / 256) * 210;
+            const uint32_t e = i % 256, n = e / 128, r = e % 128, k = r / 32, l = r % 32;
+            const float d = h2f(ld_u16(blk + 208));
+            const uint8_t lb = blk[64 * n + l + 32 * (k & 1)];
+            const uint32_t lo4 = k < 2 ? (lb & 15) : (lb >> 4);
+            const uint32_t hi2 = (blk[128 + 32 * n + l] >> (2 * k)) & 3;
+            const int q = (int)(lo4 | (hi2 << 4)) - 32;
+            const float sc = (float)(int8_t)blk[192 + 8 * n + l / 16 + 2 * k];
+            return d * sc * (float)q;
+        }
+        default:
+            return 0.0f;
+    }
+}
+
+}  // namespace halo_mi::dev

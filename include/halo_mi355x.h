@@ -1,0 +1,192 @@
+/*
+ * halo_mi355x: MI355X (gfx950) quantized matrix-multiply backend, C ABI.
+ *
+ * This is the seam between host code and the hand-written HIP kernels. It replaces the HIP
+ * backend's launcher seam of the reference (backends/hip/src/launch.h:16-37:
+ * `int launch_gemv_*(const kern::GemvParams&, const kern::Launch&, void* stream)`, returning
+ * the hipError_t as an int). Every entry point takes plain pointers, sizes and a hipStream_t
+ * passed as `void*`, validates its arguments on the host, enqueues work, and returns a status
+ * code; no exception crosses the ABI. halo_mi_last_error() gives the message of the last
+ * failing call on the calling thread.
+ *
+ * Device pointers are HIP device memory on the current device. `stream` may be NULL (the
+ * null stream). Work is asynchronous: outputs are valid after the stream is synchronized.
+ *
+ * Status codes follow the reference's error mapping (include/halo/backend/backend.h:24-26):
+ * shape / alias / range / alignment -> HALO_MI_E_KERNEL, dtype or limit -> HALO_MI_E_UNSUPPORTED,
+ * unknown variant id -> HALO_MI_E_CONFIG, allocation -> HALO_MI_E_MEMORY, a HIP runtime error
+ * -> HALO_MI_E_DEVICE.
+ */
+#ifndef HALO_MI355X_H
+#define HALO_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------- */
+enum {
+    HALO_MI_OK = 0,
+    HALO_MI_E_KERNEL = 1,      /* shape, alias, range or alignment problem */
+    HALO_MI_E_UNSUPPORTED = 2, /* weight type or limit not supported */
+    HALO_MI_E_CONFIG = 3,      /* unknown variant id */
+    HALO_MI_E_MEMORY = 4,      /* allocation failure */
+    HALO_MI_E_DEVICE = 5       /* HIP runtime / launch failure */
+};
+
+/* Message of the last failing call on this thread ("" when none). */
+const char* halo_mi_last_error(void);
+
+/* ---- weight types (ggml ids, include/halo/tensor/dtype.h:18-49) ------------------------- */
+enum {
+    HALO_MI_F32 = 0,
+    HALO_MI_Q4_0 = 2,
+    HALO_MI_Q8_0 = 8,
+    HALO_MI_Q4_K = 12,
+    HALO_MI_Q6_K = 14
+};
+
+/* ---- weight layouts ---------------------------------------------------------------------- */
+/*
+ * HALO_MI_LAYOUT_GGUF: rows of GGUF blocks exactly as in the file (w_stride bytes apart, any
+ *   alignment). What the reference imports (src/backend/hip_adapter.cpp:502-515).
+ * HALO_MI_LAYOUT_SLAB: the device layout written by halo_mi_repack_slab(). Rows are grouped
+ *   in slabs of 64; inside a slab every plane is slot-major and row-minor, so one wave's
+ *   load of a slot covers 64 rows contiguously. A slab has exactly 64 * row_bytes bytes; the
+ *   last slab of a matrix is zero-padded to 64 rows. The GGUF bytes are recoverable with
+ *   halo_mi_unpack_slab().
+ */
+enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
+
+/* Rows per slab. */
+#define HALO_MI_SLAB_ROWS 64u
+
+/* ---- gemv variants (append-only ids; 0 = default for the layout) ------------------------ */
+/*
+ * Counterpart of the reference's KernelChoice registry (backend.h:173-176, ids pinned by
+ * tests/unit/backend/test_hip_backend.cpp:925-981).
+ *   0 HALO_MI_GEMV_DEFAULT   GGUF layout -> gemv_gguf_ref; SLAB layout -> gemv_slab_auto.
+ *   1 HALO_MI_GEMV_GGUF_REF  GGUF layout, 8 lanes per output in cpu::detail::dot's order:
+ *                            bit-identical to the CPU backend.
+ *   2 HALO_MI_GEMV_SLAB      SLAB layout, wave64 row-per-lane weight stream, split-K inside
+ *                            the workgroup; n_vec 1..8. Within the summation bound.
+ *   3 HALO_MI_GEMM_SLAB_BF16 SLAB layout, bf16 MFMA GEMM (dequantized W and x rounded to
+ *                            bf16, fp32 accumulate); any n_vec.
+ *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8, else 3.
+ */
+enum {
+    HALO_MI_GEMV_DEFAULT = 0,
+    HALO_MI_GEMV_GGUF_REF = 1,
+    HALO_MI_GEMV_SLAB = 2,
+    HALO_MI_GEMM_SLAB_BF16 = 3,
+    HALO_MI_GEMV_SLAB_AUTO = 4
+};
+
+/*
+ * y[t][n] = sum_i x[t][i] * W[n][i] for t < n_vec, n < rows, i < cols.
+ * Replaces backend::GemvArgs + Backend::gemv (include/halo/backend/backend.h:283-314, :562)
+ * at the launcher level, as kern::GemvParams does (backends/hip/kernels/gemv.h:267-281).
+ *   w: device weights in `layout`; for GGUF, w_stride = bytes between rows (0 = row_bytes);
+ *      for SLAB, w_stride must be 0.
+ *   x: n_vec rows of cols fp32, x_stride floats apart (0 = cols).
+ *   y: n_vec rows of rows fp32, y_stride floats apart (0 = rows). y must not overlap x or w.
+ */
+typedef struct halo_mi_gemv_params {
+    uint32_t type;
+    uint32_t layout;
+    const void* w;
+    uint64_t w_stride;
+    const float* x;
+    uint64_t x_stride;
+    float* y;
+    uint64_t y_stride;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t n_vec;
+    uint32_t variant;
+} halo_mi_gemv_params;
+
+int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
+
+/*
+ * Fused FFN gate/up: out[t][n] = silu((Wg x_t)[n]) * (Wu x_t)[n], silu(v) = v / (1 + exp(-v)).
+ * The reference composes it as gemv(gate), gemv(up), swiglu (src/models/qwen35.cpp:789-805;
+ * backends/cpu/ops_basic.cpp:165-167); here both matmuls and the epilogue are one launch.
+ * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto,
+ * 2 = gemv kernel (n_vec <= 8), 3 = bf16 MFMA GEMM. out may not overlap x, Wg or Wu.
+ */
+typedef struct halo_mi_gate_up_params {
+    uint32_t type;
+    uint32_t layout;
+    const void* w_gate;
+    const void* w_up;
+    const float* x;
+    uint64_t x_stride;
+    float* out;
+    uint64_t out_stride;
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t n_vec;
+    uint32_t variant;
+} halo_mi_gate_up_params;
+
+int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream);
+
+/*
+ * Dequantize rows [first_row, first_row + n_rows) of W to fp32 (out rows out_stride floats
+ * apart, 0 = cols), bit-identical to tensor::dequantize_row (src/tensor/quant.cpp:430-435).
+ * Works on both layouts; it shares its unpacking code with the gemv/gemm kernels.
+ * The reference counterpart at the backend level is GET_ROWS (backend.h:254-263).
+ */
+int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t w_stride,
+                         uint32_t rows, uint32_t cols, uint32_t first_row, uint32_t n_rows,
+                         float* out, uint64_t out_stride, void* stream);
+
+/* ---- geometry ------------------------------------------------------------------------------ */
+/* Bytes of one GGUF row of `cols` elements (src/tensor/quant.cpp:411-418); 0 on error. */
+uint64_t halo_mi_row_bytes(uint32_t type, uint32_t cols);
+/* Bytes of the SLAB image of a rows x cols matrix (rows rounded up to 64); 0 on error. */
+uint64_t halo_mi_slab_bytes(uint32_t type, uint32_t rows, uint32_t cols);
+
+/* ---- upload and repack (north-star part (c)) ------------------------------------------------ */
+/*
+ * Device-side repack: GGUF rows (src_stride bytes apart, any alignment) -> SLAB image.
+ * Replaces the reference's load-time repack (src/tensor/repack.cpp:100-124, called from
+ * src/models/qwen35.cpp:324-346) with a layout for this backend's kernels.
+ */
+int halo_mi_repack_slab(uint32_t type, const void* src, uint64_t src_stride, uint32_t rows,
+                        uint32_t cols, void* dst, void* stream);
+/* Exact inverse on the device: SLAB image -> GGUF rows (dst_stride bytes apart, 0 = dense). */
+int halo_mi_unpack_slab(uint32_t type, const void* src, uint32_t rows, uint32_t cols, void* dst,
+                        uint64_t dst_stride, void* stream);
+/* Host versions of the same two maps (identical bytes). */
+int halo_mi_repack_slab_host(uint32_t type, const void* src, uint64_t src_stride, uint32_t rows,
+                             uint32_t cols, void* dst);
+int halo_mi_unpack_slab_host(uint32_t type, const void* src, uint32_t rows, uint32_t cols,
+                             void* dst, uint64_t dst_stride);
+/*
+ * Upload from host memory (e.g. the mmap'd GGUF tensor, GgufFile::tensor_data,
+ * src/model/gguf.cpp:540-549) straight into a SLAB image on the device. Streams the rows in
+ * chunks of about `chunk_bytes` (0 = 64 MiB) through one device staging buffer and repacks
+ * each chunk on the device; the call returns after the last chunk has been repacked.
+ * Replaces Backend::import_host_readonly's device copy (src/backend/hip_adapter.cpp:502-515)
+ * plus the loader's repack step.
+ */
+int halo_mi_upload_slab(uint32_t type, const void* host_src, uint64_t src_stride, uint32_t rows,
+                        uint32_t cols, void* dst, uint64_t chunk_bytes, void* stream);
+
+/* ---- synthetic inputs (no reference counterpart: the reference has no quantizer) ----------- */
+/* Portable SplitMix64 + Box-Muller normal fill: out[i] = mean + std * N(0, 1), seed-determined. */
+void halo_mi_fill_normal(uint64_t seed, float* out, uint64_t n, float mean, float std);
+/* fp32 -> GGUF blocks for Q4_0 / Q8_0 / Q4_K / Q6_K; n must be a multiple of the block size.
+ * `threads` = 0 uses all host threads. Deterministic for any thread count. */
+int halo_mi_quantize(uint32_t type, const float* src, uint64_t n, void* dst, uint32_t threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,339 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Mirrors the reference's GEMV/GEMM tests (tests/unit/hip/test_hip_gemv.cpp:31-323): random
+valid blocks with a subnormal fp16 scale in every row, an unaligned row stride and start,
+strided x / y views with sentinels in the padding, and acceptance either bitwise (the
+reference-order variant, and every dequantized weight) or within a derived bound.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import (F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
+                     gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 999.0
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def dense_of(buf, t, rows, cols, stride, offset):
+    rb = row_bytes(t, cols)
+    return np.concatenate([buf[offset + r * stride: offset + r * stride + rb] for r in range(rows)])
+
+
+def slab_of(hl, dev, t, dense, rows, cols):
+    """SLAB image built on the device from dense GGUF rows."""
+    import torch
+
+    src = to_dev(dense, dev)
+    dst = torch.empty(hl.slab_bytes(t, rows, cols), dtype=torch.uint8, device=dev)
+    hl.repack_slab(t, src, rows, cols, dst)
+    return dst
+
+
+def strided_xy(dev, x, rows, x_pad, y_pad):
+    import torch
+
+    n_vec, cols = x.shape
+    xs, ys = cols + x_pad, rows + y_pad
+    xh = np.full((n_vec, xs), 12345.0, np.float32)
+    xh[:, :cols] = x
+    xd = to_dev(xh, dev)
+    yd = torch.full((n_vec, ys), SENTINEL, dtype=torch.float32, device=dev)
+    return xd, xs, yd, ys
+
+
+CASES = [
+    # (rows, cols, n_vec, stride_pad, offset, x_pad, y_pad): test_hip_gemv.cpp:213-230 shapes
+    (37, 512, 1, 0, 0, 0, 0),
+    (13, 5120, 3, 3, 1, 5, 3),
+]
+
+
+# ---- dequantization is bit-exact --------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("case", CASES)
+def test_dequant_gguf_and_slab_bitwise(hl, oracle, dev, t, case):
+    import torch
+
+    rows, cols, _, pad, off, _, _ = case
+    say("dequant", NAMES[t], rows, cols, pad, off)
+    buf, stride = make_weights(t, rows, cols, seed=rows + cols + t, stride_pad=pad, offset=off)
+    ref = oracle.dequantize_rows(t, buf[off:], rows, cols, stride)
+    wd = to_dev(buf, dev)
+    out = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+    hl.dequant_rows(t, hl.Layout.GGUF, wd.data_ptr() + off, rows, cols, out, w_stride=stride)
+    assert isclose_bits(host(out), ref), "GGUF dequant differs from tensor::dequantize_row"
+    slab = slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, off), rows, cols)
+    out2 = torch.full((rows, cols), -1.0, dtype=torch.float32, device=dev)
+    hl.dequant_rows(t, hl.Layout.SLAB, slab, rows, cols, out2)
+    assert isclose_bits(host(out2), ref), "SLAB dequant differs from tensor::dequantize_row"
+    # a row range in the middle of a slab
+    if rows > 5:
+        part = torch.empty((3, cols), dtype=torch.float32, device=dev)
+        hl.dequant_rows(t, hl.Layout.SLAB, slab, rows, cols, part, first_row=2, n_rows=3)
+        assert isclose_bits(host(part), ref[2:5])
+
+
+# ---- repack / unpack / upload -------------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+def test_repack_device_equals_host_and_unpacks(hl, dev, t):
+    import torch
+
+    rows, cols = 70, 768 if t in (Q4_K, Q6_K) else 544
+    say("repack", NAMES[t], rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=5 + t, stride_pad=5, offset=3)
+    dense = dense_of(buf, t, rows, cols, stride, 3)
+    host_slab = hl.repack_slab_host(t, dense, rows, cols)
+    wd = to_dev(buf, dev)
+    slab = torch.full((hl.slab_bytes(t, rows, cols),), 0xAB, dtype=torch.uint8, device=dev)
+    hl.repack_slab(t, wd.data_ptr() + 3, rows, cols, slab, src_stride=stride)
+    assert np.array_equal(host(slab), host_slab)
+    back = torch.zeros(rows * row_bytes(t, cols), dtype=torch.uint8, device=dev)
+    hl.unpack_slab(t, slab, rows, cols, back)
+    assert np.array_equal(host(back), dense)
+    up = torch.zeros_like(slab)
+    hl.upload_slab(t, buf[3:], rows, cols, up, src_stride=stride, chunk_bytes=row_bytes(t, cols) * 64)
+    assert np.array_equal(host(up), host_slab)
+
+
+# ---- GEMV -------------------------------------------------------------------------------
+
+
+def run_gemv(hl, dev, t, w, layout, x, rows, cols, variant, x_pad=0, y_pad=0, w_stride=0):
+    xd, xs, yd, ys = strided_xy(dev, x, rows, x_pad, y_pad)
+    hl.gemv(t, w, xd, yd, rows, cols, x.shape[0], layout=layout, w_stride=w_stride, x_stride=xs, y_stride=ys,
+            variant=variant)
+    y = host(yd)
+    assert np.all(y[:, rows:] == SENTINEL), "y padding overwritten"
+    return y[:, :rows]
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES + (F32,))
+@pytest.mark.parametrize("case", CASES)
+def test_gemv_gguf_ref_bitwise(hl, oracle, dev, t, case):
+    rows, cols, n_vec, pad, off, xp, yp = case
+    if t == F32:
+        cols, pad, off = 100, 4, 4  # dot tail (100 % 8) and 4-byte aligned rows
+    say("gemv_gguf_ref", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=100 + t + rows, stride_pad=pad, offset=off)
+    x = np.random.default_rng(1000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    ref = oracle.matmul(t, buf[off:], rows, cols, x, w_stride=stride)
+    wd = to_dev(buf, dev)
+    y = run_gemv(hl, dev, t, wd.data_ptr() + off, hl.Layout.GGUF, x, rows, cols, hl.Variant.GGUF_REF, xp, yp, stride)
+    assert isclose_bits(y, ref), "reference-order gemv is not bitwise cpu::matmul"
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("case", CASES + [(130, 1024, 4, 0, 0, 1, 2), (64, 256, 6, 0, 0, 0, 0)])
+def test_gemv_slab_within_bound(hl, oracle, dev, t, case):
+    rows, cols, n_vec, pad, off, xp, yp = case
+    say("gemv_slab", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=200 + t + rows, stride_pad=pad, offset=off)
+    dense = dense_of(buf, t, rows, cols, stride, off)
+    x = np.random.default_rng(2000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMV, xp, yp)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    slab gemv {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+
+
+# ---- GEMM (bf16 MFMA) ---------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("case", [(37, 5120, 17, 0, 0, 5, 3), (16, 256, 2, 0, 0, 0, 0), (33, 768, 40, 0, 0, 0, 0),
+                                  (130, 1024, 130, 0, 0, 4, 1)])
+def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case):
+    rows, cols, n_vec, pad, off, xp, yp = case
+    say("gemm_bf16", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=300 + t + rows, stride_pad=pad, offset=off)
+    dense = dense_of(buf, t, rows, cols, stride, off)
+    x = np.random.default_rng(3000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    if xp % 4:
+        xp += 4 - xp % 4  # the MFMA path wants 16-byte aligned x rows
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMM_BF16, xp, yp)
+    err = np.abs(y.astype(np.float64) - ref)
+    tol = gemm_tol(oracle, t, dense, rows, cols, x)
+    print(f"    gemm vs cpu: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    emu, etol = gemm_emulated(oracle, t, dense, rows, cols, x)
+    eerr = np.abs(y.astype(np.float64) - emu)
+    print(f"    gemm vs bf16-exact products: worst |d|/bound = {max_ratio(eerr, etol):.4f}")
+    assert np.all(eerr <= etol)
+
+
+# ---- fused gate/up + SwiGLU ---------------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q6_K, Q4_0, Q8_0))
+@pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3)])
+def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
+    import torch
+
+    rows, cols = 96, 1024
+    say("gate_up", NAMES[t], rows, cols, n_vec, variant)
+    bg, sg = make_weights(t, rows, cols, seed=400 + t)
+    bu, su = make_weights(t, rows, cols, seed=500 + t)
+    dg, du = dense_of(bg, t, rows, cols, sg, 0), dense_of(bu, t, rows, cols, su, 0)
+    x = np.random.default_rng(4000 + n_vec).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    ref = oracle.gate_up_swiglu(t, dg, du, rows, cols, x)
+    g = oracle.matmul(t, dg, rows, cols, x)
+    u = oracle.matmul(t, du, rows, cols, x)
+    sgd, sud = slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols)
+    out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gate_up_swiglu(t, sgd, sud, to_dev(x, dev), out, rows, cols, n_vec, variant=variant)
+    y = host(out)
+    if variant == 2:
+        tg, tu = slab_gemv_tol(oracle, t, dg, rows, cols, x), slab_gemv_tol(oracle, t, du, rows, cols, x)
+    else:
+        tg, tu = gemm_tol(oracle, t, dg, rows, cols, x), gemm_tol(oracle, t, du, rows, cols, x)
+    tol = swiglu_tol(g, u, tg, tu, ref)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    gate_up worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+
+
+# ---- host validation: error codes (test_hip_gemv.cpp:285-323) -------------------------------
+
+
+def test_gemv_rejects_bad_arguments(hl, dev):
+    import torch
+
+    w = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    x = torch.zeros(128, dtype=torch.float32, device=dev)
+    y = torch.zeros(64, dtype=torch.float32, device=dev)
+
+    def code(**kw):
+        args = dict(t=Q8_0, w=w, x=x, y=y, rows=2, cols=128, n_vec=1, layout=hl.Layout.GGUF, variant=0)
+        args.update(kw)
+        t = args.pop("t")
+        try:
+            hl.gemv(t, args.pop("w"), args.pop("x"), args.pop("y"), args.pop("rows"), args.pop("cols"),
+                    args.pop("n_vec"), **args)
+        except hl.HaloError as e:
+            return e.code, str(e)
+        return None, ""
+
+    assert code()[0] is None  # valid baseline
+    assert code(t=3)[0] == hl.ErrorCode.Unsupported  # Q4_1: not on this path
+    c, msg = code(cols=100)
+    assert c == hl.ErrorCode.Kernel and "multiple of the block size 32" in msg
+    c, msg = code(y=w.data_ptr() + 16)
+    assert c == hl.ErrorCode.Kernel and "y overlaps w" in msg
+    assert code(variant=9)[0] == hl.ErrorCode.Config
+    assert code(variant=hl.Variant.SLAB_GEMV)[0] == hl.ErrorCode.Config  # GGUF bytes, SLAB kernel
+    c, msg = code(t=F32, cols=64, w=w.data_ptr() + 2)
+    assert c == hl.ErrorCode.Kernel and "4-byte aligned" in msg
+    c, msg = code(layout=hl.Layout.SLAB, w_stride=300)
+    assert c == hl.ErrorCode.Kernel
+    c, msg = code(n_vec=2, x_stride=64)
+    assert c == hl.ErrorCode.Kernel and "x row stride" in msg
+    torch.cuda.synchronize()
+
+
+# ---- BASELINE shapes (full size) ------------------------------------------------------------
+
+
+def synth(hl, t, rows, cols, seed, outliers=0.0):
+    from helpers import synth_matrix
+
+    return synth_matrix(hl, t, rows, cols, seed, outlier_cols=outliers)
+
+
+@pytest.mark.parametrize("t,rows,cols,seed,outliers", [
+    (Q4_K, 17408, 5120, 2, 0.0),     # config 2: FFN gate/up shape
+    (Q6_K, 5120, 17408, 3, 0.0),     # config 3: ffn_down
+    (Q4_0, 4096, 4096, 0, 0.0),      # config 1
+])
+@pytest.mark.parametrize("n_vec", [1, 4])
+def test_baseline_shapes_gemv(hl, oracle, dev, t, rows, cols, seed, outliers, n_vec):
+    say("baseline gemv", NAMES[t], rows, cols, n_vec)
+    wq = synth(hl, t, rows, cols, seed, outliers)
+    x = hl.fill_normal(seed + 1000, n_vec * cols).reshape(n_vec, cols)
+    ref = oracle.matmul(t, wq, rows, cols, x)
+    slab = slab_of(hl, dev, t, wq, rows, cols)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.DEFAULT)
+    tol = slab_gemv_tol(oracle, t, wq, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    {NAMES[t]} {rows}x{cols} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}, "
+          f"max rel err = {float(np.max(err / (np.abs(ref) + 1e-6))):.2e}")
+    assert np.all(err <= tol)
+
+
+def test_baseline_q6_k_head(hl, oracle, dev):
+    """config 3b: 151936 x 5120 Q6_K with 1% of the columns scaled x8."""
+    t, rows, cols = Q6_K, 151936, 5120
+    say("baseline head", rows, cols)
+    wq = synth(hl, t, rows, cols, 3, 0.01)
+    x = hl.fill_normal(1003, cols).reshape(1, cols)
+    ref = oracle.matmul(t, wq, rows, cols, x)
+    slab = slab_of(hl, dev, t, wq, rows, cols)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.DEFAULT)
+    tol = slab_gemv_tol(oracle, t, wq, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    head worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    assert int(np.argmax(y[0])) == int(np.argmax(ref[0])) or abs(float(y[0].max() - ref[0].max())) <= tol.max()
+
+
+@pytest.mark.parametrize("n_vec", [2, 8, 64, 512])
+def test_baseline_gate_up(hl, oracle, dev, n_vec):
+    """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices; the oracle checks the
+    first 512 output columns (rows of W are independent)."""
+    import torch
+
+    t, rows, cols, chk = Q4_K, 17408, 5120, 512
+    say("baseline gate_up", n_vec)
+    wg = synth(hl, t, rows, cols, 4)
+    wu = synth(hl, t, rows, cols, 44)
+    x = hl.fill_normal(1004, n_vec * cols).reshape(n_vec, cols)
+    rb = row_bytes(t, cols)
+    ref = oracle.gate_up_swiglu(t, wg[:chk * rb], wu[:chk * rb], chk, cols, x)
+    g = oracle.matmul(t, wg[:chk * rb], chk, cols, x)
+    u = oracle.matmul(t, wu[:chk * rb], chk, cols, x)
+    out = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
+    hl.gate_up_swiglu(t, slab_of(hl, dev, t, wg, rows, cols), slab_of(hl, dev, t, wu, rows, cols), to_dev(x, dev), out,
+                      rows, cols, n_vec)
+    y = host(out)[:, :chk]
+    if n_vec <= 8:
+        tg = slab_gemv_tol(oracle, t, wg[:chk * rb], chk, cols, x)
+        tu = slab_gemv_tol(oracle, t, wu[:chk * rb], chk, cols, x)
+    else:
+        tg = gemm_tol(oracle, t, wg[:chk * rb], chk, cols, x)
+        tu = gemm_tol(oracle, t, wu[:chk * rb], chk, cols, x)
+    tol = swiglu_tol(g, u, tg, tu, ref)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    gate_up M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}, "
+          f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
+    assert np.all(err <= tol)
+    assert np.all(np.isfinite(host(out)))

@@ -1,0 +1,332 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker of the HIP path.
+
+Every check here is independent of the oracle's own formulas: known-answer blocks from the
+reference's tests, literal decodings of the block formats, a library routine (numpy's fp16
+widening), closed forms, brute force in fp64, and invariants of cpu::matmul.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+from helpers import F32, Q4_0, Q4_K, Q6_K, Q8_0, U, depth_cpu
+
+
+def f16_bytes(v: float) -> bytes:
+    return np.array([v], dtype=np.float16).tobytes()
+
+
+# ---- fp16 -> fp32 (include/halo/tensor/fp16.h:19-37) -------------------------------------
+
+
+def fp16_ldexp(h: int) -> float:
+    """Independent definition (tests/unit/tensor/test_fp16.cpp:17-30 of the reference)."""
+    sign = -1.0 if h >> 15 else 1.0
+    exp = (h >> 10) & 0x1F
+    mant = h & 0x3FF
+    if exp == 0:
+        return sign * math.ldexp(mant, -24)
+    if exp == 31:
+        return sign * math.inf if mant == 0 else math.nan
+    return sign * math.ldexp(mant | 0x400, exp - 25)
+
+
+def test_fp16_all_patterns_widen_exactly(oracle):
+    lib = oracle.lib()
+    got = np.array([lib.oracle_fp16_to_fp32(h) for h in range(65536)], dtype=np.float32)
+    npy = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    for h in range(65536):
+        ref = fp16_ldexp(h)
+        if math.isnan(ref):
+            assert math.isnan(got[h]) and (np.signbit(got[h]) == bool(h >> 15)), hex(h)
+        else:
+            assert float(got[h]) == ref and np.signbit(got[h]) == bool(h >> 15), hex(h)
+    # numpy's widening is exact too: identical bits except NaN payload quieting
+    nan = np.isnan(npy)
+    assert np.array_equal(got[~nan].view(np.uint32), npy[~nan].view(np.uint32))
+    # NaN: sign and payload kept, quiet bit set
+    for h in (0x7C01, 0xFC01, 0x7E00, 0x7D55):
+        bits = struct.unpack("<I", struct.pack("<f", got[h]))[0]
+        assert bits == ((h & 0x8000) << 16) | 0x7F800000 | ((h & 0x3FF) << 13) | 0x400000
+
+
+# ---- geometry (src/tensor/dtype.cpp:19-51, tests/unit/tensor/test_dequant.cpp:37-50) --------
+
+
+def test_row_bytes_geometry_and_checks(oracle):
+    assert oracle.row_bytes(F32, 5120) == 20480
+    assert oracle.row_bytes(Q6_K, 5120) == 20 * 210
+    assert oracle.row_bytes(Q4_0, 5120) == 160 * 18
+    assert oracle.row_bytes(Q4_K, 5120) == 2880
+    assert oracle.row_bytes(Q6_K, 17408) == 14280
+    assert oracle.row_bytes(Q8_0, 0) == 0
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.row_bytes(Q4_K, 100)
+    assert e.value.code == oracle.EMODEL
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.row_bytes(F32, -1)
+    assert e.value.code == oracle.EMODEL
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.row_bytes(5, 32)  # removed ggml id: refused, not a crash
+    assert e.value.code == oracle.EUNSUPPORTED
+
+
+# ---- known-answer blocks ----------------------------------------------------------------
+
+
+def test_q8_0_hand_built_block(oracle):
+    """tests/unit/tensor/test_dequant.cpp:52-59."""
+    blk = f16_bytes(0.5) + bytes((j - 16) & 0xFF for j in range(32))
+    y = oracle.dequantize_row(Q8_0, np.frombuffer(blk, np.uint8), 32)
+    assert np.array_equal(y, np.array([0.5 * (j - 16) for j in range(32)], np.float32))
+
+
+def test_q4_0_hand_built_block_nibble_order(oracle):
+    """tests/unit/tensor/test_dequant.cpp:61-72: low nibbles -> 0..15, high -> 16..31."""
+    blk = f16_bytes(2.0) + bytes(((15 - j) << 4) | j for j in range(16))
+    y = oracle.dequantize_row(Q4_0, np.frombuffer(blk, np.uint8), 32)
+    for j in range(16):
+        assert y[j] == 2.0 * (j - 8)
+        assert y[j + 16] == 2.0 * (7 - j)
+
+
+# Literal 6-bit (scale, min) decodings of one 12-byte Q4_K scales field, worked out by hand
+# from the ggml packing (bytes 0-3: sc[0..3] + top bits of sc[4..7]; bytes 4-7: m[0..3] + top
+# bits of m[4..7]; bytes 8-11: low nibbles of sc[4..7] | m[4..7]).
+Q4K_SCALES = bytes([0x41, 0x02, 0x83, 0xC4, 0x05, 0x46, 0x87, 0xC8, 0x9A, 0xBC, 0xDE, 0xF1])
+Q4K_SC_M = [(1, 5), (2, 6), (3, 7), (4, 8), (26, 9), (12, 27), (46, 45), (49, 63)]
+
+
+def q4k_block(d: float, dmin: float, scales: bytes, qs: bytes) -> np.ndarray:
+    assert len(scales) == 12 and len(qs) == 128
+    return np.frombuffer(f16_bytes(d) + f16_bytes(dmin) + scales + qs, np.uint8)
+
+
+def test_q4_k_literal_scale_min_table(oracle):
+    # quant bytes: group g byte l holds q_lo = l % 16 and q_hi = 15 - l % 16
+    qs = bytes(((15 - l % 16) << 4) | (l % 16) for g in range(4) for l in range(32))
+    y = oracle.dequantize_row(Q4_K, q4k_block(1.0, 0.5, Q4K_SCALES, qs), 256)
+    for e in range(256):
+        g, hi, l = e // 64, (e % 64) // 32, e % 32
+        sc, m = Q4K_SC_M[2 * g + hi]
+        q = (15 - l % 16) if hi else (l % 16)
+        assert y[e] == np.float32(sc * q - 0.5 * m), e
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q4_k_single_subblock_scale(oracle, j):
+    """Only sub-block j has sc = 1 (d = 1, dmin = 0, all quants 15): exactly its 32 elements
+    are 15, every other element is 0."""
+    s = bytearray(12)
+    if j < 4:
+        s[j] = 1
+    else:
+        s[j + 4] = 1
+    y = oracle.dequantize_row(Q4_K, q4k_block(1.0, 0.0, bytes(s), bytes([0xFF] * 128)), 256)
+    exp = np.zeros(256, np.float32)
+    exp[32 * j: 32 * j + 32] = 15.0
+    assert np.array_equal(y, exp)
+
+
+@pytest.mark.parametrize("j", range(8))
+def test_q4_k_single_subblock_min_high_bits(oracle, j):
+    """m[j] = 63 (for j >= 4 its top two bits live in byte j), d = 0, dmin = 1: sub-block j is
+    -63, the rest 0."""
+    s = bytearray(12)
+    if j < 4:
+        s[j + 4] = 63
+    else:
+        s[j] = 0xC0  # top bits of m[j] -> byte j (= j - 4 + 4)
+        s[j + 4] = 0xF0  # low nibble of m[j] in the high half of byte j + 4
+    y = oracle.dequantize_row(Q4_K, q4k_block(0.0, 1.0, bytes(s), bytes(128)), 256)
+    exp = np.zeros(256, np.float32)
+    exp[32 * j: 32 * j + 32] = -63.0
+    assert np.array_equal(y, -np.abs(y)) and np.array_equal(y, exp)
+
+
+def q6k_block(ql: bytes, qh: bytes, sc: bytes, d: float) -> np.ndarray:
+    return np.frombuffer(ql + qh + sc + f16_bytes(d), np.uint8)
+
+
+def test_q6_k_extremes(oracle):
+    ones = bytes([1] * 16)
+    y = oracle.dequantize_row(Q6_K, q6k_block(bytes(128), bytes(64), ones, 1.0), 256)
+    assert np.all(y == -32.0)  # q = 0 -> -32
+    y = oracle.dequantize_row(Q6_K, q6k_block(bytes([0xFF] * 128), bytes([0xFF] * 64), ones, 1.0), 256)
+    assert np.all(y == 31.0)  # q = 63 -> +31
+
+
+def test_q6_k_high_bit_quarters_and_nibble_halves(oracle):
+    """qh byte 0b11100100 gives quarter k the top bits k; ql low nibble 5 serves quarters 0-1,
+    high nibble 9 quarters 2-3: element value 16 k + nibble - 32 (d = 1, all scales 1)."""
+    ones = bytes([1] * 16)
+    y = oracle.dequantize_row(Q6_K, q6k_block(bytes([0x95] * 128), bytes([0b11100100] * 64), ones, 1.0), 256)
+    for e in range(256):
+        k = (e % 128) // 32
+        nib = 5 if k < 2 else 9
+        assert y[e] == 16 * k + nib - 32, e
+
+
+def test_q6_k_scale_index_map(oracle):
+    """Scales sc[i] = i + 1; q = 33 everywhere (value sc * 1): element e of half n, quarter k,
+    lane l uses scale 8 n + l // 16 + 2 k (16 weights per scale, in the order of the format)."""
+    sc = bytes(range(1, 17))
+    # q = 33 = 0b100001: low nibble 1, top bits 2
+    y = oracle.dequantize_row(Q6_K, q6k_block(bytes([0x11] * 128), bytes([0b10101010] * 64), sc, 1.0), 256)
+    expect = []
+    for n in range(2):
+        for k in range(4):
+            for l in range(32):
+                expect.append(8 * n + l // 16 + 2 * k + 1)
+    assert np.array_equal(y, np.array(expect, np.float32))
+
+
+def test_q6_k_negative_scale_and_fp16_subnormal_d(oracle):
+    d = 2.0 ** -20  # fp16 subnormal
+    sc = bytes([0x80] * 16)  # int8 -128
+    y = oracle.dequantize_row(Q6_K, q6k_block(bytes([0xFF] * 128), bytes([0xFF] * 64), sc, d), 256)
+    assert np.all(y == np.float32(d * -128 * 31))
+
+
+def test_dequant_rejects_bad_arguments(oracle):
+    """tests/unit/tensor/test_dequant.cpp:74-87."""
+    src = np.zeros(210, np.uint8)
+    dst = np.zeros(256, np.float32)
+    lib = oracle.lib()
+    assert lib.oracle_dequantize_row(Q6_K, src.ctypes.data, dst.ctypes.data, 255) == oracle.EMODEL
+    assert lib.oracle_dequantize_row(Q6_K, src.ctypes.data, dst.ctypes.data, -256) == oracle.EMODEL
+    assert lib.oracle_dequantize_row(16, src.ctypes.data, dst.ctypes.data, 256) == oracle.EUNSUPPORTED
+    assert lib.oracle_dequantize_row(Q6_K, src.ctypes.data, dst.ctypes.data, 256) == oracle.OK
+    assert oracle.dequantize_row(Q6_K, src, 0).size == 0
+
+
+# ---- dot order, vec_dot_row, matmul ----------------------------------------------------------
+
+
+def test_dot_fixed_8_lane_order_known_answer(oracle):
+    """cpu::detail::dot: partial j sums i = j mod 8, combined ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)),
+    then the tail. With a = [2^24, 1 x 7], b = 1: p0 + p4 = 2^24 + 1 rounds (ties to even) to
+    2^24, p1 + p5 = 2, right half = 4, total 2^24 + 6. A sequential sum would give 2^24."""
+    a = np.array([2.0 ** 24] + [1.0] * 7, np.float32)
+    assert oracle.dot(a, np.ones(8, np.float32)) == 16777222.0
+    # tail (n % 8 elements) is summed separately and added last: 2^24 + 6 + 1 -> 2^24 + 8
+    a9 = np.append(a, np.float32(1.0))
+    assert oracle.dot(a9, np.ones(9, np.float32)) == 16777224.0
+    # a sequential reduction would lose every 1: the order is really being pinned
+    s = np.float32(0)
+    for v in a:
+        s = np.float32(s + v)
+    assert s == 16777216.0
+
+
+def test_vec_dot_row_matches_sequential_double(oracle):
+    """tests/unit/tensor/test_dequant.cpp:90-112."""
+    rng = np.random.default_rng(7)
+    n = 1024
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+        row = rng.integers(0, 256, size=oracle.row_bytes(t, n), dtype=np.uint8)
+        row[1::2] &= 0xBF  # cap exponents: every fp16 field stays finite
+        x = ((rng.integers(0, 2001, n) - 1000) / 1000.0).astype(np.float32)
+        w = oracle.dequantize_row(t, row, n)
+        ref = 0.0
+        for i in range(n):
+            ref += float(w[i]) * float(x[i])
+        assert oracle.vec_dot_row(t, row, x) == np.float32(ref), t
+
+
+def brute_force_fp64(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    return x.astype(np.float64) @ w.astype(np.float64).T
+
+
+@pytest.mark.parametrize("t,k,n", [(1, 5120, 67), (7, 512, 37), (3, 256, 1)])
+def test_matmul_within_derived_bound_of_fp64(oracle, t, k, n):
+    """y within d_cpu * u * sum|x w| of the exact fp64 product (cf. test_ops.cpp:446-471)."""
+    rng = np.random.default_rng(10 + k)
+    for wt in (Q4_K, Q6_K, Q4_0, Q8_0):
+        row = rng.integers(0, 256, size=n * oracle.row_bytes(wt, k), dtype=np.uint8)
+        row[1::2] &= 0xBF
+        x = rng.standard_normal((t, k)).astype(np.float32)
+        y = oracle.matmul(wt, row, n, k, x)
+        w = oracle.dequantize_rows(wt, row, n, k)
+        ref = brute_force_fp64(w, x)
+        mag = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+        tol = (depth_cpu(k) + 1) * U * mag + 1e-38
+        assert np.all(np.abs(y - ref) <= tol), wt
+        # and each output is exactly the fixed-order dot of its dequantized row
+        for ti in range(t):
+            for ni in range(0, n, max(1, n // 5)):
+                assert y[ti, ni] == oracle.dot(x[ti], w[ni])
+
+
+def test_matmul_dense_equals_dequantized_bitwise(oracle):
+    rng = np.random.default_rng(3)
+    k, n = 512, 45
+    wq = rng.integers(0, 256, size=n * oracle.row_bytes(Q4_K, k), dtype=np.uint8)
+    wq[1::2] &= 0xBF
+    w = oracle.dequantize_rows(Q4_K, wq, n, k)
+    x = rng.standard_normal((4, k)).astype(np.float32)
+    assert np.array_equal(oracle.matmul(Q4_K, wq, n, k, x).view(np.uint32),
+                          oracle.matmul(F32, w.view(np.uint8), n, k, x).view(np.uint32))
+
+
+def test_matmul_padded_stride_equals_dense(oracle):
+    rng = np.random.default_rng(4)
+    k, n, pad = 512, 21, 3
+    rb = oracle.row_bytes(Q6_K, k)
+    wq = rng.integers(0, 256, size=n * rb, dtype=np.uint8)
+    wq[1::2] &= 0xBF
+    padded = np.zeros(n * (rb + pad), np.uint8)
+    for r in range(n):
+        padded[r * (rb + pad): r * (rb + pad) + rb] = wq[r * rb:(r + 1) * rb]
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    assert np.array_equal(oracle.matmul(Q6_K, wq, n, k, x), oracle.matmul(Q6_K, padded, n, k, x, w_stride=rb + pad))
+
+
+def test_matmul_thread_count_invariance(oracle):
+    """Bitwise identical for any thread count (thread_pool.h:8-10; test_ops.cpp:517-565)."""
+    rng = np.random.default_rng(12)
+    k, n = 768 // 256 * 256, 150
+    wq = rng.integers(0, 256, size=n * oracle.row_bytes(Q4_K, k), dtype=np.uint8)
+    wq[1::2] &= 0xBF
+    x = rng.standard_normal((9, k)).astype(np.float32)
+    base = oracle.matmul(Q4_K, wq, n, k, x, threads=1)
+    for th in (2, 3, 7, 16, 64):
+        assert np.array_equal(oracle.matmul(Q4_K, wq, n, k, x, threads=th).view(np.uint32), base.view(np.uint32)), th
+
+
+def test_partition_range_literal(oracle):
+    import ctypes
+
+    lib = oracle.lib()
+    got = []
+    for i in range(3):
+        b, e = ctypes.c_size_t(), ctypes.c_size_t()
+        lib.oracle_partition_range(10, 3, i, ctypes.byref(b), ctypes.byref(e))
+        got.append((b.value, e.value))
+    assert got == [(0, 4), (4, 7), (7, 10)]
+
+
+def test_swiglu_closed_forms(oracle):
+    g = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 88.0, -100.0], np.float32)
+    u = np.array([5.0, 2.0, 3.0, 1.0, 1.0, 0.5, 7.0], np.float32)
+    out = oracle.swiglu(g, u)
+    assert out[0] == 0.0
+    assert out[3] == np.float32(30.0)  # sigmoid(30) rounds to 1 in fp32
+    ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
+    # fp32 overflow of exp(100) makes silu(-100) exactly -0: an absolute floor covers it
+    assert np.all(np.abs(out - ref) <= 8 * U * np.abs(ref) + 1e-37)
+
+
+def test_gate_up_composition_equals_parts(oracle):
+    rng = np.random.default_rng(5)
+    k, n = 512, 40
+    wg = rng.integers(0, 256, size=n * oracle.row_bytes(Q4_K, k), dtype=np.uint8)
+    wu = rng.integers(0, 256, size=n * oracle.row_bytes(Q4_K, k), dtype=np.uint8)
+    wg[1::2] &= 0xBF
+    wu[1::2] &= 0xBF
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    out = oracle.gate_up_swiglu(Q4_K, wg, wu, n, k, x)
+    g = oracle.matmul(Q4_K, wg, n, k, x)
+    u = oracle.matmul(Q4_K, wu, n, k, x)
+    assert np.array_equal(out, oracle.swiglu(g, u))
