@@ -122,12 +122,32 @@ SIGNATURES = {
 }
 
 
+def hip_runtimes() -> list[str]:
+    """Paths of the HIP runtime libraries mapped into this process."""
+    with open("/proc/self/maps") as f:
+        return sorted({line.split()[-1] for line in f if "libamdhip64" in line})
+
+
 @functools.lru_cache(maxsize=None)
 def lib() -> ctypes.CDLL:
-    """The loaded library. Raises (never falls back) when it has not been built."""
+    """The loaded library. Raises (never falls back) when it has not been built.
+
+    The process must hold exactly one HIP runtime. torch bundles its own libamdhip64 (soname
+    libamdhip64.so.7, but its own libraries ask for it as "libamdhip64.so"), so if this library
+    were loaded first it would pull in /opt/rocm's copy and a later torch import would load a
+    second one: torch's streams and allocations would then reach the wrong runtime. Importing
+    torch first makes this library bind to torch's runtime by soname.
+    """
     if not _LIB_PATH.exists():
         raise RuntimeError(f"{_LIB_PATH} is missing: build it with `python -m halo_amd.build` (hipcc, gfx950)")
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     so = ctypes.CDLL(str(_LIB_PATH))
+    runtimes = hip_runtimes()
+    if len(runtimes) > 1:
+        raise RuntimeError(f"two HIP runtimes are loaded in this process: {runtimes}")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(so, name)
         fn.restype = res

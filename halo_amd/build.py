@@ -3,6 +3,8 @@
 The library is compiled with hipcc for gfx950 only. Flags:
   -fno-gpu-flush-denormals-to-zero   fp16/fp32 subnormal scales must survive (bit-exact dequant)
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
+  -mcode-object-version=5            loadable by the HIP runtime torch bundles (ROCm 7.0) as well
+                                     as /opt/rocm's (7.2)
 """
 from __future__ import annotations
 
@@ -25,6 +27,7 @@ HIP_FLAGS = [
     "-shared",
     "-pthread",
     "-fno-gpu-flush-denormals-to-zero",
+    "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
 ]

@@ -73,12 +73,19 @@ def gemv_mag(oracle, t: int, wbytes: np.ndarray, rows: int, cols: int, x: np.nda
     """sum_i |x_i| (|a_i| + |b_i| + 2 |off_i|) per output: the magnitude that bounds the rounding
     error of both the CPU dot and the SLAB kernels' factored sums (w = a - b; off = the offset
     the kernels take out of the quant, see oracle_dequant_terms)."""
+    ax = np.abs(np.asarray(x, np.float64).reshape(-1, cols))
     if t == F32:
         w = wbytes.view(np.float32).reshape(rows, cols).astype(np.float64)
-        return np.abs(x.astype(np.float64)) @ np.abs(w).T
-    a, b, off = oracle.dequant_terms(t, wbytes, rows, cols)
-    m = np.abs(a.astype(np.float64)) + np.abs(b.astype(np.float64)) + 2 * np.abs(off.astype(np.float64))
-    return np.abs(x.astype(np.float64)) @ m.T
+        return ax @ np.abs(w).T
+    rb = row_bytes(t, cols)
+    out = np.empty((ax.shape[0], rows), np.float64)
+    step = 4096  # rows per chunk: bounds the host memory of the full-size cases
+    for r0 in range(0, rows, step):
+        n = min(step, rows - r0)
+        a, b, off = oracle.dequant_terms(t, wbytes[r0 * rb:(r0 + n) * rb], n, cols)
+        m = np.abs(a.astype(np.float64)) + np.abs(b.astype(np.float64)) + 2 * np.abs(off.astype(np.float64))
+        out[:, r0:r0 + n] = ax @ m.T
+    return out
 
 
 def depth_cpu(cols: int) -> int:

@@ -164,3 +164,11 @@ def test_host_repack_rejects(hl):
     with pytest.raises(hl.HaloError) as e:
         hl.repack_slab_host(Q4_K, np.zeros(144, np.uint8), 1, 100)
     assert e.value.code == hl.ErrorCode.Kernel
+
+
+def test_single_hip_runtime_in_process(hl):
+    """Regression: loading the library before torch used to map /opt/rocm's HIP runtime next to
+    torch's bundled copy, so torch's streams reached the wrong runtime."""
+    import torch  # noqa: F401
+
+    assert len(hl._lib.hip_runtimes()) == 1
