@@ -27,6 +27,7 @@ from ._lib import (  # noqa: F401
     repack_slab_host,
     row_bytes,
     slab_bytes,
+    swiglu,
     unpack_slab,
     unpack_slab_host,
     upload_slab,

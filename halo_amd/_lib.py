@@ -109,6 +109,7 @@ SIGNATURES = {
     "halo_mi_last_error": (ctypes.c_char_p, []),
     "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
+    "halo_mi_swiglu": (_INT, [_VP, _U64, _VP, _U64, _VP, _U64, _U32, _U32, _VP]),
     "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
     "halo_mi_row_bytes": (_U64, [_U32, _U32]),
     "halo_mi_slab_bytes": (_U64, [_U32, _U32, _U32]),
@@ -243,6 +244,12 @@ def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: in
     p = _GateUpParams(int(t), int(layout), _ptr(w_gate), _ptr(w_up), _ptr(x), int(x_stride), _ptr(out), int(out_stride),
                       int(rows), int(cols), int(n_vec), int(variant))
     _check(lib().halo_mi_gate_up_swiglu(ctypes.byref(p), _stream(stream)))
+
+
+def swiglu(gate, up, out, rows: int, cols: int, *, gate_stride: int = 0, up_stride: int = 0, out_stride: int = 0,
+           stream=None) -> None:
+    _check(lib().halo_mi_swiglu(_ptr(gate), int(gate_stride), _ptr(up), int(up_stride), _ptr(out), int(out_stride),
+                                int(rows), int(cols), _stream(stream)))
 
 
 def dequant_rows(t: int, layout: int, w, rows: int, cols: int, out, *, first_row: int = 0, n_rows: int | None = None,

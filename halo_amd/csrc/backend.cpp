@@ -1,0 +1,505 @@
+// The MI355X backend: halo_mi355x_backend.hpp over the halo_mi355x C ABI.
+//
+// Host validation follows the reference CPU/HIP adapters (src/backend/cpu_backend.cpp:98-162
+// Resolver; src/backend/hip_adapter.cpp:612-632 gemv) on device addresses: ownership, range,
+// alignment, stride and aliasing are checked before anything is enqueued.
+#include "../../include/halo_mi355x_backend.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <cstdarg>
+#include <cstdio>
+#include <limits>
+
+#include "../../include/halo_mi355x.h"
+
+namespace halo_mi::backend {
+
+namespace {
+
+[[noreturn]] void fail(ErrorCode code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+void fail(ErrorCode code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    throw Error(code, buf);
+}
+
+#define CHECK(cond, code, ...)              \
+    do {                                    \
+        if (!(cond)) fail((code), __VA_ARGS__); \
+    } while (0)
+
+// C-ABI status -> ErrorCode, with the library's message.
+void check_abi(int rc) {
+    if (rc == HALO_MI_OK) return;
+    const ErrorCode code = rc == HALO_MI_E_KERNEL        ? ErrorCode::Kernel
+                           : rc == HALO_MI_E_UNSUPPORTED ? ErrorCode::Unsupported
+                           : rc == HALO_MI_E_CONFIG      ? ErrorCode::Config
+                           : rc == HALO_MI_E_MEMORY      ? ErrorCode::Memory
+                                                         : ErrorCode::Device;
+    throw Error(code, halo_mi_last_error());
+}
+
+constexpr std::uint64_t kF32 = 4;
+
+std::uint64_t mul_u64(std::uint64_t a, std::uint64_t b, const char* op, const char* what) {
+    CHECK(a == 0 || b <= std::numeric_limits<std::uint64_t>::max() / a, ErrorCode::Kernel, "%s: %s size overflows", op, what);
+    return a * b;
+}
+
+const char* type_name(DType t) {
+    switch (t) {
+        case DType::F32: return "F32";
+        case DType::Q4_0: return "Q4_0";
+        case DType::Q8_0: return "Q8_0";
+        case DType::Q4_K: return "Q4_K";
+        case DType::Q6_K: return "Q6_K";
+    }
+    return "?";
+}
+
+// ---- buffers --------------------------------------------------------------------------------
+
+struct SlabMeta {
+    DType type = DType::F32;
+    std::uint32_t rows = 0, cols = 0;
+};
+
+class DeviceBuffer final : public Buffer {
+public:
+    DeviceBuffer(const Backend* owner, void* mem, std::uint64_t bytes, Tier tier, bool writable, bool host, WeightLayout layout,
+                 SlabMeta meta)
+        : owner_(owner), mem_(mem), bytes_(bytes), tier_(tier), writable_(writable), host_(host), layout_(layout), meta_(meta) {}
+    ~DeviceBuffer() override {
+        if (host_) (void)hipHostFree(mem_);
+        else (void)hipFree(mem_);
+    }
+    std::uint64_t bytes() const noexcept override { return bytes_; }
+    Tier tier() const noexcept override { return tier_; }
+    const Backend* backend() const noexcept override { return owner_; }
+    bool writable() const noexcept override { return writable_; }
+    const std::byte* host_data() const noexcept override { return host_ ? static_cast<const std::byte*>(mem_) : nullptr; }
+    std::byte* host_ptr() const noexcept override { return host_ && writable_ ? static_cast<std::byte*>(mem_) : nullptr; }
+    void* device_ptr() const noexcept override { return mem_; }
+    WeightLayout layout() const noexcept override { return layout_; }
+    const SlabMeta& meta() const noexcept { return meta_; }
+
+private:
+    const Backend* owner_;
+    void* mem_;
+    std::uint64_t bytes_;
+    Tier tier_;
+    bool writable_, host_;
+    WeightLayout layout_;
+    SlabMeta meta_;
+};
+
+// ---- streams --------------------------------------------------------------------------------
+
+class MiBackend;
+
+class HipStream final : public Stream {
+public:
+    HipStream(MiBackend* owner, hipStream_t s) : owner_(owner), s_(s) {}
+    ~HipStream() override { (void)hipStreamDestroy(s_); }
+    void submit() override {}
+    void wait() override;
+    void abort() noexcept override { (void)hipStreamSynchronize(s_); }
+    void* native() const noexcept override { return s_; }
+    const MiBackend* owner() const noexcept { return owner_; }
+
+private:
+    MiBackend* owner_;
+    hipStream_t s_;
+};
+
+// ---- operand resolution ---------------------------------------------------------------------
+
+enum class Access : std::uint8_t { Read, Write };
+
+struct Operand {
+    const char* name = "";
+    std::uint8_t* base = nullptr;  // device address of row 0
+    std::uint64_t stride = 0;      // bytes between rows
+    std::uint64_t extent = 0;      // bytes touched
+    const DeviceBuffer* buf = nullptr;
+};
+
+class Resolver {
+public:
+    Resolver(const Backend* self, const char* op) : self_(self), op_(op) {}
+
+    // rows x row_bytes at ref; `align` = required alignment of address and stride.
+    Operand get(const TensorRef& ref, std::uint64_t rows, std::uint64_t row_bytes, std::uint64_t align, Access access,
+                const char* name) const {
+        Operand o;
+        o.name = name;
+        o.stride = ref.row_stride != 0 ? ref.row_stride : row_bytes;
+        if ((rows == 0 || row_bytes == 0) && ref.empty()) return o;
+        CHECK(!ref.empty(), ErrorCode::Kernel, "%s: operand %s is empty", op_, name);
+        const auto* b = dynamic_cast<const DeviceBuffer*>(ref.buffer);
+        CHECK(b != nullptr && b->backend() == self_, ErrorCode::Kernel, "%s: operand %s belongs to another backend", op_, name);
+        CHECK(access == Access::Read || b->writable(), ErrorCode::Kernel, "%s: output %s is read-only", op_, name);
+        CHECK(rows <= 1 || o.stride >= row_bytes, ErrorCode::Kernel, "%s: operand %s row stride %llu < row bytes %llu", op_,
+              name, (unsigned long long)o.stride, (unsigned long long)row_bytes);
+        o.extent = rows == 0 ? 0 : mul_u64(rows - 1, o.stride, op_, name) + row_bytes;
+        CHECK(ref.offset <= b->bytes(), ErrorCode::Kernel, "%s: operand %s offset %llu past buffer end %llu", op_, name,
+              (unsigned long long)ref.offset, (unsigned long long)b->bytes());
+        const std::uint64_t avail = b->bytes() - ref.offset;
+        const std::uint64_t limit = ref.bytes != 0 ? ref.bytes : avail;
+        CHECK(limit <= avail, ErrorCode::Kernel, "%s: operand %s range exceeds buffer of %llu bytes", op_, name,
+              (unsigned long long)b->bytes());
+        CHECK(o.extent <= limit, ErrorCode::Kernel, "%s: operand %s needs %llu bytes, view has %llu", op_, name,
+              (unsigned long long)o.extent, (unsigned long long)limit);
+        o.base = static_cast<std::uint8_t*>(b->device_ptr()) + ref.offset;
+        o.buf = b;
+        CHECK(reinterpret_cast<std::uintptr_t>(o.base) % align == 0 && o.stride % align == 0, ErrorCode::Kernel,
+              "%s: operand %s is not %llu-byte aligned", op_, name, (unsigned long long)align);
+        return o;
+    }
+
+    Operand f32(const TensorRef& ref, std::uint64_t rows, std::uint64_t cols, Access access, const char* name) const {
+        return get(ref, rows, mul_u64(cols, kF32, op_, name), kF32, access, name);
+    }
+
+    // A SLAB weight operand: whole slabs of a buffer imported with import_weights.
+    Operand slab(const TensorRef& ref, DType type, std::uint32_t rows, std::uint32_t cols, const char* name) const {
+        Operand o;
+        o.name = name;
+        CHECK(!ref.empty(), ErrorCode::Kernel, "%s: operand %s is empty", op_, name);
+        const auto* b = dynamic_cast<const DeviceBuffer*>(ref.buffer);
+        CHECK(b != nullptr && b->backend() == self_, ErrorCode::Kernel, "%s: operand %s belongs to another backend", op_, name);
+        CHECK(b->layout() == WeightLayout::Slab, ErrorCode::Config, "%s: operand %s is not in the SLAB layout", op_, name);
+        const SlabMeta& m = b->meta();
+        CHECK(m.type == type && m.cols == cols, ErrorCode::Kernel, "%s: operand %s holds %s x %u, op asks %s x %u", op_, name,
+              type_name(m.type), m.cols, type_name(type), cols);
+        CHECK(ref.row_stride == 0, ErrorCode::Kernel, "%s: a SLAB operand has no row stride", op_);
+        const std::uint64_t sb = halo_mi_slab_bytes(static_cast<std::uint32_t>(type), HALO_MI_SLAB_ROWS, cols);
+        CHECK(sb != 0 && ref.offset % sb == 0, ErrorCode::Kernel, "%s: operand %s offset %llu is not a whole slab (%llu B)", op_,
+              name, (unsigned long long)ref.offset, (unsigned long long)sb);
+        const std::uint64_t first = ref.offset / sb * HALO_MI_SLAB_ROWS;
+        CHECK(first <= m.rows && rows <= m.rows - first, ErrorCode::Kernel, "%s: operand %s rows [%llu, %llu) out of %u", op_,
+              name, (unsigned long long)first, (unsigned long long)(first + rows), m.rows);
+        o.extent = halo_mi_slab_bytes(static_cast<std::uint32_t>(type), rows, cols);
+        CHECK(ref.bytes == 0 || ref.bytes >= o.extent, ErrorCode::Kernel, "%s: operand %s needs %llu bytes", op_, name,
+              (unsigned long long)o.extent);
+        o.base = static_cast<std::uint8_t*>(b->device_ptr()) + ref.offset;
+        o.buf = b;
+        return o;
+    }
+
+    void no_overlap(const Operand& out, const Operand& other) const {
+        if (out.extent == 0 || other.extent == 0) return;
+        const auto lo1 = reinterpret_cast<std::uintptr_t>(out.base), lo2 = reinterpret_cast<std::uintptr_t>(other.base);
+        CHECK(!(lo1 < lo2 + other.extent && lo2 < lo1 + out.extent), ErrorCode::Kernel, "%s: output %s overlaps operand %s",
+              op_, out.name, other.name);
+    }
+
+    const char* op() const noexcept { return op_; }
+
+private:
+    const Backend* self_;
+    const char* op_;
+};
+
+// ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
+
+constexpr std::array<VariantInfo, 8> kVariants{{
+    {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
+    {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
+    {kGemvSlab, "gemv_slab_w64", OpId::Gemv, {}},
+    {kGemmSlabBf16, "gemm_slab_bf16_mfma", OpId::Gemv, {}},
+    {kGemvSlabAuto, "gemv_slab_auto", OpId::Gemv, {}},
+    {kSwiglu, "swiglu_b256", OpId::Swiglu, {}},
+    {kGateUpGemv, "gate_up_gemv_w64", OpId::GateUpSwiglu, {}},
+    {kGateUpGemm, "gate_up_gemm_bf16_mfma", OpId::GateUpSwiglu, {}},
+}};
+
+bool has_variant(OpId op, std::uint32_t id) {
+    if (id == 0) return true;
+    return std::any_of(kVariants.begin(), kVariants.end(), [&](const VariantInfo& v) { return v.op == op && v.id == id; });
+}
+
+// ---- the backend ----------------------------------------------------------------------------
+
+class MiBackend final : public Backend {
+public:
+    explicit MiBackend(int device) : device_(device) {
+        int n = 0;
+        CHECK(hipGetDeviceCount(&n) == hipSuccess && device >= 0 && device < n, ErrorCode::Device,
+              "mi355x backend: no HIP device %d (%d visible)", device, n);
+        CHECK(hipSetDevice(device) == hipSuccess, ErrorCode::Device, "mi355x backend: hipSetDevice(%d) failed", device);
+        hipDeviceProp_t prop{};
+        if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+            name_ = prop.gcnArchName;
+            cus_ = prop.multiProcessorCount;
+        }
+    }
+
+    Kind kind() const noexcept override { return Kind::Hip; }
+    std::string describe() const override {
+        char buf[256];
+        std::snprintf(buf, sizeof buf, "mi355x (%s, %d CUs, device %d): SLAB wave64 gemv + bf16 MFMA gemm", name_.c_str(), cus_,
+                      device_);
+        return buf;
+    }
+    Limits limits() const noexcept override {
+        Limits l;
+        l.max_n_vec = std::numeric_limits<std::uint32_t>::max();
+        return l;
+    }
+    bool lost() const noexcept override { return lost_; }
+
+    void poison(bool kernel_fault) {
+        if (kernel_fault) poisoned_ = true;
+        else lost_ = true;
+    }
+
+    std::unique_ptr<Buffer> allocate(std::uint64_t bytes, Tier tier) override {
+        check_alive("allocate");
+        void* mem = nullptr;
+        const std::uint64_t n = std::max<std::uint64_t>(bytes, 1);
+        if (tier == Tier::Vram) {
+            CHECK(hipMalloc(&mem, n) == hipSuccess, ErrorCode::Memory, "mi355x backend: cannot allocate %llu bytes",
+                  (unsigned long long)bytes);
+            (void)hipMemset(mem, 0, n);  // zero-filled like the CPU backend's allocate
+            return std::make_unique<DeviceBuffer>(this, mem, bytes, tier, true, false, WeightLayout::Gguf, SlabMeta{});
+        }
+        CHECK(hipHostMalloc(&mem, n, hipHostMallocDefault) == hipSuccess, ErrorCode::Memory,
+              "mi355x backend: cannot allocate %llu pinned bytes", (unsigned long long)bytes);
+        std::memset(mem, 0, n);
+        return std::make_unique<DeviceBuffer>(this, mem, bytes, tier, true, true, WeightLayout::Gguf, SlabMeta{});
+    }
+
+    std::unique_ptr<Buffer> import_host(std::span<std::byte>) override {
+        // As the reference's HIP backend on a device (hip_adapter.cpp:495-500).
+        fail(ErrorCode::Unsupported, "mi355x backend: import_host is not supported on a device (copy into a backend buffer)");
+    }
+
+    std::unique_ptr<Buffer> import_host_readonly(std::span<const std::byte> bytes) override {
+        check_alive("import_host_readonly");
+        void* mem = nullptr;
+        const std::uint64_t n = std::max<std::uint64_t>(bytes.size(), 1);
+        CHECK(hipMalloc(&mem, n) == hipSuccess, ErrorCode::Memory, "mi355x backend: cannot allocate %llu bytes",
+              (unsigned long long)bytes.size());
+        if (!bytes.empty() && hipMemcpy(mem, bytes.data(), bytes.size(), hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(mem);
+            fail(ErrorCode::Device, "mi355x backend: weight upload failed");
+        }
+        return std::make_unique<DeviceBuffer>(this, mem, bytes.size(), Tier::Vram, false, false, WeightLayout::Gguf, SlabMeta{});
+    }
+
+    std::unique_ptr<Buffer> import_weights(std::span<const std::byte> gguf, DType type, std::uint32_t rows, std::uint32_t cols,
+                                           std::uint64_t row_stride) override {
+        check_alive("import_weights");
+        const auto t = static_cast<std::uint32_t>(type);
+        const std::uint64_t rb = halo_mi_row_bytes(t, cols);
+        CHECK(type != DType::F32 && rb != 0, ErrorCode::Unsupported, "import_weights: %s x %u has no SLAB layout", type_name(type),
+              cols);
+        const std::uint64_t stride = row_stride ? row_stride : rb;
+        CHECK(rows == 0 || gguf.size() >= (rows - 1) * stride + rb, ErrorCode::Kernel,
+              "import_weights: %zu bytes hold fewer than %u rows", gguf.size(), rows);
+        const std::uint64_t bytes = halo_mi_slab_bytes(t, rows, cols);
+        void* mem = nullptr;
+        CHECK(hipMalloc(&mem, std::max<std::uint64_t>(bytes, 1)) == hipSuccess, ErrorCode::Memory,
+              "import_weights: cannot allocate %llu bytes", (unsigned long long)bytes);
+        auto buf = std::make_unique<DeviceBuffer>(this, mem, bytes, Tier::Vram, false, false, WeightLayout::Slab,
+                                                  SlabMeta{type, rows, cols});
+        check_abi(halo_mi_upload_slab(t, gguf.data(), stride, rows, cols, mem, 0, nullptr));
+        return buf;
+    }
+
+    std::unique_ptr<Stream> create_stream() override {
+        check_alive("create_stream");
+        hipStream_t s = nullptr;
+        CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess, ErrorCode::Device,
+              "mi355x backend: cannot create a stream");
+        return std::make_unique<HipStream>(this, s);
+    }
+
+    void upload(Stream& s, TensorRef dst, std::span<const std::byte> src) override {
+        HipStream& st = stream(s, "upload");
+        const Resolver r(this, "upload");
+        const Operand d = r.get(dst, 1, src.size(), 1, Access::Write, "dst");
+        if (src.empty()) return;
+        CHECK(hipMemcpyAsync(d.base, src.data(), src.size(), hipMemcpyHostToDevice, (hipStream_t)st.native()) == hipSuccess,
+              ErrorCode::Device, "upload: hipMemcpyAsync failed");
+    }
+
+    void download(Stream& s, TensorRef src, std::span<std::byte> dst) override {
+        HipStream& st = stream(s, "download");
+        const Resolver r(this, "download");
+        const Operand o = r.get(src, 1, dst.size(), 1, Access::Read, "src");
+        if (dst.empty()) return;
+        CHECK(hipMemcpyAsync(dst.data(), o.base, dst.size(), hipMemcpyDeviceToHost, (hipStream_t)st.native()) == hipSuccess,
+              ErrorCode::Device, "download: hipMemcpyAsync failed");
+    }
+
+    std::span<const VariantInfo> variants(OpId op, std::string_view) const override {
+        auto first = std::find_if(kVariants.begin(), kVariants.end(), [&](const VariantInfo& v) { return v.op == op; });
+        auto last = std::find_if(first, kVariants.end(), [&](const VariantInfo& v) { return v.op != op; });
+        return {first, last};
+    }
+
+    void dequant_rows(Stream& s, const DequantRowsArgs& a) override {
+        HipStream& st = stream(s, "GET_ROWS");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kDequantRows, ErrorCode::Config,
+              "GET_ROWS: unknown kernel variant id %u", a.kernel.variant_id);
+        const Resolver r(this, "GET_ROWS");
+        const auto t = static_cast<std::uint32_t>(a.type);
+        const std::uint64_t rb = row_bytes(a.type, a.cols, r.op());
+        CHECK(a.first_row <= a.n_rows_table && a.n_rows <= a.n_rows_table - a.first_row, ErrorCode::Kernel,
+              "GET_ROWS: rows [%u, %u) out of %u", a.first_row, a.first_row + a.n_rows, a.n_rows_table);
+        const bool slab = !a.table.empty() && a.table.buffer->layout() == WeightLayout::Slab;
+        const Operand table = slab ? r.slab(a.table, a.type, a.n_rows_table, a.cols, "table")
+                                   : r.get(a.table, a.n_rows_table, rb, a.type == DType::F32 ? kF32 : 1, Access::Read, "table");
+        const Operand out = r.f32(a.out, a.n_rows, a.cols, Access::Write, "out");
+        r.no_overlap(out, table);
+        if (a.n_rows == 0 || a.cols == 0) return;
+        check_abi(halo_mi_dequant_rows(t, slab ? HALO_MI_LAYOUT_SLAB : HALO_MI_LAYOUT_GGUF, table.base, slab ? 0 : table.stride,
+                                       a.n_rows_table, a.cols, a.first_row, a.n_rows, reinterpret_cast<float*>(out.base),
+                                       out.stride / kF32, st.native()));
+    }
+
+    void gemv(Stream& s, const GemvArgs& a) override {
+        HipStream& st = stream(s, "MATMUL");
+        CHECK(has_variant(OpId::Gemv, a.kernel.variant_id), ErrorCode::Config, "MATMUL: unknown kernel variant id %u",
+              a.kernel.variant_id);
+        CHECK(a.norm_w.empty(), ErrorCode::Unsupported, "MATMUL: a fused norm (GemvArgs::norm_w) is Vulkan-only");
+        CHECK(a.gates.n_v == 0, ErrorCode::Unsupported, "MATMUL: the GDN gates epilogue (GemvArgs::gates) is Vulkan-only");
+        const Resolver r(this, "MATMUL");
+        const auto t = static_cast<std::uint32_t>(a.wtype);
+        const std::uint64_t rb = row_bytes(a.wtype, a.cols, r.op());
+        const bool slab = !a.w.empty() && a.w.buffer->layout() == WeightLayout::Slab;
+        std::uint32_t variant = a.kernel.variant_id;
+        if (variant == 0) variant = slab ? kGemvSlabAuto : kGemvGgufRef;
+        CHECK(slab == (variant != kGemvGgufRef), ErrorCode::Config, "MATMUL: variant %u does not read the %s layout", variant,
+              slab ? "SLAB" : "GGUF");
+        const Operand w = slab ? r.slab(a.w, a.wtype, a.rows, a.cols, "w")
+                               : r.get(a.w, a.rows, rb, a.wtype == DType::F32 ? kF32 : 1, Access::Read, "w");
+        const Operand x = r.f32(a.x, a.n_vec, a.cols, Access::Read, "x");
+        const Operand y = r.f32(a.y, a.n_vec, a.rows, Access::Write, "y");
+        r.no_overlap(y, x);
+        r.no_overlap(y, w);
+        if (a.n_vec == 0 || a.rows == 0) return;
+        if (variant == kGemmSlabBf16 || (variant == kGemvSlabAuto && a.n_vec > 8))
+            CHECK(reinterpret_cast<std::uintptr_t>(x.base) % 16 == 0 && x.stride % 16 == 0, ErrorCode::Kernel,
+                  "MATMUL: the MFMA GEMM needs 16-byte aligned x rows");
+        halo_mi_gemv_params p{t,      slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
+                              w.base, slab ? 0 : w.stride,
+                              reinterpret_cast<const float*>(x.base), x.stride / kF32,
+                              reinterpret_cast<float*>(y.base), y.stride / kF32,
+                              a.rows, a.cols, a.n_vec, variant};
+        check_abi(halo_mi_gemv(&p, st.native()));
+    }
+
+    void swiglu(Stream& s, const EltwiseArgs& a) override {
+        HipStream& st = stream(s, "SWIGLU");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kSwiglu, ErrorCode::Config, "SWIGLU: unknown kernel variant id %u",
+              a.kernel.variant_id);
+        const Resolver r(this, "SWIGLU");
+        const Operand g = r.f32(a.a, a.rows, a.cols, Access::Read, "a");
+        const Operand u = r.f32(a.b, a.rows, a.cols, Access::Read, "b");
+        const Operand out = r.f32(a.out, a.rows, a.cols, Access::Write, "out");
+        r.no_overlap(out, g);
+        r.no_overlap(out, u);
+        if (a.rows == 0 || a.cols == 0) return;
+        check_abi(halo_mi_swiglu(reinterpret_cast<const float*>(g.base), g.stride / kF32, reinterpret_cast<const float*>(u.base),
+                                 u.stride / kF32, reinterpret_cast<float*>(out.base), out.stride / kF32, a.rows, a.cols,
+                                 st.native()));
+    }
+
+    void gate_up_swiglu(Stream& s, const GateUpArgs& a) override {
+        HipStream& st = stream(s, "GATE_UP_SWIGLU");
+        CHECK(has_variant(OpId::GateUpSwiglu, a.kernel.variant_id), ErrorCode::Config,
+              "GATE_UP_SWIGLU: unknown kernel variant id %u", a.kernel.variant_id);
+        const Resolver r(this, "GATE_UP_SWIGLU");
+        (void)row_bytes(a.wtype, a.cols, r.op());
+        const Operand wg = r.slab(a.w_gate, a.wtype, a.rows, a.cols, "w_gate");
+        const Operand wu = r.slab(a.w_up, a.wtype, a.rows, a.cols, "w_up");
+        const Operand x = r.f32(a.x, a.n_vec, a.cols, Access::Read, "x");
+        const Operand out = r.f32(a.out, a.n_vec, a.rows, Access::Write, "out");
+        r.no_overlap(out, x);
+        r.no_overlap(out, wg);
+        r.no_overlap(out, wu);
+        if (a.n_vec == 0 || a.rows == 0) return;
+        const std::uint32_t variant = a.kernel.variant_id == kGateUpGemv   ? HALO_MI_GEMV_SLAB
+                                      : a.kernel.variant_id == kGateUpGemm ? HALO_MI_GEMM_SLAB_BF16
+                                                                           : HALO_MI_GEMV_SLAB_AUTO;
+        halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,
+                                 reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
+                                 out.stride / kF32, a.rows, a.cols, a.n_vec, variant};
+        check_abi(halo_mi_gate_up_swiglu(&p, st.native()));
+    }
+
+private:
+    void check_alive(const char* op) const {
+        CHECK(!lost_, ErrorCode::Device, "%s: the device behind this backend is lost", op);
+        CHECK(!poisoned_, ErrorCode::Kernel, "%s: a previous kernel fault poisoned this backend", op);
+    }
+
+    HipStream& stream(Stream& s, const char* op) {
+        check_alive(op);
+        auto* hs = dynamic_cast<HipStream*>(&s);
+        CHECK(hs != nullptr && hs->owner() == this, ErrorCode::Kernel, "%s: stream belongs to another backend", op);
+        return *hs;
+    }
+
+    static std::uint64_t row_bytes(DType t, std::uint32_t cols, const char* op) {
+        const std::uint64_t rb = halo_mi_row_bytes(static_cast<std::uint32_t>(t), cols);
+        if (rb == 0) {
+            const bool known = t == DType::F32 || t == DType::Q4_0 || t == DType::Q8_0 || t == DType::Q4_K || t == DType::Q6_K;
+            CHECK(!known, ErrorCode::Kernel, "%s: %u elements is not a multiple of the %s block size", op, cols, type_name(t));
+            fail(ErrorCode::Unsupported, "%s: no kernel for weight type %u", op, static_cast<unsigned>(t));
+        }
+        return rb;
+    }
+
+    int device_;
+    int cus_ = 0;
+    std::string name_;
+    bool lost_ = false, poisoned_ = false;
+};
+
+void HipStream::wait() {
+    const hipError_t e = hipStreamSynchronize(s_);
+    if (e == hipSuccess) return;
+    const bool kernel_fault = e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorIllegalInstruction;
+    owner_->poison(kernel_fault);
+    throw Error(kernel_fault ? ErrorCode::Kernel : ErrorCode::Device, std::string("stream wait: ") + hipGetErrorString(e));
+}
+
+}  // namespace
+
+std::string_view to_string(ErrorCode c) noexcept {
+    switch (c) {
+        case ErrorCode::Model: return "MODEL_ERROR";
+        case ErrorCode::Memory: return "MEMORY_ERROR";
+        case ErrorCode::Backend: return "BACKEND_ERROR";
+        case ErrorCode::Kernel: return "KERNEL_ERROR";
+        case ErrorCode::Config: return "CONFIG_ERROR";
+        case ErrorCode::Api: return "API_ERROR";
+        case ErrorCode::Device: return "DEVICE_ERROR";
+        case ErrorCode::Unsupported: return "UNSUPPORTED_ERROR";
+        case ErrorCode::Io: return "IO_ERROR";
+        case ErrorCode::Cancelled: return "CANCELLED";
+    }
+    return "UNKNOWN_ERROR";
+}
+
+Error::Error(ErrorCode code, const std::string& message)
+    : std::runtime_error(std::string(to_string(code)) + ": " + message), code_(code) {}
+
+void Backend::unsupported(OpId op) const {
+    fail(ErrorCode::Unsupported, "op %u is not implemented by the mi355x backend", static_cast<unsigned>(op));
+}
+
+std::unique_ptr<Backend> make_mi355x_backend(int device) { return std::make_unique<MiBackend>(device); }
+
+}  // namespace halo_mi::backend

@@ -379,6 +379,18 @@ __global__ __launch_bounds__(1024) void k_gemv_slab(GemvSlabArgs a) {
 }
 
 // ==========================================================================================
+// SWIGLU (backends/cpu/ops_basic.cpp:165-167): out = silu(g) * u, rows x cols
+// ==========================================================================================
+
+__global__ void k_swiglu(const float* __restrict__ g, uint64_t gs, const float* __restrict__ u, uint64_t us,
+                         float* __restrict__ out, uint64_t os, uint32_t rows, uint32_t cols) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)rows * cols) return;
+    const uint64_t r = idx / cols, c = idx % cols;
+    out[r * os + c] = silu_f(g[r * gs + c]) * u[r * us + c];
+}
+
+// ==========================================================================================
 // SLAB GEMM on bf16 MFMA (M >= 8)
 // ==========================================================================================
 
@@ -692,6 +704,29 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     GemmArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                p->rows, p->cols, p->n_vec};
     return launch_gemm_slab<true>(p->type, a, st);
+}
+
+int halo_mi_swiglu(const float* gate, uint64_t gate_stride, const float* up, uint64_t up_stride, float* out,
+                   uint64_t out_stride, uint32_t rows, uint32_t cols, void* stream) {
+    clear_error();
+    const char* op = "SWIGLU";
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    if (!gate || !up || !out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (gate_stride == 0) gate_stride = cols;
+    if (up_stride == 0) up_stride = cols;
+    if (out_stride == 0) out_stride = cols;
+    if (rows > 1 && (gate_stride < cols || up_stride < cols || out_stride < cols))
+        return set_error(HALO_MI_E_KERNEL, "%s: row stride < cols", op);
+    if ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(out)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: operands must be 4-byte aligned", op);
+    const uint64_t oext = extent(rows, out_stride * 4, (uint64_t)cols * 4);
+    if (ranges_overlap(out, oext, gate, extent(rows, gate_stride * 4, (uint64_t)cols * 4)) ||
+        ranges_overlap(out, oext, up, extent(rows, up_stride * 4, (uint64_t)cols * 4)))
+        return set_error(HALO_MI_E_KERNEL, "%s: out overlaps an input", op);
+    const uint64_t n = (uint64_t)rows * cols;
+    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream), gate,
+                       gate_stride, up, up_stride, out, out_stride, rows, cols);
+    return hip_status(hipGetLastError(), "swiglu launch");
 }
 
 int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t w_stride, uint32_t rows, uint32_t cols,

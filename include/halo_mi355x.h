@@ -136,6 +136,14 @@ typedef struct halo_mi_gate_up_params {
 int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream);
 
 /*
+ * SWIGLU: out[r][c] = silu(gate[r][c]) * up[r][c] for rows x cols fp32 (strides in floats,
+ * 0 = cols). The reference's op (backends/cpu/ops_basic.cpp:165-167, EltwiseArgs at
+ * include/halo/backend/backend.h:420-427). out may not overlap gate or up.
+ */
+int halo_mi_swiglu(const float* gate, uint64_t gate_stride, const float* up, uint64_t up_stride, float* out,
+                   uint64_t out_stride, uint32_t rows, uint32_t cols, void* stream);
+
+/*
  * Dequantize rows [first_row, first_row + n_rows) of W to fp32 (out rows out_stride floats
  * apart, 0 = cols), bit-identical to tensor::dequantize_row (src/tensor/quant.cpp:430-435).
  * Works on both layouts; it shares its unpacking code with the gemv/gemm kernels.
