@@ -64,7 +64,8 @@ def time_graph(torch, launch, n_copies, steps, warmup):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # capture on the warmed-up stream: the library's per-stream split-K workspace exists there
+    with torch.cuda.graph(g, stream=s):
         for i in range(n_copies):
             launch(i)
     reps_w = max(1, math.ceil(warmup / n_copies))

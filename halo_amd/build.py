@@ -16,7 +16,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libhalo_mi355x.so"
-SOURCES = [PKG / "csrc" / "kernels.hip", PKG / "csrc" / "host_utils.cpp"]
+SOURCES = [PKG / "csrc" / "kernels.hip", PKG / "csrc" / "host_utils.cpp", PKG / "csrc" / "backend.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [

@@ -11,6 +11,7 @@
 #include <array>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <limits>
 
 #include "../../include/halo_mi355x.h"
@@ -470,7 +471,7 @@ private:
 void HipStream::wait() {
     const hipError_t e = hipStreamSynchronize(s_);
     if (e == hipSuccess) return;
-    const bool kernel_fault = e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorIllegalInstruction;
+    const bool kernel_fault = e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorAssert;
     owner_->poison(kernel_fault);
     throw Error(kernel_fault ? ErrorCode::Kernel : ErrorCode::Device, std::string("stream wait: ") + hipGetErrorString(e));
 }

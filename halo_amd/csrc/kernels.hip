@@ -15,7 +15,11 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "common.h"
 #include "decode.h"
@@ -28,8 +32,6 @@ using namespace dev;
 
 constexpr uint32_t kMaxGemvVec = 4;  // vectors per slab-gemv launch
 
-typedef __attribute__((address_space(4))) const float cfloat;  // constant address space
-constexpr uint32_t kMaxWaves = 16;   // waves per workgroup
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
@@ -198,8 +200,17 @@ __global__ __launch_bounds__(256) void k_gemv_gguf_ref(uint32_t type, const uint
 }
 
 // ==========================================================================================
-// SLAB GEMV: one row per lane, K split over the waves of the workgroup
+// SLAB GEMV: one row per lane; a one-wave workgroup owns a (slab, K chunk) unit
 // ==========================================================================================
+//
+// The grid is slabs x ks units (ks K chunks per slab, chosen so the chip gets many more
+// units than CUs). A unit first issues the loads of its first slot group (8 slots = 256
+// weights per row: eight contiguous 1 KB wave loads plus the group's scale records), then
+// stages its slice of x in LDS while they are in flight, and streams the remaining groups
+// with the next group's loads issued before the current group is computed. With ks > 1 the
+// per-row partials go to a workspace; the unit that finishes last for a slab (an atomic
+// counter per slab) adds the ks partials in chunk order and writes y, so the result does
+// not depend on scheduling.
 
 struct GemvSlabArgs {
     const uint8_t* w0;  // slab image (gate, or the only matrix)
@@ -209,147 +220,337 @@ struct GemvSlabArgs {
     float* y;
     uint64_t y_stride;
     uint32_t rows, cols, n_vec;
+    uint32_t ks;          // K chunks per slab
+    float* partials;      // [slabs][ks][NA][64] when ks > 1
+    uint32_t* counters;   // [slabs], zero between launches
 };
 
-// 16 low-nibble and 16 high-nibble weights of a 4-bit slot record against x[0..31]:
-// lo = sum x[t] q_lo[t], hi = sum x[16+t] (16 q_hi[t]) (the high nibbles are left in place,
-// i.e. scaled by 16, and rescaled by the caller).
-__device__ __forceinline__ void dot_nibbles(const uint4& q, cfloat* xs, float& lo, float& hi) {
+// ---- inner products of one 32-weight slot against x[0..31] (x in LDS, 16-byte aligned) ----
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+
+// AND with a mask the compiler cannot see through: it would otherwise fold the mask into
+// per-byte bit-field extracts and lose the v_cvt_f32_ubyteN patterns.
+template <uint32_t M>
+__device__ __forceinline__ uint32_t and_opaque(uint32_t v) {
+    uint32_t r;
+    __asm__("v_and_b32 %0, %1, %2" : "=v"(r) : "i"(M), "v"(v));
+    return r;
+}
+template <uint32_t M>
+__device__ __forceinline__ uint32_t xor_opaque(uint32_t v) {
+    uint32_t r;
+    __asm__("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(M), "v"(v));
+    return r;
+}
+
+// (a & m) | b, opaque to the compiler (keeps the byte-convert patterns, see and_opaque)
+__device__ __forceinline__ uint32_t and_or_opaque(uint32_t a, uint32_t m, uint32_t b) {
+    uint32_t r;
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(b));
+    return r;
+}
+
+// Q6_K slot record -> 6-bit quants as bytes, like q6_slot_bytes (decode.h), for the GEMV.
+__device__ __forceinline__ void q6_slot_bytes_gemv(const uint4& ql, const uint2& qh, uint32_t lo[4], uint32_t hi[4]) {
+    const uint32_t L[4] = {ql.x, ql.y, ql.z, ql.w};
+    const uint32_t H[2] = {qh.x, qh.y};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t a = L[2 * w], b = L[2 * w + 1], h = H[w];
+        lo[2 * w] = and_or_opaque(a, 0x0F0F0F0Fu, h & 0x30303030u);
+        hi[2 * w] = and_or_opaque(a >> 4, 0x0F0F0F0Fu, (h >> 2) & 0x30303030u);
+        lo[2 * w + 1] = and_or_opaque(b, 0x0F0F0F0Fu, (h << 4) & 0x30303030u);
+        hi[2 * w + 1] = and_or_opaque(b >> 4, 0x0F0F0F0Fu, (h << 2) & 0x30303030u);
+    }
+}
+
+// Value of the fp8 (e4m3) code 1 on this device: every code c < 16 converts to exactly
+// c * fp8_unit(), so v_cvt_pk_f32_fp8 turns two 4-bit quants into two exact floats.
+__device__ __forceinline__ float fp8_unit() { return __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0]; }
+
+// 4-bit slot record: lo = sum x[t] q[t] (t < 16), hi = sum x[16 + t] q[16 + t], both in units
+// of fp8_unit().
+__device__ __forceinline__ void dot_nibbles(const uint4& q, const float* xs, float& lo, float& hi) {
+    const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+    const float4* x4 = reinterpret_cast<const float4*>(xs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = Q[i] & 0x0F0F0F0Fu, b = (Q[i] >> 4) & 0x0F0F0F0Fu;
+        const float2v a01 = __builtin_amdgcn_cvt_pk_f32_fp8(a, false), a23 = __builtin_amdgcn_cvt_pk_f32_fp8(a, true);
+        const float2v b01 = __builtin_amdgcn_cvt_pk_f32_fp8(b, false), b23 = __builtin_amdgcn_cvt_pk_f32_fp8(b, true);
+        const float4 xl = x4[i], xh = x4[4 + i];
+        lo = fmaf(xl.x, a01[0], lo);
+        lo = fmaf(xl.y, a01[1], lo);
+        lo = fmaf(xl.z, a23[0], lo);
+        lo = fmaf(xl.w, a23[1], lo);
+        hi = fmaf(xh.x, b01[0], hi);
+        hi = fmaf(xh.y, b01[1], hi);
+        hi = fmaf(xh.z, b23[0], hi);
+        hi = fmaf(xh.w, b23[1], hi);
+    }
+}
+
+// Byte quants (one per weight) A (t < 16) and B (16 + t), unsigned.
+__device__ __forceinline__ void dot_bytes(const uint32_t A[4], const uint32_t B[4], const float* xs, float& lo,
+                                          float& hi) {
+    const float4* x4 = reinterpret_cast<const float4*>(xs);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 xl = x4[i], xh = x4[4 + i];
+        lo = fmaf(xl.x, ubyte(A[i], 0), lo);
+        lo = fmaf(xl.y, ubyte(A[i], 1), lo);
+        lo = fmaf(xl.z, ubyte(A[i], 2), lo);
+        lo = fmaf(xl.w, ubyte(A[i], 3), lo);
+        hi = fmaf(xh.x, ubyte(B[i], 0), hi);
+        hi = fmaf(xh.y, ubyte(B[i], 1), hi);
+        hi = fmaf(xh.z, ubyte(B[i], 2), hi);
+        hi = fmaf(xh.w, ubyte(B[i], 3), hi);
+    }
+}
+
+// The loaded records of one slot group (up to 8 slots) of one row.
+template <uint32_t T>
+struct SlotGroup;
+
+template <>
+struct SlotGroup<kQ4_K> {
+    uint4 q[8];
+    uint4 hdr;
+};
+template <>
+struct SlotGroup<kQ6_K> {
+    uint4 ql[8];
+    uint2 qh[8];
+    uint4 sc;
+    uint32_t d;
+};
+template <>
+struct SlotGroup<kQ4_0> {
+    uint4 q[8];
+    uint32_t d[8];
+};
+template <>
+struct SlotGroup<kQ8_0> {
+    uint4 qa[8], qb[8];
+    uint32_t d[8];
+};
+
+template <uint32_t T>
+__device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __restrict__ slab, const SlabGeom& g,
+                                           uint32_t lane, uint32_t grp, uint32_t S) {
+    const uint32_t sb = grp * 8;
+    if constexpr (T == kQ4_K) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G.q[j] = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+        G.hdr = *reinterpret_cast<const uint4*>(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 16);
+    } else if constexpr (T == kQ6_K) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            G.ql[j] = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+            G.qh[j] = *reinterpret_cast<const uint2*>(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+        }
+        G.sc = *reinterpret_cast<const uint4*>(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+        G.d = *reinterpret_cast<const uint16_t*>(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
+    } else if constexpr (T == kQ4_0) {
+        const uint32_t n = min(8u, S - sb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((uint32_t)j < n) {
+                G.q[j] = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+                G.d[j] = *reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 2);
+            }
+    } else {
+        const uint32_t n = min(8u, S - sb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((uint32_t)j < n) {
+                G.qa[j] = *reinterpret_cast<const uint4*>(slab + g.q_off + (((uint64_t)(sb + j) * 2) * 64 + lane) * 16);
+                G.qb[j] = *reinterpret_cast<const uint4*>(slab + g.q_off + (((uint64_t)(sb + j) * 2 + 1) * 64 + lane) * 16);
+                G.d[j] = *reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 2);
+            }
+    }
+}
+
+// x through the constant address space: wave-uniform loads become scalar loads, so x is
+// read through the scalar cache into SGPRs and fed to the FMAs as scalar operands.
+typedef __attribute__((address_space(4))) const float cfloat;
+typedef __attribute__((address_space(4))) const float4 cfloat4;
+
+// 4-bit slot record against x (SGPR): lo = sum x[t] q[t] (t < 16), hi = sum x[16 + t] q[16 + t],
+// in units of fp8_unit().
+__device__ __forceinline__ void dot_nibbles_s(const uint4& q, cfloat* xs, float& lo, float& hi) {
     const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t a = Q[i] & 0x0F0F0F0Fu, b = Q[i] & 0xF0F0F0F0u;
+        const uint32_t a = Q[i] & 0x0F0F0F0Fu, b = (Q[i] >> 4) & 0x0F0F0F0Fu;
+        const float2v a01 = __builtin_amdgcn_cvt_pk_f32_fp8(a, false), a23 = __builtin_amdgcn_cvt_pk_f32_fp8(a, true);
+        const float2v b01 = __builtin_amdgcn_cvt_pk_f32_fp8(b, false), b23 = __builtin_amdgcn_cvt_pk_f32_fp8(b, true);
+        lo = fmaf(xs[4 * i + 0], a01[0], lo);
+        lo = fmaf(xs[4 * i + 1], a01[1], lo);
+        lo = fmaf(xs[4 * i + 2], a23[0], lo);
+        lo = fmaf(xs[4 * i + 3], a23[1], lo);
+        hi = fmaf(xs[16 + 4 * i + 0], b01[0], hi);
+        hi = fmaf(xs[16 + 4 * i + 1], b01[1], hi);
+        hi = fmaf(xs[16 + 4 * i + 2], b23[0], hi);
+        hi = fmaf(xs[16 + 4 * i + 3], b23[1], hi);
+    }
+}
+
+__device__ __forceinline__ void dot_bytes_s(const uint32_t A[4], const uint32_t B[4], cfloat* xs, float& lo, float& hi) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            lo = fmaf(xs[4 * i + k], ubyte(a, k), lo);
-            hi = fmaf(xs[16 + 4 * i + k], ubyte(b, k), hi);
+            lo = fmaf(xs[4 * i + k], ubyte(A[i], k), lo);
+            hi = fmaf(xs[16 + 4 * i + k], ubyte(B[i], k), hi);
         }
-    }
 }
 
-// One slot (32 weights) of one row for NV x vectors, added to acc[]. xsum = LDS sums of the
-// two 16-element halves of every slot of every vector: xsum[(v * S + s) * 2 + h].
-template <uint32_t T, int NV>
-__device__ __forceinline__ void slab_slot_gemv(const uint8_t* __restrict__ slab, const SlabGeom& g, uint32_t lane,
-                                               uint32_t s, cfloat* x, uint64_t x_stride,
-                                               const float* xsum, uint32_t S, float acc[NV]) {
-    if constexpr (T == kQ4_K) {
-        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + lane) * 16);
-        const uint4 hdr = *reinterpret_cast<const uint4*>(slab + g.aux_off + ((uint64_t)(s >> 3) * 64 + lane) * 16);
-        float d1, m1;
-        q4k_scales(hdr, s & 7u, d1, m1);
+// Half-slot sums (16 x values each) of the up-to-4 slot groups starting at group gb, held one
+// per lane: lane 16 i + h has half-slot h of group gb + i. Read back with xsum_at (readlane),
+// so the main loop never waits on memory for them.
+__device__ __forceinline__ float wave_xsums(const float* __restrict__ x, uint32_t gb, uint32_t S, uint32_t lane) {
+    const uint32_t e = gb * 256 + lane * 16;  // this lane's 16 elements
+    float s = 0.0f;
+    if (e < S * 32) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            cfloat* xs = x + v * x_stride + (uint64_t)s * 32;
-            float lo = 0.0f, hi = 0.0f;
-            dot_nibbles(q, xs, lo, hi);
-            const float sq = fmaf(hi, 0.0625f, lo);
-            const float X = xsum[(v * S + s) * 2] + xsum[(v * S + s) * 2 + 1];
-            acc[v] = fmaf(d1, sq, acc[v]);
-            acc[v] = fmaf(-m1, X, acc[v]);
+        for (int k = 0; k < 16; k += 4) s += (x[e + k] + x[e + k + 1]) + (x[e + k + 2] + x[e + k + 3]);
+    }
+    return s;
+}
+__device__ __forceinline__ float xsum_at(float xsv, uint32_t idx) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xsv), idx));
+}
+
+// One loaded group against NV vectors; x of vector v at x + v * x_stride (SGPR loads),
+// X[v][h] the group's half-slot sums.
+template <uint32_t T, int NV>
+__device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t grp, uint32_t gi, uint32_t S, cfloat* x,
+                                              uint64_t x_stride, const float (&xsv)[NV], float inv_unit,
+                                              float acc[NV]) {
+    const uint32_t sbase = grp * 8, hb = gi * 16;  // this group's half-slot sums: lanes hb .. hb + 15
+    if constexpr (T == kQ4_K) {
+        // d is scaled by 1 / fp8_unit (a power of two: exact) to undo the fp8 conversion
+        const float d = h2f(G.hdr.x & 0xFFFFu) * inv_unit, dmin = h2f(G.hdr.x >> 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sc, m;
+            q4k_sc_m(G.hdr.y, G.hdr.z, G.hdr.w, j, sc, m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_nibbles_s(G.q[j], x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(d1, lo + hi, acc[v]);
+                acc[v] = fmaf(-m1, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), acc[v]);
+            }
+        }
+    } else if constexpr (T == kQ6_K) {
+        const float d = h2f(G.d);
+        const uint32_t SC[4] = {G.sc.x, G.sc.y, G.sc.z, G.sc.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float dA = d * sbyte(SC[j >> 1], 2 * (j & 1)), dB = d * sbyte(SC[j >> 1], 2 * (j & 1) + 1);
+            uint32_t lo6[4], hi6[4];
+            q6_slot_bytes_gemv(G.ql[j], G.qh[j], lo6, hi6);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_bytes_s(lo6, hi6, x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(dA, fmaf(-32.0f, xsum_at(xsv[v], hb + 2 * j), lo), acc[v]);
+                acc[v] = fmaf(dB, fmaf(-32.0f, xsum_at(xsv[v], hb + 2 * j + 1), hi), acc[v]);
+            }
         }
     } else if constexpr (T == kQ4_0) {
-        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + lane) * 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)s * 64 + lane) * 2));
+        const uint32_t n = min(8u, S - sbase);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            cfloat* xs = x + v * x_stride + (uint64_t)s * 32;
-            float lo = 0.0f, hi = 0.0f;
-            dot_nibbles(q, xs, lo, hi);
-            const float X = xsum[(v * S + s) * 2] + xsum[(v * S + s) * 2 + 1];
-            float t = fmaf(hi, 0.0625f, lo);
-            t = fmaf(-8.0f, X, t);
-            acc[v] = fmaf(d, t, acc[v]);
+        for (int j = 0; j < 8; ++j) {
+            if ((uint32_t)j >= n) break;
+            const float d = h2f(G.d[j]);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_nibbles_s(G.q[j], x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                const float t = fmaf(-8.0f, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), (lo + hi) * inv_unit);
+                acc[v] = fmaf(d, t, acc[v]);
+            }
         }
-    } else if constexpr (T == kQ8_0) {
-        const uint4 qa = *reinterpret_cast<const uint4*>(slab + g.q_off + (((uint64_t)s * 2) * 64 + lane) * 16);
-        const uint4 qb = *reinterpret_cast<const uint4*>(slab + g.q_off + (((uint64_t)s * 2 + 1) * 64 + lane) * 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)s * 64 + lane) * 2));
-        const uint32_t A[4] = {qa.x, qa.y, qa.z, qa.w}, B[4] = {qb.x, qb.y, qb.z, qb.w};
+    } else {  // Q8_0
+        const uint32_t n = min(8u, S - sbase);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            cfloat* xs = x + v * x_stride + (uint64_t)s * 32;
-            float lo = 0.0f, hi = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            if ((uint32_t)j >= n) break;
+            const float d = h2f(G.d[j]);
+            // int8 q -> q + 128 as an unsigned byte; the 128 is taken back with the x sums
+            const uint32_t A[4] = {xor_opaque<0x80808080u>(G.qa[j].x), xor_opaque<0x80808080u>(G.qa[j].y),
+                                   xor_opaque<0x80808080u>(G.qa[j].z), xor_opaque<0x80808080u>(G.qa[j].w)};
+            const uint32_t B[4] = {xor_opaque<0x80808080u>(G.qb[j].x), xor_opaque<0x80808080u>(G.qb[j].y),
+                                   xor_opaque<0x80808080u>(G.qb[j].z), xor_opaque<0x80808080u>(G.qb[j].w)};
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    lo = fmaf(xs[4 * i + k], sbyte(A[i], k), lo);
-                    hi = fmaf(xs[16 + 4 * i + k], sbyte(B[i], k), hi);
-                }
-            acc[v] = fmaf(d, lo + hi, acc[v]);
-        }
-    } else {  // Q6_K
-        const uint4 ql = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + lane) * 16);
-        const uint2 qh = *reinterpret_cast<const uint2*>(slab + g.aux_off + ((uint64_t)s * 64 + lane) * 8);
-        const uint32_t sb = s >> 3, j = s & 7u;
-        const uint4 sc4 = *reinterpret_cast<const uint4*>(slab + g.sc_off + ((uint64_t)sb * 64 + lane) * 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.d_off + ((uint64_t)sb * 64 + lane) * 2));
-        const uint32_t SC[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-        const uint32_t scw = SC[j >> 1];
-        const float dA = d * sbyte(scw, 2 * (j & 1)), dB = d * sbyte(scw, 2 * (j & 1) + 1);
-        uint32_t lo6[4], hi6[4];
-        q6_slot_bytes(ql, qh, lo6, hi6);
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            cfloat* xs = x + v * x_stride + (uint64_t)s * 32;
-            float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    lo = fmaf(xs[4 * i + k], ubyte(lo6[i], k), lo);
-                    hi = fmaf(xs[16 + 4 * i + k], ubyte(hi6[i], k), hi);
-                }
-            const float ta = fmaf(-32.0f, xsum[(v * S + s) * 2], lo);
-            const float tb = fmaf(-32.0f, xsum[(v * S + s) * 2 + 1], hi);
-            acc[v] = fmaf(dA, ta, acc[v]);
-            acc[v] = fmaf(dB, tb, acc[v]);
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_bytes_s(A, B, x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(d, fmaf(-128.0f, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), lo + hi), acc[v]);
+            }
         }
     }
 }
 
-// grid.x = slabs; block = 64 * waves. LDS: xsum [NV][S][2], red [waves][NV * (PAIR ? 2 : 1)][64].
+// grid.x = slabs * ks; block = 64 * nw (nw waves). Dynamic LDS: the waves' partials
+// [nw][NA][64].
 template <uint32_t T, int NV, bool PAIR>
-__global__ __launch_bounds__(1024) void k_gemv_slab(GemvSlabArgs a) {
+__global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
     extern __shared__ float smem[];
-    const uint32_t S = a.cols / kSlot;
-    // wave index via readfirstlane so the compiler knows it (and the slot loop) is uniform
-    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nw = blockDim.x >> 6;
-    float* xsum = smem;
-    float* red = smem + NV * S * 2;
-    // x is read-only and wave-uniform in the main loop: reading it through the constant
-    // address space lets the compiler use scalar loads (x lands in SGPRs, no VGPR cost).
-    cfloat* x = reinterpret_cast<cfloat*>(reinterpret_cast<uintptr_t>(a.x));
-    for (uint32_t i = threadIdx.x; i < NV * S * 2; i += blockDim.x) {
-        const uint32_t v = i / (S * 2), r = i % (S * 2);
-        const float* xp = a.x + v * a.x_stride + (uint64_t)r * 16;
-        float sum = 0.0f;
-        for (int k = 0; k < 16; ++k) sum += xp[k];
-        xsum[i] = sum;
-    }
-    __syncthreads();
-    const uint32_t base = S / nw, extra = S % nw;
-    const uint32_t s0 = wave * base + min(wave, extra);
-    const uint32_t s1 = s0 + base + (wave < extra ? 1u : 0u);
-    const SlabGeom g = slab_geom(T, a.cols);
-    const uint8_t* slab0 = a.w0 + (uint64_t)blockIdx.x * g.slab_bytes;
+    constexpr int NA = PAIR ? 2 * NV : NV;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
+    const uint32_t slab = blockIdx.x / a.ks, c = blockIdx.x % a.ks;
+    // this workgroup's groups [g0, g1), then this wave's share [w0, w1)
+    const uint32_t base = ngrp / a.ks, extra = ngrp % a.ks;
+    const uint32_t g0 = c * base + min(c, extra), g1 = g0 + base + (c < extra ? 1u : 0u);
+    const uint32_t wb = (g1 - g0) / nw, we = (g1 - g0) % nw;
+    const uint32_t w0 = g0 + wave * wb + min(wave, we), w1 = w0 + wb + (wave < we ? 1u : 0u);
+    const SlabGeom geo = slab_geom(T, a.cols);
+    const uint8_t* slab0 = a.w0 + (uint64_t)slab * geo.slab_bytes;
+    const uint8_t* slab1 = PAIR ? a.w1 + (uint64_t)slab * geo.slab_bytes : nullptr;
+    cfloat* xc = reinterpret_cast<cfloat*>(reinterpret_cast<uintptr_t>(a.x));
+    float* red = smem;
+
+    // 1 / fp8_unit, built from the exponent bits (exact for a power of two)
+    const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
     float acc0[NV], acc1[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc0[v] = acc1[v] = 0.0f;
-    if constexpr (PAIR) {
-        const uint8_t* slab1 = a.w1 + (uint64_t)blockIdx.x * g.slab_bytes;
-#pragma unroll 2
-        for (uint32_t s = s0; s < s1; ++s) {
-            slab_slot_gemv<T, NV>(slab0, g, lane, s, x, a.x_stride, xsum, S, acc0);
-            slab_slot_gemv<T, NV>(slab1, g, lane, s, x, a.x_stride, xsum, S, acc1);
-        }
-    } else {
-#pragma unroll 4
-        for (uint32_t s = s0; s < s1; ++s) slab_slot_gemv<T, NV>(slab0, g, lane, s, x, a.x_stride, xsum, S, acc0);
+    SlotGroup<T> cur0, cur1;
+    if (w0 < w1) {
+        load_group<T>(cur0, slab0, geo, lane, w0, S);
+        if constexpr (PAIR) load_group<T>(cur1, slab1, geo, lane, w0, S);
     }
-    constexpr int NA = PAIR ? 2 * NV : NV;
+    float xsv[NV];  // half-slot sums of this wave's groups (at most 4), one per lane
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xsv[v] = wave_xsums(a.x + (uint64_t)v * a.x_stride, w0, S, lane);
+    for (uint32_t grp = w0; grp < w1; ++grp) {
+        if constexpr (PAIR) {
+            compute_group<T, NV>(cur0, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+            if (grp + 1 < w1) load_group<T>(cur0, slab0, geo, lane, grp + 1, S);
+            compute_group<T, NV>(cur1, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc1);
+            if (grp + 1 < w1) load_group<T>(cur1, slab1, geo, lane, grp + 1, S);
+        } else {
+            // Ping-pong between two register buffers: the next group is always in flight. The
+            // prefetch is unconditional (past the last group it reloads the last one, an L2
+            // hit) so the compiler can wait for exactly the older loads (vmcnt counts in order).
+            SlotGroup<T> nxt;
+            load_group<T>(nxt, slab0, geo, lane, min(grp + 1, w1 - 1), S);
+            compute_group<T, NV>(cur0, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+            if (grp + 1 >= w1) break;
+            ++grp;
+            load_group<T>(cur0, slab0, geo, lane, min(grp + 1, w1 - 1), S);
+            compute_group<T, NV>(nxt, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+        }
+    }
+    // waves -> wave 0, in wave order
     if (nw > 1) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -369,13 +570,48 @@ __global__ __launch_bounds__(1024) void k_gemv_slab(GemvSlabArgs a) {
             acc1[v] = u;
         }
     }
-    const uint32_t row = blockIdx.x * kSlabRows + lane;
+    const uint32_t row = slab * kSlabRows + lane;
+    if (a.ks > 1) {
+        // Cross-workgroup reduction without cache maintenance: partials are written and read
+        // with relaxed device-scope atomic accesses (each one coherent across the XCDs' L2s),
+        // the stores are complete (s_waitcnt) before the counter increment, and the counter is
+        // a device-scope atomic. The last chunk of a slab adds the partials in chunk order.
+        float* P = a.partials + ((uint64_t)slab * a.ks + c) * NA * 64;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            __hip_atomic_store(P + v * 64 + lane, acc0[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if constexpr (PAIR)
+                __hip_atomic_store(P + (NV + v) * 64 + lane, acc1[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the partial stores are performed before the count
+        uint32_t prev = 0;
+        if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev != a.ks - 1) return;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc0[v] = acc1[v] = 0.0f;
+        for (uint32_t cc = 0; cc < a.ks; ++cc) {  // fixed chunk order: deterministic
+            const float* Q = a.partials + ((uint64_t)slab * a.ks + cc) * NA * 64;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                acc0[v] += __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (PAIR)
+                    acc1[v] += __hip_atomic_load(Q + (NV + v) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (row >= a.rows) return;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         if ((uint32_t)v >= a.n_vec) break;
         a.y[(uint64_t)v * a.y_stride + row] = PAIR ? silu_f(acc0[v]) * acc1[v] : acc0[v];
     }
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
 }
 
 // ==========================================================================================
@@ -535,36 +771,112 @@ bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb) {
 // Extent in bytes of `rows` rows of `row_bytes` spaced `stride` bytes apart.
 uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes) { return rows ? (rows - 1) * stride + row_bytes : 0; }
 
-uint32_t pick_waves(uint32_t slabs, uint32_t S) {
-    // Aim for about 2048 waves in flight over the chip (256 CUs), at most 16 per workgroup.
-    uint32_t nw = (2048u + slabs - 1) / std::max(slabs, 1u);
-    nw = std::clamp(nw, 1u, kMaxWaves);
-    return std::min(nw, std::max(S, 1u));
+// ---- split-K workspace, one per (device, stream) ------------------------------------------
+// Calls on one stream run in order, so they can share it. It is allocated on the first call
+// on a stream (hipMalloc; counters cleared by a fill kernel on that stream, never a memset);
+// a call on a stream that is being captured into a graph and has no workspace yet runs
+// without split-K.
+constexpr uint64_t kPartialFloats = 8ull << 20;  // 32 MiB
+constexpr uint64_t kCounters = 1ull << 20;        // slabs (64M rows)
+
+struct Workspace {
+    float* partials = nullptr;
+    uint32_t* counters = nullptr;
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int workspace_for(hipStream_t st, Workspace** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv: hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find({dev, st});
+    if (it != g_ws.end()) {
+        *out = &it->second;
+        return HALO_MI_OK;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (st != nullptr && hipStreamIsCapturing(st, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+        *out = nullptr;  // cannot allocate under capture: caller runs without split-K
+        return HALO_MI_OK;
+    }
+    Workspace w;
+    if (hipMalloc(&w.partials, kPartialFloats * sizeof(float)) != hipSuccess)
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K workspace");
+    if (hipMalloc(&w.counters, kCounters * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K counters");
+    }
+    hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)(kCounters / 256)), dim3(256), 0, st, w.counters, kCounters, 0u);
+    if (hipGetLastError() != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
+    *out = &(g_ws[{dev, st}] = w);
+    return HALO_MI_OK;
+}
+
+// Work split of a slab-GEMV launch: ks K chunks per slab (more than one only when the slabs
+// alone cannot fill the chip; the chunks then meet in the workspace), nw waves per workgroup
+// (about two slot groups per wave, so each wave streams with one group in flight).
+struct GemvSplit {
+    uint32_t ks, nw;
+};
+
+GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t na, bool have_ws) {
+    // Measured on MI355X (17408 x 5120 and 151936 x 5120 Q4_K): about 4 workgroups per CU, and
+    // one slot group per wave for mid-size matrices, two for large ones.
+    static const uint32_t target_wg = [] {
+        const char* e = std::getenv("HALO_MI_GEMV_WGS");  // tuning knob: min workgroups per launch
+        return e ? (uint32_t)std::max(1, std::atoi(e)) : 1088u;
+    }();
+    static const int gpw_env = [] {
+        const char* e = std::getenv("HALO_MI_GEMV_GPW");  // tuning knob: slot groups per wave
+        return e ? std::max(1, std::atoi(e)) : 0;
+    }();
+    const uint32_t groups_per_wave = gpw_env ? (uint32_t)gpw_env : (slabs >= 1024 ? 2u : 1u);
+    const uint32_t ngrp = (S + 7) / 8;
+    uint32_t ks = 1;
+    if (have_ws && slabs < target_wg) ks = std::min((target_wg + slabs - 1) / std::max(slabs, 1u), ngrp);
+    while (ks > 1 && (uint64_t)slabs * ks * na * 64 > kPartialFloats) --ks;
+    const uint32_t gwg = (ngrp + ks - 1) / ks;
+    uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
+    // a wave holds the x sums of at most 4 groups (one per lane)
+    while (ks < ngrp && (gwg + nw - 1) / nw > 4) {
+        if (nw < 16) ++nw;
+        else ++ks;
+        const uint32_t g2 = (ngrp + ks - 1) / ks;
+        if ((g2 + nw - 1) / nw <= 4) break;
+    }
+    return {ks, nw};
 }
 
 template <uint32_t T, int NV, bool PAIR>
-int launch_gemv_slab_t(const GemvSlabArgs& a, uint32_t slabs, hipStream_t st) {
+int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_t st) {
     const uint32_t S = a.cols / kSlot;
-    const uint32_t nw = pick_waves(slabs, S);
-    const size_t lds = ((size_t)NV * S * 2 + (size_t)nw * NV * (PAIR ? 2 : 1) * 64) * sizeof(float);
-    if (lds > 160 * 1024) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_slab: %u columns need %zu B of LDS", a.cols, lds);
-    hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs), dim3(64 * nw), lds, st, a);
+    constexpr uint32_t NA = PAIR ? 2 * NV : NV;
+    const GemvSplit sp = pick_split(slabs, S, NV, NA, ws != nullptr && slabs <= kCounters);
+    a.ks = sp.ks;
+    a.partials = ws ? ws->partials : nullptr;
+    a.counters = ws ? ws->counters : nullptr;
+    const size_t lds = (size_t)sp.nw * NA * 64 * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks), dim3(64 * sp.nw), lds, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
 }
 
 template <uint32_t T, bool PAIR>
-int launch_gemv_slab_nv(const GemvSlabArgs& a, uint32_t slabs, hipStream_t st) {
+int launch_gemv_slab_nv(const GemvSlabArgs& a, uint32_t slabs, Workspace* ws, hipStream_t st) {
     switch (a.n_vec) {
-        case 1: return launch_gemv_slab_t<T, 1, PAIR>(a, slabs, st);
-        case 2: return launch_gemv_slab_t<T, 2, PAIR>(a, slabs, st);
-        case 3: return launch_gemv_slab_t<T, 3, PAIR>(a, slabs, st);
-        default: return launch_gemv_slab_t<T, 4, PAIR>(a, slabs, st);
+        case 1: return launch_gemv_slab_t<T, 1, PAIR>(a, slabs, ws, st);
+        case 2: return launch_gemv_slab_t<T, 2, PAIR>(a, slabs, ws, st);
+        case 3: return launch_gemv_slab_t<T, 3, PAIR>(a, slabs, ws, st);
+        default: return launch_gemv_slab_t<T, 4, PAIR>(a, slabs, ws, st);
     }
 }
 
 template <bool PAIR>
 int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+    Workspace* ws = nullptr;
+    if (int rc = workspace_for(st, &ws)) return rc;
     const uint32_t total = a.n_vec;
     for (uint32_t t0 = 0; t0 < total; t0 += kMaxGemvVec) {
         GemvSlabArgs c = a;
@@ -573,10 +885,10 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
         c.y = a.y + (uint64_t)t0 * a.y_stride;
         int rc;
         switch (type) {
-            case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, st); break;
-            case kQ8_0: rc = launch_gemv_slab_nv<kQ8_0, PAIR>(c, slabs, st); break;
-            case kQ4_K: rc = launch_gemv_slab_nv<kQ4_K, PAIR>(c, slabs, st); break;
-            default: rc = launch_gemv_slab_nv<kQ6_K, PAIR>(c, slabs, st); break;
+            case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, ws, st); break;
+            case kQ8_0: rc = launch_gemv_slab_nv<kQ8_0, PAIR>(c, slabs, ws, st); break;
+            case kQ4_K: rc = launch_gemv_slab_nv<kQ4_K, PAIR>(c, slabs, ws, st); break;
+            default: rc = launch_gemv_slab_nv<kQ6_K, PAIR>(c, slabs, ws, st); break;
         }
         if (rc) return rc;
     }
