@@ -136,6 +136,20 @@ def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
             "event_median_us": med * 1e3, "event_mean_us": mean * 1e3}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary written by `python -m halo_amd.profiling traffic` (None when it is absent)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return {"traffic_bytes": round(t["traffic_bytes"]), "source": os.path.relpath(TRAFFIC_FILE, ROOT)}
+
+
 def cpu_baseline(t, wq, rows, cols, x, seconds):
     """The oracle (a C port of the reference's cpu::matmul) on all host cores, best of N
     after one warm-up, for about `seconds` of CPU time."""
@@ -144,7 +158,7 @@ def cpu_baseline(t, wq, rows, cols, x, seconds):
     threads = orc.default_threads()
     orc.matmul(t, wq, rows, cols, x, threads=threads)
     best, spent, runs = float("inf"), 0.0, 0
-    while spent < seconds and runs < 1000:
+    while runs == 0 or (spent < seconds and runs < 1000):
         t0 = time.perf_counter()
         orc.matmul(t, wq, rows, cols, x, threads=threads)
         dt = time.perf_counter() - t0
@@ -163,6 +177,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after the benchmark, copy a buffer of this many MiB 4 times (a plain copy kernel of "
+                         "known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1).",
@@ -181,8 +198,11 @@ def main() -> int:
 
     log("config 2: Q4_K GEMV 17408x5120 M=1")
     head = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps, args.warmup)
-    kernel_us = head["event_median_us"]
+    # average launch duration: HIP events around the timed region (graph replays on the current
+    # stream, the stream the kernels are launched on) divided by the launches in it
+    kernel_us = head["ms"] * 1e3
     achieved = head["bytes"] / (kernel_us * 1e-6) / 1e9
+    traffic = measured_traffic()
     extra = {}
     if not args.no_extra:
         log("config 2: Q4_K GEMV M=4")
@@ -221,12 +241,21 @@ def main() -> int:
         "config": {"workload": "Q4_K dequant-GEMV 17408x5120 M=1 (config 2), SLAB layout, "
                                f"{math.ceil(MALL_BYTES / (17408 * 2880)) + 1}+ rotating weight copies"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel_us": round(kernel_us, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["traffic_bytes"] if traffic else None,
+                     "algorithmic_bytes": head["bytes"], "kernel_us": round(kernel_us, 3),
+                     "kernel_us_eager_median": round(head["event_median_us"], 3),
+                     "traffic_source": traffic["source"] if traffic else None},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    if args.calibration_copy_mib > 0:
+        a = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
     return 0
 
 

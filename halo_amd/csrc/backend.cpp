@@ -380,6 +380,8 @@ public:
         const bool slab = !a.w.empty() && a.w.buffer->layout() == WeightLayout::Slab;
         std::uint32_t variant = a.kernel.variant_id;
         if (variant == 0) variant = slab ? kGemvSlabAuto : kGemvGgufRef;
+        // rows must not depend on the batch unless the caller accepts the GEMM's numerics
+        if (variant == kGemvSlabAuto && !a.allow_gemm) variant = kGemvSlab;
         CHECK(slab == (variant != kGemvGgufRef), ErrorCode::Config, "MATMUL: variant %u does not read the %s layout", variant,
               slab ? "SLAB" : "GGUF");
         const Operand w = slab ? r.slab(a.w, a.wtype, a.rows, a.cols, "w")
@@ -432,7 +434,8 @@ public:
         if (a.n_vec == 0 || a.rows == 0) return;
         const std::uint32_t variant = a.kernel.variant_id == kGateUpGemv   ? HALO_MI_GEMV_SLAB
                                       : a.kernel.variant_id == kGateUpGemm ? HALO_MI_GEMM_SLAB_BF16
-                                                                           : HALO_MI_GEMV_SLAB_AUTO;
+                                      : a.allow_gemm                       ? HALO_MI_GEMV_SLAB_AUTO
+                                                                           : HALO_MI_GEMV_SLAB;
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,
                                  reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
                                  out.stride / kF32, a.rows, a.cols, a.n_vec, variant};

@@ -137,7 +137,10 @@ struct GemvArgs {
     KernelChoice kernel{};
     TensorRef norm_w{};  // Vulkan-only in the reference: rejected here
     float norm_eps = 1e-6f;
-    bool allow_gemm = false;  // accepted; the bf16 GEMM variant is chosen by kernel id or by n_vec
+    /// As in the reference: off (the default), every row of y is bitwise the row an n_vec == 1 call
+    /// gives, whatever n_vec (the SLAB default then runs the GEMV kernel at every n_vec). On, the
+    /// SLAB default may run the bf16 MFMA GEMM for n_vec > 8 (its own tolerance, not batch-invariant).
+    bool allow_gemm = false;
     struct Gates {
         TensorRef dt_bias{}, a{};
         std::uint32_t n_v = 0;
@@ -157,6 +160,7 @@ struct GateUpArgs {
     TensorRef w_gate{}, w_up{}, x{}, out{};
     std::uint32_t rows = 0, cols = 0, n_vec = 1;
     KernelChoice kernel{};
+    bool allow_gemm = false;  ///< same meaning as GemvArgs::allow_gemm
 };
 
 class Stream {

@@ -165,6 +165,23 @@ def test_gemv_slab_within_bound(hl, oracle, dev, t, case):
     assert np.all(err <= tol)
 
 
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("rows,cols", [(130, 1024), (576, 5120)])
+def test_gemv_slab_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
+    """GemvArgs::allow_gemm == false (include/halo/backend/backend.h:298-302): every row of a
+    batched call is bitwise the row of an n_vec == 1 call, whatever n_vec."""
+    say("gemv_slab batch invariance", NAMES[t], rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=250 + t + rows)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(2500 + t).standard_normal((9, cols)).astype(np.float32)
+    singles = np.stack([run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[i:i + 1], rows, cols, hl.Variant.SLAB_GEMV, 0, 0)[0]
+                        for i in range(9)])
+    for n_vec in (2, 3, 4, 5, 9):
+        y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[:n_vec], rows, cols, hl.Variant.SLAB_GEMV, 0, 0)
+        assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
+
+
 # ---- GEMM (bf16 MFMA) ---------------------------------------------------------------------
 
 
