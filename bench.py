@@ -136,6 +136,18 @@ def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
             "event_median_us": med * 1e3, "event_mean_us": mean * 1e3}
 
 
+# name -> (kind, type, rows, cols, M, seed): the workloads of the extra figures
+WORKLOADS = {
+    "q4k_gemv_17408x5120_m1": ("gemv", "Q4_K", 17408, 5120, 1, 2),
+    "q4k_gemv_17408x5120_m4": ("gemv", "Q4_K", 17408, 5120, 4, 2),
+    "q6k_gemv_5120x17408_m1": ("gemv", "Q6_K", 5120, 17408, 1, 3),
+    "q6k_gemv_5120x17408_m4": ("gemv", "Q6_K", 5120, 17408, 4, 3),
+    "q4k_gate_up_swiglu_m2": ("gemm", "Q4_K", 17408, 5120, 2, 4),
+    "q4k_gate_up_swiglu_m8": ("gemm", "Q4_K", 17408, 5120, 8, 4),
+    "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
+    "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
+}
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
 
 
@@ -177,6 +189,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--only", choices=sorted(WORKLOADS),
+                    help="run one workload alone and print its figures (for profiling); no headline line")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the benchmark, copy a buffer of this many MiB 4 times (a plain copy kernel of "
                          "known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -195,6 +209,18 @@ def main() -> int:
         return 1
     hl.lib()
     Q4_K, Q6_K = int(hl.DType.Q4_K), int(hl.DType.Q6_K)
+    if args.only:
+        kind, t, rows, cols, m, seed = WORKLOADS[args.only]
+        t = int(getattr(hl.DType, t))
+        log(f"only {args.only}")
+        if kind == "gemv":
+            r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
+            out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
+        else:
+            r = gemm_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
+            out = {"workload": args.only, "TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 3)}
+        print(json.dumps(out), flush=True)
+        return 0
 
     log("config 2: Q4_K GEMV 17408x5120 M=1")
     head = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps, args.warmup)
