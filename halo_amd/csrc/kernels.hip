@@ -1114,6 +1114,13 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
                 read_b((q + 1) % kPcBufs, 0, B0);  // stage i + 1 (zeros or junk past the end, unused)
                 mma(q, 1, B1);
                 load_a(q, s_begin + i0 + q + kPcADepth);
+                // issue order: W reads for the second half first, so neither batch of MFMAs waits
+                // for LDS; then the next stage's first W reads behind the first batch
+                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: B1
+                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 0
+                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: next B0
+                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 1
+                __builtin_amdgcn_sched_group_barrier(0x020, 2 * MBW, 0);    // VMEM read: x ring
                 pc_barrier();  // B_{i+1}
             }
         }

@@ -326,31 +326,39 @@ def test_baseline_q6_k_head(hl, oracle, dev):
 @pytest.mark.parametrize("n_vec", [2, 8, 64, 512])
 def test_baseline_gate_up(hl, oracle, dev, n_vec):
     """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices; the oracle checks the
-    first 512 output columns (rows of W are independent)."""
+    first 512 and the last 1088 output columns (rows of W are independent; at M = 512 the last
+    17 slabs are the K-split tiles of the GEMM launch)."""
     import torch
 
-    t, rows, cols, chk = Q4_K, 17408, 5120, 512
+    t, rows, cols = Q4_K, 17408, 5120
     say("baseline gate_up", n_vec)
     wg = synth(hl, t, rows, cols, 4)
     wu = synth(hl, t, rows, cols, 44)
     x = hl.fill_normal(1004, n_vec * cols).reshape(n_vec, cols)
     rb = row_bytes(t, cols)
-    ref = oracle.gate_up_swiglu(t, wg[:chk * rb], wu[:chk * rb], chk, cols, x)
-    g = oracle.matmul(t, wg[:chk * rb], chk, cols, x)
-    u = oracle.matmul(t, wu[:chk * rb], chk, cols, x)
     out = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
-    hl.gate_up_swiglu(t, slab_of(hl, dev, t, wg, rows, cols), slab_of(hl, dev, t, wu, rows, cols), to_dev(x, dev), out,
-                      rows, cols, n_vec)
-    y = host(out)[:, :chk]
-    if n_vec <= 8:
-        tg = slab_gemv_tol(oracle, t, wg[:chk * rb], chk, cols, x)
-        tu = slab_gemv_tol(oracle, t, wu[:chk * rb], chk, cols, x)
-    else:
-        tg = gemm_tol(oracle, t, wg[:chk * rb], chk, cols, x)
-        tu = gemm_tol(oracle, t, wu[:chk * rb], chk, cols, x)
-    tol = swiglu_tol(g, u, tg, tu, ref)
-    err = np.abs(y.astype(np.float64) - ref)
-    print(f"    gate_up M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}, "
-          f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
-    assert np.all(err <= tol)
+    sg, su, xd = slab_of(hl, dev, t, wg, rows, cols), slab_of(hl, dev, t, wu, rows, cols), to_dev(x, dev)
+    hl.gate_up_swiglu(t, sg, su, xd, out, rows, cols, n_vec)
+    yall = host(out)
+    # the split-K partial sums are added in a fixed order: a second call is bitwise identical
+    hl.gate_up_swiglu(t, sg, su, xd, out, rows, cols, n_vec)
+    assert isclose_bits(host(out), yall), "gate/up result changed between two identical calls"
+    for c0, c1 in ((0, 512), (rows - 1088, rows)):
+        n = c1 - c0
+        wg_c, wu_c = wg[c0 * rb:c1 * rb], wu[c0 * rb:c1 * rb]
+        ref = oracle.gate_up_swiglu(t, wg_c, wu_c, n, cols, x)
+        g = oracle.matmul(t, wg_c, n, cols, x)
+        u = oracle.matmul(t, wu_c, n, cols, x)
+        y = yall[:, c0:c1]
+        if n_vec <= 8:
+            tg = slab_gemv_tol(oracle, t, wg_c, n, cols, x)
+            tu = slab_gemv_tol(oracle, t, wu_c, n, cols, x)
+        else:
+            tg = gemm_tol(oracle, t, wg_c, n, cols, x)
+            tu = gemm_tol(oracle, t, wu_c, n, cols, x)
+        tol = swiglu_tol(g, u, tg, tu, ref)
+        err = np.abs(y.astype(np.float64) - ref)
+        print(f"    gate_up M={n_vec} columns [{c0}, {c1}): worst |d|/bound = {max_ratio(err, tol):.4f}, "
+              f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
+        assert np.all(err <= tol)
     assert np.all(np.isfinite(host(out)))
