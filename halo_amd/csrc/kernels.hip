@@ -31,6 +31,9 @@ namespace {
 using namespace dev;
 
 constexpr uint32_t kMaxGemvVec = 4;  // vectors per slab-gemv launch
+// Auto choice for the fused gate/up pair: the GEMV kernel streams each weight matrix once per
+// 4 vectors, so beyond one launch the MFMA GEMM (which streams it once) is faster.
+constexpr uint32_t kGateUpGemvMax = 4;
 
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
@@ -497,46 +500,45 @@ __device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t gr
     }
 }
 
-// grid.x = slabs * ks; block = 64 * nw (nw waves). Dynamic LDS: the waves' partials
-// [nw][NA][64].
+// grid.x = slabs * ks * MATS; block = 64 * nw (nw waves). Dynamic LDS: the waves' partials
+// [nw][NV][64]. With PAIR (MATS = 2) a workgroup streams one matrix only (chunks [0, ks) the
+// gate rows, [ks, 2 ks) the up rows of the same slab) and the gate and up sums meet in the
+// split-K fix-up, which applies SiLU: the pair costs no registers over a single GEMV.
 template <uint32_t T, int NV, bool PAIR>
 __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
     extern __shared__ float smem[];
-    constexpr int NA = PAIR ? 2 * NV : NV;
+    constexpr uint32_t MATS = PAIR ? 2 : 1;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
-    const uint32_t slab = blockIdx.x / a.ks, c = blockIdx.x % a.ks;
+    const uint32_t nch = a.ks * MATS;  // chunks per slab
+    const uint32_t slab = blockIdx.x / nch, c = blockIdx.x % nch;
+    const uint32_t mat = c / a.ks, cc = c % a.ks;
     // this workgroup's groups [g0, g1), then this wave's share [w0, w1)
     const uint32_t base = ngrp / a.ks, extra = ngrp % a.ks;
-    const uint32_t g0 = c * base + min(c, extra), g1 = g0 + base + (c < extra ? 1u : 0u);
+    const uint32_t g0 = cc * base + min(cc, extra), g1 = g0 + base + (cc < extra ? 1u : 0u);
     const uint32_t wb = (g1 - g0) / nw, we = (g1 - g0) % nw;
     const uint32_t w0 = g0 + wave * wb + min(wave, we), w1 = w0 + wb + (wave < we ? 1u : 0u);
     const SlabGeom geo = slab_geom(T, a.cols);
-    const uint8_t* slab0 = a.w0 + (uint64_t)slab * geo.slab_bytes;
-    const uint8_t* slab1 = PAIR ? a.w1 + (uint64_t)slab * geo.slab_bytes : nullptr;
+    const uint8_t* slab0 = (mat ? a.w1 : a.w0) + (uint64_t)slab * geo.slab_bytes;
     cfloat* xc = reinterpret_cast<cfloat*>(reinterpret_cast<uintptr_t>(a.x));
     float* red = smem;
 
     // 1 / fp8_unit, built from the exponent bits (exact for a power of two)
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
-    float acc0[NV], acc1[NV];
+    float acc0[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc0[v] = acc1[v] = 0.0f;
-    SlotGroup<T> cur0, cur1;
-    if (w0 < w1) {
-        load_group<T>(cur0, slab0, geo, lane, w0, S);
-        if constexpr (PAIR) load_group<T>(cur1, slab1, geo, lane, w0, S);
-    }
+    for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
+    SlotGroup<T> cur0;
+    if (w0 < w1) load_group<T>(cur0, slab0, geo, lane, w0, S);
     float xsv[NV];  // half-slot sums of this wave's groups (at most 4), one per lane
 #pragma unroll
     for (int v = 0; v < NV; ++v) xsv[v] = wave_xsums(a.x + (uint64_t)v * a.x_stride, w0, S, lane);
     for (uint32_t grp = w0; grp < w1; ++grp) {
-        if constexpr (PAIR) {
+        if constexpr (T == kQ8_0) {
+            // a Q8_0 group is 72 registers: one buffer, the next group loaded after this one
             compute_group<T, NV>(cur0, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
             if (grp + 1 < w1) load_group<T>(cur0, slab0, geo, lane, grp + 1, S);
-            compute_group<T, NV>(cur1, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc1);
-            if (grp + 1 < w1) load_group<T>(cur1, slab1, geo, lane, grp + 1, S);
         } else {
             // Ping-pong between two register buffers: the next group is always in flight. The
             // prefetch is unconditional (past the last group it reloads the last one, an L2
@@ -553,50 +555,42 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
     // waves -> wave 0, in wave order
     if (nw > 1) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            red[(wave * NA + v) * 64 + lane] = acc0[v];
-            if constexpr (PAIR) red[(wave * NA + NV + v) * 64 + lane] = acc1[v];
-        }
+        for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
-            float s = red[v * 64 + lane], u = PAIR ? red[(NV + v) * 64 + lane] : 0.0f;
-            for (uint32_t w = 1; w < nw; ++w) {
-                s += red[(w * NA + v) * 64 + lane];
-                if constexpr (PAIR) u += red[(w * NA + NV + v) * 64 + lane];
-            }
+            float s = red[v * 64 + lane];
+            for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
             acc0[v] = s;
-            acc1[v] = u;
         }
     }
     const uint32_t row = slab * kSlabRows + lane;
-    if (a.ks > 1) {
+    float acc1[NV];  // the up sums (PAIR)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
+    if (nch > 1) {
         // Cross-workgroup reduction without cache maintenance: partials are written and read
         // with relaxed device-scope atomic accesses (each one coherent across the XCDs' L2s),
         // the stores are complete (s_waitcnt) before the counter increment, and the counter is
         // a device-scope atomic. The last chunk of a slab adds the partials in chunk order.
-        float* P = a.partials + ((uint64_t)slab * a.ks + c) * NA * 64;
+        float* P = a.partials + ((uint64_t)slab * nch + c) * NV * 64;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            __hip_atomic_store(P + v * 64 + lane, acc0[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if constexpr (PAIR)
-                __hip_atomic_store(P + (NV + v) * 64 + lane, acc1[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int v = 0; v < NV; ++v) __hip_atomic_store(P + v * 64 + lane, acc0[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);  // the partial stores are performed before the count
         uint32_t prev = 0;
         if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         prev = __builtin_amdgcn_readfirstlane(prev);
-        if (prev != a.ks - 1) return;
+        if (prev != nch - 1) return;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) acc0[v] = acc1[v] = 0.0f;
-        for (uint32_t cc = 0; cc < a.ks; ++cc) {  // fixed chunk order: deterministic
-            const float* Q = a.partials + ((uint64_t)slab * a.ks + cc) * NA * 64;
+        for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
+        for (uint32_t k = 0; k < nch; ++k) {  // fixed chunk order: deterministic
+            const float* Q = a.partials + ((uint64_t)slab * nch + k) * NV * 64;
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
-                acc0[v] += __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if constexpr (PAIR)
-                    acc1[v] += __hip_atomic_load(Q + (NV + v) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float q = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (k < a.ks) acc0[v] += q;
+                else acc1[v] += q;
             }
         }
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1324,7 +1318,7 @@ struct GemvSplit {
     uint32_t ks, nw;
 };
 
-GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t na, bool have_ws) {
+GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, bool have_ws) {
     // Measured on MI355X (17408 x 5120 and 151936 x 5120 Q4_K): about 4 workgroups per CU, and
     // one slot group per wave for mid-size matrices, two for large ones.
     static const uint32_t target_wg = [] {
@@ -1338,8 +1332,9 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t na, bool 
     const uint32_t groups_per_wave = gpw_env ? (uint32_t)gpw_env : (slabs >= 1024 ? 2u : 1u);
     const uint32_t ngrp = (S + 7) / 8;
     uint32_t ks = 1;
-    if (have_ws && slabs < target_wg) ks = std::min((target_wg + slabs - 1) / std::max(slabs, 1u), ngrp);
-    while (ks > 1 && (uint64_t)slabs * ks * na * 64 > kPartialFloats) --ks;
+    const uint32_t units = std::max(slabs, 1u) * mats;
+    if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
+    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * 64 > kPartialFloats) --ks;
     const uint32_t gwg = (ngrp + ks - 1) / ks;
     uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
     // a wave holds the x sums of at most 4 groups (one per lane)
@@ -1355,13 +1350,13 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t na, bool 
 template <uint32_t T, int NV, bool PAIR>
 int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_t st) {
     const uint32_t S = a.cols / kSlot;
-    constexpr uint32_t NA = PAIR ? 2 * NV : NV;
-    const GemvSplit sp = pick_split(slabs, S, NV, NA, ws != nullptr && slabs <= kCounters);
+    constexpr uint32_t MATS = PAIR ? 2 : 1;
+    const GemvSplit sp = pick_split(slabs, S, NV, MATS, ws != nullptr && slabs <= kCounters);
     a.ks = sp.ks;
     a.partials = ws ? ws->partials : nullptr;
     a.counters = ws ? ws->counters : nullptr;
-    const size_t lds = (size_t)sp.nw * NA * 64 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks), dim3(64 * sp.nw), lds, st, a);
+    const size_t lds = (size_t)sp.nw * NV * 64 * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
 }
 
@@ -1380,6 +1375,11 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
     Workspace* ws = nullptr;
     if (int rc = workspace_for(st, &ws)) return rc;
+    // the pair's gate and up sums always meet in the workspace
+    if (PAIR && !ws)
+        return set_error(HALO_MI_E_MEMORY, "gate_up: this stream is being captured and has no workspace yet "
+                                           "(make one call on it before capturing)");
+    if (PAIR && slabs > kCounters) return set_error(HALO_MI_E_UNSUPPORTED, "gate_up: %u rows exceed the workspace", a.rows);
     const uint32_t total = a.n_vec;
     for (uint32_t t0 = 0; t0 < total; t0 += kMaxGemvVec) {
         GemvSlabArgs c = a;
@@ -1594,7 +1594,7 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     if (ranges_overlap(p->out, oext, p->w_gate, wbytes) || ranges_overlap(p->out, oext, p->w_up, wbytes))
         return set_error(HALO_MI_E_KERNEL, "%s: out overlaps a weight operand", op);
     if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
-        variant = p->n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+        variant = p->n_vec <= kGateUpGemvMax ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
     auto st = static_cast<hipStream_t>(stream);
     if (variant == HALO_MI_GEMV_SLAB) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,

@@ -72,7 +72,9 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *   1 HALO_MI_GEMV_GGUF_REF  GGUF layout, 8 lanes per output in cpu::detail::dot's order:
  *                            bit-identical to the CPU backend.
  *   2 HALO_MI_GEMV_SLAB      SLAB layout, wave64 row-per-lane weight stream, split-K inside
- *                            the workgroup; n_vec 1..8. Within the summation bound.
+ *                            the workgroup and across workgroups (fixed-order fix-up); any
+ *                            n_vec (4 per pass over the weights). Within the summation bound;
+ *                            every row is bitwise independent of n_vec.
  *   3 HALO_MI_GEMM_SLAB_BF16 SLAB layout, bf16 MFMA GEMM (dequantized W and x rounded to
  *                            bf16, fp32 accumulate); any n_vec.
  *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8, else 3.
@@ -115,8 +117,9 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
  * Fused FFN gate/up: out[t][n] = silu((Wg x_t)[n]) * (Wu x_t)[n], silu(v) = v / (1 + exp(-v)).
  * The reference composes it as gemv(gate), gemv(up), swiglu (src/models/qwen35.cpp:789-805;
  * backends/cpu/ops_basic.cpp:165-167); here both matmuls and the epilogue are one launch.
- * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto,
- * 2 = gemv kernel (n_vec <= 8), 3 = bf16 MFMA GEMM. out may not overlap x, Wg or Wu.
+ * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto
+ * (gemv kernel for n_vec <= 4, else the GEMM), 2 = gemv kernel (any n_vec, 4 vectors per pass
+ * over the weights), 3 = bf16 MFMA GEMM. out may not overlap x, Wg or Wu.
  */
 typedef struct halo_mi_gate_up_params {
     uint32_t type;
