@@ -56,9 +56,23 @@ def build_oracle() -> Path:
     return ROOT / "oracle" / "liboracle.so"
 
 
+CPP_TEST_SRC = ROOT / "tests" / "cpp" / "backend_pair.cpp"
+CPP_TEST_BIN = ROOT / "tests" / "cpp" / "backend_pair"
+
+
+def build_cpp_tests() -> Path:
+    """The C++ test of the Backend adapter (host code only: g++, linked against the library
+    and the oracle, found through $ORIGIN-relative run paths)."""
+    _run(["g++", "-std=c++20", "-O1", "-Wall", "-o", str(CPP_TEST_BIN), str(CPP_TEST_SRC),
+          "-L" + str(PKG), "-lhalo_mi355x", "-L" + str(ROOT / "oracle"), "-loracle",
+          "-Wl,-rpath,$ORIGIN/../../halo_amd:$ORIGIN/../../oracle"])
+    return CPP_TEST_BIN
+
+
 def build_all() -> None:
     build_oracle()
     build_library()
+    build_cpp_tests()
 
 
 if __name__ == "__main__":
