@@ -146,6 +146,9 @@ WORKLOADS = {
     "q4k_gate_up_swiglu_m8": ("gemm", "Q4_K", 17408, 5120, 8, 4),
     "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
     "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
+    "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
+    "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
+    "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
 }
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
@@ -160,6 +163,54 @@ def measured_traffic():
     except (OSError, ValueError):
         return None
     return {"traffic_bytes": round(t["traffic_bytes"]), "source": os.path.relpath(TRAFFIC_FILE, ROOT)}
+
+
+# one synthetic Q4_K_M-mixed hybrid layer, hidden 5120: (name, type, rows, cols)
+LAYER = [
+    ("gdn_in", "Q4_K", 12288, 5120),
+    ("gdn_out", "Q4_K", 5120, 6144),
+    ("q", "Q4_K", 6144, 5120),
+    ("k", "Q4_K", 1024, 5120),
+    ("v", "Q6_K", 1024, 5120),
+    ("o", "Q4_K", 5120, 6144),
+    ("gate_up", "Q4_K", 17408, 5120),  # two matrices, one fused gate/up/SwiGLU call
+    ("down", "Q6_K", 5120, 17408),
+]
+
+
+def layer_case(hl, torch, m, steps, warmup, seed=5):
+    """All matmuls of one config-5 layer as one step (the fused gate/up pair is one call), over
+    enough copies of the layer's weights that the MALL cannot serve repeats."""
+    mats = []
+    one_copy = 0
+    for i, (name, tn, rows, cols) in enumerate(LAYER):
+        t = int(getattr(hl.DType, tn))
+        ws = [make_weights(hl, t, rows, cols, seed * 100 + 10 * i + j) for j in range(2 if name == "gate_up" else 1)]
+        dev = []
+        for wq in ws:
+            d = torch.empty(hl.slab_bytes(t, rows, cols), dtype=torch.uint8, device="cuda")
+            hl.repack_slab(t, torch.from_numpy(wq).to("cuda"), rows, cols, d)
+            dev.append(d)
+            one_copy += d.numel()
+        mats.append((name, t, rows, cols, dev, sum(len(w) for w in ws)))
+    n_copies = max(2, math.ceil(MALL_BYTES / one_copy) + 1)
+    copies = [mats] + [[(n, t, r, c, [d.clone() for d in dv], wb) for (n, t, r, c, dv, wb) in mats] for _ in range(n_copies - 1)]
+    xs = {c: torch.from_numpy(hl.fill_normal(seed + 1000 + c, m * c).reshape(m, c)).to("cuda") for c in {5120, 6144, 17408}}
+    ys = {name: torch.empty((m, rows), dtype=torch.float32, device="cuda") for name, _, rows, _, _, _ in mats}
+
+    def launch(i):
+        for name, t, rows, cols, dev, _ in copies[i]:
+            if name == "gate_up":
+                hl.gate_up_swiglu(t, dev[0], dev[1], xs[cols], ys[name], rows, cols, m)
+            else:
+                hl.gemv(t, dev[0], xs[cols], ys[name], rows, cols, m)
+
+    ms, nsteps = time_graph(torch, launch, n_copies, steps, warmup)
+    algo = sum(wb + 4 * m * cols + 4 * m * rows for name, _, rows, cols, _, wb in mats)
+    flops = sum((4.0 if name == "gate_up" else 2.0) * m * rows * cols for name, _, rows, cols, _, _ in mats)
+    del copies, mats
+    torch.cuda.empty_cache()
+    return {"ms": ms, "steps": nsteps, "bytes": algo, "gbs": algo / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
 def cpu_baseline(t, wq, rows, cols, x, seconds):
@@ -211,8 +262,13 @@ def main() -> int:
     Q4_K, Q6_K = int(hl.DType.Q4_K), int(hl.DType.Q6_K)
     if args.only:
         kind, t, rows, cols, m, seed = WORKLOADS[args.only]
-        t = int(getattr(hl.DType, t))
         log(f"only {args.only}")
+        if kind == "layer":
+            r = layer_case(hl, torch, m, args.steps, args.warmup, seed)
+            print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                              "TFLOP/s": round(r["tflops"], 2)}), flush=True)
+            return 0
+        t = int(getattr(hl.DType, t))
         if kind == "gemv":
             r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
             out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
@@ -243,6 +299,14 @@ def main() -> int:
         r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
         extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                             "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("config 1 on the GPU: Q4_0 GEMV 4096x4096 M=1")
+        r = gemv_case(hl, torch, int(hl.DType.Q4_0), 4096, 4096, 1, 0, args.steps // 2, args.warmup)
+        extra["q4_0_gemv_4096x4096_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}
+        for m in (1, 4, 512):
+            log(f"config 5: hybrid layer (8 matmuls, 269 MB of weights) M={m}")
+            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5)
+            extra[f"hybrid_layer_m{m}"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                           "TFLOP/s": round(r["tflops"], 2)}
         for m in (2, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
             r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, max(20, args.steps // 20), 5)

@@ -584,13 +584,29 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
         if (prev != nch - 1) return;
 #pragma unroll
         for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
-        for (uint32_t k = 0; k < nch; ++k) {  // fixed chunk order: deterministic
-            const float* Q = a.partials + ((uint64_t)slab * nch + k) * NV * 64;
+        // Fixed chunk order (deterministic). The loads of 8 chunks are issued before any is
+        // used, so the fix-up costs one memory round trip per 8 chunks, not one per chunk;
+        // past the last chunk the address is clamped and the value dropped (straight-line code).
+        constexpr uint32_t KB = 8;
+        const float* Pslab = a.partials + (uint64_t)slab * nch * NV * 64;
+        for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
+            float q[KB][NV];
 #pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                const float q = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (k < a.ks) acc0[v] += q;
-                else acc1[v] += q;
+            for (uint32_t kk = 0; kk < KB; ++kk) {
+                const float* Q = Pslab + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
+#pragma unroll
+                for (int v = 0; v < NV; ++v)
+                    q[kk][v] = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (uint32_t kk = 0; kk < KB; ++kk) {
+                const uint32_t k = k0 + kk;
+                if (k >= nch) break;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    if (k < a.ks) acc0[v] += q[kk][v];
+                    else acc1[v] += q[kk][v];
+                }
             }
         }
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1319,11 +1335,11 @@ struct GemvSplit {
 };
 
 GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, bool have_ws) {
-    // Measured on MI355X (17408 x 5120 and 151936 x 5120 Q4_K): about 4 workgroups per CU, and
-    // one slot group per wave for mid-size matrices, two for large ones.
-    static const uint32_t target_wg = [] {
+    // One slot group per wave for mid-size matrices, two for large ones (measured on MI355X,
+    // 17408 x 5120 and 151936 x 5120 Q4_K).
+    static const uint32_t target_env = [] {
         const char* e = std::getenv("HALO_MI_GEMV_WGS");  // tuning knob: min workgroups per launch
-        return e ? (uint32_t)std::max(1, std::atoi(e)) : 1088u;
+        return e ? (uint32_t)std::max(1, std::atoi(e)) : 0u;
     }();
     static const int gpw_env = [] {
         const char* e = std::getenv("HALO_MI_GEMV_GPW");  // tuning knob: slot groups per wave
@@ -1333,6 +1349,9 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, boo
     const uint32_t ngrp = (S + 7) / 8;
     uint32_t ks = 1;
     const uint32_t units = std::max(slabs, 1u) * mats;
+    // Measured on MI355X: about 4 workgroups per slab up to 1088 per launch; small matrices
+    // gain more from a short split-K fix-up than from more workgroups (floor of 128).
+    const uint32_t target_wg = target_env ? target_env : std::clamp(4 * units, 128u, 1088u);
     if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
     while (ks > 1 && (uint64_t)slabs * ks * mats * nv * 64 > kPartialFloats) --ks;
     const uint32_t gwg = (ngrp + ks - 1) / ks;
@@ -1452,11 +1471,12 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, a.x + m_start * a.x_stride,
                            a.x_stride, mc, m_tiles * BM, a.cols, ws->xb);
         float* y = a.y + m_start * a.y_stride;
-        // whole rounds of tiles, then the rest split over K
+        // whole rounds of tiles, then the rest split over K; a matrix whose tiles cannot fill
+        // half the chip is split over K altogether
         const uint64_t tiles = (uint64_t)units * m_tiles;
         uint32_t main_units = units, kc = 1;
-        if (tiles > cus && tiles % cus != 0 && S % 8 == 0) {
-            main_units = (uint32_t)(tiles / cus * cus / m_tiles);
+        if (S % 8 == 0 && ((tiles > cus && tiles % cus != 0) || 2 * tiles < cus)) {
+            main_units = tiles > cus ? (uint32_t)(tiles / cus * cus / m_tiles) : 0u;
             const uint64_t rest = (uint64_t)(units - main_units) * m_tiles;
             kc = (uint32_t)std::min<uint64_t>({cus / std::max<uint64_t>(rest, 1), S / 8, 16});
             while (kc > 1 && rest * kc * BM * kPcW > kPartialFloats) --kc;

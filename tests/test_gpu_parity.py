@@ -362,3 +362,30 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
               f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
         assert np.all(err <= tol)
     assert np.all(np.isfinite(host(out)))
+
+
+# config 5: the hybrid layer's projections (the FFN pair is test_baseline_gate_up)
+@pytest.mark.parametrize("name,t,rows,cols", [
+    ("gdn_in", Q4_K, 12288, 5120), ("gdn_out", Q4_K, 5120, 6144), ("q", Q4_K, 6144, 5120),
+    ("k", Q4_K, 1024, 5120), ("v", Q6_K, 1024, 5120), ("down", Q6_K, 5120, 17408)])
+def test_baseline_hybrid_layer_shapes(hl, oracle, dev, name, t, rows, cols):
+    """Each projection of the config-5 layer at M = 1 (GEMV) and M = 512 (bf16 GEMM, the
+    default for more than 8 vectors), checked on its first and last 256 rows."""
+    import torch
+
+    say("hybrid layer", name, NAMES[t], rows, cols)
+    wq = synth(hl, t, rows, cols, 500 + rows + cols)
+    rb = row_bytes(t, cols)
+    slab = slab_of(hl, dev, t, wq, rows, cols)
+    for n_vec in (1, 512):
+        x = hl.fill_normal(600 + n_vec, n_vec * cols).reshape(n_vec, cols)
+        y = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
+        hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, n_vec)
+        yh = host(y)
+        for r0 in (0, rows - 256):
+            part = wq[r0 * rb:(r0 + 256) * rb]
+            ref = oracle.matmul(t, part, 256, cols, x)
+            tol = slab_gemv_tol(oracle, t, part, 256, cols, x) if n_vec == 1 else gemm_tol(oracle, t, part, 256, cols, x)
+            err = np.abs(yh[:, r0:r0 + 256].astype(np.float64) - ref)
+            print(f"    {name} M={n_vec} rows [{r0}, {r0 + 256}): worst |d|/bound = {max_ratio(err, tol):.4f}")
+            assert np.all(err <= tol)
