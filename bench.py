@@ -146,6 +146,7 @@ WORKLOADS = {
     "q4k_gate_up_swiglu_m8": ("gemm", "Q4_K", 17408, 5120, 8, 4),
     "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
     "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
+    "upload_q4k_17408x5120": ("upload", "Q4_K", 17408, 5120, 0, 2),
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
     "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
@@ -176,6 +177,45 @@ LAYER = [
     ("gate_up", "Q4_K", 17408, 5120),  # two matrices, one fused gate/up/SwiGLU call
     ("down", "Q6_K", 5120, 17408),
 ]
+
+
+def upload_case(hl, torch, t, rows, cols, seed, reps=10):
+    """North-star part (c): GGUF rows -> SLAB image. The device repack (GGUF bytes already in
+    HBM; reads and writes the matrix once: 2 x bytes of traffic) and the host upload from
+    pinned memory through halo_mi_upload_slab (PCIe-inclusive; never the headline value)."""
+    wq = make_weights(hl, t, rows, cols, seed)
+    nbytes = len(wq)
+    src = torch.from_numpy(wq).to("cuda")
+    dst = torch.empty(hl.slab_bytes(t, rows, cols), dtype=torch.uint8, device="cuda")
+    hl.repack_slab(t, src, rows, cols, dst)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        hl.repack_slab(t, src, rows, cols, dst)
+    e1.record()
+    torch.cuda.synchronize()
+    repack_ms = e0.elapsed_time(e1) / reps
+    pinned = torch.from_numpy(wq).pin_memory()
+    host = pinned.numpy()
+    hl.upload_slab(t, host, rows, cols, dst)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        hl.upload_slab(t, host, rows, cols, dst)
+    torch.cuda.synchronize()
+    upload_ms = (time.perf_counter() - t0) * 1e3 / reps
+    # pageable host memory, as from an mmap'd GGUF file
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        hl.upload_slab(t, wq, rows, cols, dst)
+    torch.cuda.synchronize()
+    pageable_ms = (time.perf_counter() - t0) * 1e3 / reps
+    del src, dst, pinned
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "repack_us": repack_ms * 1e3, "repack_gbs": 2 * nbytes / (repack_ms * 1e-3) / 1e9,
+            "upload_ms": upload_ms, "upload_gbs": nbytes / (upload_ms * 1e-3) / 1e9,
+            "pageable_ms": pageable_ms, "pageable_gbs": nbytes / (pageable_ms * 1e-3) / 1e9}
 
 
 def layer_case(hl, torch, m, steps, warmup, seed=5):
@@ -263,6 +303,10 @@ def main() -> int:
     if args.only:
         kind, t, rows, cols, m, seed = WORKLOADS[args.only]
         log(f"only {args.only}")
+        if kind == "upload":
+            r = upload_case(hl, torch, int(getattr(hl.DType, t)), rows, cols, seed)
+            print(json.dumps({"workload": args.only, **{k: round(v, 3) for k, v in r.items()}}), flush=True)
+            return 0
         if kind == "layer":
             r = layer_case(hl, torch, m, args.steps, args.warmup, seed)
             print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
@@ -299,6 +343,15 @@ def main() -> int:
         r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
         extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                             "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("part (c): GGUF -> SLAB repack and host upload, Q4_K 17408x5120")
+        r = upload_case(hl, torch, Q4_K, 17408, 5120, 2)
+        extra["q4k_17408x5120_repack_device"] = {"us": round(r["repack_us"], 2), "GB/s": round(r["repack_gbs"], 1),
+                                                  "note": "reads + writes the 50 MB matrix once"}
+        extra["q4k_17408x5120_upload_from_pinned_host"] = {"ms": round(r["upload_ms"], 3), "GB/s": round(r["upload_gbs"], 1),
+                                                           "note": "PCIe-inclusive, 64 MiB chunks through one staging buffer"}
+        extra["q4k_17408x5120_upload_from_pageable_host"] = {"ms": round(r["pageable_ms"], 3),
+                                                             "GB/s": round(r["pageable_gbs"], 1),
+                                                             "note": "as from an mmap'd GGUF file"}
         log("config 1 on the GPU: Q4_0 GEMV 4096x4096 M=1")
         r = gemv_case(hl, torch, int(hl.DType.Q4_0), 4096, 4096, 1, 0, args.steps // 2, args.warmup)
         extra["q4_0_gemv_4096x4096_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}
