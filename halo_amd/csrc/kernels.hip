@@ -797,12 +797,15 @@ struct GemmPcArgs {
     float* y;
     uint64_t y_stride;
     uint32_t rows, cols, n_vec;
-    uint32_t unit0;        // first W tile of this launch
-    uint32_t units;        // W tiles of this launch (PAIR: slabs; else pairs of slabs)
+    uint32_t units;        // W tiles [0, units) run whole (PAIR: slabs; else pairs of slabs), all M tiles
     uint32_t m_tiles;
-    uint32_t xcd_map;      // workgroups grouped by XCD so an XCD reuses one slice of x
-    uint32_t kchunks;      // > 1: each tile's K is split in chunks whose fp32 partials go to
-    float* partials;       //   partials[(tile * kchunks + chunk)][BM][128] (k_gemm_pc_reduce)
+    uint32_t xcd_map;      // whole tiles grouped by XCD so an XCD reuses one slice of x
+    // W tiles [units, units + split_units) (all M tiles) run as kchunks K chunks each, one
+    // workgroup per chunk after the whole tiles; their fp32 partials go to
+    // partials[(split tile * kchunks + chunk)][BM][128] and k_gemm_pc_reduce adds them.
+    uint32_t split_units;
+    uint32_t kchunks;
+    float* partials;
 };
 
 // Producer barrier: its LDS writes are complete, then s_barrier. Global loads stay in flight.
@@ -1040,23 +1043,30 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     const SlabGeom g = slab_geom(T, a.cols);
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
 
-    // workgroup -> (K chunk, W tile u, M tile mt)
-    const uint32_t chunk = blockIdx.x % a.kchunks, wg = blockIdx.x / a.kchunks;
-    uint32_t u, mt;
-    if (a.xcd_map) {
-        const uint32_t grp = 8 / a.m_tiles, xcd = wg % 8;
-        mt = xcd / grp;
-        u = (wg / 8) * grp + xcd % grp;
+    // workgroup -> (W tile u, M tile mt) for a whole tile, or (split tile st, K chunk)
+    const uint32_t whole = a.units * a.m_tiles;
+    const bool split = blockIdx.x >= whole;
+    uint32_t u, mt, st = 0, chunk = 0;
+    if (!split) {
+        const uint32_t wg = blockIdx.x;
+        if (a.xcd_map) {
+            const uint32_t grp = 8 / a.m_tiles, xcd = wg % 8;
+            mt = xcd / grp;
+            u = (wg / 8) * grp + xcd % grp;
+        } else {
+            u = wg / a.m_tiles;
+            mt = wg % a.m_tiles;
+        }
     } else {
-        u = wg / a.m_tiles;
-        mt = wg % a.m_tiles;
+        st = (blockIdx.x - whole) / a.kchunks;
+        chunk = (blockIdx.x - whole) % a.kchunks;
+        u = a.units + st / a.m_tiles;
+        mt = st % a.m_tiles;
     }
-    const uint32_t tile = wg;  // index of this tile within the launch (partials)
-    u += a.unit0;
     const uint32_t m0 = mt * BM;
     // this chunk's stages: whole groups of 8 slots when K is split
     uint32_t s_begin = 0, s_end = S;
-    if (a.kchunks > 1) {
+    if (split) {
         const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
         const uint32_t g0 = chunk * base + min(chunk, extra);
         s_begin = 8 * g0;
@@ -1134,9 +1144,9 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
                 pc_barrier();  // B_{i+1}
             }
         }
-        if (a.kchunks > 1) {
+        if (split) {
             // fp32 partial tile [BM][128] of this chunk
-            float* P = a.partials + ((uint64_t)tile * a.kchunks + chunk) * BM * kPcW;
+            float* P = a.partials + ((uint64_t)st * a.kchunks + chunk) * BM * kPcW;
 #pragma unroll
             for (int i = 0; i < MBW; ++i)
 #pragma unroll
@@ -1227,20 +1237,11 @@ template <bool PAIR, int BM>
 __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     constexpr uint32_t NC = PAIR ? 64 : kPcW;  // output columns per tile
-    const uint64_t tiles = (uint64_t)a.units * a.m_tiles;
+    const uint64_t tiles = (uint64_t)a.split_units * a.m_tiles;
     if (idx >= tiles * BM * NC) return;
     const uint32_t tile = (uint32_t)(idx / (BM * NC)), e = (uint32_t)(idx % (BM * NC));
     const uint32_t ml = e / NC, nl = e % NC;
-    uint32_t u, mt;
-    if (a.xcd_map) {
-        const uint32_t grp = 8 / a.m_tiles, xcd = tile % 8;
-        mt = xcd / grp;
-        u = (tile / 8) * grp + xcd % grp;
-    } else {
-        u = tile / a.m_tiles;
-        mt = tile % a.m_tiles;
-    }
-    u += a.unit0;
+    const uint32_t u = a.units + tile / a.m_tiles, mt = tile % a.m_tiles;
     const uint32_t m = mt * BM + ml;
     if (m >= a.n_vec) return;
     const float* P = a.partials + (uint64_t)tile * a.kchunks * BM * kPcW + ml * kPcW;
@@ -1454,7 +1455,7 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
         return (uint32_t)std::max(n, 1);
     }();
     auto launch = [&](const GemmPcArgs& p) {
-        const dim3 grid(p.units * p.m_tiles * p.kchunks);
+        const dim3 grid(p.units * p.m_tiles + p.split_units * p.m_tiles * p.kchunks);
         switch (MB) {
             case 1: launch_gemm_pc_type<PAIR, 1>(type, p, grid, st); break;
             case 2: launch_gemm_pc_type<PAIR, 2>(type, p, grid, st); break;
@@ -1482,17 +1483,13 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
             while (kc > 1 && rest * kc * BM * kPcW > kPartialFloats) --kc;
             if (kc < 2) main_units = units;  // nothing to gain: one launch
         }
-        if (main_units > 0) {
-            GemmPcArgs p{a.w0, a.w1, ws->xb, y, a.y_stride, a.rows, a.cols, mc, 0u, main_units, m_tiles, 0u, 1u, nullptr};
-            p.xcd_map = xcd_ok(main_units, m_tiles);
-            launch(p);
-        }
-        if (main_units < units) {
-            GemmPcArgs p{a.w0, a.w1, ws->xb, y, a.y_stride, a.rows, a.cols, mc, main_units, units - main_units, m_tiles, 0u,
-                         kc, ws->partials};
-            p.xcd_map = xcd_ok(units - main_units, m_tiles);
-            launch(p);
-            const uint64_t outs = (uint64_t)p.units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
+        // one launch: the whole tiles, then the split tiles' chunks (dispatched as CUs free up)
+        GemmPcArgs p{a.w0, a.w1, ws->xb, y, a.y_stride, a.rows, a.cols, mc, main_units, m_tiles, 0u,
+                     units - main_units, kc, ws->partials};
+        p.xcd_map = xcd_ok(main_units, m_tiles);
+        launch(p);
+        if (p.split_units > 0) {
+            const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
             const dim3 rg((uint32_t)((outs + 255) / 256));
             switch (MB) {
                 case 1: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 64>), rg, dim3(256), 0, st, p); break;
