@@ -45,24 +45,50 @@ __device__ __forceinline__ float sbyte(uint32_t v, int k) { return (float)(int)(
 // Repack / unpack / dequantize
 // ==========================================================================================
 
+// One thread per (slab, block, row), row fastest: the 64 threads of a (slab, block) write each
+// of the block's slot records as one contiguous 1 KB, and each reads its row's block.
 __global__ void k_repack_slab(uint32_t type, const uint8_t* __restrict__ src, uint64_t src_stride, uint32_t rows,
                               uint32_t cols, uint8_t* __restrict__ dst) {
     const SlabGeom g = slab_geom(type, cols);
     const uint32_t nblk = cols / block_elems(type), S = cols / kSlot;
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint64_t padded = (uint64_t)(rows + kSlabRows - 1) / kSlabRows * kSlabRows;
-    if (idx >= padded * nblk) return;
-    const uint64_t row = idx / nblk;
-    const uint32_t b = (uint32_t)(idx % nblk);
+    const uint64_t slabs = (rows + kSlabRows - 1) / kSlabRows;
+    if (idx >= slabs * nblk * kSlabRows) return;
+    const uint32_t r = (uint32_t)(idx % kSlabRows);
+    const uint64_t sb = idx / kSlabRows;
+    const uint32_t b = (uint32_t)(sb % nblk);
+    const uint64_t slab = sb / nblk, row = slab * kSlabRows + r;
+    uint8_t* out = dst + slab * g.slab_bytes;
+    const uint8_t* s = src + row * src_stride + (uint64_t)b * block_bytes(type);
+    if (type == kQ4_K && ((reinterpret_cast<uintptr_t>(s) | src_stride) % 16) == 0) {
+        // vector path: 9 x 16 B in; 8 slot records and the header out as 16-byte stores
+        uint4 blk[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) blk[i] = row < rows ? reinterpret_cast<const uint4*>(s)[i] : uint4{0, 0, 0, 0};
+        *reinterpret_cast<uint4*>(out + g.aux_off + ((uint64_t)b * 64 + r) * 16) = blk[0];
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {  // 32 quant bytes: sub-blocks 2 grp (low nibbles), 2 grp + 1 (high)
+            const uint4 A = blk[1 + 2 * grp], B = blk[2 + 2 * grp];
+            const uint32_t a[4] = {A.x, A.y, A.z, A.w}, c[4] = {B.x, B.y, B.z, B.w};
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                lo[k] = (a[k] & 0x0F0F0F0Fu) | ((c[k] & 0x0F0F0F0Fu) << 4);
+                hi[k] = ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0xF0F0F0F0u);
+            }
+            *reinterpret_cast<uint4*>(out + g.q_off + (((uint64_t)b * 8 + 2 * grp) * 64 + r) * 16) = uint4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<uint4*>(out + g.q_off + (((uint64_t)b * 8 + 2 * grp + 1) * 64 + r) * 16) = uint4{hi[0], hi[1], hi[2], hi[3]};
+        }
+        return;
+    }
     uint8_t blk[210];
     const uint32_t bb = block_bytes(type);
     if (row < rows) {
-        const uint8_t* s = src + row * src_stride + (uint64_t)b * bb;
         for (uint32_t i = 0; i < bb; ++i) blk[i] = s[i];
     } else {
         for (uint32_t i = 0; i < bb; ++i) blk[i] = 0;
     }
-    slab_pack_block(type, blk, dst + (row / kSlabRows) * g.slab_bytes, g, S, (uint32_t)(row % kSlabRows), b);
+    slab_pack_block(type, blk, out, g, S, r, b);
 }
 
 __global__ void k_unpack_slab(uint32_t type, const uint8_t* __restrict__ src, uint32_t rows, uint32_t cols,

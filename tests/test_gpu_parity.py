@@ -101,23 +101,24 @@ def test_dequant_gguf_and_slab_bitwise(hl, oracle, dev, t, case):
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
-def test_repack_device_equals_host_and_unpacks(hl, dev, t):
+@pytest.mark.parametrize("pad,off", [(5, 3), (0, 0)])  # unaligned rows (byte path); 16-byte aligned rows
+def test_repack_device_equals_host_and_unpacks(hl, dev, t, pad, off):
     import torch
 
     rows, cols = 70, 768 if t in (Q4_K, Q6_K) else 544
-    say("repack", NAMES[t], rows, cols)
-    buf, stride = make_weights(t, rows, cols, seed=5 + t, stride_pad=5, offset=3)
-    dense = dense_of(buf, t, rows, cols, stride, 3)
+    say("repack", NAMES[t], rows, cols, pad, off)
+    buf, stride = make_weights(t, rows, cols, seed=5 + t, stride_pad=pad, offset=off)
+    dense = dense_of(buf, t, rows, cols, stride, off)
     host_slab = hl.repack_slab_host(t, dense, rows, cols)
     wd = to_dev(buf, dev)
     slab = torch.full((hl.slab_bytes(t, rows, cols),), 0xAB, dtype=torch.uint8, device=dev)
-    hl.repack_slab(t, wd.data_ptr() + 3, rows, cols, slab, src_stride=stride)
+    hl.repack_slab(t, wd.data_ptr() + off, rows, cols, slab, src_stride=stride)
     assert np.array_equal(host(slab), host_slab)
     back = torch.zeros(rows * row_bytes(t, cols), dtype=torch.uint8, device=dev)
     hl.unpack_slab(t, slab, rows, cols, back)
     assert np.array_equal(host(back), dense)
     up = torch.zeros_like(slab)
-    hl.upload_slab(t, buf[3:], rows, cols, up, src_stride=stride, chunk_bytes=row_bytes(t, cols) * 64)
+    hl.upload_slab(t, buf[off:], rows, cols, up, src_stride=stride, chunk_bytes=row_bytes(t, cols) * 64)
     assert np.array_equal(host(up), host_slab)
 
 
