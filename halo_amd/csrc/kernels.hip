@@ -921,15 +921,15 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
     }
 }
 
-// Workgroup size bound: the 4-bit single-vector kernel fits 128 VGPRs (16 waves per
-// workgroup); the others need more registers than that and run at most 8 waves.
-template <uint32_t T, int NV>
-constexpr uint32_t mx_max_threads() { return ((T == kQ4_K || T == kQ4_0) && NV == 1) ? 1024u : 512u; }
+// Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
+// the Q8_0 and Q6_K loops (two register groups); the others run at most 8 waves.
+template <uint32_t T, int NV, bool ONE>
+constexpr uint32_t mx_max_threads() { return (NV == 1 && (ONE || (T != kQ8_0 && T != kQ6_K))) ? 1024u : 512u; }
 
 // grid, split and LDS as k_gemv_slab, plus one A table per wave after the partials. ONE: every
 // wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
 template <uint32_t T, int NV, bool PAIR, bool ONE>
-__global__ __launch_bounds__((mx_max_threads<T, NV>())) void k_gemv_mx(GemvSlabArgs a) {
+__global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
     extern __shared__ float smem[];
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     constexpr int M = mx_blocks<NV>();
@@ -1764,15 +1764,25 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
         hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
         return hip_status(hipGetLastError(), "gemv_slab launch");
     }
-    // the MFMA kernel adds one A table per wave; at most 64 KB of LDS per workgroup
-    uint32_t nw = std::min(sp.nw, mx_max_threads<T, NV>() / 64);
+    // MFMA kernel. Below 1024 slabs it runs one slot group per wave: enough K chunks that a
+    // chunk's groups fit one workgroup (at most 16 waves, 64 KB of LDS with the waves' A tables).
     const size_t per_wave = NV * 64 * sizeof(float) + mx_table_bytes<NV>();
+    const uint32_t ngrp = (S + 7) / 8;
+    uint32_t nw1 = mx_max_threads<T, NV, true>() / 64;
+    while (nw1 > 1 && nw1 * per_wave > 65536) --nw1;
+    if (ws && slabs < 1024 && slabs <= kCounters) {
+        uint32_t ks = std::max(a.ks, (ngrp + nw1 - 1) / nw1);
+        ks = std::min(ks, ngrp);
+        if ((uint64_t)slabs * ks * MATS * NV * 64 <= kPartialFloats) a.ks = ks;
+    }
+    const uint32_t gwg = (ngrp + a.ks - 1) / a.ks;  // groups of the largest chunk
+    if (gwg <= nw1 && (a.ks == 1 || ws)) {
+        hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave, st, a);
+        return hip_status(hipGetLastError(), "gemv_slab launch");
+    }
+    uint32_t nw = std::min(sp.nw, mx_max_threads<T, NV, false>() / 64);
     while (nw > 1 && nw * per_wave > 65536) --nw;
-    const uint32_t ngrp = (S + 7) / 8, gwg = (ngrp + a.ks - 1) / a.ks;  // groups of the largest chunk
-    if (gwg <= nw)
-        hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), dim3(slabs * a.ks * MATS), dim3(64 * nw), nw * per_wave, st, a);
-    else
-        hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), dim3(slabs * a.ks * MATS), dim3(64 * nw), nw * per_wave, st, a);
+    hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), dim3(slabs * a.ks * MATS), dim3(64 * nw), nw * per_wave, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
 }
 
