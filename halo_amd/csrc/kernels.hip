@@ -250,7 +250,7 @@ struct GemvSlabArgs {
     uint64_t y_stride;
     uint32_t rows, cols, n_vec;
     uint32_t ks;          // K chunks per slab
-    float* partials;      // [slabs][ks][NA][64] when ks > 1
+    uint64_t* slots;      // [slabs][chunks][NV][64] partials as (value, ready) words, 0 between launches
     uint32_t* counters;   // [slabs], zero between launches
 };
 
@@ -568,30 +568,37 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
     if (nch > 1) {
-        // Cross-workgroup reduction without cache maintenance: partials are written and read
-        // with relaxed device-scope atomic accesses (each one coherent across the XCDs' L2s),
-        // the stores are complete (s_waitcnt) before the counter increment, and the counter is
-        // a device-scope atomic. The last chunk of a slab adds the partials in chunk order.
-        float* P = a.partials + ((uint64_t)slab * nch + c) * NV * 64;
+        // Split-K meeting point, without cache maintenance and without waiting for stores.
+        // Each chunk stores its partials as 64-bit words (fp32 bits, 1 = ready): one atomic
+        // access carries the value and its mark. Then it counts its arrival (device-scope
+        // atomic). The chunk that arrives last for a slab loads the other chunks' words,
+        // re-reads any whose store is still in flight (bounded), adds the chunks in chunk
+        // order (deterministic), and clears the words and the counter for the next launch.
+        uint64_t* P = a.slots + (uint64_t)slab * nch * NV * 64;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) __hip_atomic_store(P + v * 64 + lane, acc0[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);  // the partial stores are performed before the count
+        for (int v = 0; v < NV; ++v)
+            __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
+                               (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         uint32_t prev = 0;
         if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         prev = __builtin_amdgcn_readfirstlane(prev);
         if (prev != nch - 1) return;
+        float own[NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
-        // Fixed chunk order (deterministic). The loads of 8 chunks are issued before any is
-        // used, so the fix-up costs one memory round trip per 8 chunks, not one per chunk;
-        // past the last chunk the address is clamped and the value dropped (straight-line code).
+        for (int v = 0; v < NV; ++v) {
+            own[v] = acc0[v];
+            acc0[v] = 0.0f;
+        }
+        // The loads of 8 chunks are issued before any is used (one memory round trip per 8
+        // chunks); past the last chunk the address is clamped and the value dropped.
         constexpr uint32_t KB = 8;
-        const float* Pslab = a.partials + (uint64_t)slab * nch * NV * 64;
+        constexpr uint32_t kSpinLimit = 1u << 16;  // the stores are already issued: a few round trips
         for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
-            float q[KB][NV];
+            uint64_t q[KB][NV];
 #pragma unroll
             for (uint32_t kk = 0; kk < KB; ++kk) {
-                const float* Q = Pslab + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
+                const uint64_t* Q = P + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
 #pragma unroll
                 for (int v = 0; v < NV; ++v)
                     q[kk][v] = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -602,11 +609,23 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                 if (k >= nch) break;
 #pragma unroll
                 for (int v = 0; v < NV; ++v) {
-                    if (k < a.ks) acc0[v] += q[kk][v];
-                    else acc1[v] += q[kk][v];
+                    float val = own[v];
+                    if (k != c) {
+                        uint64_t w = q[kk][v];
+                        for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin)
+                            w = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                        val = (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
+                    }
+                    if (k < a.ks) acc0[v] += val;
+                    else acc1[v] += val;
                 }
             }
         }
+        for (uint32_t k = 0; k < nch; ++k)
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+                __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (row >= a.rows) return;
@@ -1663,12 +1682,14 @@ uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes) { return row
 // on a stream (hipMalloc; counters cleared by a fill kernel on that stream, never a memset);
 // a call on a stream that is being captured into a graph and has no workspace yet runs
 // without split-K.
-constexpr uint64_t kPartialFloats = 8ull << 20;  // 32 MiB
+constexpr uint64_t kPartialFloats = 8ull << 20;  // GEMM split-tile partials: 32 MiB
+constexpr uint64_t kSlots = 4ull << 20;          // GEMV split-K words: 32 MiB
 constexpr uint64_t kCounters = 1ull << 20;        // slabs (64M rows)
 constexpr uint64_t kXbElems = 16ull << 20;        // bf16 copy of x for the GEMM: 32 MiB
 
 struct Workspace {
     float* partials = nullptr;
+    uint64_t* slots = nullptr;
     uint32_t* counters = nullptr;
     __bf16* xb = nullptr;
 };
@@ -1702,7 +1723,15 @@ int workspace_for(hipStream_t st, Workspace** out) {
         (void)hipFree(w.counters);
         return set_error(HALO_MI_E_MEMORY, "gemm: cannot allocate the bf16 staging buffer for x");
     }
+    if (hipMalloc(&w.slots, kSlots * sizeof(uint64_t)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        (void)hipFree(w.counters);
+        (void)hipFree(w.xb);
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K slots");
+    }
     hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)(kCounters / 256)), dim3(256), 0, st, w.counters, kCounters, 0u);
+    hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)(2 * kSlots / 256)), dim3(256), 0, st,
+                       reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u);
     if (hipGetLastError() != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
     *out = &(g_ws[{dev, st}] = w);
     return HALO_MI_OK;
@@ -1734,7 +1763,7 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, boo
     // gain more from a short split-K fix-up than from more workgroups (floor of 128).
     const uint32_t target_wg = target_env ? target_env : std::clamp(4 * units, 128u, 1088u);
     if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
-    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * 64 > kPartialFloats) --ks;
+    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * 64 > kSlots) --ks;
     const uint32_t gwg = (ngrp + ks - 1) / ks;
     uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
     // a wave holds the x sums of at most 4 groups (one per lane)
@@ -1753,7 +1782,7 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     const GemvSplit sp = pick_split(slabs, S, NV, MATS, ws != nullptr && slabs <= kCounters);
     a.ks = sp.ks;
-    a.partials = ws ? ws->partials : nullptr;
+    a.slots = ws ? ws->slots : nullptr;
     a.counters = ws ? ws->counters : nullptr;
     static const bool valu = [] {
         const char* e = std::getenv("HALO_MI_GEMV_VALU");
@@ -1773,7 +1802,7 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
     if (ws && slabs < 1024 && slabs <= kCounters) {
         uint32_t ks = std::max(a.ks, (ngrp + nw1 - 1) / nw1);
         ks = std::min(ks, ngrp);
-        if ((uint64_t)slabs * ks * MATS * NV * 64 <= kPartialFloats) a.ks = ks;
+        if ((uint64_t)slabs * ks * MATS * NV * 64 <= kSlots) a.ks = ks;
     }
     const uint32_t gwg = (ngrp + a.ks - 1) / a.ks;  // groups of the largest chunk
     if (gwg <= nw1 && (a.ks == 1 || ws)) {

@@ -183,6 +183,30 @@ def test_gemv_slab_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
         assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
 
 
+@pytest.mark.parametrize("t", (Q4_K, Q6_K))
+def test_gemv_split_k_state_is_clean_between_calls(hl, oracle, dev, t):
+    """Split-K calls of different shapes share the stream's workspace (arrival counters and
+    partial words). A call after calls of other shapes (other chunk counts over the same
+    counters and words) must give the same bits as the first call, within the bound."""
+    shapes = [(576, 5120, 1), (640, 17408, 1), (576, 5120, 4), (130, 1024, 3), (576, 5120, 1)]
+    mats = {}
+    for rows, cols, _ in shapes:
+        if (rows, cols) not in mats:
+            buf, stride = make_weights(t, rows, cols, seed=700 + rows)
+            dense = dense_of(buf, t, rows, cols, stride, 0)
+            mats[(rows, cols)] = (dense, slab_of(hl, dev, t, dense, rows, cols))
+    outs = []
+    for i, (rows, cols, n_vec) in enumerate(shapes):
+        say("gemv split-K state", NAMES[t], rows, cols, n_vec)
+        dense, slab = mats[(rows, cols)]
+        x = np.random.default_rng(7000 + cols + n_vec).standard_normal((n_vec, cols)).astype(np.float32)
+        y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMV, 0, 0)
+        ref = oracle.matmul(t, dense, rows, cols, x)
+        assert np.all(np.abs(y.astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dense, rows, cols, x)), shapes[i]
+        outs.append(y)
+    assert isclose_bits(outs[0], outs[-1]), "a later call of the same shape gave different bits"
+
+
 # ---- GEMM (bf16 MFMA) ---------------------------------------------------------------------
 
 
