@@ -547,9 +547,19 @@ __device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t gr
 // End of a slab-GEMV workgroup: the waves' partial sums meet in LDS in wave order, then (split
 // K) the workgroups of a slab meet in the workspace, and the result (SiLU(gate) * up for the
 // pair) is written. acc0 holds this wave's sums in fp32, rows = lanes.
+// Split-K: the workgroup's start ticket for its slab (0 .. nch - 1), taken when it starts and
+// used only at its end, so the device-scope round trip overlaps the weight stream.
+__device__ __forceinline__ uint32_t gemv_ticket(const GemvSlabArgs& a, uint32_t slab, uint32_t nch) {
+    uint32_t t = 0;
+    if (nch > 1 && threadIdx.x == 0)
+        t = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return t;
+}
+
 template <int NV, bool PAIR>
 __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
-                                            uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch) {
+                                            uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
+                                            uint32_t ticket) {
     // waves -> wave 0, in wave order
     if (nw > 1) {
 #pragma unroll
@@ -568,22 +578,22 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
     if (nch > 1) {
-        // Split-K meeting point, without cache maintenance and without waiting for stores.
-        // Each chunk stores its partials as 64-bit words (fp32 bits, 1 = ready): one atomic
-        // access carries the value and its mark. Then it counts its arrival (device-scope
-        // atomic). The chunk that arrives last for a slab loads the other chunks' words,
-        // re-reads any whose store is still in flight (bounded), adds the chunks in chunk
-        // order (deterministic), and clears the words and the counter for the next launch.
+        // Split-K meeting point, without cache maintenance and without a round trip at the end
+        // of most workgroups. The workgroup with the slab's last start ticket is the reducer:
+        // every other chunk of the slab started before it, so they are all running. The others
+        // store their partials as 64-bit words (fp32 bits, 1 = ready: one atomic access
+        // carries the value and its mark) and finish. The reducer loads those words, re-reads
+        // (bounded, with a pause) any not yet ready, adds the chunks in chunk order
+        // (deterministic), and clears the words and the ticket counter for the next launch.
         uint64_t* P = a.slots + (uint64_t)slab * nch * NV * 64;
+        if (__builtin_amdgcn_readfirstlane(ticket) != nch - 1) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
-            __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
-                               (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t prev = 0;
-        if (lane == 0) prev = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        prev = __builtin_amdgcn_readfirstlane(prev);
-        if (prev != nch - 1) return;
+            for (int v = 0; v < NV; ++v)
+                __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
+                                   (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
         float own[NV];
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -593,7 +603,7 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
         // The loads of 8 chunks are issued before any is used (one memory round trip per 8
         // chunks); past the last chunk the address is clamped and the value dropped.
         constexpr uint32_t KB = 8;
-        constexpr uint32_t kSpinLimit = 1u << 16;  // the stores are already issued: a few round trips
+        constexpr uint32_t kSpinLimit = 1u << 20;  // the other chunks are running: a few microseconds
         for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
             uint64_t q[KB][NV];
 #pragma unroll
@@ -612,9 +622,11 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                     float val = own[v];
                     if (k != c) {
                         uint64_t w = q[kk][v];
-                        for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin)
+                        for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin) {
+                            __builtin_amdgcn_s_sleep(2);
                             w = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
+                        }
                         val = (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
                     }
                     if (k < a.ks) acc0[v] += val;
@@ -623,9 +635,11 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
             }
         }
         for (uint32_t k = 0; k < nch; ++k)
+            if (k != c)
 #pragma unroll
-            for (int v = 0; v < NV; ++v)
-                __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int v = 0; v < NV; ++v)
+                    __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (row >= a.rows) return;
@@ -667,6 +681,7 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
     for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
     SlotGroup<T> cur0;
     if (w0 < w1) load_group<T>(cur0, slab0, geo, lane, w0, S);
+    const uint32_t ticket = gemv_ticket(a, slab, nch);
     float xsv[NV];  // half-slot sums of this wave's groups (at most 4), one per lane
 #pragma unroll
     for (int v = 0; v < NV; ++v) xsv[v] = wave_xsums(a.x + (uint64_t)v * a.x_stride, w0, S, lane);
@@ -688,7 +703,7 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
             compute_group<T, NV>(nxt, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
         }
     }
-    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch);
+    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -774,15 +789,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 // x of one slot group, lane = 8 s + r: x[slot 8 grp + s][4 r .. 4 r + 3] (zero past the end).
+// Branch-free (the address is clamped, the value selected after): a load under a branch would
+// make the compiler wait for it before the weight loads that follow are issued.
 template <int NV>
 __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], const float* __restrict__ x, uint64_t x_stride,
                                           uint32_t grp, uint32_t S, uint32_t lane) {
     const uint32_t slot = grp * 8 + (lane >> 3);
-    const uint64_t e = (uint64_t)slot * 32 + 4 * (lane & 7);
+    const bool in = slot < S;
+    const uint64_t e = (uint64_t)min(slot, S - 1) * 32 + 4 * (lane & 7);
 #pragma unroll
     for (int v = 0; v < NV; ++v)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[v][i] = slot < S ? x[(uint64_t)v * x_stride + e + i] : 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            const float t = x[(uint64_t)v * x_stride + e + i];
+            xr[v][i] = in ? t : 0.0f;
+        }
 }
 
 // Builds this wave's A table for one group from xr, reads it back as register pairs, and
@@ -971,11 +992,13 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
     float xr[NV][4];
+    uint32_t ticket = 0;
     if constexpr (ONE) {
         if (w0 < w1) {
             SlotGroup<T> G;
             mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
             load_group<T>(G, slab0, geo, lane, w0, S);
+            ticket = gemv_ticket(a, slab, nch);
             s16x4 A[4 * M];
             int es[NV];
             float xs[NV];
@@ -983,8 +1006,10 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
             mx_group<T, NV>(G, A, xs, min(8u, S - w0 * 8), acc0);
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
+        } else {
+            ticket = gemv_ticket(a, slab, nch);
         }
-        gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch);
+        gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
         return;
     }
     SlotGroup<T> cur, nxt;
@@ -992,6 +1017,7 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
         mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
         load_group<T>(cur, slab0, geo, lane, w0, S);
     }
+    ticket = gemv_ticket(a, slab, nch);
     // One group: build its A table from xr, prefetch x and the weights of the next group (past
     // the last group: the last one again, an L2 hit, so the loop stays branch-free), multiply.
     auto step = [&](const SlotGroup<T>& G, SlotGroup<T>& next, uint32_t grp) {
@@ -1015,7 +1041,7 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
         ++grp;
         step(nxt, cur, grp);
     }
-    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch);
+    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
 __global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
