@@ -38,6 +38,7 @@ class Variant(enum.IntEnum):
     SLAB_GEMV = 2
     SLAB_GEMM_BF16 = 3
     SLAB_AUTO = 4
+    SLAB_GEMM_BF16_M512 = 5
 
 
 class ErrorCode(enum.IntEnum):

@@ -11,12 +11,17 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libhalo_mi355x.so"
-SOURCES = [PKG / "csrc" / "kernels.hip", PKG / "csrc" / "host_utils.cpp", PKG / "csrc" / "backend.cpp"]
+CSRC = PKG / "csrc"
+# the kernel files first: they take longest and are compiled in parallel with the rest
+SOURCES = [CSRC / "k_gemv.hip", CSRC / "k_gemm.hip", CSRC / "k_dequant.hip", CSRC / "api.cpp",
+           CSRC / "host_utils.cpp", CSRC / "backend.cpp"]
+OBJ_DIR = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [
@@ -24,7 +29,6 @@ HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-std=c++20",
     "-fPIC",
-    "-shared",
     "-pthread",
     "-fno-gpu-flush-denormals-to-zero",
     "-mcode-object-version=5",
@@ -44,9 +48,19 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
         sys.stderr.write(err + "\n")
 
 
+def _compile(src: Path) -> Path:
+    obj = OBJ_DIR / (src.name + ".o")
+    _run([HIPCC, *HIP_FLAGS, "-c", "-o", str(obj), str(src)])
+    return obj
+
+
 def build_library() -> Path:
+    """Every source to an object (in parallel), then one shared library."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=max(1, min(len(SOURCES), os.cpu_count() or 1))) as ex:
+        objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, *HIP_FLAGS, "-o", str(tmp), *map(str, SOURCES)])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
     return LIB
 

@@ -1,0 +1,305 @@
+// The extern "C" entry points of the halo_mi355x library (include/halo_mi355x.h): argument
+// validation with the reference's error mapping (include/halo/backend/backend.h:24-26), the
+// per-stream workspace, and the dispatch to the kernel files' launchers.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "launch.h"
+
+namespace halo_mi {
+
+int hip_status(hipError_t e, const char* op) {
+    if (e == hipSuccess) return HALO_MI_OK;
+    return set_error(HALO_MI_E_DEVICE, "%s: %s", op, hipGetErrorString(e));
+}
+
+bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb) {
+    if (na == 0 || nb == 0 || a == nullptr || b == nullptr) return false;
+    const auto pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + nb && pb < pa + na;
+}
+
+uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes) { return rows ? (rows - 1) * stride + row_bytes : 0; }
+
+
+
+namespace {
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+}  // namespace
+
+int workspace_for(hipStream_t st, Workspace** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv: hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find({dev, st});
+    if (it != g_ws.end()) {
+        *out = &it->second;
+        return HALO_MI_OK;
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (st != nullptr && hipStreamIsCapturing(st, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone) {
+        *out = nullptr;  // cannot allocate under capture: caller runs without split-K
+        return HALO_MI_OK;
+    }
+    Workspace w;
+    if (hipMalloc(&w.partials, kPartialFloats * sizeof(float)) != hipSuccess)
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K workspace");
+    if (hipMalloc(&w.counters, kCounters * sizeof(uint32_t)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K counters");
+    }
+    if (hipMalloc(&w.xb, kXbElems * sizeof(__bf16)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        (void)hipFree(w.counters);
+        return set_error(HALO_MI_E_MEMORY, "gemm: cannot allocate the bf16 staging buffer for x");
+    }
+    if (hipMalloc(&w.slots, kSlots * sizeof(uint64_t)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        (void)hipFree(w.counters);
+        (void)hipFree(w.xb);
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K slots");
+    }
+    if (launch_fill_u32(w.counters, kCounters, 0u, st) != HALO_MI_OK ||
+        launch_fill_u32(reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u, st) != HALO_MI_OK)
+        return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
+    *out = &(g_ws[{dev, st}] = w);
+    return HALO_MI_OK;
+}
+
+
+int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, uint64_t y_stride, uint32_t rows,
+             uint32_t cols, uint32_t n_vec) {
+    if (n_vec == 0 || rows == 0 || cols == 0) return HALO_MI_OK;
+    if (!x || !y) return set_error(HALO_MI_E_KERNEL, "%s: operand x or y is empty", op);
+    if (n_vec > 1 && x_stride < cols)
+        return set_error(HALO_MI_E_KERNEL, "%s: x row stride %llu < %u floats", op, (unsigned long long)x_stride, cols);
+    if (n_vec > 1 && y_stride < rows)
+        return set_error(HALO_MI_E_KERNEL, "%s: y row stride %llu < %u floats", op, (unsigned long long)y_stride, rows);
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: x and y must be 4-byte aligned", op);
+    if (ranges_overlap(y, extent(n_vec, y_stride * 4, (uint64_t)rows * 4), x, extent(n_vec, x_stride * 4, (uint64_t)cols * 4)))
+        return set_error(HALO_MI_E_KERNEL, "%s: y overlaps x", op);
+    return HALO_MI_OK;
+}
+
+
+// The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
+uint32_t gemm_tiles(uint32_t variant) {
+    return variant == HALO_MI_GEMM_SLAB_BF16 ? kGemmTilesPc : variant == HALO_MI_GEMM_SLAB_BF16_M512 ? kGemmTilesLm
+                                                                                                   : kGemmTilesAuto;
+}
+
+}  // namespace halo_mi
+
+using namespace halo_mi;
+
+extern "C" {
+
+int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
+    clear_error();
+    if (!p) return set_error(HALO_MI_E_KERNEL, "gemv: null params");
+    const char* op = "MATMUL";
+    int code;
+    const uint64_t rb = row_bytes_checked(p->type, p->cols, &code, op);
+    if (code) return code;
+    uint32_t variant = p->variant;
+    if (variant > HALO_MI_GEMM_SLAB_BF16_M512)
+        return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
+    if (variant == HALO_MI_GEMV_DEFAULT)
+        variant = p->layout == HALO_MI_LAYOUT_SLAB ? HALO_MI_GEMV_SLAB_AUTO : HALO_MI_GEMV_GGUF_REF;
+    const uint64_t xs = p->x_stride ? p->x_stride : p->cols;
+    const uint64_t ys = p->y_stride ? p->y_stride : p->rows;
+    if ((code = check_xy(op, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec))) return code;
+    if (p->n_vec == 0 || p->rows == 0) return HALO_MI_OK;
+    if (!p->w) return set_error(HALO_MI_E_KERNEL, "%s: operand w is empty", op);
+    auto st = static_cast<hipStream_t>(stream);
+    const uint64_t yext = extent(p->n_vec, ys * 4, (uint64_t)p->rows * 4);
+    if (variant == HALO_MI_GEMV_GGUF_REF) {
+        if (p->layout != HALO_MI_LAYOUT_GGUF)
+            return set_error(HALO_MI_E_CONFIG, "%s: variant %u needs the GGUF layout", op, variant);
+        const uint64_t ws = p->w_stride ? p->w_stride : rb;
+        if (p->rows > 1 && ws < rb)
+            return set_error(HALO_MI_E_KERNEL, "%s: operand w row stride %llu < row bytes %llu", op, (unsigned long long)ws,
+                             (unsigned long long)rb);
+        if (p->type == kF32 && ((reinterpret_cast<uintptr_t>(p->w) | ws) % 4))
+            return set_error(HALO_MI_E_KERNEL, "%s: operand w is not 4-byte aligned", op);
+        if (ranges_overlap(p->y, yext, p->w, extent(p->rows, ws, rb))) return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
+        return launch_gemv_gguf_ref(p->type, static_cast<const uint8_t*>(p->w), ws, p->x, xs, p->y, ys, p->rows, p->cols,
+                                    p->n_vec, st);
+    }
+    if (p->layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: variant %u needs the SLAB layout", op, variant);
+    if (!is_quant(p->type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
+    if (p->w_stride != 0) return set_error(HALO_MI_E_KERNEL, "%s: a SLAB operand has no row stride", op);
+    if (reinterpret_cast<uintptr_t>(p->w) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
+    if (ranges_overlap(p->y, yext, p->w, halo_mi_slab_bytes(p->type, p->rows, p->cols)))
+        return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
+    if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = p->n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+    if (variant == HALO_MI_GEMV_SLAB) {
+        GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
+        return launch_gemv_slab<false>(p->type, a, st);
+    }
+    if (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
+        return set_error(HALO_MI_E_KERNEL, "%s: the MFMA GEMM needs 16-byte aligned x rows", op);
+    GemmArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
+    a.tiles = gemm_tiles(p->variant);
+    return launch_gemm_pc<false>(p->type, a, st);
+}
+
+int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
+    clear_error();
+    if (!p) return set_error(HALO_MI_E_KERNEL, "gate_up: null params");
+    const char* op = "GATE_UP_SWIGLU";
+    int code;
+    (void)row_bytes_checked(p->type, p->cols, &code, op);
+    if (code) return code;
+    if (p->layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: needs the SLAB layout", op);
+    if (!is_quant(p->type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
+    uint32_t variant = p->variant;
+    if (variant == HALO_MI_GEMV_GGUF_REF || variant > HALO_MI_GEMM_SLAB_BF16_M512)
+        return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
+    const uint64_t xs = p->x_stride ? p->x_stride : p->cols;
+    const uint64_t os = p->out_stride ? p->out_stride : p->rows;
+    if ((code = check_xy(op, p->x, xs, p->out, os, p->rows, p->cols, p->n_vec))) return code;
+    if (p->n_vec == 0 || p->rows == 0) return HALO_MI_OK;
+    if (!p->w_gate || !p->w_up) return set_error(HALO_MI_E_KERNEL, "%s: operand w_gate or w_up is empty", op);
+    if ((reinterpret_cast<uintptr_t>(p->w_gate) | reinterpret_cast<uintptr_t>(p->w_up)) % 16)
+        return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
+    const uint64_t wbytes = halo_mi_slab_bytes(p->type, p->rows, p->cols);
+    const uint64_t oext = extent(p->n_vec, os * 4, (uint64_t)p->rows * 4);
+    if (ranges_overlap(p->out, oext, p->w_gate, wbytes) || ranges_overlap(p->out, oext, p->w_up, wbytes))
+        return set_error(HALO_MI_E_KERNEL, "%s: out overlaps a weight operand", op);
+    if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
+        variant = p->n_vec <= kGateUpGemvMax ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+    auto st = static_cast<hipStream_t>(stream);
+    if (variant == HALO_MI_GEMV_SLAB) {
+        GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
+                       p->rows, p->cols, p->n_vec};
+        return launch_gemv_slab<true>(p->type, a, st);
+    }
+    if (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
+        return set_error(HALO_MI_E_KERNEL, "%s: the MFMA GEMM needs 16-byte aligned x rows", op);
+    GemmArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
+               p->rows, p->cols, p->n_vec};
+    a.tiles = gemm_tiles(p->variant);
+    return launch_gemm_pc<true>(p->type, a, st);
+}
+
+int halo_mi_swiglu(const float* gate, uint64_t gate_stride, const float* up, uint64_t up_stride, float* out,
+                   uint64_t out_stride, uint32_t rows, uint32_t cols, void* stream) {
+    clear_error();
+    const char* op = "SWIGLU";
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    if (!gate || !up || !out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (gate_stride == 0) gate_stride = cols;
+    if (up_stride == 0) up_stride = cols;
+    if (out_stride == 0) out_stride = cols;
+    if (rows > 1 && (gate_stride < cols || up_stride < cols || out_stride < cols))
+        return set_error(HALO_MI_E_KERNEL, "%s: row stride < cols", op);
+    if ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(out)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: operands must be 4-byte aligned", op);
+    const uint64_t oext = extent(rows, out_stride * 4, (uint64_t)cols * 4);
+    if (ranges_overlap(out, oext, gate, extent(rows, gate_stride * 4, (uint64_t)cols * 4)) ||
+        ranges_overlap(out, oext, up, extent(rows, up_stride * 4, (uint64_t)cols * 4)))
+        return set_error(HALO_MI_E_KERNEL, "%s: out overlaps an input", op);
+    return launch_swiglu(gate, gate_stride, up, up_stride, out, out_stride, rows, cols, static_cast<hipStream_t>(stream));
+}
+
+int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t w_stride, uint32_t rows, uint32_t cols,
+                         uint32_t first_row, uint32_t n_rows, float* out, uint64_t out_stride, void* stream) {
+    clear_error();
+    const char* op = "DEQUANT";
+    int code;
+    const uint64_t rb = row_bytes_checked(type, cols, &code, op);
+    if (code) return code;
+    if (first_row > rows || n_rows > rows - first_row)
+        return set_error(HALO_MI_E_KERNEL, "%s: rows [%u, %u) out of %u", op, first_row, first_row + n_rows, rows);
+    if (n_rows == 0 || cols == 0) return HALO_MI_OK;
+    if (!w || !out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (out_stride == 0) out_stride = cols;
+    if (n_rows > 1 && out_stride < cols) return set_error(HALO_MI_E_KERNEL, "%s: out stride < cols", op);
+    auto st = static_cast<hipStream_t>(stream);
+    if (layout == HALO_MI_LAYOUT_GGUF) {
+        if (w_stride == 0) w_stride = rb;
+        if (rows > 1 && w_stride < rb) return set_error(HALO_MI_E_KERNEL, "%s: w stride < row bytes", op);
+        return launch_dequant_gguf(type, static_cast<const uint8_t*>(w), w_stride, cols, first_row, n_rows, out, out_stride,
+                                   st);
+    }
+    if (layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: unknown layout %u", op, layout);
+    if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, type);
+    return launch_dequant_slab(type, static_cast<const uint8_t*>(w), cols, first_row, n_rows, out, out_stride, st);
+}
+
+int halo_mi_repack_slab(uint32_t type, const void* src, uint64_t src_stride, uint32_t rows, uint32_t cols, void* dst,
+                        void* stream) {
+    clear_error();
+    int code;
+    const uint64_t rb = row_bytes_checked(type, cols, &code, "repack_slab");
+    if (code) return code;
+    if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "repack_slab: type %u has no SLAB layout", type);
+    if (src_stride == 0) src_stride = rb;
+    if (rows > 1 && src_stride < rb) return set_error(HALO_MI_E_KERNEL, "repack_slab: row stride < row bytes");
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    if (ranges_overlap(dst, halo_mi_slab_bytes(type, rows, cols), src, extent(rows, src_stride, rb)))
+        return set_error(HALO_MI_E_KERNEL, "repack_slab: dst overlaps src");
+    return launch_repack_slab(type, static_cast<const uint8_t*>(src), src_stride, rows, cols, static_cast<uint8_t*>(dst),
+                              static_cast<hipStream_t>(stream));
+}
+
+int halo_mi_unpack_slab(uint32_t type, const void* src, uint32_t rows, uint32_t cols, void* dst, uint64_t dst_stride,
+                        void* stream) {
+    clear_error();
+    int code;
+    const uint64_t rb = row_bytes_checked(type, cols, &code, "unpack_slab");
+    if (code) return code;
+    if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "unpack_slab: type %u has no SLAB layout", type);
+    if (dst_stride == 0) dst_stride = rb;
+    if (rows > 1 && dst_stride < rb) return set_error(HALO_MI_E_KERNEL, "unpack_slab: row stride < row bytes");
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    return launch_unpack_slab(type, static_cast<const uint8_t*>(src), rows, cols, static_cast<uint8_t*>(dst), dst_stride,
+                              static_cast<hipStream_t>(stream));
+}
+
+int halo_mi_upload_slab(uint32_t type, const void* host_src, uint64_t src_stride, uint32_t rows, uint32_t cols, void* dst,
+                        uint64_t chunk_bytes, void* stream) {
+    clear_error();
+    int code;
+    const uint64_t rb = row_bytes_checked(type, cols, &code, "upload_slab");
+    if (code) return code;
+    if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "upload_slab: type %u has no SLAB layout", type);
+    if (src_stride == 0) src_stride = rb;
+    if (rows > 1 && src_stride < rb) return set_error(HALO_MI_E_KERNEL, "upload_slab: row stride < row bytes");
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    if (chunk_bytes == 0) chunk_bytes = 64ull << 20;
+    // Chunks are whole slabs so every repack writes complete slabs.
+    uint64_t chunk_rows = std::max<uint64_t>(chunk_bytes / rb / kSlabRows, 1) * kSlabRows;
+    chunk_rows = std::min<uint64_t>(chunk_rows, (uint64_t)(rows + kSlabRows - 1) / kSlabRows * kSlabRows);
+    auto st = static_cast<hipStream_t>(stream);
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, chunk_rows * rb);
+    if (e != hipSuccess) return set_error(HALO_MI_E_MEMORY, "upload_slab: cannot allocate %llu staging bytes",
+                                          (unsigned long long)(chunk_rows * rb));
+    const SlabGeom g = slab_geom(type, cols);
+    const auto* src = static_cast<const uint8_t*>(host_src);
+    int rc = HALO_MI_OK;
+    for (uint64_t r0 = 0; r0 < rows && rc == HALO_MI_OK; r0 += chunk_rows) {
+        const uint32_t n = (uint32_t)std::min<uint64_t>(chunk_rows, rows - r0);
+        if (src_stride == rb) e = hipMemcpyAsync(staging, src + r0 * rb, (uint64_t)n * rb, hipMemcpyHostToDevice, st);
+        else e = hipMemcpy2DAsync(staging, rb, src + r0 * src_stride, src_stride, rb, n, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) { rc = hip_status(e, "upload_slab copy"); break; }
+        rc = halo_mi_repack_slab(type, staging, rb, n, cols, static_cast<uint8_t*>(dst) + (r0 / kSlabRows) * g.slab_bytes, st);
+        if (rc == HALO_MI_OK) {
+            e = hipStreamSynchronize(st);  // the staging buffer is reused by the next chunk
+            if (e != hipSuccess) rc = hip_status(e, "upload_slab sync");
+        }
+    }
+    (void)hipFree(staging);
+    return rc;
+}
+
+}  // extern "C"

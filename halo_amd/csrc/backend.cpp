@@ -211,15 +211,17 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 8> kVariants{{
+constexpr std::array<VariantInfo, 10> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
     {kGemvSlab, "gemv_slab_w64", OpId::Gemv, {}},
     {kGemmSlabBf16, "gemm_slab_bf16_mfma", OpId::Gemv, {}},
     {kGemvSlabAuto, "gemv_slab_auto", OpId::Gemv, {}},
+    {kGemmSlabBf16M512, "gemm_slab_bf16_mfma_m512", OpId::Gemv, {}},
     {kSwiglu, "swiglu_b256", OpId::Swiglu, {}},
     {kGateUpGemv, "gate_up_gemv_w64", OpId::GateUpSwiglu, {}},
     {kGateUpGemm, "gate_up_gemm_bf16_mfma", OpId::GateUpSwiglu, {}},
+    {kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512", OpId::GateUpSwiglu, {}},
 }};
 
 bool has_variant(OpId op, std::uint32_t id) {
@@ -391,14 +393,15 @@ public:
         r.no_overlap(y, x);
         r.no_overlap(y, w);
         if (a.n_vec == 0 || a.rows == 0) return;
-        if (variant == kGemmSlabBf16 || (variant == kGemvSlabAuto && a.n_vec > 8))
+        if (variant == kGemmSlabBf16 || variant == kGemmSlabBf16M512 || (variant == kGemvSlabAuto && a.n_vec > 8))
             CHECK(reinterpret_cast<std::uintptr_t>(x.base) % 16 == 0 && x.stride % 16 == 0, ErrorCode::Kernel,
                   "MATMUL: the MFMA GEMM needs 16-byte aligned x rows");
         halo_mi_gemv_params p{t,      slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
                               w.base, slab ? 0 : w.stride,
                               reinterpret_cast<const float*>(x.base), x.stride / kF32,
                               reinterpret_cast<float*>(y.base), y.stride / kF32,
-                              a.rows, a.cols, a.n_vec, variant};
+                              a.rows, a.cols, a.n_vec,
+                              variant == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512 : variant};
         check_abi(halo_mi_gemv(&p, st.native()));
     }
 
@@ -434,6 +437,7 @@ public:
         if (a.n_vec == 0 || a.rows == 0) return;
         const std::uint32_t variant = a.kernel.variant_id == kGateUpGemv   ? HALO_MI_GEMV_SLAB
                                       : a.kernel.variant_id == kGateUpGemm ? HALO_MI_GEMM_SLAB_BF16
+                                      : a.kernel.variant_id == kGateUpGemmM512 ? HALO_MI_GEMM_SLAB_BF16_M512
                                       : a.allow_gemm                       ? HALO_MI_GEMV_SLAB_AUTO
                                                                            : HALO_MI_GEMV_SLAB;
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,

@@ -1,0 +1,215 @@
+// gfx950 kernels of the halo_mi355x library: GGUF <-> SLAB repack, exact dequantization
+// (bit-identical to tensor::dequantize_row, src/tensor/quant.cpp:430-435 of the reference) and
+// a fill kernel for workspace initialisation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+
+#include "device.h"
+#include "launch.h"
+
+namespace halo_mi {
+namespace {
+
+using namespace dev;
+
+// ==========================================================================================
+// Repack / unpack / dequantize
+// ==========================================================================================
+
+// One thread per (slab, block, row), row fastest: the 64 threads of a (slab, block) write each
+// of the block's slot records as one contiguous 1 KB, and each reads its row's block.
+__global__ void k_repack_slab(uint32_t type, const uint8_t* __restrict__ src, uint64_t src_stride, uint32_t rows,
+                              uint32_t cols, uint8_t* __restrict__ dst) {
+    const SlabGeom g = slab_geom(type, cols);
+    const uint32_t nblk = cols / block_elems(type), S = cols / kSlot;
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t slabs = (rows + kSlabRows - 1) / kSlabRows;
+    if (idx >= slabs * nblk * kSlabRows) return;
+    const uint32_t r = (uint32_t)(idx % kSlabRows);
+    const uint64_t sb = idx / kSlabRows;
+    const uint32_t b = (uint32_t)(sb % nblk);
+    const uint64_t slab = sb / nblk, row = slab * kSlabRows + r;
+    uint8_t* out = dst + slab * g.slab_bytes;
+    const uint8_t* s = src + row * src_stride + (uint64_t)b * block_bytes(type);
+    if (type == kQ4_K && ((reinterpret_cast<uintptr_t>(s) | src_stride) % 16) == 0) {
+        // vector path: 9 x 16 B in; 8 slot records and the header out as 16-byte stores
+        uint4 blk[9];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) blk[i] = row < rows ? reinterpret_cast<const uint4*>(s)[i] : uint4{0, 0, 0, 0};
+        *reinterpret_cast<uint4*>(out + g.aux_off + ((uint64_t)b * 64 + r) * 16) = blk[0];
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {  // 32 quant bytes: sub-blocks 2 grp (low nibbles), 2 grp + 1 (high)
+            const uint4 A = blk[1 + 2 * grp], B = blk[2 + 2 * grp];
+            const uint32_t a[4] = {A.x, A.y, A.z, A.w}, c[4] = {B.x, B.y, B.z, B.w};
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                lo[k] = (a[k] & 0x0F0F0F0Fu) | ((c[k] & 0x0F0F0F0Fu) << 4);
+                hi[k] = ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0xF0F0F0F0u);
+            }
+            *reinterpret_cast<uint4*>(out + g.q_off + (((uint64_t)b * 8 + 2 * grp) * 64 + r) * 16) = uint4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<uint4*>(out + g.q_off + (((uint64_t)b * 8 + 2 * grp + 1) * 64 + r) * 16) = uint4{hi[0], hi[1], hi[2], hi[3]};
+        }
+        return;
+    }
+    uint8_t blk[210];
+    const uint32_t bb = block_bytes(type);
+    if (row < rows) {
+        for (uint32_t i = 0; i < bb; ++i) blk[i] = s[i];
+    } else {
+        for (uint32_t i = 0; i < bb; ++i) blk[i] = 0;
+    }
+    slab_pack_block(type, blk, out, g, S, r, b);
+}
+
+__global__ void k_unpack_slab(uint32_t type, const uint8_t* __restrict__ src, uint32_t rows, uint32_t cols,
+                              uint8_t* __restrict__ dst, uint64_t dst_stride) {
+    const SlabGeom g = slab_geom(type, cols);
+    const uint32_t nblk = cols / block_elems(type), S = cols / kSlot;
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)rows * nblk) return;
+    const uint64_t row = idx / nblk;
+    const uint32_t b = (uint32_t)(idx % nblk);
+    uint8_t blk[210];
+    slab_unpack_block(type, src + (row / kSlabRows) * g.slab_bytes, blk, g, S, (uint32_t)(row % kSlabRows), b);
+    uint8_t* d = dst + row * dst_stride + (uint64_t)b * block_bytes(type);
+    for (uint32_t i = 0; i < block_bytes(type); ++i) d[i] = blk[i];
+}
+
+__global__ void k_dequant_gguf(uint32_t type, const uint8_t* __restrict__ w, uint64_t w_stride, uint32_t cols,
+                               uint32_t first_row, uint32_t n_rows, float* __restrict__ out, uint64_t out_stride) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)n_rows * cols) return;
+    const uint64_t r = idx / cols;
+    const uint32_t i = (uint32_t)(idx % cols);
+    out[r * out_stride + i] = gguf_elem(type, w + (first_row + r) * w_stride, i);
+}
+
+// Exact fp32 weights of slot s of the row at lane r of `slab` (the reference's expressions).
+template <uint32_t T>
+__device__ __forceinline__ void slab_slot_weights(const uint8_t* __restrict__ slab, const SlabGeom& g, uint32_t r,
+                                                  uint32_t s, float w[32]) {
+#pragma clang fp contract(off)
+    if constexpr (T == kQ4_0) {
+        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)s * 64 + r) * 2));
+        const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t b = (Q[i] >> (8 * k)) & 0xFFu;
+                w[4 * i + k] = (float)((int)(b & 15u) - 8) * d;
+                w[16 + 4 * i + k] = (float)((int)(b >> 4) - 8) * d;
+            }
+    } else if constexpr (T == kQ8_0) {
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.aux_off + ((uint64_t)s * 64 + r) * 2));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + (((uint64_t)s * 2 + h) * 64 + r) * 16);
+            const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) w[16 * h + 4 * i + k] = sbyte(Q[i], k) * d;
+        }
+    } else if constexpr (T == kQ4_K) {
+        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
+        const uint4 hdr = *reinterpret_cast<const uint4*>(slab + g.aux_off + ((uint64_t)(s / 8) * 64 + r) * 16);
+        float d1, m1;
+        q4k_scales(hdr, s % 8, d1, m1);
+        const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t b = (Q[i] >> (8 * k)) & 0xFFu;
+                w[4 * i + k] = d1 * (float)(b & 15u) - m1;
+                w[16 + 4 * i + k] = d1 * (float)(b >> 4) - m1;
+            }
+    } else {  // Q6_K
+        const uint4 ql = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
+        const uint2 qh = *reinterpret_cast<const uint2*>(slab + g.aux_off + ((uint64_t)s * 64 + r) * 8);
+        const uint32_t sb = s / 8, j = s % 8;
+        const uint8_t* scp = slab + g.sc_off + ((uint64_t)sb * 64 + r) * 16;
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(slab + g.d_off + ((uint64_t)sb * 64 + r) * 2));
+        const float dA = d * (float)(int8_t)scp[2 * j], dB = d * (float)(int8_t)scp[2 * j + 1];
+        uint32_t lo[4], hi[4];
+        q6_slot_bytes(ql, qh, lo, hi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                w[4 * i + k] = dA * (float)((int)((lo[i] >> (8 * k)) & 0xFFu) - 32);
+                w[16 + 4 * i + k] = dB * (float)((int)((hi[i] >> (8 * k)) & 0xFFu) - 32);
+            }
+    }
+}
+
+template <uint32_t T>
+__global__ void k_dequant_slab(const uint8_t* __restrict__ w, uint32_t cols, uint32_t first_row, uint32_t n_rows,
+                               float* __restrict__ out, uint64_t out_stride) {
+    const SlabGeom g = slab_geom(T, cols);
+    const uint32_t S = cols / kSlot;
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)n_rows * S) return;
+    const uint32_t s = (uint32_t)(idx % S);
+    const uint64_t row = first_row + idx / S;
+    float wv[32];
+    slab_slot_weights<T>(w + (row / kSlabRows) * g.slab_bytes, g, (uint32_t)(row % kSlabRows), s, wv);
+    float* o = out + (idx / S) * out_stride + (uint64_t)s * 32;
+    for (int i = 0; i < 32; ++i) o[i] = wv[i];
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+}  // namespace
+
+int launch_repack_slab(uint32_t type, const uint8_t* src, uint64_t src_stride, uint32_t rows, uint32_t cols,
+                       uint8_t* dst, hipStream_t st) {
+    const uint64_t n = (uint64_t)(rows + kSlabRows - 1) / kSlabRows * kSlabRows * (cols / block_elems(type));
+    hipLaunchKernelGGL(k_repack_slab, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, type, src, src_stride, rows,
+                       cols, dst);
+    return hip_status(hipGetLastError(), "repack_slab launch");
+}
+
+int launch_unpack_slab(uint32_t type, const uint8_t* src, uint32_t rows, uint32_t cols, uint8_t* dst,
+                       uint64_t dst_stride, hipStream_t st) {
+    const uint64_t n = (uint64_t)rows * (cols / block_elems(type));
+    hipLaunchKernelGGL(k_unpack_slab, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, type, src, rows, cols, dst,
+                       dst_stride);
+    return hip_status(hipGetLastError(), "unpack_slab launch");
+}
+
+int launch_dequant_gguf(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t cols, uint32_t first_row,
+                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st) {
+    const uint64_t n = (uint64_t)n_rows * cols;
+    hipLaunchKernelGGL(k_dequant_gguf, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, type, w, w_stride, cols,
+                       first_row, n_rows, out, out_stride);
+    return hip_status(hipGetLastError(), "dequant_gguf launch");
+}
+
+int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t first_row, uint32_t n_rows, float* out,
+                        uint64_t out_stride, hipStream_t st) {
+    const uint64_t n = (uint64_t)n_rows * (cols / kSlot);
+    const dim3 grid((uint32_t)((n + 255) / 256)), block(256);
+    switch (type) {
+        case kQ4_0: hipLaunchKernelGGL(k_dequant_slab<kQ4_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        case kQ8_0: hipLaunchKernelGGL(k_dequant_slab<kQ8_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        case kQ4_K: hipLaunchKernelGGL(k_dequant_slab<kQ4_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        default: hipLaunchKernelGGL(k_dequant_slab<kQ6_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+    }
+    return hip_status(hipGetLastError(), "dequant_slab launch");
+}
+
+int launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st) {
+    hipLaunchKernelGGL(k_fill_u32, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, p, n, v);
+    return hip_status(hipGetLastError(), "fill launch");
+}
+
+}  // namespace halo_mi

@@ -1,0 +1,827 @@
+// gfx950 GEMM kernels of the halo_mi355x library (M >= 8), bf16 MFMA with exact dequantization:
+//   k_gemm_pc  producer / consumer workgroups (M <= 256)
+//   k_gemm_lm  512-row M tiles, every wave dequantizes and multiplies (M > 256)
+// plus the fused SwiGLU epilogue and the standalone SWIGLU op.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+
+#include "device.h"
+#include "launch.h"
+
+namespace halo_mi {
+namespace {
+
+using namespace dev;
+
+// ==========================================================================================
+// SWIGLU (backends/cpu/ops_basic.cpp:165-167): out = silu(g) * u, rows x cols
+// ==========================================================================================
+
+__global__ void k_swiglu(const float* __restrict__ g, uint64_t gs, const float* __restrict__ u, uint64_t us,
+                         float* __restrict__ out, uint64_t os, uint32_t rows, uint32_t cols) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)rows * cols) return;
+    const uint64_t r = idx / cols, c = idx % cols;
+    out[r * os + c] = silu_f(g[r * gs + c]) * u[r * us + c];
+}
+
+// ==========================================================================================
+// SLAB GEMM, producer / consumer workgroups on v_mfma_f32_32x32x16_bf16
+// ==========================================================================================
+//
+// x is first rounded to bf16 (RNE) and stored in MFMA A-fragment order (k_x_to_frag). A
+// workgroup owns a BM x 128 tile of the output: BM x rows times 128 W rows, which are gate rows
+// [64 u, 64 u + 64) followed by the up rows of the same range (PAIR), or two consecutive slabs.
+// It has 8 waves:
+//   waves 0-3 (consumers) hold the tile in fp32 accumulators, load their x fragments straight
+//     from the fragment-ordered buffer (a ring of kPcADepth stages in registers), read the W
+//     fragments from LDS and run the MFMAs;
+//   waves 4-7 (producers) keep kPcDepth stages of W records in flight, dequantize W exactly
+//     (the reference's expressions, see pc_dequant), round to bf16 (RNE) and write the stage
+//     two ahead of the consumers to LDS.
+// A stage is one 32-weight slot of K; one barrier per stage. LDS carries only W (the measured
+// LDS bandwidth, about 100 B/clk per CU, could not also carry x at the MFMA rate).
+
+constexpr int kPcLd = 40;     // LDS row pitch in bf16 (32 k + 8 pad: 80 B, conflict-free reads)
+constexpr int kPcW = 128;     // W rows per tile
+constexpr int kPcDepth = 4;   // stages of producer W loads in flight (a ring of registers)
+constexpr int kPcADepth = 4;  // stages of consumer x-fragment loads in flight
+constexpr uint32_t kPcOob = 0x80000000u;  // buffer offset past every resource: the load returns 0
+constexpr int kPcBufs = 4;    // LDS stages (the producers write two stages ahead)
+constexpr int kPcUnroll = 8;  // producer loop unroll: ring slot, LDS buffer and Q4_K sub-block static
+
+struct GemmPcArgs {
+    const uint8_t* w0;     // gate (PAIR) or the matrix
+    const uint8_t* w1;     // up (PAIR) or null
+    const __bf16* xf;      // x in fragment order (k_x_to_frag), m_tiles * BM rows, rows >= n_vec zero
+    float* y;
+    uint64_t y_stride;
+    uint32_t rows, cols, n_vec;
+    uint32_t units;        // W tiles [0, units) run whole (PAIR: slabs; else pairs of slabs), all M tiles
+    uint32_t m_tiles;
+    uint32_t xcd_map;      // whole tiles grouped by XCD so an XCD reuses one slice of x
+    // W tiles [units, units + split_units) (all M tiles) run as kchunks K chunks each, one
+    // workgroup per chunk after the whole tiles; their fp32 partials go to
+    // partials[(split tile * kchunks + chunk)][BM][128] and k_gemm_pc_reduce adds them.
+    uint32_t split_units;
+    uint32_t kchunks;
+    float* partials;
+};
+
+// Producer barrier: its LDS writes are complete, then s_barrier. Global loads stay in flight.
+// The memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void pc_sync() { __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Consumer barrier: its outstanding LDS reads target a stage no producer writes before the
+// next barrier, so it does not wait for them.
+__device__ __forceinline__ void pc_barrier() { __asm__ __volatile__("s_barrier" ::: "memory"); }
+
+// Load of a T at a wave-uniform base plus a 32-bit per-lane byte offset (scalar base address,
+// vector offset).
+template <typename V>
+__device__ __forceinline__ V ldg(const uint8_t* ubase, uint32_t voff) {
+    return *reinterpret_cast<const V*>(ubase + voff);
+}
+
+// x fp32 -> bf16 (RNE) in MFMA A-fragment order. For 32-row block b of x, slot s of K and half
+// k16 of the slot, 1 KB holds, for lane l, the 8 values x[32 b + l % 32][32 s + 16 k16 + 8 (l / 32) + e]
+// (the A operand of v_mfma_f32_32x32x16_bf16). Rows in [n_vec, m_pad) are zero. One thread
+// writes one lane's 16 bytes: the writes of a wave are one contiguous 1 KB.
+__global__ void k_x_to_frag(const float* __restrict__ x, uint64_t x_stride, uint32_t n_vec, uint32_t m_pad,
+                            uint32_t cols, __bf16* __restrict__ out) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)m_pad * (cols / 8)) return;
+    const uint32_t S = cols / kSlot;
+    const uint32_t l = (uint32_t)(idx & 63u);
+    const uint64_t f = idx >> 6;  // fragment index: (b * S + s) * 2 + k16
+    const uint32_t k16 = (uint32_t)(f & 1u), sl = (uint32_t)((f >> 1) % S);
+    const uint32_t b = (uint32_t)((f >> 1) / S);
+    const uint32_t m = 32 * b + (l & 31u), k = 32 * sl + 16 * k16 + 8 * (l >> 5);
+    bf16x8 v;
+    if (m < n_vec) {
+        const float4 a = *reinterpret_cast<const float4*>(x + (uint64_t)m * x_stride + k);
+        const float4 c = *reinterpret_cast<const float4*>(x + (uint64_t)m * x_stride + k + 4);
+        v = bf16x8{(__bf16)a.x, (__bf16)a.y, (__bf16)a.z, (__bf16)a.w, (__bf16)c.x, (__bf16)c.y, (__bf16)c.z, (__bf16)c.w};
+    } else {
+        v = bf16x8{};
+    }
+    *reinterpret_cast<bf16x8*>(out + idx * 8) = v;
+}
+
+// One producer thread's share of one slot: 16 weights of one row (half h of the slot record:
+// elements 8h..8h+7 and 16+8h..16+8h+7) and what scales them.
+template <uint32_t T>
+struct PcW;
+template <>
+struct PcW<kQ4_K> {
+    uint2 q;
+    uint4 hdr;
+};
+template <>
+struct PcW<kQ4_0> {
+    uint2 q;
+    uint32_t d;
+};
+template <>
+struct PcW<kQ8_0> {
+    uint2 qa, qb;
+    uint32_t d;
+};
+template <>
+struct PcW<kQ6_K> {
+    uint2 ql;
+    uint32_t qh, sc, d;
+};
+
+// Buffer resource over [base, base + bytes) for raw buffer loads (gfx9 dword 3: 32-bit data
+// format, untyped access). Offsets past `bytes` read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ uint2 bld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    return uint2{v[0], v[1]};
+}
+__device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// Per-lane byte offsets of a producer thread's records inside one stage of a slab.
+struct PcOff {
+    uint32_t q, aux, sc, d;
+};
+
+template <uint32_t T>
+__device__ __forceinline__ PcOff pc_offsets(uint32_t r, uint32_t h) {
+    if constexpr (T == kQ4_K) return {r * 16 + 8 * h, r * 16, 0, 0};
+    else if constexpr (T == kQ4_0 || T == kQ8_0) return {r * 16 + 8 * h, r * 2, 0, 0};
+    else return {r * 16 + 8 * h, r * 8 + 4 * h, r * 16, r * 2};
+}
+
+// Stage s (slot s of K) of one producer thread's records; `slab` is the wave's slab resource.
+// Stage s of one producer thread's records; `slab` is the wave's slab resource. A stage that is
+// not live reads past the resource (no branch): zero records, i.e. zero weights.
+template <uint32_t T>
+__device__ __forceinline__ void pc_load_w(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
+                                          uint32_t s, bool live) {
+    const uint32_t sb = s / 8;
+    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
+    if constexpr (T == kQ4_K) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
+    } else if constexpr (T == kQ4_0) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+    } else if constexpr (T == kQ8_0) {
+        R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
+        R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
+        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+    } else {
+        R.ql = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 512));
+        R.sc = bld16(slab, o.sc, so(g.sc_off + sb * 1024 + 2 * (s % 8)));
+        R.d = bld16(slab, o.d, so(g.d_off + sb * 128));
+    }
+}
+
+// q4k_sc_m for a sub-block index known only at run time, without branches.
+__device__ __forceinline__ void q4k_sc_m_sel(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j, uint32_t& sc,
+                                             uint32_t& m) {
+    const uint32_t sh = 8 * (j & 3u);
+    const uint32_t b8 = (s2 >> sh) & 0xFFu;
+    const uint32_t lsc = (s0 >> sh) & 63u, lm = (s1 >> sh) & 63u;
+    const uint32_t hsc = (b8 & 15u) | (((s0 >> (sh + 6)) & 3u) << 4);
+    const uint32_t hm = (b8 >> 4) | (((s1 >> (sh + 6)) & 3u) << 4);
+    sc = j < 4 ? lsc : hsc;
+    m = j < 4 ? lm : hm;
+}
+
+// The 16 weights of a PcW, exact (each is one correctly rounded fp32 operation on exact
+// products, equal to the reference's expression), then rounded to bf16.
+//   Q4_K d1 q - m1 = fma(d1 / u, q u, -m1)      (q u from the fp8 convert, u = fp8_unit())
+//   Q4_0 (q - 8) d = fma(d / u, q u, -8 d)      (exact: d (q - 8) is representable)
+//   Q8_0 q d       = fma(d, q + 128, -128 d)    (q + 128 as an unsigned byte; exact)
+//   Q6_K (d sc)(q - 32) = fma(d sc, q, -32 d sc) (exact)
+template <uint32_t T>
+__device__ __forceinline__ void pc_dequant(const PcW<T>& R, uint32_t h, uint32_t j, float inv_unit, bf16x8& lo,
+                                           bf16x8& hi) {
+    float a[8], b[8];
+    if constexpr (T == kQ4_K || T == kQ4_0) {
+        float sA, oA;
+        if constexpr (T == kQ4_K) {
+            uint32_t sc, m;
+            q4k_sc_m_sel(R.hdr.y, R.hdr.z, R.hdr.w, j, sc, m);
+            const float d1 = h2f(R.hdr.x & 0xFFFFu) * (float)sc, m1 = h2f(R.hdr.x >> 16) * (float)m;
+            sA = d1 * inv_unit;
+            oA = -m1;
+        } else {
+            const float d = h2f(R.d);
+            sA = d * inv_unit;
+            oA = -8.0f * d;
+        }
+        const uint32_t Q[2] = {R.q.x, R.q.y};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t lc = and_opaque<0x0F0F0F0Fu>(Q[w]), hc = and_opaque<0x0F0F0F0Fu>(Q[w] >> 4);
+            const float2v l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lc, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lc, true);
+            const float2v h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hc, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hc, true);
+            a[4 * w + 0] = fmaf(sA, l01[0], oA);
+            a[4 * w + 1] = fmaf(sA, l01[1], oA);
+            a[4 * w + 2] = fmaf(sA, l23[0], oA);
+            a[4 * w + 3] = fmaf(sA, l23[1], oA);
+            b[4 * w + 0] = fmaf(sA, h01[0], oA);
+            b[4 * w + 1] = fmaf(sA, h01[1], oA);
+            b[4 * w + 2] = fmaf(sA, h23[0], oA);
+            b[4 * w + 3] = fmaf(sA, h23[1], oA);
+        }
+    } else if constexpr (T == kQ8_0) {
+        const float d = h2f(R.d), o = -128.0f * d;
+        const uint32_t A[2] = {xor_opaque<0x80808080u>(R.qa.x), xor_opaque<0x80808080u>(R.qa.y)};
+        const uint32_t B[2] = {xor_opaque<0x80808080u>(R.qb.x), xor_opaque<0x80808080u>(R.qb.y)};
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[4 * w + k] = fmaf(d, ubyte(A[w], k), o);
+                b[4 * w + k] = fmaf(d, ubyte(B[w], k), o);
+            }
+    } else {
+        const float d = h2f(R.d);
+        const float dA = d * sbyte(R.sc, 0), dB = d * sbyte(R.sc, 1);
+        const float oA = -32.0f * dA, oB = -32.0f * dB;
+        const uint32_t x0 = R.ql.x, x1 = R.ql.y, hq = R.qh;
+        const uint32_t L[2] = {and_or_opaque(x0, 0x0F0F0F0Fu, hq & 0x30303030u), and_or_opaque(x1, 0x0F0F0F0Fu, (hq << 4) & 0x30303030u)};
+        const uint32_t H[2] = {and_or_opaque(x0 >> 4, 0x0F0F0F0Fu, (hq >> 2) & 0x30303030u),
+                               and_or_opaque(x1 >> 4, 0x0F0F0F0Fu, (hq << 2) & 0x30303030u)};
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[4 * w + k] = fmaf(dA, ubyte(L[w], k), oA);
+                b[4 * w + k] = fmaf(dB, ubyte(H[w], k), oB);
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        lo[i] = (__bf16)a[i];
+        hi[i] = (__bf16)b[i];
+    }
+}
+
+// Row (M index) of accumulator element r (0..15) held by `lane` in a 32x32 MFMA result; the
+// column (N index) is lane % 32.
+__device__ __forceinline__ uint32_t mfma32_row(uint32_t r, uint32_t lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// grid = units * m_tiles * kchunks, block = 512; BM = 64 MB x rows per tile.
+//
+// A workgroup runs the stages (slots of K) [s_begin, s_end) of its tile; s_begin is a multiple
+// of 8 (one Q4_K / Q6_K super-block). Barrier B_i (i = 0..n_pad) orders them: the producers
+// write local stages 0 and 1 before B_0 and stage i + 2 between B_i and B_{i+1} (LDS buffer
+// (i + 2) % 4); the consumers compute stage i between B_i and B_{i+1}, and read the first W
+// fragments of stage i + 1 at its end (complete since B_i). A buffer is rewritten two barriers
+// after its last read.
+//
+// Consumer waves: WM along M x WN along N; a wave owns MBW 32-row x blocks and NBW 32-row W
+// blocks. With PAIR its first NBW / 2 W blocks are gate rows and the others the up rows of the
+// same range, so every lane holds matching gate and up sums.
+template <uint32_t T, bool PAIR, int MB>
+__global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
+    constexpr int BM = 64 * MB;
+    constexpr int WM = MB == 1 ? 2 : 4, WN = 4 / WM;
+    constexpr int MBW = BM / WM / 32, NBW = 4 / WN;
+    constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage (W only)
+    __shared__ __bf16 lds[kPcBufs * STAGE];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t S = a.cols / kSlot;
+    const SlabGeom g = slab_geom(T, a.cols);
+    const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+
+    // workgroup -> (W tile u, M tile mt) for a whole tile, or (split tile st, K chunk)
+    const uint32_t whole = a.units * a.m_tiles;
+    const bool split = blockIdx.x >= whole;
+    uint32_t u, mt, st = 0, chunk = 0;
+    if (!split) {
+        const uint32_t wg = blockIdx.x;
+        if (a.xcd_map) {
+            const uint32_t grp = 8 / a.m_tiles, xcd = wg % 8;
+            mt = xcd / grp;
+            u = (wg / 8) * grp + xcd % grp;
+        } else {
+            u = wg / a.m_tiles;
+            mt = wg % a.m_tiles;
+        }
+    } else {
+        st = (blockIdx.x - whole) / a.kchunks;
+        chunk = (blockIdx.x - whole) % a.kchunks;
+        u = a.units + st / a.m_tiles;
+        mt = st % a.m_tiles;
+    }
+    const uint32_t m0 = mt * BM;
+    // this chunk's stages: whole groups of 8 slots when K is split
+    uint32_t s_begin = 0, s_end = S;
+    if (split) {
+        const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
+        const uint32_t g0 = chunk * base + min(chunk, extra);
+        s_begin = 8 * g0;
+        s_end = 8 * (g0 + base + (chunk < extra ? 1u : 0u));
+    }
+    const uint32_t n = s_end - s_begin;
+    const uint32_t n_pad = (n + kPcUnroll - 1) / kPcUnroll * kPcUnroll;
+
+    if (wave < 4) {
+        // ---------------- consumers ----------------
+        const uint32_t wm = wave % WM, wn = wave / WM;
+        floatx16 acc[MBW][NBW];
+#pragma unroll
+        for (int i = 0; i < MBW; ++i)
+#pragma unroll
+            for (int j = 0; j < NBW; ++j) acc[i][j] = floatx16{};
+        const uint32_t lr = lane & 31u, koff = 8 * (lane >> 5);
+        uint32_t wrow[NBW];  // first W-tile row of each of this wave's W blocks
+#pragma unroll
+        for (int j = 0; j < NBW; ++j)
+            wrow[j] = PAIR ? (j < NBW / 2 ? 32 * (wn * NBW / 2 + j) : 64 + 32 * (wn * NBW / 2 + j - NBW / 2))
+                           : 32 * (wn * NBW + j);
+        uint32_t boff[NBW];
+#pragma unroll
+        for (int j = 0; j < NBW; ++j) boff[j] = (wrow[j] + lr) * kPcLd + koff;
+        // x fragments: this M tile's fragment-ordered rows; block (wm * MBW + i), slot s, half k
+        // is at ((blk * S + s) * 2 + k) KB, lane l at 16 l bytes
+        const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf + (uint64_t)m0 * a.cols, (uint32_t)(BM * a.cols * 2));
+        const uint32_t xlane = lane * 16;
+        uint4 AR[kPcADepth][MBW][2];
+        // stages past s_end read zeros (out of range), so padded stages add exactly 0
+        auto load_a = [&](int slot, uint32_t s) {
+#pragma unroll
+            for (int i = 0; i < MBW; ++i)
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+                    AR[slot][i][k] = bld128(xres, xlane, s < s_end ? (((wm * MBW + i) * S + s) * 2 + k) * 1024 : kPcOob);
+        };
+        bf16x8 B0[NBW], B1[NBW];
+        auto read_b = [&](uint32_t buf, int k, bf16x8 (&B)[NBW]) {
+            const __bf16* st = lds + buf * STAGE + 16 * k;
+#pragma unroll
+            for (int j = 0; j < NBW; ++j) B[j] = *reinterpret_cast<const bf16x8*>(st + boff[j]);
+        };
+        auto mma = [&](int slot, int k, const bf16x8 (&B)[NBW]) {
+#pragma unroll
+            for (int i = 0; i < MBW; ++i)
+#pragma unroll
+                for (int j = 0; j < NBW; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, AR[slot][i][k]), B[j],
+                                                                        acc[i][j], 0, 0, 0);
+        };
+#pragma unroll
+        for (int p = 0; p < kPcADepth; ++p) load_a(p, s_begin + p);
+        pc_barrier();  // B_0: stages 0 and 1 are in LDS
+        read_b(0, 0, B0);
+        // stage i: x fragments from ring slot i % 4, W from LDS buffer i % 4; unrolled so both
+        // are static, and branch-free so the loads' waits are exact (padded stages are zeros)
+        static_assert(kPcADepth == kPcBufs, "one static index for the x ring and the LDS buffers");
+        for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcBufs) {
+#pragma unroll
+            for (int q = 0; q < kPcBufs; ++q) {
+                read_b(q, 1, B1);
+                mma(q, 0, B0);
+                read_b((q + 1) % kPcBufs, 0, B0);  // stage i + 1 (zeros or junk past the end, unused)
+                mma(q, 1, B1);
+                load_a(q, s_begin + i0 + q + kPcADepth);
+                // issue order: W reads for the second half first, so neither batch of MFMAs waits
+                // for LDS; then the next stage's first W reads behind the first batch
+                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: B1
+                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 0
+                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: next B0
+                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 1
+                __builtin_amdgcn_sched_group_barrier(0x020, 2 * MBW, 0);    // VMEM read: x ring
+                pc_barrier();  // B_{i+1}
+            }
+        }
+        if (split) {
+            // fp32 partial tile [BM][128] of this chunk
+            float* P = a.partials + ((uint64_t)st * a.kchunks + chunk) * BM * kPcW;
+#pragma unroll
+            for (int i = 0; i < MBW; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t ml = (wm * MBW + i) * 32 + mfma32_row(r, lane);
+#pragma unroll
+                    for (int j = 0; j < NBW; ++j) P[ml * kPcW + wrow[j] + lr] = acc[i][j][r];
+                }
+            return;
+        }
+        // epilogue: columns of this lane, rows m per accumulator element
+#pragma unroll
+        for (int i = 0; i < MBW; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m0 + (wm * MBW + i) * 32 + mfma32_row(r, lane);
+                if (m >= a.n_vec) continue;
+                float* yrow = a.y + (uint64_t)m * a.y_stride;
+                if constexpr (PAIR) {
+#pragma unroll
+                    for (int j = 0; j < NBW / 2; ++j) {
+                        const uint32_t col = u * kSlabRows + wrow[j] + lr;
+                        if (col < a.rows) yrow[col] = silu_f(acc[i][j][r]) * acc[i][j + NBW / 2][r];
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NBW; ++j) {
+                        const uint32_t col = 2 * u * kSlabRows + wrow[j] + lr;
+                        if (col < a.rows) yrow[col] = acc[i][j][r];
+                    }
+                }
+            }
+        return;
+    }
+
+    // ---------------- producers ----------------
+    const uint32_t pt = tid - 256;
+    const uint32_t mat = __builtin_amdgcn_readfirstlane(pt >> 7);  // one matrix per wave
+    const uint32_t r = (pt >> 1) & 63u, h = pt & 1u;
+    const uint8_t* slab_ptr;
+    if constexpr (PAIR) {
+        slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)u * g.slab_bytes;
+    } else {
+        // a missing second slab reads the last one again: its outputs are never stored
+        slab_ptr = a.w0 + (uint64_t)min(2 * u + mat, slabs - 1) * g.slab_bytes;
+    }
+    const __amdgpu_buffer_rsrc_t slab = make_rsrc(slab_ptr, (uint32_t)g.slab_bytes);
+    const PcOff off = pc_offsets<T>(r, h);
+    const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
+    const uint32_t wdst = (mat * 64 + r) * kPcLd + 8 * h;
+    PcW<T> R[kPcDepth];
+    auto load = [&](int slot, uint32_t s) { pc_load_w<T>(R[slot], slab, g, off, s, s < s_end); };
+    // j: the stage's slot within its super-block (static in the unrolled loop)
+    auto store = [&](int slot, uint32_t j, int buf) {
+        bf16x8 lo, hi;
+        pc_dequant<T>(R[slot], h, j, inv_unit, lo, hi);
+        __bf16* st = lds + buf * STAGE;
+        *reinterpret_cast<bf16x8*>(st + wdst) = lo;
+        *reinterpret_cast<bf16x8*>(st + wdst + 16) = hi;
+    };
+#pragma unroll
+    for (int p = 0; p < kPcDepth; ++p) load(p, s_begin + p);
+    store(0, 0, 0);
+    load(0, s_begin + kPcDepth);
+    store(1, 1, 1);
+    load(1, s_begin + kPcDepth + 1);
+    pc_sync();  // B_0
+    // iteration i writes local stage i + 2 from ring slot (i + 2) % 4 into buffer (i + 2) % 4;
+    // unrolled by 8 so slot, buffer and sub-block are static, and branch-free so the loads'
+    // waits are exact (stages past the end are junk that no consumer reads)
+    for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcUnroll) {
+#pragma unroll
+        for (int q = 0; q < kPcUnroll; ++q) {
+            const int k = (q + 2) % kPcDepth;
+            store(k, (q + 2) % 8, (q + 2) % kPcBufs);
+            load(k, s_begin + i0 + q + 2 + kPcDepth);
+            pc_sync();  // B_{i+1}
+            // keep each stage's work between its barriers: hoisting a later stage's decode would
+            // make it wait for that stage's loads
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// Sum of the K-chunk partials of a split launch (in chunk order) and the epilogue.
+// grid = (tiles * BM * 128 / 256), block 256; one output element (pair) per thread.
+template <bool PAIR, int BM>
+__global__ void k_gemm_pc_reduce(GemmPcArgs a) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    constexpr uint32_t NC = PAIR ? 64 : kPcW;  // output columns per tile
+    const uint64_t tiles = (uint64_t)a.split_units * a.m_tiles;
+    if (idx >= tiles * BM * NC) return;
+    const uint32_t tile = (uint32_t)(idx / (BM * NC)), e = (uint32_t)(idx % (BM * NC));
+    const uint32_t ml = e / NC, nl = e % NC;
+    const uint32_t u = a.units + tile / a.m_tiles, mt = tile % a.m_tiles;
+    const uint32_t m = mt * BM + ml;
+    if (m >= a.n_vec) return;
+    const float* P = a.partials + (uint64_t)tile * a.kchunks * BM * kPcW + ml * kPcW;
+    float s0 = 0.0f, s1 = 0.0f;
+    for (uint32_t c = 0; c < a.kchunks; ++c) {
+        s0 += P[(uint64_t)c * BM * kPcW + nl];
+        if constexpr (PAIR) s1 += P[(uint64_t)c * BM * kPcW + 64 + nl];
+    }
+    float* yrow = a.y + (uint64_t)m * a.y_stride;
+    if constexpr (PAIR) {
+        const uint32_t col = u * kSlabRows + nl;
+        if (col < a.rows) yrow[col] = silu_f(s0) * s1;
+    } else {
+        const uint32_t col = 2 * u * kSlabRows + nl;
+        if (col < a.rows) yrow[col] = s0;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Large-M GEMM: k_gemm_lm<T, PAIR> (M > 256)
+//
+// A workgroup owns a 512 x 128 tile: the 512 x rows of one M tile times 128 W rows (PAIR: the
+// 64 gate rows of slab u, then the 64 up rows of the same slab; else slabs 2u and 2u + 1).
+// Four waves, each of which both dequantizes and multiplies. With no producer waves a wave can
+// hold 256 fp32 accumulators, twice k_gemm_pc's, which halves the LDS bytes and the barriers
+// per MFMA:
+//   - wave w dequantizes W-tile rows [32 w, 32 w + 32) of every stage (lane: row 32 w + lane % 32,
+//     half lane / 32 of the slot record) with pc_dequant, rounds to bf16 and writes them to LDS
+//     (two buffers of one stage each);
+//   - wave w multiplies x rows [128 w, 128 w + 128) (4 blocks of 32; fragments straight from the
+//     fragment-ordered staging buffer) by all 128 W rows (4 blocks of 32, from LDS): 16 32x32
+//     accumulators, 32 v_mfma_f32_32x32x16_bf16 per stage.
+// Per stage the LDS carries 8 KB of writes and 32 KB of reads for 128 MFMAs, one barrier.
+//
+// Iteration i (stage i of this workgroup's range; LDS buffer i % 2 holds stage i, x ring slot
+// i % 2 its x fragments): read the 8 W fragments of stage i, MFMAs of the first K half, reload
+// that half's x fragments with stage i + 2, dequantize stage i + 1 (its records were loaded four
+// iterations ago) into buffer (i + 1) % 2, load stage i + 5's records into the freed ring slot,
+// MFMAs of the second half, reload its x fragments, barrier (after this wave's LDS accesses
+// complete). Buffer (i + 1) % 2 was last read in iteration i - 1, which every wave finished
+// before the barrier that ended it. Stages past the end read zeros (out-of-range buffer loads),
+// so the loop is branch-free and padded stages add exactly 0.
+// ------------------------------------------------------------------------------------------
+constexpr int kLmBM = 512;    // x rows per tile
+constexpr int kLmWDepth = 4;  // stages of W records in flight per wave
+constexpr uint32_t kLmMinRows = 256;  // x rows above which the GEMM takes k_gemm_lm
+
+template <uint32_t T, bool PAIR>
+__global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
+    constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage
+    __shared__ __bf16 lds[2 * STAGE];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = a.cols / kSlot;
+    const SlabGeom g = slab_geom(T, a.cols);
+    const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+
+    // workgroup -> (W tile u, M tile mt) for a whole tile, or (split tile st, K chunk)
+    const uint32_t whole = a.units * a.m_tiles;
+    const bool split = blockIdx.x >= whole;
+    uint32_t u, mt, st = 0, chunk = 0;
+    if (!split) {
+        u = blockIdx.x / a.m_tiles;
+        mt = blockIdx.x % a.m_tiles;
+    } else {
+        st = (blockIdx.x - whole) / a.kchunks;
+        chunk = (blockIdx.x - whole) % a.kchunks;
+        u = a.units + st / a.m_tiles;
+        mt = st % a.m_tiles;
+    }
+    uint32_t s_begin = 0, s_end = S;
+    if (split) {
+        const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
+        const uint32_t g0 = chunk * base + min(chunk, extra);
+        s_begin = 8 * g0;
+        s_end = 8 * (g0 + base + (chunk < extra ? 1u : 0u));
+    }
+    const uint32_t n_pad = (s_end - s_begin + kPcUnroll - 1) / kPcUnroll * kPcUnroll;
+
+    // ---- dequantization role: W-tile rows [32 wave, 32 wave + 32) ----
+    const uint32_t r = lane & 31u, h = lane >> 5;
+    const uint32_t mat = wave >> 1, srow = 32 * (wave & 1u) + r;
+    const uint8_t* slab_ptr;
+    if constexpr (PAIR) {
+        slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)u * g.slab_bytes;
+    } else {
+        // a missing second slab reads the last one again: its outputs are never stored
+        slab_ptr = a.w0 + (uint64_t)min(2 * u + mat, slabs - 1) * g.slab_bytes;
+    }
+    const __amdgpu_buffer_rsrc_t wres = make_rsrc(slab_ptr, (uint32_t)g.slab_bytes);
+    const PcOff off = pc_offsets<T>(srow, h);
+    const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
+    const uint32_t wdst = (32 * wave + r) * kPcLd + 8 * h;
+    PcW<T> R[kLmWDepth];
+    auto load_w = [&](int slot, uint32_t s) { pc_load_w<T>(R[slot], wres, g, off, s, s < s_end); };
+    auto store_w = [&](int slot, uint32_t j, int buf) {
+        bf16x8 lo, hi;
+        pc_dequant<T>(R[slot], h, j, inv_unit, lo, hi);
+        __bf16* dst = lds + buf * STAGE + wdst;
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 16) = hi;
+    };
+
+    // ---- multiply role: x rows [128 wave, 128 wave + 128) x all 128 W rows ----
+    floatx16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
+    const uint32_t lr = lane & 31u;
+    const uint32_t boff = lr * kPcLd + 8 * (lane >> 5);  // + 32 j rows, + 16 for the second K half
+    const uint32_t m0 = mt * kLmBM;
+    const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf + (uint64_t)m0 * a.cols, (uint32_t)((uint64_t)kLmBM * a.cols * 2));
+    const uint32_t xlane = lane * 16;
+    uint4 A[2][2][4];  // [ring slot][K half][x block]
+    auto load_a = [&](int slot, int k, uint32_t s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            A[slot][k][i] = bld128(xres, xlane, s < s_end ? (((4 * wave + i) * S + s) * 2 + k) * 1024 : kPcOob);
+    };
+    auto mma = [&](int slot, int k, const bf16x8 (&B)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A[slot][k][i]), B[j],
+                                                                    acc[i][j], 0, 0, 0);
+    };
+
+    // prologue: W records of stages 0..3, stage 0 into LDS buffer 0, x of stages 0 and 1
+#pragma unroll
+    for (int p = 0; p < kLmWDepth; ++p) load_w(p, s_begin + p);
+    load_a(0, 0, s_begin);
+    load_a(0, 1, s_begin);
+    load_a(1, 0, s_begin + 1);
+    load_a(1, 1, s_begin + 1);
+    store_w(0, 0, 0);
+    load_w(0, s_begin + kLmWDepth);
+    pc_sync();
+    for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcUnroll) {
+#pragma unroll
+        for (int q = 0; q < kPcUnroll; ++q) {
+            const int xb = q & 1;
+            const __bf16* Lb = lds + xb * STAGE + boff;
+            bf16x8 B0[4], B1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) B0[j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) B1[j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd + 16);
+            mma(xb, 0, B0);
+            load_a(xb, 0, s_begin + i0 + q + 2);
+            const int ws = (q + 1) % kLmWDepth;
+            store_w(ws, (q + 1) % 8, (q + 1) & 1);
+            load_w(ws, s_begin + i0 + q + 1 + kLmWDepth);
+            mma(xb, 1, B1);
+            load_a(xb, 1, s_begin + i0 + q + 2);
+            pc_sync();
+            // keep each stage's work between its barriers: hoisting a later stage's decode would
+            // make it wait for that stage's loads (and with them every load in flight)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    if (split) {
+        // fp32 partial tile [512][128] of this chunk
+        float* P = a.partials + ((uint64_t)st * a.kchunks + chunk) * kLmBM * kPcW;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t ml = 128 * wave + 32 * i + mfma32_row(e, lane);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) P[ml * kPcW + 32 * j + lr] = acc[i][j][e];
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t m = m0 + 128 * wave + 32 * i + mfma32_row(e, lane);
+            if (m >= a.n_vec) continue;
+            float* yrow = a.y + (uint64_t)m * a.y_stride;
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint32_t col = u * kSlabRows + 32 * j + lr;
+                    if (col < a.rows) yrow[col] = silu_f(acc[i][j][e]) * acc[i][j + 2][e];
+                }
+                // one row of outputs at a time: interleaving the SiLUs of many rows would need
+                // more VGPRs than the accumulators leave
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t col = 2 * u * kSlabRows + 32 * j + lr;
+                    if (col < a.rows) yrow[col] = acc[i][j][e];
+                }
+            }
+        }
+}
+
+template <bool PAIR>
+void launch_gemm_lm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
+    switch (type) {
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_lm<kQ4_0, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_lm<kQ8_0, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_lm<kQ4_K, PAIR>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_lm<kQ6_K, PAIR>), grid, dim3(256), 0, st, a); break;
+    }
+}
+
+template <bool PAIR, int MB>
+void launch_gemm_pc_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
+    switch (type) {
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_pc<kQ4_0, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_pc<kQ8_0, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_pc<kQ4_K, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_pc<kQ6_K, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+    }
+}
+
+
+}  // namespace
+
+// x -> bf16 staging (in chunks of rows that fit the workspace), then the producer/consumer GEMM.
+// When the tiles do not fill whole rounds of the chip (e.g. 272 slabs on 256 CUs), the tiles
+// past the last whole round are split over K so that the last round is spread over all CUs:
+// their fp32 partials go to the workspace and k_gemm_pc_reduce adds them in a fixed order.
+template <bool PAIR>
+int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
+    Workspace* ws = nullptr;
+    if (int rc = workspace_for(st, &ws)) return rc;
+    if (!ws)
+        return set_error(HALO_MI_E_MEMORY, "gemm: this stream is being captured and has no workspace yet "
+                                           "(make one call on it before capturing)");
+    const int MB = a.n_vec <= 64 ? 1 : a.n_vec <= 128 ? 2 : 4;
+    const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+    const uint32_t units = PAIR ? slabs : (slabs + 1) / 2;
+    const uint32_t S = a.cols / kSlot;
+    static const uint32_t cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return (uint32_t)std::max(n, 1);
+    }();
+    // k_gemm_lm (512-row M tiles) when its tiles alone fill the GPU; with fewer, the smaller
+    // tiles of k_gemm_pc spread the work over more CUs
+    const bool lm = a.tiles == kGemmTilesLm ||
+                    (a.tiles == kGemmTilesAuto && a.n_vec > kLmMinRows &&
+                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus);
+    const uint32_t BM = lm ? (uint32_t)kLmBM : 64u * MB;
+    const uint64_t cap_rows = kXbElems / a.cols / BM * BM;
+    if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
+    if ((uint64_t)BM * a.cols * 2 > 0xFFFFFFFFull)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for one M tile", a.cols);
+    auto launch = [&](const GemmPcArgs& p) {
+        const dim3 grid(p.units * p.m_tiles + p.split_units * p.m_tiles * p.kchunks);
+        if (lm) {
+            launch_gemm_lm_type<PAIR>(type, p, grid, st);
+            return;
+        }
+        switch (MB) {
+            case 1: launch_gemm_pc_type<PAIR, 1>(type, p, grid, st); break;
+            case 2: launch_gemm_pc_type<PAIR, 2>(type, p, grid, st); break;
+            default: launch_gemm_pc_type<PAIR, 4>(type, p, grid, st); break;
+        }
+    };
+    auto xcd_ok = [](uint32_t n_units, uint32_t m_tiles) {
+        return (m_tiles <= 8 && 8 % m_tiles == 0 && ((uint64_t)n_units * m_tiles) % 8 == 0) ? 1u : 0u;
+    };
+    for (uint64_t m_start = 0; m_start < a.n_vec; m_start += cap_rows) {
+        const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, a.n_vec - m_start);
+        const uint32_t m_tiles = (mc + BM - 1) / BM;
+        const uint64_t n8 = (uint64_t)m_tiles * BM * (a.cols / 8);
+        hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, a.x + m_start * a.x_stride,
+                           a.x_stride, mc, m_tiles * BM, a.cols, ws->xb);
+        float* y = a.y + m_start * a.y_stride;
+        // whole rounds of tiles, then the rest split over K; a matrix whose tiles cannot fill
+        // half the chip is split over K altogether
+        const uint64_t tiles = (uint64_t)units * m_tiles;
+        uint32_t main_units = units, kc = 1;
+        if (S % 8 == 0 && ((tiles > cus && tiles % cus != 0) || 2 * tiles < cus)) {
+            main_units = tiles > cus ? (uint32_t)(tiles / cus * cus / m_tiles) : 0u;
+            const uint64_t rest = (uint64_t)(units - main_units) * m_tiles;
+            kc = (uint32_t)std::min<uint64_t>({cus / std::max<uint64_t>(rest, 1), S / 8, 16});
+            while (kc > 1 && rest * kc * BM * kPcW > kPartialFloats) --kc;
+            if (kc < 2) main_units = units;  // nothing to gain: one launch
+        }
+        // one launch: the whole tiles, then the split tiles' chunks (dispatched as CUs free up)
+        GemmPcArgs p{a.w0, a.w1, ws->xb, y, a.y_stride, a.rows, a.cols, mc, main_units, m_tiles, 0u,
+                     units - main_units, kc, ws->partials};
+        p.xcd_map = lm ? 0u : xcd_ok(main_units, m_tiles);
+        launch(p);
+        if (p.split_units > 0) {
+            const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
+            const dim3 rg((uint32_t)((outs + 255) / 256));
+            if (lm) hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, kLmBM>), rg, dim3(256), 0, st, p);
+            else switch (MB) {
+                case 1: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 64>), rg, dim3(256), 0, st, p); break;
+                case 2: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 128>), rg, dim3(256), 0, st, p); break;
+                default: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 256>), rg, dim3(256), 0, st, p); break;
+            }
+        }
+        if (int rc = hip_status(hipGetLastError(), "gemm_pc launch")) return rc;
+    }
+    return HALO_MI_OK;
+}
+
+template int launch_gemm_pc<false>(uint32_t, const GemmArgs&, hipStream_t);
+template int launch_gemm_pc<true>(uint32_t, const GemmArgs&, hipStream_t);
+
+int launch_swiglu(const float* g, uint64_t gs, const float* u, uint64_t us, float* out, uint64_t os, uint32_t rows,
+                  uint32_t cols, hipStream_t st) {
+    const uint64_t n = (uint64_t)rows * cols;
+    hipLaunchKernelGGL(k_swiglu, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, g, gs, u, us, out, os, rows, cols);
+    return hip_status(hipGetLastError(), "swiglu launch");
+}
+
+}  // namespace halo_mi

@@ -1,0 +1,99 @@
+// Internal host-side interface between the C ABI (api.hip) and the kernel files of the
+// halo_mi355x library: argument blocks, the per-stream workspace, validation helpers and the
+// launchers each kernel file exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.h"
+#include "slab_layout.h"
+
+namespace halo_mi {
+
+constexpr uint32_t kMaxGemvVec = 4;  // vectors per slab-gemv launch
+// Auto choice for the fused gate/up pair: the GEMV kernel streams each weight matrix once per
+// 4 vectors, so beyond one launch the MFMA GEMM (which streams it once) is faster.
+constexpr uint32_t kGateUpGemvMax = 4;
+
+struct GemvSlabArgs {
+    const uint8_t* w0;  // slab image (gate, or the only matrix)
+    const uint8_t* w1;  // up matrix (PAIR) or null
+    const float* x;
+    uint64_t x_stride;
+    float* y;
+    uint64_t y_stride;
+    uint32_t rows, cols, n_vec;
+    uint32_t ks;          // K chunks per slab
+    uint64_t* slots;      // [slabs][chunks][NV][64] partials as (value, ready) words, 0 between launches
+    uint32_t* counters;   // [slabs], zero between launches
+};
+
+// M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
+constexpr uint32_t kGemmTilesAuto = 0, kGemmTilesPc = 1, kGemmTilesLm = 2;
+
+struct GemmArgs {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const float* x;
+    uint64_t x_stride;
+    float* y;
+    uint64_t y_stride;
+    uint32_t rows, cols, n_vec;
+    uint32_t tiles = kGemmTilesAuto;  // M tile family: kGemmTiles*
+};
+
+// ---- split-K workspace, one per (device, stream) ------------------------------------------
+// Calls on one stream run in order, so they can share it. It is allocated on the first call
+// on a stream (hipMalloc; counters cleared by a fill kernel on that stream, never a memset);
+// a call on a stream that is being captured into a graph and has no workspace yet runs
+// without split-K.
+constexpr uint64_t kPartialFloats = 8ull << 20;  // GEMM split-tile partials: 32 MiB
+constexpr uint64_t kSlots = 4ull << 20;          // GEMV split-K words: 32 MiB
+constexpr uint64_t kCounters = 1ull << 20;        // slabs (64M rows)
+constexpr uint64_t kXbElems = 16ull << 20;        // bf16 copy of x for the GEMM: 32 MiB
+
+struct Workspace {
+    float* partials = nullptr;
+    uint64_t* slots = nullptr;
+    uint32_t* counters = nullptr;
+    __bf16* xb = nullptr;
+};
+
+// The workspace of (current device, st); *out is null when st is being captured and has none yet.
+int workspace_for(hipStream_t st, Workspace** out);
+
+// HIP status -> library status (HALO_MI_E_DEVICE with the runtime's message).
+int hip_status(hipError_t e, const char* op);
+// Whether byte ranges [a, a + na) and [b, b + nb) overlap (empty ranges never do).
+bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb);
+// Extent in bytes of `rows` rows of `row_bytes` spaced `stride` bytes apart.
+uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes);
+// Common checks for the x / y operands of a gemv-shaped call.
+int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, uint64_t y_stride, uint32_t rows,
+             uint32_t cols, uint32_t n_vec);
+
+// ---- launchers (arguments already validated; they return a status) ---------------------------
+// k_dequant.hip
+int launch_repack_slab(uint32_t type, const uint8_t* src, uint64_t src_stride, uint32_t rows, uint32_t cols,
+                       uint8_t* dst, hipStream_t st);
+int launch_unpack_slab(uint32_t type, const uint8_t* src, uint32_t rows, uint32_t cols, uint8_t* dst,
+                       uint64_t dst_stride, hipStream_t st);
+int launch_dequant_gguf(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t cols, uint32_t first_row,
+                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st);
+int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t first_row, uint32_t n_rows, float* out,
+                        uint64_t out_stride, hipStream_t st);
+int launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st);
+// k_gemv.hip
+int launch_gemv_gguf_ref(uint32_t type, const uint8_t* w, uint64_t w_stride, const float* x, uint64_t x_stride, float* y,
+                         uint64_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_vec, hipStream_t st);
+template <bool PAIR>
+int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st);
+// k_gemm.hip
+template <bool PAIR>
+int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st);
+int launch_swiglu(const float* g, uint64_t gs, const float* u, uint64_t us, float* out, uint64_t os, uint32_t rows,
+                  uint32_t cols, hipStream_t st);
+
+}  // namespace halo_mi

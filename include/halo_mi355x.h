@@ -76,15 +76,20 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *                            n_vec (4 per pass over the weights). Within the summation bound;
  *                            every row is bitwise independent of n_vec.
  *   3 HALO_MI_GEMM_SLAB_BF16 SLAB layout, bf16 MFMA GEMM (dequantized W and x rounded to
- *                            bf16, fp32 accumulate); any n_vec.
- *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8, else 3.
+ *                            bf16, fp32 accumulate) on M tiles of 64 / 128 / 256 rows by n_vec;
+ *                            any n_vec.
+ *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8; else 5 when n_vec > 256 and its
+ *                            tiles fill the GPU, else 3.
+ *   5 HALO_MI_GEMM_SLAB_BF16_M512  the bf16 MFMA GEMM on 512-row M tiles (every wave both
+ *                            dequantizes and multiplies; same numerics as 3); any n_vec.
  */
 enum {
     HALO_MI_GEMV_DEFAULT = 0,
     HALO_MI_GEMV_GGUF_REF = 1,
     HALO_MI_GEMV_SLAB = 2,
     HALO_MI_GEMM_SLAB_BF16 = 3,
-    HALO_MI_GEMV_SLAB_AUTO = 4
+    HALO_MI_GEMV_SLAB_AUTO = 4,
+    HALO_MI_GEMM_SLAB_BF16_M512 = 5
 };
 
 /*
@@ -118,8 +123,9 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
  * The reference composes it as gemv(gate), gemv(up), swiglu (src/models/qwen35.cpp:789-805;
  * backends/cpu/ops_basic.cpp:165-167); here both matmuls and the epilogue are one launch.
  * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto
- * (gemv kernel for n_vec <= 4, else the GEMM), 2 = gemv kernel (any n_vec, 4 vectors per pass
- * over the weights), 3 = bf16 MFMA GEMM. out may not overlap x, Wg or Wu.
+ * (gemv kernel for n_vec <= 4, else the GEMM, its M tiles chosen as for halo_mi_gemv), 2 = gemv
+ * kernel (any n_vec, 4 vectors per pass over the weights), 3 / 5 = bf16 MFMA GEMM on 64..256 /
+ * 512-row M tiles. out may not overlap x, Wg or Wu.
  */
 typedef struct halo_mi_gate_up_params {
     uint32_t type;

@@ -225,5 +225,7 @@ inline constexpr std::uint32_t kDequantRows = 5;
 inline constexpr std::uint32_t kSwiglu = 6;
 inline constexpr std::uint32_t kGateUpGemv = 7;
 inline constexpr std::uint32_t kGateUpGemm = 8;
+inline constexpr std::uint32_t kGemmSlabBf16M512 = 9;  // == HALO_MI_GEMM_SLAB_BF16_M512 (MATMUL)
+inline constexpr std::uint32_t kGateUpGemmM512 = 10;   // GATE_UP_SWIGLU on the 512-row-tile GEMM
 
 }  // namespace halo_mi::backend

@@ -170,7 +170,7 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
     // fused gate/up (GEMV pair and bf16 GEMM variants) against the oracle's composition
     const std::vector<double> tu = slab_bound(type, wu, rows, cols, x, n_vec);
     const std::vector<double> gg = gemm_bound(type, wg, rows, cols, x, n_vec), gu = gemm_bound(type, wu, rows, cols, x, n_vec);
-    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm}) {
+    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512}) {
         hb::GateUpArgs g;
         g.wtype = static_cast<hb::DType>(type);
         g.w_gate = hb::TensorRef::of(*w_slab);
@@ -185,7 +185,7 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
         download_y(*yb, y);
         bool ok2 = true;
         for (size_t i = 0; i < y.size(); ++i) {
-            const bool gemm = variant == hb::kGateUpGemm;
+            const bool gemm = variant != hb::kGateUpGemv;
             const double dg = gemm ? gg[i] : tol[i], du = gemm ? gu[i] : tu[i];
             const double o = silu((double)ref[i]) * uref[i];
             const double bound = 1.1 * dg * (std::fabs((double)uref[i]) + du) + (std::fabs(silu(ref[i])) + 1.1 * dg) * du +
@@ -223,7 +223,26 @@ int main(int argc, char** argv) {
         check(be->kind() == hb::Kind::Hip, "kind() is Hip");
         check(!be->describe().empty(), "describe()");
         check(!be->lost(), "not lost");
-        check(!be->variants(hb::OpId::Gemv).empty(), "gemv variants registered");
+        // the registry's id -> name map is pinned: ids are append-only and never reused
+        // (as the reference pins its own, tests/unit/backend/test_hip_backend.cpp:925-981)
+        const std::pair<hb::OpId, std::vector<std::pair<uint32_t, std::string>>> pinned[] = {
+            {hb::OpId::GetRows, {{hb::kDequantRows, "dequant_rows_exact"}}},
+            {hb::OpId::Gemv,
+             {{hb::kGemvGgufRef, "gemv_gguf_ref_b256"}, {hb::kGemvSlab, "gemv_slab_w64"},
+              {hb::kGemmSlabBf16, "gemm_slab_bf16_mfma"}, {hb::kGemvSlabAuto, "gemv_slab_auto"},
+              {hb::kGemmSlabBf16M512, "gemm_slab_bf16_mfma_m512"}}},
+            {hb::OpId::Swiglu, {{hb::kSwiglu, "swiglu_b256"}}},
+            {hb::OpId::GateUpSwiglu,
+             {{hb::kGateUpGemv, "gate_up_gemv_w64"}, {hb::kGateUpGemm, "gate_up_gemm_bf16_mfma"},
+              {hb::kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512"}}},
+        };
+        for (const auto& [op, want] : pinned) {
+            const auto got = be->variants(op);
+            bool same = got.size() == want.size();
+            for (size_t i = 0; same && i < want.size(); ++i)
+                same = got[i].id == want[i].first && std::string(got[i].name) == want[i].second && got[i].op == op;
+            check(same, "variant registry of op " + std::to_string((int)op) + " is the pinned id -> name map");
+        }
         auto st = be->create_stream();
         std::vector<std::byte> host(64);
         check(code_of([&] { (void)be->import_host(std::span<std::byte>(host)); }) == (int)hb::ErrorCode::Unsupported,

@@ -212,10 +212,12 @@ def test_gemv_split_k_state_is_clean_between_calls(hl, oracle, dev, t):
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("case", [(37, 5120, 17, 0, 0, 5, 3), (16, 256, 2, 0, 0, 0, 0), (33, 768, 40, 0, 0, 0, 0),
-                                  (130, 1024, 130, 0, 0, 4, 1)])
-def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case):
+                                  (130, 1024, 130, 0, 0, 4, 1),
+                                  (130, 1024, 300, 0, 0, 4, 1), (200, 768, 600, 0, 0, 0, 0)])
+@pytest.mark.parametrize("variant", [3, 5])  # M tiles of 64..256 rows (k_gemm_pc) / 512 rows (k_gemm_lm)
+def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case, variant):
     rows, cols, n_vec, pad, off, xp, yp = case
-    say("gemm_bf16", NAMES[t], rows, cols, n_vec)
+    say("gemm_bf16", NAMES[t], rows, cols, n_vec, variant)
     buf, stride = make_weights(t, rows, cols, seed=300 + t + rows, stride_pad=pad, offset=off)
     dense = dense_of(buf, t, rows, cols, stride, off)
     x = np.random.default_rng(3000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
@@ -223,7 +225,7 @@ def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case):
     slab = slab_of(hl, dev, t, dense, rows, cols)
     if xp % 4:
         xp += 4 - xp % 4  # the MFMA path wants 16-byte aligned x rows
-    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMM_BF16, xp, yp)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, variant, xp, yp)
     err = np.abs(y.astype(np.float64) - ref)
     tol = gemm_tol(oracle, t, dense, rows, cols, x)
     print(f"    gemm vs cpu: worst |d|/bound = {max_ratio(err, tol):.4f}")
@@ -238,7 +240,8 @@ def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case):
 
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K, Q4_0, Q8_0))
-@pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3)])
+@pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3), (300, 3), (17, 5), (300, 5),
+                                           (600, 5)])
 def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
     import torch
 
@@ -255,7 +258,7 @@ def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
     out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
     hl.gate_up_swiglu(t, sgd, sud, to_dev(x, dev), out, rows, cols, n_vec, variant=variant)
     y = host(out)
-    if variant == 2:
+    if variant == hl.Variant.SLAB_GEMV:
         tg, tu = slab_gemv_tol(oracle, t, dg, rows, cols, x), slab_gemv_tol(oracle, t, du, rows, cols, x)
     else:
         tg, tu = gemm_tol(oracle, t, dg, rows, cols, x), gemm_tol(oracle, t, du, rows, cols, x)
