@@ -16,6 +16,16 @@ namespace {
 
 using namespace dev;
 
+// SiLU for the GEMM epilogues: v * rcp(1 + 2^(-v log2 e)) on v_exp_f32 and v_rcp_f32 (five
+// instructions instead of the IEEE divide and expf). Relative error at most (1.5 |v| + 8) 2^-24:
+// the rounded argument moves 2^(.) by at most 1.5 |v| 2^-24 relative, v_exp_f32 and v_rcp_f32
+// are within 1 ulp, the add and multiplies round once each, and 1 / (1 + e) damps the error of
+// e by e / (1 + e) <= 1. The bf16 GEMM's own error bound is larger by orders of magnitude; the
+// GEMV pair (fp32 throughout) keeps the IEEE form.
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.44269504088896341f));
+}
+
 // ==========================================================================================
 // SWIGLU (backends/cpu/ops_basic.cpp:165-167): out = silu(g) * u, rows x cols
 // ==========================================================================================
@@ -432,7 +442,7 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
 #pragma unroll
                     for (int j = 0; j < NBW / 2; ++j) {
                         const uint32_t col = u * kSlabRows + wrow[j] + lr;
-                        if (col < a.rows) yrow[col] = silu_f(acc[i][j][r]) * acc[i][j + NBW / 2][r];
+                        if (col < a.rows) yrow[col] = silu_fast(acc[i][j][r]) * acc[i][j + NBW / 2][r];
                     }
                 } else {
 #pragma unroll
@@ -516,7 +526,7 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
     float* yrow = a.y + (uint64_t)m * a.y_stride;
     if constexpr (PAIR) {
         const uint32_t col = u * kSlabRows + nl;
-        if (col < a.rows) yrow[col] = silu_f(s0) * s1;
+        if (col < a.rows) yrow[col] = silu_fast(s0) * s1;
     } else {
         const uint32_t col = 2 * u * kSlabRows + nl;
         if (col < a.rows) yrow[col] = s0;
@@ -533,19 +543,26 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
 // per MFMA:
 //   - wave w dequantizes W-tile rows [32 w, 32 w + 32) of every stage (lane: row 32 w + lane % 32,
 //     half lane / 32 of the slot record) with pc_dequant, rounds to bf16 and writes them to LDS
-//     (two buffers of one stage each);
+//     (three buffers of one stage each);
 //   - wave w multiplies x rows [128 w, 128 w + 128) (4 blocks of 32; fragments straight from the
 //     fragment-ordered staging buffer) by all 128 W rows (4 blocks of 32, from LDS): 16 32x32
 //     accumulators, 32 v_mfma_f32_32x32x16_bf16 per stage.
 // Per stage the LDS carries 8 KB of writes and 32 KB of reads for 128 MFMAs, one barrier.
 //
-// Iteration i (stage i of this workgroup's range; LDS buffer i % 2 holds stage i, x ring slot
-// i % 2 its x fragments): read the 8 W fragments of stage i, MFMAs of the first K half, reload
-// that half's x fragments with stage i + 2, dequantize stage i + 1 (its records were loaded four
-// iterations ago) into buffer (i + 1) % 2, load stage i + 5's records into the freed ring slot,
-// MFMAs of the second half, reload its x fragments, barrier (after this wave's LDS accesses
-// complete). Buffer (i + 1) % 2 was last read in iteration i - 1, which every wave finished
-// before the barrier that ended it. Stages past the end read zeros (out-of-range buffer loads),
+// Iteration i (stage i of this workgroup's range; LDS buffer i % 3 holds stage i, x ring slot
+// i % 2 its x fragments; stage i's W fragments are already in registers):
+//   region A: the first K half's MFMAs, with stage i + 1's W fragments read from LDS (written
+//     in iteration i - 1, complete since the barrier that ended it), stage i + 2 dequantized
+//     (its records were loaded four iterations ago) and that half's x fragments reloaded with
+//     stage i + 2 in between;
+//   region B: the second K half's MFMAs, with stage i + 2 written to buffer (i + 2) % 3, stage
+//     i + 6's records loaded into the freed ring slot and the second half's x fragments
+//     reloaded in between; then the barrier (after this wave's LDS accesses complete).
+// Buffer (i + 2) % 3 was last read in iteration i - 2, which every wave finished before the
+// barrier that ended it. The next stage's first MFMAs need nothing from LDS, so the barrier's
+// latency and the LDS round trip overlap the MFMA pipe. Both regions interleave the other
+// instructions between the MFMAs (sched_group_barrier), so the dequantization's VALU work
+// co-issues with the matrix core. Stages past the end read zeros (out-of-range buffer loads),
 // so the loop is branch-free and padded stages add exactly 0.
 // ------------------------------------------------------------------------------------------
 constexpr int kLmBM = 512;    // x rows per tile
@@ -555,7 +572,7 @@ constexpr uint32_t kLmMinRows = 256;  // x rows above which the GEMM takes k_gem
 template <uint32_t T, bool PAIR>
 __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
     constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage
-    __shared__ __bf16 lds[2 * STAGE];
+    __shared__ __bf16 lds[3 * STAGE];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = a.cols / kSlot;
@@ -633,8 +650,16 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A[slot][k][i]), B[j],
                                                                     acc[i][j], 0, 0, 0);
     };
+    auto read_b = [&](uint32_t buf, bf16x8 (&B)[2][4]) {
+        const __bf16* Lb = lds + buf * STAGE + boff;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) B[0][j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) B[1][j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd + 16);
+    };
 
-    // prologue: W records of stages 0..3, stage 0 into LDS buffer 0, x of stages 0 and 1
+    // prologue: W records of stages 0..3; stages 0 and 1 dequantized into LDS buffers 0 and 1;
+    // x of stages 0 and 1; stage 0's W fragments
 #pragma unroll
     for (int p = 0; p < kLmWDepth; ++p) load_w(p, s_begin + p);
     load_a(0, 0, s_begin);
@@ -642,29 +667,59 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
     load_a(1, 0, s_begin + 1);
     load_a(1, 1, s_begin + 1);
     store_w(0, 0, 0);
+    store_w(1, 1, 1);
     load_w(0, s_begin + kLmWDepth);
+    load_w(1, s_begin + kLmWDepth + 1);
     pc_sync();
+    bf16x8 Bc[2][4];  // W fragments of the current stage: [K half][W block]
+    read_b(0, Bc);
+    uint32_t bufc = 0;  // LDS buffer of the current stage (stage i in buffer i % 3)
     for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcUnroll) {
 #pragma unroll
         for (int q = 0; q < kPcUnroll; ++q) {
-            const int xb = q & 1;
-            const __bf16* Lb = lds + xb * STAGE + boff;
-            bf16x8 B0[4], B1[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) B0[j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) B1[j] = *reinterpret_cast<const bf16x8*>(Lb + 32 * j * kPcLd + 16);
-            mma(xb, 0, B0);
+            const int xb = q & 1, ws = (q + 2) % kLmWDepth;
+            const uint32_t bufn = bufc == 2 ? 0u : bufc + 1, bufw = bufn == 2 ? 0u : bufn + 1;
+            bf16x8 Bn[2][4];
+            // Region A: the first K half's 16 MFMAs (distinct accumulators, any order) with the
+            // next stage's W fragments read in between and stage i + 2 dequantized in between.
+            mma(xb, 0, Bc[0]);
+            read_b(bufn, Bn);
+            bf16x8 lo, hi;
+            pc_dequant<T>(R[ws], h, (q + 2) % 8, inv_unit, lo, hi);
             load_a(xb, 0, s_begin + i0 + q + 2);
-            const int ws = (q + 1) % kLmWDepth;
-            store_w(ws, (q + 1) % 8, (q + 1) & 1);
-            load_w(ws, s_begin + i0 + q + 1 + kLmWDepth);
-            mma(xb, 1, B1);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                if (k < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // a DS read
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);                 // up to 5 VALU
+                if (k >= 12) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // a VMEM read
+            }
+            // Both K halves update every accumulator: a region boundary keeps each pair 16 MFMAs
+            // apart (the scheduler would otherwise issue a dependent pair back to back).
+            __builtin_amdgcn_sched_barrier(0);
+            // Region B: the second K half's MFMAs with the LDS writes of stage i + 2 and the loads
+            // of stage i + 6's W records and stage i + 2's x fragments in between.
+            mma(xb, 1, Bc[1]);
+            __bf16* dst = lds + bufw * STAGE + wdst;
+            *reinterpret_cast<bf16x8*>(dst) = lo;
+            *reinterpret_cast<bf16x8*>(dst + 16) = hi;
+            load_w(ws, s_begin + i0 + q + 2 + kLmWDepth);
             load_a(xb, 1, s_begin + i0 + q + 2);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                if (k < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);      // a DS write
+                if (k >= 2 && k < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a VMEM read
+            }
             pc_sync();
             // keep each stage's work between its barriers: hoisting a later stage's decode would
             // make it wait for that stage's loads (and with them every load in flight)
             __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Bc[k][j] = Bn[k][j];
+            bufc = bufn;
         }
     }
 
@@ -692,7 +747,7 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const uint32_t col = u * kSlabRows + 32 * j + lr;
-                    if (col < a.rows) yrow[col] = silu_f(acc[i][j][e]) * acc[i][j + 2][e];
+                    if (col < a.rows) yrow[col] = silu_fast(acc[i][j][e]) * acc[i][j + 2][e];
                 }
                 // one row of outputs at a time: interleaving the SiLUs of many rows would need
                 // more VGPRs than the accumulators leave

@@ -188,8 +188,13 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
             const bool gemm = variant != hb::kGateUpGemv;
             const double dg = gemm ? gg[i] : tol[i], du = gemm ? gu[i] : tu[i];
             const double o = silu((double)ref[i]) * uref[i];
-            const double bound = 1.1 * dg * (std::fabs((double)uref[i]) + du) + (std::fabs(silu(ref[i])) + 1.1 * dg) * du +
-                                 16 * std::ldexp(1.0, -24) * std::fabs(o) + 1e-30;
+            const double u24 = std::ldexp(1.0, -24);
+            double bound = 1.1 * dg * (std::fabs((double)uref[i]) + du) + (std::fabs(silu(ref[i])) + 1.1 * dg) * du +
+                           16 * u24 * std::fabs(o) + 1e-30;
+            // the GEMM epilogue's SiLU (v_exp_f32 / v_rcp_f32): relative error <= (1.5 |g| + 8) 2^-24
+            if (gemm)
+                bound += (1.5 * (std::fabs((double)ref[i]) + dg) + 8) * u24 * (std::fabs(silu(ref[i])) + 1.1 * dg) *
+                         (std::fabs((double)uref[i]) + du);
             ok2 &= std::fabs((double)y[i] - o) <= bound;
         }
         check(ok2, tn + ": gate_up_swiglu variant " + std::to_string(variant) + " within the bound");

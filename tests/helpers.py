@@ -139,12 +139,17 @@ def silu64(v):
     return v / (1.0 + np.exp(-v))
 
 
-def swiglu_tol(g, u, dg, du, out):
+def swiglu_tol(g, u, dg, du, out, fast=False):
     """|silu(g) u - silu(g') u'| for |g - g'| <= dg, |u - u'| <= du, plus the epilogue's own
-    rounding (exp, divide, multiply; a few ulp). silu' is bounded by 1.1 everywhere."""
+    rounding (exp, divide, multiply; a few ulp). silu' is bounded by 1.1 everywhere.
+    fast: the GEMM epilogues' SiLU on v_exp_f32 / v_rcp_f32, relative error at most
+    (1.5 |g'| + 8) 2^-24 on silu(g'), taken at the worst g' within dg."""
     g = np.asarray(g, np.float64)
     u = np.asarray(u, np.float64)
-    return 1.1 * dg * (np.abs(u) + du) + (np.abs(silu64(g)) + 1.1 * dg) * du + 16 * U * np.abs(out) + 1e-30
+    tol = 1.1 * dg * (np.abs(u) + du) + (np.abs(silu64(g)) + 1.1 * dg) * du + 16 * U * np.abs(out) + 1e-30
+    if fast:
+        tol = tol + (1.5 * (np.abs(g) + dg) + 8) * U * (np.abs(silu64(g)) + 1.1 * dg) * (np.abs(u) + du)
+    return tol
 
 
 def max_ratio(err, tol) -> float:

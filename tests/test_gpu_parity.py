@@ -258,11 +258,12 @@ def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
     out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
     hl.gate_up_swiglu(t, sgd, sud, to_dev(x, dev), out, rows, cols, n_vec, variant=variant)
     y = host(out)
-    if variant == hl.Variant.SLAB_GEMV:
+    gemv = variant == hl.Variant.SLAB_GEMV
+    if gemv:
         tg, tu = slab_gemv_tol(oracle, t, dg, rows, cols, x), slab_gemv_tol(oracle, t, du, rows, cols, x)
     else:
         tg, tu = gemm_tol(oracle, t, dg, rows, cols, x), gemm_tol(oracle, t, du, rows, cols, x)
-    tol = swiglu_tol(g, u, tg, tu, ref)
+    tol = swiglu_tol(g, u, tg, tu, ref, fast=not gemv)
     err = np.abs(y.astype(np.float64) - ref)
     print(f"    gate_up worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
@@ -351,6 +352,9 @@ def test_baseline_q6_k_head(hl, oracle, dev):
     assert int(np.argmax(y[0])) == int(np.argmax(ref[0])) or abs(float(y[0].max() - ref[0].max())) <= tol.max()
 
 
+GATE_UP_GEMV_MAX = 4  # kGateUpGemvMax: the gate/up auto choice runs the GEMV pair up to 4 vectors
+
+
 @pytest.mark.parametrize("n_vec", [2, 8, 64, 512])
 def test_baseline_gate_up(hl, oracle, dev, n_vec):
     """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices; the oracle checks the
@@ -378,13 +382,14 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
         g = oracle.matmul(t, wg_c, n, cols, x)
         u = oracle.matmul(t, wu_c, n, cols, x)
         y = yall[:, c0:c1]
-        if n_vec <= 8:
+        gemv = n_vec <= GATE_UP_GEMV_MAX  # the auto choice: the GEMV pair up to 4 vectors, then the GEMM
+        if gemv:
             tg = slab_gemv_tol(oracle, t, wg_c, n, cols, x)
             tu = slab_gemv_tol(oracle, t, wu_c, n, cols, x)
         else:
             tg = gemm_tol(oracle, t, wg_c, n, cols, x)
             tu = gemm_tol(oracle, t, wu_c, n, cols, x)
-        tol = swiglu_tol(g, u, tg, tu, ref)
+        tol = swiglu_tol(g, u, tg, tu, ref, fast=not gemv)
         err = np.abs(y.astype(np.float64) - ref)
         print(f"    gate_up M={n_vec} columns [{c0}, {c1}): worst |d|/bound = {max_ratio(err, tol):.4f}, "
               f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
