@@ -73,12 +73,13 @@ struct GemmPcArgs {
     uint32_t units;        // W tiles [0, units) run whole (PAIR: slabs; else pairs of slabs), all M tiles
     uint32_t m_tiles;
     uint32_t xcd_map;      // whole tiles grouped by XCD so an XCD reuses one slice of x
-    // W tiles [units, units + split_units) (all M tiles) run as kchunks K chunks each, one
-    // workgroup per chunk after the whole tiles; their fp32 partials go to
+    // W tiles [split_unit0, split_unit0 + split_units) (all M tiles) run as kchunks K chunks each,
+    // one workgroup per chunk after the whole tiles; their fp32 partials go to
     // partials[(split tile * kchunks + chunk)][BM][128] and k_gemm_pc_reduce adds them.
     uint32_t split_units;
     uint32_t kchunks;
     float* partials;
+    uint32_t split_unit0 = 0;  // W tile of the first split tile (units when both kinds share a launch)
 };
 
 // Producer barrier: its LDS writes are complete, then s_barrier. Global loads stay in flight.
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     } else {
         st = (blockIdx.x - whole) / a.kchunks;
         chunk = (blockIdx.x - whole) % a.kchunks;
-        u = a.units + st / a.m_tiles;
+        u = a.split_unit0 + st / a.m_tiles;
         mt = st % a.m_tiles;
     }
     const uint32_t m0 = mt * BM;
@@ -514,7 +515,7 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
     if (idx >= tiles * BM * NC) return;
     const uint32_t tile = (uint32_t)(idx / (BM * NC)), e = (uint32_t)(idx % (BM * NC));
     const uint32_t ml = e / NC, nl = e % NC;
-    const uint32_t u = a.units + tile / a.m_tiles, mt = tile % a.m_tiles;
+    const uint32_t u = a.split_unit0 + tile / a.m_tiles, mt = tile % a.m_tiles;
     const uint32_t m = mt * BM + ml;
     if (m >= a.n_vec) return;
     const float* P = a.partials + (uint64_t)tile * a.kchunks * BM * kPcW + ml * kPcW;
@@ -565,12 +566,16 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
 // co-issues with the matrix core. Stages past the end read zeros (out-of-range buffer loads),
 // so the loop is branch-free and padded stages add exactly 0.
 // ------------------------------------------------------------------------------------------
-constexpr int kLmBM = 512;    // x rows per tile
+constexpr int kLmBM = 512;    // x rows per tile (MBW = 4)
 constexpr int kLmWDepth = 4;  // stages of W records in flight per wave
 constexpr uint32_t kLmMinRows = 256;  // x rows above which the GEMM takes k_gemm_lm
 
-template <uint32_t T, bool PAIR>
+// MBW: 32-row x blocks per wave, so the tile has 128 MBW x rows. 4 for the main tiles; 1 for
+// the K-split tiles that spread a launch's last partial round over the GPU (a quarter of the
+// rows per tile, so four times the tiles, and a quarter of the partial sums per chunk).
+template <uint32_t T, bool PAIR, int MBW>
 __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
+    constexpr uint32_t BM = 128 * MBW;
     constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage
     __shared__ __bf16 lds[3 * STAGE];
     const uint32_t lane = threadIdx.x & 63u;
@@ -589,7 +594,7 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
     } else {
         st = (blockIdx.x - whole) / a.kchunks;
         chunk = (blockIdx.x - whole) % a.kchunks;
-        u = a.units + st / a.m_tiles;
+        u = a.split_unit0 + st / a.m_tiles;
         mt = st % a.m_tiles;
     }
     uint32_t s_begin = 0, s_end = S;
@@ -625,26 +630,26 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
         *reinterpret_cast<bf16x8*>(dst + 16) = hi;
     };
 
-    // ---- multiply role: x rows [128 wave, 128 wave + 128) x all 128 W rows ----
-    floatx16 acc[4][4];
+    // ---- multiply role: x rows [32 MBW wave, 32 MBW (wave + 1)) x all 128 W rows ----
+    floatx16 acc[MBW][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MBW; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx16{};
     const uint32_t lr = lane & 31u;
     const uint32_t boff = lr * kPcLd + 8 * (lane >> 5);  // + 32 j rows, + 16 for the second K half
-    const uint32_t m0 = mt * kLmBM;
-    const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf + (uint64_t)m0 * a.cols, (uint32_t)((uint64_t)kLmBM * a.cols * 2));
+    const uint32_t m0 = mt * BM;
+    const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf + (uint64_t)m0 * a.cols, (uint32_t)((uint64_t)BM * a.cols * 2));
     const uint32_t xlane = lane * 16;
-    uint4 A[2][2][4];  // [ring slot][K half][x block]
+    uint4 A[2][2][MBW];  // [ring slot][K half][x block]
     auto load_a = [&](int slot, int k, uint32_t s) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            A[slot][k][i] = bld128(xres, xlane, s < s_end ? (((4 * wave + i) * S + s) * 2 + k) * 1024 : kPcOob);
+        for (int i = 0; i < MBW; ++i)
+            A[slot][k][i] = bld128(xres, xlane, s < s_end ? (((MBW * wave + i) * S + s) * 2 + k) * 1024 : kPcOob);
     };
     auto mma = [&](int slot, int k, const bf16x8 (&B)[4]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MBW; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A[slot][k][i]), B[j],
@@ -687,12 +692,14 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
             bf16x8 lo, hi;
             pc_dequant<T>(R[ws], h, (q + 2) % 8, inv_unit, lo, hi);
             load_a(xb, 0, s_begin + i0 + q + 2);
+            if constexpr (MBW == 4) {  // with fewer MFMAs the VALU work dominates: no pattern
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
-                if (k < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // a DS read
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);                 // up to 5 VALU
-                if (k >= 12) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // a VMEM read
+                for (int k = 0; k < 16; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                    if (k < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // a DS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);                 // up to 5 VALU
+                    if (k >= 12) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // a VMEM read
+                }
             }
             // Both K halves update every accumulator: a region boundary keeps each pair 16 MFMAs
             // apart (the scheduler would otherwise issue a dependent pair back to back).
@@ -705,11 +712,13 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
             *reinterpret_cast<bf16x8*>(dst + 16) = hi;
             load_w(ws, s_begin + i0 + q + 2 + kLmWDepth);
             load_a(xb, 1, s_begin + i0 + q + 2);
+            if constexpr (MBW == 4) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
-                if (k < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);      // a DS write
-                if (k >= 2 && k < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a VMEM read
+                for (int k = 0; k < 16; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                    if (k < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);      // a DS write
+                    if (k >= 2 && k < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // a VMEM read
+                }
             }
             pc_sync();
             // keep each stage's work between its barriers: hoisting a later stage's decode would
@@ -724,23 +733,23 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
     }
 
     if (split) {
-        // fp32 partial tile [512][128] of this chunk
-        float* P = a.partials + ((uint64_t)st * a.kchunks + chunk) * kLmBM * kPcW;
+        // fp32 partial tile [BM][128] of this chunk
+        float* P = a.partials + ((uint64_t)st * a.kchunks + chunk) * BM * kPcW;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MBW; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t ml = 128 * wave + 32 * i + mfma32_row(e, lane);
+                const uint32_t ml = 32 * (MBW * wave + i) + mfma32_row(e, lane);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) P[ml * kPcW + 32 * j + lr] = acc[i][j][e];
             }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MBW; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const uint32_t m = m0 + 128 * wave + 32 * i + mfma32_row(e, lane);
+            const uint32_t m = m0 + 32 * (MBW * wave + i) + mfma32_row(e, lane);
             if (m >= a.n_vec) continue;
             float* yrow = a.y + (uint64_t)m * a.y_stride;
             if constexpr (PAIR) {
@@ -762,13 +771,13 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
         }
 }
 
-template <bool PAIR>
+template <bool PAIR, int MBW>
 void launch_gemm_lm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
     switch (type) {
-        case kQ4_0: hipLaunchKernelGGL((k_gemm_lm<kQ4_0, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kQ8_0: hipLaunchKernelGGL((k_gemm_lm<kQ8_0, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kQ4_K: hipLaunchKernelGGL((k_gemm_lm<kQ4_K, PAIR>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm_lm<kQ6_K, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_lm<kQ4_0, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_lm<kQ8_0, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_lm<kQ4_K, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_lm<kQ6_K, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
     }
 }
 
@@ -782,13 +791,95 @@ void launch_gemm_pc_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStrea
     }
 }
 
+// k_gemm_pc_reduce over the split tiles of p (BM-row tiles)
+template <bool PAIR, int BM>
+void launch_reduce(const GemmPcArgs& p, hipStream_t st) {
+    const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
+    hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, BM>), dim3((uint32_t)((outs + 255) / 256)), dim3(256), 0, st, p);
+}
+
+// Rows [m_start, m_start + mc) of x to bf16 fragments, zero-padded to m_pad rows.
+void stage_x(const GemmArgs& a, uint64_t m_start, uint32_t mc, uint32_t m_pad, __bf16* xb, hipStream_t st) {
+    const uint64_t n8 = (uint64_t)m_pad * (a.cols / 8);
+    hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, a.x + m_start * a.x_stride,
+                       a.x_stride, mc, m_pad, a.cols, xb);
+}
+
+uint32_t cu_count() {
+    static const uint32_t cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        return (uint32_t)std::max(n, 1);
+    }();
+    return cus;
+}
+
+// The k_gemm_lm path. Whole rounds of 512-row tiles; the W tiles past the last whole round run
+// as 128-row tiles split over K (four times the tiles of a 512-row tile and a quarter of the
+// partial sums per chunk), so the partial round is spread over the GPU; k_gemm_pc_reduce adds
+// their partials in chunk order. With fewer 512-row tiles than CUs, those are split over K.
+template <bool PAIR>
+int launch_gemm_lm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t units, hipStream_t st) {
+    const uint32_t S = a.cols / kSlot, cus = cu_count();
+    const uint64_t cap_rows = kXbElems / a.cols / kLmBM * kLmBM;
+    if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
+    if ((uint64_t)kLmBM * a.cols * 2 > 0xFFFFFFFFull)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for one M tile", a.cols);
+    for (uint64_t m_start = 0; m_start < a.n_vec; m_start += cap_rows) {
+        const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, a.n_vec - m_start);
+        const uint32_t m_tiles = (mc + kLmBM - 1) / kLmBM;
+        stage_x(a, m_start, mc, m_tiles * kLmBM, ws->xb, st);
+        const uint64_t tiles = (uint64_t)units * m_tiles;
+        GemmPcArgs p{a.w0, a.w1, ws->xb, a.y + m_start * a.y_stride, a.y_stride, a.rows, a.cols, mc, units, m_tiles, 0u,
+                     0u, 1u, ws->partials};
+        if (tiles >= cus) {
+            uint32_t main_units = (uint32_t)(tiles / cus * cus / m_tiles), rest = units - main_units, kc = 0;
+            const uint32_t mt_t = (mc + 127) / 128;
+            if (rest > 0 && S % 8 == 0) {
+                const uint64_t tt = (uint64_t)rest * mt_t;
+                kc = (uint32_t)std::min<uint64_t>({std::max<uint64_t>(cus / tt, 1), S / 8, 16});
+                while (kc > 1 && tt * kc * 128 * kPcW > kPartialFloats) --kc;
+                if (tt * kc * 128 * kPcW > kPartialFloats) kc = 0;  // partials do not fit: run them whole
+            }
+            if (rest > 0 && kc == 0) main_units = units, rest = 0;
+            p.units = main_units;
+            launch_gemm_lm_type<PAIR, 4>(type, p, dim3(main_units * m_tiles), st);
+            if (rest > 0) {
+                GemmPcArgs t = p;
+                t.units = 0;
+                t.m_tiles = mt_t;
+                t.split_units = rest;
+                t.kchunks = kc;
+                t.split_unit0 = main_units;
+                launch_gemm_lm_type<PAIR, 1>(type, t, dim3(rest * mt_t * kc), st);
+                launch_reduce<PAIR, 128>(t, st);
+            }
+        } else {
+            uint32_t kc = S % 8 == 0 ? (uint32_t)std::min<uint64_t>({cus / tiles, S / 8, 16}) : 1u;
+            while (kc > 1 && tiles * kc * kLmBM * kPcW > kPartialFloats) --kc;
+            if (kc >= 2) {
+                p.units = 0;
+                p.split_units = units;
+                p.kchunks = kc;
+                launch_gemm_lm_type<PAIR, 4>(type, p, dim3((uint32_t)(tiles * kc)), st);
+                launch_reduce<PAIR, kLmBM>(p, st);
+            } else {
+                launch_gemm_lm_type<PAIR, 4>(type, p, dim3((uint32_t)tiles), st);
+            }
+        }
+        if (int rc = hip_status(hipGetLastError(), "gemm_lm launch")) return rc;
+    }
+    return HALO_MI_OK;
+}
 
 }  // namespace
 
-// x -> bf16 staging (in chunks of rows that fit the workspace), then the producer/consumer GEMM.
-// When the tiles do not fill whole rounds of the chip (e.g. 272 slabs on 256 CUs), the tiles
-// past the last whole round are split over K so that the last round is spread over all CUs:
-// their fp32 partials go to the workspace and k_gemm_pc_reduce adds them in a fixed order.
+// x -> bf16 staging (in chunks of rows that fit the workspace), then the GEMM: k_gemm_lm for
+// large M (launch_gemm_lm), else the producer/consumer k_gemm_pc. When k_gemm_pc's tiles do not
+// fill whole rounds of the chip (e.g. 272 slabs on 256 CUs), the tiles past the last whole round
+// are split over K so that the last round is spread over all CUs: their fp32 partials go to the
+// workspace and k_gemm_pc_reduce adds them in a fixed order.
 template <bool PAIR>
 int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     Workspace* ws = nullptr;
@@ -799,29 +890,19 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     const int MB = a.n_vec <= 64 ? 1 : a.n_vec <= 128 ? 2 : 4;
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
     const uint32_t units = PAIR ? slabs : (slabs + 1) / 2;
-    const uint32_t S = a.cols / kSlot;
-    static const uint32_t cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n = 256;
-        return (uint32_t)std::max(n, 1);
-    }();
+    const uint32_t S = a.cols / kSlot, cus = cu_count();
     // k_gemm_lm (512-row M tiles) when its tiles alone fill the GPU; with fewer, the smaller
     // tiles of k_gemm_pc spread the work over more CUs
-    const bool lm = a.tiles == kGemmTilesLm ||
-                    (a.tiles == kGemmTilesAuto && a.n_vec > kLmMinRows &&
-                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus);
-    const uint32_t BM = lm ? (uint32_t)kLmBM : 64u * MB;
+    if (a.tiles == kGemmTilesLm || (a.tiles == kGemmTilesAuto && a.n_vec > kLmMinRows &&
+                                    (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus))
+        return launch_gemm_lm<PAIR>(type, a, ws, units, st);
+    const uint32_t BM = 64u * MB;
     const uint64_t cap_rows = kXbElems / a.cols / BM * BM;
     if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
     if ((uint64_t)BM * a.cols * 2 > 0xFFFFFFFFull)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for one M tile", a.cols);
     auto launch = [&](const GemmPcArgs& p) {
         const dim3 grid(p.units * p.m_tiles + p.split_units * p.m_tiles * p.kchunks);
-        if (lm) {
-            launch_gemm_lm_type<PAIR>(type, p, grid, st);
-            return;
-        }
         switch (MB) {
             case 1: launch_gemm_pc_type<PAIR, 1>(type, p, grid, st); break;
             case 2: launch_gemm_pc_type<PAIR, 2>(type, p, grid, st); break;
@@ -834,9 +915,7 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     for (uint64_t m_start = 0; m_start < a.n_vec; m_start += cap_rows) {
         const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, a.n_vec - m_start);
         const uint32_t m_tiles = (mc + BM - 1) / BM;
-        const uint64_t n8 = (uint64_t)m_tiles * BM * (a.cols / 8);
-        hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, a.x + m_start * a.x_stride,
-                           a.x_stride, mc, m_tiles * BM, a.cols, ws->xb);
+        stage_x(a, m_start, mc, m_tiles * BM, ws->xb, st);
         float* y = a.y + m_start * a.y_stride;
         // whole rounds of tiles, then the rest split over K; a matrix whose tiles cannot fill
         // half the chip is split over K altogether
@@ -852,16 +931,14 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
         // one launch: the whole tiles, then the split tiles' chunks (dispatched as CUs free up)
         GemmPcArgs p{a.w0, a.w1, ws->xb, y, a.y_stride, a.rows, a.cols, mc, main_units, m_tiles, 0u,
                      units - main_units, kc, ws->partials};
-        p.xcd_map = lm ? 0u : xcd_ok(main_units, m_tiles);
+        p.split_unit0 = main_units;
+        p.xcd_map = xcd_ok(main_units, m_tiles);
         launch(p);
         if (p.split_units > 0) {
-            const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
-            const dim3 rg((uint32_t)((outs + 255) / 256));
-            if (lm) hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, kLmBM>), rg, dim3(256), 0, st, p);
-            else switch (MB) {
-                case 1: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 64>), rg, dim3(256), 0, st, p); break;
-                case 2: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 128>), rg, dim3(256), 0, st, p); break;
-                default: hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, 256>), rg, dim3(256), 0, st, p); break;
+            switch (MB) {
+                case 1: launch_reduce<PAIR, 64>(p, st); break;
+                case 2: launch_reduce<PAIR, 128>(p, st); break;
+                default: launch_reduce<PAIR, 256>(p, st); break;
             }
         }
         if (int rc = hip_status(hipGetLastError(), "gemm_pc launch")) return rc;

@@ -236,6 +236,52 @@ def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case, variant):
     assert np.all(eerr <= etol)
 
 
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("pair", [False, True])
+@pytest.mark.parametrize("kind", ["one", "many"])
+def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
+    """512-row tiles that do not fill whole rounds of the GPU: the W units past the last whole
+    round run as 128-row tiles split over K (k_gemm_lm with one x block per wave) whose partials
+    are reduced in chunk order. one: one unit more than a round (300 x rows); many: 3000 x rows
+    in 6 M tiles over 50 units (8 units remain). Checked against the oracle on the first rows
+    and on the last 256 rows (the remaining units) for the plain GEMM and for the gate/up pair."""
+    import torch
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    cols = 512  # 16 slots: split tiles take two K chunks
+    n_vec, units = (300, cus + 1) if kind == "one" else (3000, 50)
+    rows = 64 * units * (1 if pair else 2)
+    say("gemm m512 partial round", kind, NAMES[t], rows, cols, n_vec, "pair" if pair else "plain")
+    rb = row_bytes(t, cols)
+    x = np.random.default_rng(8000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    xd = to_dev(x, dev)
+    wa = synth(hl, t, rows, cols, 80 + t)
+    sa = slab_of(hl, dev, t, wa, rows, cols)
+    out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    if pair:
+        wb = synth(hl, t, rows, cols, 90 + t)
+        sb = slab_of(hl, dev, t, wb, rows, cols)
+        hl.gate_up_swiglu(t, sa, sb, xd, out, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMM_BF16_M512)
+    else:
+        hl.gemv(t, sa, xd, out, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMM_BF16_M512)
+    y = host(out)
+    for r0, r1 in ((0, 128), (rows - 256, rows)):
+        n = r1 - r0
+        pa = wa[r0 * rb:r1 * rb]
+        ga = oracle.matmul(t, pa, n, cols, x)
+        ta = gemm_tol(oracle, t, pa, n, cols, x)
+        if pair:
+            pb = wb[r0 * rb:r1 * rb]
+            ub = oracle.matmul(t, pb, n, cols, x)
+            ref = oracle.gate_up_swiglu(t, pa, pb, n, cols, x)
+            tol = swiglu_tol(ga, ub, ta, gemm_tol(oracle, t, pb, n, cols, x), ref, fast=True)
+        else:
+            ref, tol = ga, ta
+        err = np.abs(y[:, r0:r1].astype(np.float64) - ref)
+        print(f"    rows [{r0}, {r1}): worst |d|/bound = {max_ratio(err, tol):.4f}")
+        assert np.all(err <= tol)
+
+
 # ---- fused gate/up + SwiGLU ---------------------------------------------------------------
 
 
