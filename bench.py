@@ -115,6 +115,25 @@ def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0):
             "event_median_us": med * 1e3, "event_mean_us": mean * 1e3, "wq": wq, "x": x.cpu().numpy()}
 
 
+def lm_head_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0):
+    """The LM head (halo_mi_lm_head): the gemv over the vocabulary with the argmax fused into
+    its epilogue, the logits not kept. Same bytes as the plain GEMV plus 12 B of result words
+    per vector."""
+    wq = make_weights(hl, t, rows, cols, seed, outliers)
+    copies = device_copies(hl, torch, t, wq, rows, cols)
+    x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
+    res = torch.empty((m, 3), dtype=torch.int32, device="cuda")
+
+    def launch(i):
+        hl.lm_head(t, copies[i], x, res, rows, cols, m)
+
+    ms, n = time_graph(torch, launch, len(copies), steps, warmup)
+    algo = len(wq) + 4 * m * cols + 12 * m
+    del copies
+    torch.cuda.empty_cache()
+    return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9}
+
+
 def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
     wg = make_weights(hl, t, rows, cols, seed)
     wu = make_weights(hl, t, rows, cols, seed + 40)
@@ -147,6 +166,7 @@ WORKLOADS = {
     "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
     "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
     "upload_q4k_17408x5120": ("upload", "Q4_K", 17408, 5120, 0, 2),
+    "q6k_lm_head_151936x5120_m1": ("head", "Q6_K", 151936, 5120, 1, 3),
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
     "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
@@ -313,6 +333,10 @@ def main() -> int:
                               "TFLOP/s": round(r["tflops"], 2)}), flush=True)
             return 0
         t = int(getattr(hl.DType, t))
+        if kind == "head":
+            r = lm_head_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup, outliers=0.01)
+            print(json.dumps({"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}), flush=True)
+            return 0
         if kind == "gemv":
             r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
             out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
@@ -343,6 +367,10 @@ def main() -> int:
         r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
         extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                             "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("LM head: Q6_K 151936x5120 M=1 with the fused argmax (no logits kept)")
+        r = lm_head_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
+        extra["q6k_lm_head_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                               "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("part (c): GGUF -> SLAB repack and host upload, Q4_K 17408x5120")
         r = upload_case(hl, torch, Q4_K, 17408, 5120, 2)
         extra["q4k_17408x5120_repack_device"] = {"us": round(r["repack_us"], 2), "GB/s": round(r["repack_gbs"], 1),

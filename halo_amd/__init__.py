@@ -14,6 +14,7 @@ from ._lib import (  # noqa: F401
     HaloError,
     Layout,
     Variant,
+    ARGMAX_RESULT_BYTES,
     SLAB_ROWS,
     block_bytes,
     block_elems,
@@ -22,6 +23,7 @@ from ._lib import (  # noqa: F401
     gate_up_swiglu,
     gemv,
     lib,
+    lm_head,
     quantize,
     repack_slab,
     repack_slab_host,

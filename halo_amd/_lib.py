@@ -104,12 +104,28 @@ class _GateUpParams(ctypes.Structure):
     ]
 
 
+class _LmHeadParams(ctypes.Structure):
+    _fields_ = [
+        ("gemv", _GemvParams),
+        ("result", ctypes.c_void_p),
+        ("valid_rows", ctypes.c_uint32),
+        ("ids", ctypes.c_void_p),
+        ("ids_slots", ctypes.c_void_p),
+        ("ids_scatter", ctypes.c_void_p),
+        ("ids_scatter_len", ctypes.c_uint64),
+    ]
+
+
+ARGMAX_RESULT_BYTES = 12  # HALO_MI_ARGMAX_RESULT_BYTES: {index, value bits, poisoned} per vector
+
+
 # Every symbol include/halo_mi355x.h declares, with its ctypes signature.
 _U32, _U64, _VP, _INT = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int
 SIGNATURES = {
     "halo_mi_last_error": (ctypes.c_char_p, []),
     "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
+    "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
     "halo_mi_swiglu": (_INT, [_VP, _U64, _VP, _U64, _VP, _U64, _U32, _U32, _VP]),
     "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
     "halo_mi_row_bytes": (_U64, [_U32, _U32]),
@@ -245,6 +261,18 @@ def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: in
     p = _GateUpParams(int(t), int(layout), _ptr(w_gate), _ptr(w_up), _ptr(x), int(x_stride), _ptr(out), int(out_stride),
                       int(rows), int(cols), int(n_vec), int(variant))
     _check(lib().halo_mi_gate_up_swiglu(ctypes.byref(p), _stream(stream)))
+
+
+def lm_head(t: int, w, x, result, rows: int, cols: int, n_vec: int, *, logits=None, valid_rows: int = 0, ids=None,
+            ids_slots=None, ids_scatter=None, ids_scatter_len: int = 0, layout: int = Layout.SLAB, w_stride: int = 0,
+            x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+    """The gemv over the vocabulary and the fused argmax (halo_mi_lm_head): result receives
+    n_vec triples {index, value bits, poisoned} as uint32; logits (optional) every row."""
+    g = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(logits), int(y_stride),
+                    int(rows), int(cols), int(n_vec), int(variant))
+    p = _LmHeadParams(g, _ptr(result), int(valid_rows), _ptr(ids), _ptr(ids_slots), _ptr(ids_scatter),
+                      int(ids_scatter_len))
+    _check(lib().halo_mi_lm_head(ctypes.byref(p), _stream(stream)))
 
 
 def swiglu(gate, up, out, rows: int, cols: int, *, gate_stride: int = 0, up_stride: int = 0, out_stride: int = 0,

@@ -65,6 +65,13 @@ int workspace_for(hipStream_t st, Workspace** out) {
         (void)hipFree(w.xb);
         return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K slots");
     }
+    if (hipMalloc(&w.parts, kArgParts * sizeof(ArgPart)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        (void)hipFree(w.counters);
+        (void)hipFree(w.xb);
+        (void)hipFree(w.slots);
+        return set_error(HALO_MI_E_MEMORY, "lm_head: cannot allocate the argmax parts");
+    }
     if (launch_fill_u32(w.counters, kCounters, 0u, st) != HALO_MI_OK ||
         launch_fill_u32(reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u, st) != HALO_MI_OK)
         return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
@@ -149,6 +156,84 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     GemmArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
     a.tiles = gemm_tiles(p->variant);
     return launch_gemm_pc<false>(p->type, a, st);
+}
+
+int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
+    clear_error();
+    if (!p) return set_error(HALO_MI_E_KERNEL, "lm_head: null params");
+    const char* op = "LM_HEAD";
+    const halo_mi_gemv_params& g = p->gemv;
+    int code;
+    const uint64_t rb = row_bytes_checked(g.type, g.cols, &code, op);
+    if (code) return code;
+    uint32_t variant = g.variant;
+    if (variant > HALO_MI_GEMM_SLAB_BF16_M512)
+        return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
+    const bool slab = g.layout == HALO_MI_LAYOUT_SLAB;
+    const bool fused = slab && (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB ||
+                                variant == HALO_MI_GEMV_SLAB_AUTO);
+    if (!fused && !g.y) return set_error(HALO_MI_E_KERNEL, "%s: variant %u ranks the logits: gemv.y is needed", op, variant);
+    if ((p->ids_slots == nullptr) != (p->ids_scatter == nullptr) || (p->ids_scatter && !p->ids))
+        return set_error(HALO_MI_E_KERNEL, "%s: ids_slots and ids_scatter go together, and only with ids", op);
+    if (g.n_vec == 0) return HALO_MI_OK;
+    if (!p->result) return set_error(HALO_MI_E_KERNEL, "%s: operand result is empty", op);
+    if ((reinterpret_cast<uintptr_t>(p->result) | reinterpret_cast<uintptr_t>(p->ids) |
+         reinterpret_cast<uintptr_t>(p->ids_slots) | reinterpret_cast<uintptr_t>(p->ids_scatter)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: result and ids must be 4-byte aligned", op);
+    const uint64_t xs = g.x_stride ? g.x_stride : g.cols;
+    const uint64_t ys = g.y_stride ? g.y_stride : g.rows;
+    const uint64_t res_bytes = (uint64_t)g.n_vec * HALO_MI_ARGMAX_RESULT_BYTES, ids_bytes = (uint64_t)g.n_vec * 4;
+    const uint64_t xext = extent(g.n_vec, xs * 4, (uint64_t)g.cols * 4), yext = g.y ? extent(g.n_vec, ys * 4, (uint64_t)g.rows * 4) : 0;
+    const uint64_t wext = slab ? halo_mi_slab_bytes(g.type, g.rows, g.cols)
+                               : extent(g.rows, g.w_stride ? g.w_stride : rb, rb);
+    struct Out {
+        const void* p;
+        uint64_t n;
+        const char* name;
+    };
+    const Out outs[] = {{p->result, res_bytes, "result"},
+                        {p->ids, p->ids ? ids_bytes : 0, "ids"},
+                        {p->ids_scatter, p->ids_scatter ? p->ids_scatter_len * 4 : 0, "ids_scatter"}};
+    for (size_t i = 0; i < 3; ++i) {
+        if (ranges_overlap(outs[i].p, outs[i].n, g.x, xext) || ranges_overlap(outs[i].p, outs[i].n, g.w, wext) ||
+            ranges_overlap(outs[i].p, outs[i].n, g.y, yext) || ranges_overlap(outs[i].p, outs[i].n, p->ids_slots, p->ids_slots ? ids_bytes : 0))
+            return set_error(HALO_MI_E_KERNEL, "%s: %s overlaps an operand", op, outs[i].name);
+        for (size_t j = 0; j < i; ++j)
+            if (ranges_overlap(outs[i].p, outs[i].n, outs[j].p, outs[j].n))
+                return set_error(HALO_MI_E_KERNEL, "%s: %s overlaps %s", op, outs[i].name, outs[j].name);
+    }
+    if (g.rows == 0) return set_error(HALO_MI_E_KERNEL, "%s: no rows to rank", op);
+    auto st = static_cast<hipStream_t>(stream);
+    Workspace* ws = nullptr;
+    if ((code = workspace_for(st, &ws))) return code;
+    if (!ws)
+        return set_error(HALO_MI_E_MEMORY, "%s: this stream is being captured and has no workspace yet "
+                                           "(make one call on it before capturing)", op);
+    const uint32_t n_parts = (g.rows + kSlabRows - 1) / kSlabRows;
+    if ((uint64_t)n_parts * g.n_vec > kArgParts)
+        return set_error(HALO_MI_E_UNSUPPORTED, "%s: %u vectors of %u rows exceed the argmax workspace", op, g.n_vec, g.rows);
+    if (fused) {
+        // halo_mi_gemv's checks, with y optional
+        if (!g.x) return set_error(HALO_MI_E_KERNEL, "%s: operand x is empty", op);
+        if (g.n_vec > 1 && xs < g.cols) return set_error(HALO_MI_E_KERNEL, "%s: x row stride %llu < %u floats", op,
+                                                        (unsigned long long)xs, g.cols);
+        if (reinterpret_cast<uintptr_t>(g.x) % 4) return set_error(HALO_MI_E_KERNEL, "%s: x must be 4-byte aligned", op);
+        if (g.y && ((code = check_xy(op, g.x, xs, g.y, ys, g.rows, g.cols, g.n_vec)))) return code;
+        if (!is_quant(g.type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, g.type);
+        if (!g.w) return set_error(HALO_MI_E_KERNEL, "%s: operand w is empty", op);
+        if (g.w_stride != 0) return set_error(HALO_MI_E_KERNEL, "%s: a SLAB operand has no row stride", op);
+        if (reinterpret_cast<uintptr_t>(g.w) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
+        if (ranges_overlap(g.y, yext, g.w, wext)) return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
+        GemvSlabArgs a{static_cast<const uint8_t*>(g.w), nullptr, g.x, xs, g.y, ys, g.rows, g.cols, g.n_vec};
+        a.parts = ws->parts;
+        a.valid_rows = p->valid_rows;
+        if ((code = launch_gemv_slab<false>(g.type, a, st))) return code;
+    } else {
+        if ((code = halo_mi_gemv(&g, stream))) return code;
+        if ((code = launch_argmax_parts(g.y, ys, g.rows, g.n_vec, p->valid_rows, ws->parts, st))) return code;
+    }
+    return launch_argmax_finish(ws->parts, n_parts, g.n_vec, static_cast<uint32_t*>(p->result), p->ids, p->ids_slots,
+                                p->ids_scatter, p->ids_scatter_len, st);
 }
 
 int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {

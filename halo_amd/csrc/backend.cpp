@@ -211,7 +211,7 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 10> kVariants{{
+constexpr std::array<VariantInfo, 11> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
     {kGemvSlab, "gemv_slab_w64", OpId::Gemv, {}},
@@ -222,6 +222,7 @@ constexpr std::array<VariantInfo, 10> kVariants{{
     {kGateUpGemv, "gate_up_gemv_w64", OpId::GateUpSwiglu, {}},
     {kGateUpGemm, "gate_up_gemm_bf16_mfma", OpId::GateUpSwiglu, {}},
     {kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512", OpId::GateUpSwiglu, {}},
+    {kLmHeadFused, "lm_head_slab_argmax", OpId::LmHead, {}},
 }};
 
 bool has_variant(OpId op, std::uint32_t id) {
@@ -255,6 +256,7 @@ public:
     Limits limits() const noexcept override {
         Limits l;
         l.max_n_vec = std::numeric_limits<std::uint32_t>::max();
+        l.lm_head_ids = true;
         return l;
     }
     bool lost() const noexcept override { return lost_; }
@@ -444,6 +446,72 @@ public:
                                  reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
                                  out.stride / kF32, a.rows, a.cols, a.n_vec, variant};
         check_abi(halo_mi_gate_up_swiglu(&p, st.native()));
+    }
+
+    // LM_HEAD (CpuBackend::lm_head, src/backend/cpu_backend.cpp:669-770): the operands of the
+    // gemv (y optional), result and the optional ids, checked before anything is enqueued. The
+    // gemv's kernel choice picks the path: the default fuses the argmax into the slab gemv
+    // (SLAB weights) or ranks the logits after the reference-order gemv (GGUF weights, which
+    // then need gemv.y); an explicit gemv variant keeps its meaning.
+    void lm_head(Stream& s, const LmHeadArgs& a) override {
+        HipStream& st = stream(s, "LM_HEAD");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kLmHeadFused, ErrorCode::Config,
+              "LM_HEAD: unknown kernel variant id %u", a.kernel.variant_id);
+        const GemvArgs& g = a.gemv;
+        CHECK(has_variant(OpId::Gemv, g.kernel.variant_id), ErrorCode::Config, "LM_HEAD: unknown gemv variant id %u",
+              g.kernel.variant_id);
+        CHECK(a.ids_slots.empty() == a.ids_scatter.empty() && (a.ids_scatter.empty() || !a.ids.empty()), ErrorCode::Api,
+              "LM_HEAD: ids_slots and ids_scatter go together, and only with ids");
+        const Resolver r(this, "LM_HEAD");
+        const auto t = static_cast<std::uint32_t>(g.wtype);
+        const std::uint64_t rb = row_bytes(g.wtype, g.cols, r.op());
+        const bool slab = !g.w.empty() && g.w.buffer->layout() == WeightLayout::Slab;
+        std::uint32_t variant = g.kernel.variant_id == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512
+                                                                          : g.kernel.variant_id;
+        if (variant == 0) variant = slab ? HALO_MI_GEMV_SLAB : HALO_MI_GEMV_GGUF_REF;
+        CHECK(slab == (variant != kGemvGgufRef), ErrorCode::Config, "LM_HEAD: variant %u does not read the %s layout",
+              variant, slab ? "SLAB" : "GGUF");
+        const Operand w = slab ? r.slab(g.w, g.wtype, g.rows, g.cols, "w")
+                               : r.get(g.w, g.rows, rb, g.wtype == DType::F32 ? kF32 : 1, Access::Read, "w");
+        const Operand x = r.f32(g.x, g.n_vec, g.cols, Access::Read, "x");
+        const bool logits = !g.y.empty();
+        const Operand y = logits ? r.f32(g.y, g.n_vec, g.rows, Access::Write, "logits") : Operand{};
+        const Operand res = r.get(a.result, 1, mul_u64(g.n_vec, kArgmaxResultBytes, r.op(), "result"), 4, Access::Write,
+                                  "result");
+        for (const Operand* o : {&y, &res}) {
+            r.no_overlap(*o, x);
+            r.no_overlap(*o, w);
+        }
+        r.no_overlap(res, y);
+        Operand ids{}, slots{}, scat{};
+        if (!a.ids.empty()) {
+            ids = r.get(a.ids, 1, mul_u64(g.n_vec, 4, r.op(), "ids"), 4, Access::Write, "ids");
+            for (const Operand* o : std::initializer_list<const Operand*>{&x, &w, &y, &res}) r.no_overlap(ids, *o);
+        }
+        std::uint64_t scat_len = 0;
+        if (!a.ids_scatter.empty()) {
+            slots = r.get(a.ids_slots, 1, mul_u64(g.n_vec, 4, r.op(), "ids_slots"), 4, Access::Read, "ids_slots");
+            scat_len = a.ids_scatter.view_bytes() / 4;
+            CHECK(scat_len >= 1, ErrorCode::Api, "LM_HEAD: ids_scatter holds no int32");
+            scat = r.get(a.ids_scatter, 1, scat_len * 4, 4, Access::Write, "ids_scatter");
+            for (const Operand* o : std::initializer_list<const Operand*>{&x, &w, &y, &res, &ids, &slots})
+                r.no_overlap(scat, *o);
+            for (const Operand* o : std::initializer_list<const Operand*>{&y, &res, &ids}) r.no_overlap(*o, slots);
+        }
+        if (g.n_vec == 0) return;
+        halo_mi_lm_head_params p{};
+        p.gemv = halo_mi_gemv_params{t,      slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
+                                     w.base, slab ? 0 : w.stride,
+                                     reinterpret_cast<const float*>(x.base), x.stride / kF32,
+                                     logits ? reinterpret_cast<float*>(y.base) : nullptr, logits ? y.stride / kF32 : 0,
+                                     g.rows, g.cols, g.n_vec, variant};
+        p.result = res.base;
+        p.valid_rows = a.valid_rows;
+        p.ids = reinterpret_cast<std::int32_t*>(ids.base);
+        p.ids_slots = reinterpret_cast<const std::uint32_t*>(slots.base);
+        p.ids_scatter = reinterpret_cast<std::int32_t*>(scat.base);
+        p.ids_scatter_len = scat_len;
+        check_abi(halo_mi_lm_head(&p, st.native()));
     }
 
 private:

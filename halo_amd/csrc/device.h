@@ -44,6 +44,34 @@ __device__ __forceinline__ uint32_t and_or_opaque(uint32_t a, uint32_t m, uint32
 // c * fp8_unit(), so v_cvt_pk_f32_fp8 turns two 4-bit quants into two exact floats.
 __device__ __forceinline__ float fp8_unit() { return __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0]; }
 
+// The CPU argmax's order (cpu_backend.cpp:738-739 of the reference: a row replaces the best only
+// when strictly greater, so ties go to the lower index): (va, ia) ranks before (vb, ib).
+// Index 0xFFFFFFFF (no row) ranks after everything.
+__device__ __forceinline__ bool ranks_before(float va, uint32_t ia, float vb, uint32_t ib) {
+    if (ia == 0xFFFFFFFFu) return false;
+    if (ib == 0xFFFFFFFFu) return true;
+    return va > vb || (va == vb && ia < ib);
+}
+
+// Wave-wide argmax of one value per lane: rank (lane's value and index take part) or not, any
+// NaN flag. Every lane returns the wave's best; the order is total, so the result does not
+// depend on the reduction order.
+__device__ __forceinline__ void wave_argmax(float v, uint32_t idx, bool rank, bool is_nan, float& bv, uint32_t& bi,
+                                            uint32_t& any_nan) {
+    bv = rank ? v : 0.0f;
+    bi = rank ? idx : 0xFFFFFFFFu;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, off);
+        if (ranks_before(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    any_nan = __ballot(is_nan) != 0 ? 1u : 0u;
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 

@@ -389,7 +389,25 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                                        __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (row >= a.rows) return;
+    if constexpr (!PAIR) {
+        // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
+        // lanes of wave 0 are here; rows past the matrix take no part)
+        if (a.parts) {
+            const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+            const bool live = row < a.rows;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                if ((uint32_t)v >= a.n_vec) break;
+                const bool nan = live && acc0[v] != acc0[v];
+                const bool rank = live && !nan && (a.valid_rows == 0 || row < a.valid_rows);
+                float bv;
+                uint32_t bi, any_nan;
+                wave_argmax(acc0[v], row, rank, nan, bv, bi, any_nan);
+                if (lane == 0) a.parts[(uint64_t)v * slabs + slab] = ArgPart{bv, bi, any_nan, 0u};
+            }
+        }
+    }
+    if (row >= a.rows || !a.y) return;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         if ((uint32_t)v >= a.n_vec) break;
@@ -897,7 +915,8 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
         GemvSlabArgs c = a;
         c.n_vec = std::min(kMaxGemvVec, total - t0);
         c.x = a.x + (uint64_t)t0 * a.x_stride;
-        c.y = a.y + (uint64_t)t0 * a.y_stride;
+        c.y = a.y ? a.y + (uint64_t)t0 * a.y_stride : nullptr;
+        if (a.parts) c.parts = a.parts + (uint64_t)t0 * slabs;
         int rc;
         switch (type) {
             case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, ws, st); break;

@@ -17,17 +17,32 @@ constexpr uint32_t kMaxGemvVec = 4;  // vectors per slab-gemv launch
 // 4 vectors, so beyond one launch the MFMA GEMM (which streams it once) is faster.
 constexpr uint32_t kGateUpGemvMax = 4;
 
+// Argmax of one vector over a range of rows: the best (value, index) by the CPU's order (higher
+// value first, ties to the lower index; index kNoIndex when no row ranks) and whether any row
+// of the range was NaN.
+constexpr uint32_t kNoIndex = 0xFFFFFFFFu;
+struct ArgPart {
+    float value;
+    uint32_t index;
+    uint32_t nan;
+    uint32_t pad;
+};
+
 struct GemvSlabArgs {
     const uint8_t* w0;  // slab image (gate, or the only matrix)
     const uint8_t* w1;  // up matrix (PAIR) or null
     const float* x;
     uint64_t x_stride;
-    float* y;
+    float* y;           // may be null when parts is set (the logits are not kept)
     uint64_t y_stride;
     uint32_t rows, cols, n_vec;
     uint32_t ks;          // K chunks per slab
     uint64_t* slots;      // [slabs][chunks][NV][64] partials as (value, ready) words, 0 between launches
     uint32_t* counters;   // [slabs], zero between launches
+    // LM head (non-pair only): the argmax of each slab's 64 rows per vector, parts[v][slab]; rows
+    // at or past valid_rows (when not 0) are not ranked, but a NaN in them still counts
+    ArgPart* parts = nullptr;
+    uint32_t valid_rows = 0;
 };
 
 // M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
@@ -53,12 +68,14 @@ constexpr uint64_t kPartialFloats = 8ull << 20;  // GEMM split-tile partials: 32
 constexpr uint64_t kSlots = 4ull << 20;          // GEMV split-K words: 32 MiB
 constexpr uint64_t kCounters = 1ull << 20;        // slabs (64M rows)
 constexpr uint64_t kXbElems = 16ull << 20;        // bf16 copy of x for the GEMM: 32 MiB
+constexpr uint64_t kArgParts = 1ull << 20;        // LM-head argmax parts (16 B each): 16 MiB
 
 struct Workspace {
     float* partials = nullptr;
     uint64_t* slots = nullptr;
     uint32_t* counters = nullptr;
     __bf16* xb = nullptr;
+    ArgPart* parts = nullptr;
 };
 
 // The workspace of (current device, st); *out is null when st is being captured and has none yet.
@@ -93,6 +110,12 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st);
 // k_gemm.hip
 template <bool PAIR>
 int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st);
+// k_argmax.hip: stage 1 over a logits buffer (64-row parts, as the fused GEMV epilogue writes
+// them), and stage 2: parts -> the result words, ids and scattered ids of each vector
+int launch_argmax_parts(const float* logits, uint64_t stride, uint32_t rows, uint32_t n_vec, uint32_t valid_rows,
+                        ArgPart* parts, hipStream_t st);
+int launch_argmax_finish(const ArgPart* parts, uint32_t n_parts, uint32_t n_vec, uint32_t* result, int32_t* ids,
+                         const uint32_t* ids_slots, int32_t* ids_scatter, uint64_t scatter_len, hipStream_t st);
 int launch_swiglu(const float* g, uint64_t gs, const float* u, uint64_t us, float* out, uint64_t os, uint32_t rows,
                   uint32_t cols, hipStream_t st);
 

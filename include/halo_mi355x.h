@@ -145,6 +145,41 @@ typedef struct halo_mi_gate_up_params {
 int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream);
 
 /*
+ * LM head: the gemv over the vocabulary plus the fused argmax. Replaces Backend::lm_head and
+ * LmHeadArgs (include/halo/backend/backend.h:433-460, :572); the semantics are
+ * CpuBackend::lm_head's (src/backend/cpu_backend.cpp:669-770):
+ *   - the argmax is taken over exactly the values the gemv produces: higher value first, ties
+ *     to the lowest index;
+ *   - a NaN logit poisons only its own vector: its result is {0xFFFFFFFF, quiet NaN, 1};
+ *   - rows at or past valid_rows (when not 0) are not ranked (GGUF LM-head padding), but a NaN
+ *     in them still poisons; the logits of every row are still written;
+ *   - a vector with no ranked row reports {0xFFFFFFFF, 0.0f, 0}.
+ * gemv: the operands and variant as for halo_mi_gemv, except that y may be NULL (the logits are
+ *   not kept). With the SLAB layout and variant 0, 2 or 4 the argmax is fused into the slab
+ *   GEMV (any n_vec); the GGUF reference kernel and the MFMA GEMM variants (1, 3, 5) rank the
+ *   logits afterwards and need y.
+ * result: n_vec triples of uint32 {index, value bits, poisoned} (HALO_MI_ARGMAX_RESULT_BYTES
+ *   each, 4-byte aligned), as kArgmaxResultBytes (backend.h:430-431).
+ * ids (optional): n_vec int32 winning indices, 0 for a poisoned vector or one with no ranked row.
+ * ids_slots / ids_scatter (optional, both or neither, only with ids): vector t's id is also
+ *   written to ids_scatter[ids_slots[t]]; a slot at or past ids_scatter_len is not written.
+ * None of result, ids, ids_scatter may overlap x, w, y or each other.
+ */
+#define HALO_MI_ARGMAX_RESULT_BYTES 12u
+
+typedef struct halo_mi_lm_head_params {
+    halo_mi_gemv_params gemv;
+    void* result;
+    uint32_t valid_rows;
+    int32_t* ids;
+    const uint32_t* ids_slots;
+    int32_t* ids_scatter;
+    uint64_t ids_scatter_len;
+} halo_mi_lm_head_params;
+
+int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream);
+
+/*
  * SWIGLU: out[r][c] = silu(gate[r][c]) * up[r][c] for rows x cols fp32 (strides in floats,
  * 0 = cols). The reference's op (backends/cpu/ops_basic.cpp:165-167, EltwiseArgs at
  * include/halo/backend/backend.h:420-427). out may not overlap gate or up.

@@ -147,6 +147,24 @@ struct GemvArgs {
     } gates{};
 };
 
+/// ARGMAX result words of one vector: {index u32, value (f32 bits), nan (0/1)} (backend.h:430-431).
+inline constexpr std::uint32_t kArgmaxResultBytes = 12;
+
+/// LM_HEAD (backend.h:433-460): the gemv over the vocabulary + fused argmax (ties to the lowest
+/// index; a NaN logit poisons its own vector; rows at or past valid_rows, when not 0, are not
+/// ranked). gemv.y is optional (the full logits). result: n_vec * kArgmaxResultBytes. ids,
+/// ids_slots / ids_scatter: optional, as in the reference (Limits::lm_head_ids); a slot past
+/// ids_scatter's end is dropped (the reference's Vulkan behaviour, backend.h:453-457).
+struct LmHeadArgs {
+    GemvArgs gemv{};
+    TensorRef result{};
+    std::uint32_t valid_rows = 0;
+    KernelChoice kernel{};
+    TensorRef ids{};
+    TensorRef ids_slots{};
+    TensorRef ids_scatter{};
+};
+
 /// SWIGLU (backend.h:420-427): out = silu(a) * b, rows x cols.
 struct EltwiseArgs {
     TensorRef a{}, b{}, out{};
@@ -206,6 +224,7 @@ public:
     virtual void gemv(Stream&, const GemvArgs&) = 0;
     virtual void swiglu(Stream&, const EltwiseArgs&) = 0;
     virtual void gate_up_swiglu(Stream&, const GateUpArgs&) = 0;
+    virtual void lm_head(Stream&, const LmHeadArgs&) = 0;
     /// Any other op of the reference interface: Error(Unsupported) on this backend.
     [[noreturn]] void unsupported(OpId op) const;
 
@@ -227,5 +246,6 @@ inline constexpr std::uint32_t kGateUpGemv = 7;
 inline constexpr std::uint32_t kGateUpGemm = 8;
 inline constexpr std::uint32_t kGemmSlabBf16M512 = 9;  // == HALO_MI_GEMM_SLAB_BF16_M512 (MATMUL)
 inline constexpr std::uint32_t kGateUpGemmM512 = 10;   // GATE_UP_SWIGLU on the 512-row-tile GEMM
+inline constexpr std::uint32_t kLmHeadFused = 11;      // LM_HEAD: argmax fused into the slab gemv
 
 }  // namespace halo_mi::backend

@@ -393,3 +393,62 @@ int oracle_gate_up_swiglu(uint32_t type, const uint8_t* wg, const uint8_t* wu, u
     free(u);
     return err;
 }
+
+/* ---- LM head: matmul + fused argmax (src/backend/cpu_backend.cpp:669-770) ----------------- */
+
+/*
+ * One pass over the head matrix in slabs of 8192 rows (:724-726): each slab's logits by
+ * cpu::matmul (:729-730); per vector and row, a NaN logit poisons the vector (:734-737);
+ * otherwise rows below the argmax limit rank by value, a row replacing the best only when
+ * strictly greater, so ties go to the lowest index (:738-739). valid_rows = 0 means all rows
+ * (:721). A poisoned vector reports {-1, quiet NaN} (:745-747); the result words are {index,
+ * value bits, poisoned} (:825-833), with TopKEntry's default {-1, 0.0f} (ops.h:351-355) when
+ * no row ranks. logits (optional) receive every row's value (:740).
+ */
+int oracle_lm_head(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t rows, uint32_t cols, const float* x,
+                   uint32_t n_vec, uint32_t valid_rows, float* logits, uint32_t* result, uint32_t threads) {
+    int err;
+    const uint64_t rb = oracle_row_bytes(type, cols, &err);
+    if (err) return err;
+    if (w_stride == 0) w_stride = rb;
+    if (n_vec == 0) return ORACLE_OK;
+    const size_t kSlab = 8192;
+    const size_t slab = rows < kSlab ? rows : kSlab;
+    const size_t limit = valid_rows > 0 && valid_rows < rows ? valid_rows : rows;
+    float* buf = (float*)malloc((size_t)n_vec * (slab ? slab : 1) * sizeof(float));
+    int32_t* bi = (int32_t*)malloc(n_vec * sizeof(int32_t));
+    float* bv = (float*)malloc(n_vec * sizeof(float));
+    uint8_t* poisoned = (uint8_t*)calloc(n_vec, 1);
+    if (!buf || !bi || !bv || !poisoned) {
+        free(buf), free(bi), free(bv), free(poisoned);
+        return ORACLE_EKERNEL;
+    }
+    for (uint32_t i = 0; i < n_vec; ++i) bi[i] = -1, bv[i] = 0.0f;
+    for (size_t n0 = 0; n0 < rows && !err; n0 += slab) {
+        const size_t ns = rows - n0 < slab ? rows - n0 : slab;
+        err = oracle_matmul(type, w + n0 * w_stride, w_stride, (uint32_t)ns, cols, x, 0, n_vec, buf, slab, threads);
+        for (uint32_t i = 0; i < n_vec && !err; ++i) {
+            const float* row = buf + (size_t)i * slab;
+            for (size_t c = 0; c < ns; ++c) {
+                if (isnan(row[c])) {
+                    poisoned[i] = 1;
+                    continue;
+                }
+                if (!poisoned[i] && n0 + c < limit && (bi[i] < 0 || row[c] > bv[i])) bi[i] = (int32_t)(n0 + c), bv[i] = row[c];
+            }
+            if (logits) memcpy(logits + (size_t)i * rows + n0, row, ns * sizeof(float));
+        }
+    }
+    for (uint32_t i = 0; i < n_vec && !err; ++i) {
+        float v = bv[i];
+        int32_t idx = bi[i];
+        if (poisoned[i]) idx = -1, v = nanf("");
+        uint32_t vb;
+        memcpy(&vb, &v, 4);
+        result[3 * i] = (uint32_t)idx;
+        result[3 * i + 1] = vb;
+        result[3 * i + 2] = poisoned[i] ? 1u : 0u;
+    }
+    free(buf), free(bi), free(bv), free(poisoned);
+    return err;
+}

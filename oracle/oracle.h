@@ -84,6 +84,16 @@ int oracle_gate_up_swiglu(uint32_t type, const uint8_t* wg, const uint8_t* wu, u
                           uint32_t rows, uint32_t cols, const float* x, uint32_t n_vec, float* out,
                           uint32_t threads);
 
+/*
+ * CpuBackend::lm_head (src/backend/cpu_backend.cpp:669-770): logits by cpu::matmul in slabs of
+ * 8192 rows and the fused argmax over exactly those values (ties to the lowest index; a NaN
+ * logit poisons its vector; rows >= valid_rows, when valid_rows != 0, are not ranked).
+ * result: n_vec triples {index, value bits, poisoned} (kArgmaxResultBytes = 12,
+ * include/halo/backend/backend.h:430-431). logits: n_vec x rows floats, or NULL.
+ */
+int oracle_lm_head(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t rows, uint32_t cols, const float* x,
+                   uint32_t n_vec, uint32_t valid_rows, float* logits, uint32_t* result, uint32_t threads);
+
 /* include/halo/backends/cpu/thread_pool.h:58-64: part i of [0, n) split into `parts`. */
 void oracle_partition_range(size_t n, size_t parts, size_t i, size_t* begin, size_t* end);
 

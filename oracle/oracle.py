@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
         "oracle_matmul": (INT, [U32, VP, U64, U32, U32, VP, U64, U32, VP, U64, U32]),
         "oracle_swiglu": (None, [VP, VP, VP, ctypes.c_size_t]),
         "oracle_gate_up_swiglu": (INT, [U32, VP, VP, U64, U32, U32, VP, U32, VP, U32]),
+        "oracle_lm_head": (INT, [U32, VP, U64, U32, U32, VP, U32, U32, VP, VP, U32]),
         "oracle_partition_range": (None, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                           ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
         "oracle_default_threads": (U32, []),
@@ -130,6 +131,19 @@ def matmul(t: int, w, rows: int, cols: int, x, *, w_stride: int = 0, threads: in
     _chk(lib().oracle_matmul(int(t), w.ctypes.data, int(w_stride), int(rows), int(cols), x.ctypes.data, int(cols),
                              x.shape[0], y.ctypes.data, int(rows), int(th)), "matmul")
     return y
+
+
+def lm_head(t: int, w, rows: int, cols: int, x, *, valid_rows: int = 0, w_stride: int = 0, threads: int = 0):
+    """(result words [n_vec, 3] uint32, logits [n_vec, rows]) of CpuBackend::lm_head."""
+    w = _u8(w)
+    x = _f32(x).reshape(-1, cols)
+    n = x.shape[0]
+    logits = np.empty((n, rows), dtype=np.float32)
+    res = np.empty((n, 3), dtype=np.uint32)
+    th = threads or lib().oracle_default_threads()
+    _chk(lib().oracle_lm_head(int(t), w.ctypes.data, int(w_stride), int(rows), int(cols), x.ctypes.data, n,
+                              int(valid_rows), logits.ctypes.data, res.ctypes.data, int(th)), "lm_head")
+    return res, logits
 
 
 def swiglu(g, u) -> np.ndarray:

@@ -167,6 +167,55 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
     download_y(*y1b, y1);
     check(std::memcmp(y1.data(), y.data(), rows * 4) == 0, tn + ": row 0 of n_vec = 3 equals n_vec = 1");
 
+    // LM head: on the GGUF buffer (reference-order gemv, logits kept) the result words equal the
+    // oracle's CpuBackend::lm_head bitwise; on the SLAB buffer (argmax fused into the slab gemv,
+    // no logits) the result is the first maximum of that gemv's own rows (y from above), and
+    // the dense ids follow the index
+    {
+        std::vector<uint32_t> cpu_res((size_t)n_vec * 3), res((size_t)n_vec * 3);
+        oracle_lm_head(type, wg.data(), 0, rows, cols, x.data(), n_vec, 0, nullptr, cpu_res.data(), 1);
+        auto rb = be.allocate((size_t)n_vec * hb::kArgmaxResultBytes, hb::Tier::Vram);
+        auto ib = be.allocate((size_t)n_vec * 4, hb::Tier::Vram);
+        hb::LmHeadArgs h;
+        h.gemv = a;
+        h.gemv.w = hb::TensorRef::of(*w_gguf);
+        h.result = hb::TensorRef::of(*rb);
+        h.ids = hb::TensorRef::of(*ib);
+        be.lm_head(st, h);
+        be.download(st, hb::TensorRef::of(*rb), std::as_writable_bytes(std::span<uint32_t>(res)));
+        st.submit();
+        st.wait();
+        check(res == cpu_res, tn + ": lm_head on GGUF weights equals the CPU's result words");
+        h.gemv.w = hb::TensorRef::of(*w_slab);
+        h.gemv.y = {};
+        be.lm_head(st, h);
+        std::vector<int32_t> ids(n_vec);
+        be.download(st, hb::TensorRef::of(*rb), std::as_writable_bytes(std::span<uint32_t>(res)));
+        be.download(st, hb::TensorRef::of(*ib), std::as_writable_bytes(std::span<int32_t>(ids)));
+        st.submit();
+        st.wait();
+        bool okh = true;
+        for (uint32_t t = 0; t < n_vec; ++t) {
+            const float* row = y.data() + (size_t)t * rows;
+            uint32_t best = 0;
+            for (uint32_t n = 1; n < rows; ++n)
+                if (row[n] > row[best]) best = n;
+            uint32_t vb;
+            std::memcpy(&vb, &row[best], 4);
+            okh &= res[3 * t] == best && res[3 * t + 1] == vb && res[3 * t + 2] == 0 && ids[t] == (int32_t)best;
+        }
+        check(okh, tn + ": fused lm_head on SLAB weights is the first maximum of the slab gemv");
+        hb::LmHeadArgs bad = h;
+        bad.ids = {};
+        bad.ids_slots = hb::TensorRef::of(*ib);
+        bad.ids_scatter = hb::TensorRef::of(*ib);
+        check(code_of([&] { be.lm_head(st, bad); }) == (int)hb::ErrorCode::Api, tn + ": lm_head ids_slots without ids -> Api");
+        bad = h;
+        bad.gemv.w = hb::TensorRef::of(*w_gguf);
+        check(code_of([&] { be.lm_head(st, bad); }) == (int)hb::ErrorCode::Kernel,
+              tn + ": lm_head ranking GGUF logits without gemv.y -> Kernel");
+    }
+
     // fused gate/up (GEMV pair and bf16 GEMM variants) against the oracle's composition
     const std::vector<double> tu = slab_bound(type, wu, rows, cols, x, n_vec);
     const std::vector<double> gg = gemm_bound(type, wg, rows, cols, x, n_vec), gu = gemm_bound(type, wu, rows, cols, x, n_vec);
@@ -240,6 +289,7 @@ int main(int argc, char** argv) {
             {hb::OpId::GateUpSwiglu,
              {{hb::kGateUpGemv, "gate_up_gemv_w64"}, {hb::kGateUpGemm, "gate_up_gemm_bf16_mfma"},
               {hb::kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512"}}},
+            {hb::OpId::LmHead, {{hb::kLmHeadFused, "lm_head_slab_argmax"}}},
         };
         for (const auto& [op, want] : pinned) {
             const auto got = be->variants(op);

@@ -330,3 +330,107 @@ def test_gate_up_composition_equals_parts(oracle):
     g = oracle.matmul(Q4_K, wg, n, k, x)
     u = oracle.matmul(Q4_K, wu, n, k, x)
     assert np.array_equal(out, oracle.swiglu(g, u))
+
+
+# ---- LM head: matmul + fused argmax (src/backend/cpu_backend.cpp:669-770) ------------------
+
+QNAN_BITS = 0x7FC00000  # std::numeric_limits<float>::quiet_NaN()
+NO_INDEX = 0xFFFFFFFF   # index -1 as the u32 result word
+
+
+def _f32_head(logit_cols):
+    """F32 head weights whose logits are chosen directly: W[:, 0] = logits, x = e_0 (every
+    other product is an exact 0, so the fp32 dot returns the logit bitwise)."""
+    logits = np.asarray(logit_cols, np.float32)
+    w = np.zeros((logits.size, 8), np.float32)
+    w[:, 0] = logits
+    return w.view(np.uint8).ravel(), logits.size, 8
+
+
+def _bits(v):
+    return struct.unpack("<I", struct.pack("<f", v))[0]
+
+
+def test_lm_head_ties_go_to_the_lowest_index(oracle):
+    w, rows, cols = _f32_head([1, 5, 5, -2, 3, 5, 0, 4, 1, 2])
+    x = np.zeros((1, cols), np.float32)
+    x[0, 0] = 1
+    res, logits = oracle.lm_head(F32, w, rows, cols, x)
+    assert logits[0].tolist() == [1, 5, 5, -2, 3, 5, 0, 4, 1, 2]
+    assert res[0].tolist() == [int(np.argmax(logits[0])), _bits(5.0), 0] == [1, _bits(5.0), 0]
+
+
+def test_lm_head_zero_ties_and_infinities(oracle):
+    # equal zeros: the lower index wins (the dot starts from +0, so a -0 weight gives a +0
+    # logit); +inf beats every finite value; -inf loses to everything
+    w, rows, cols = _f32_head([-np.inf, -0.0, 0.0, -1.0])
+    x = np.zeros((1, cols), np.float32)
+    x[0, 0] = 1
+    res, logits = oracle.lm_head(F32, w, rows, cols, x)
+    assert logits[0, 1] == logits[0, 2] == 0.0
+    assert res[0].tolist() == [1, int(logits[0, 1].view(np.uint32)), 0]
+    w, rows, cols = _f32_head([3.0, np.inf, 7.0, np.inf])
+    res, _ = oracle.lm_head(F32, w, rows, cols, x)
+    assert res[0].tolist() == [1, _bits(np.inf), 0]
+
+
+def test_lm_head_nan_poisons_only_its_vector(oracle):
+    w, rows, cols = _f32_head([1, 9, 3])
+    x = np.zeros((3, cols), np.float32)
+    x[:, 0] = 1
+    x[1, 5] = np.nan  # every logit of vector 1 is NaN
+    res, _ = oracle.lm_head(F32, w, rows, cols, x)
+    assert res[0].tolist() == [1, _bits(9.0), 0]
+    assert res[1].tolist() == [NO_INDEX, QNAN_BITS, 1]
+    assert res[2].tolist() == [1, _bits(9.0), 0]
+
+
+def test_lm_head_valid_rows_clamps_the_argmax_not_the_logits(oracle):
+    w, rows, cols = _f32_head([1, 2, 3, 10, 20])
+    x = np.zeros((1, cols), np.float32)
+    x[0, 0] = 1
+    res, logits = oracle.lm_head(F32, w, rows, cols, x, valid_rows=3)
+    assert res[0].tolist() == [2, _bits(3.0), 0]
+    assert logits[0].tolist() == [1, 2, 3, 10, 20]
+    # valid_rows past the end is the whole matrix; 0 is the whole matrix
+    for vr in (0, 5, 99):
+        res, _ = oracle.lm_head(F32, w, rows, cols, x, valid_rows=vr)
+        assert res[0].tolist() == [4, _bits(20.0), 0]
+
+
+def test_lm_head_nan_past_valid_rows_still_poisons(oracle):
+    # cpu_backend.cpp:734-739: the NaN test comes before the valid_rows clamp
+    w, rows, cols = _f32_head([1, 2, np.nan])
+    x = np.zeros((1, cols), np.float32)
+    x[0, 0] = 1
+    res, _ = oracle.lm_head(F32, w, rows, cols, x, valid_rows=2)
+    assert res[0].tolist() == [NO_INDEX, QNAN_BITS, 1]
+
+
+def test_lm_head_across_8192_row_slabs(oracle):
+    # the maximum in the second slab, and a tie across the slab boundary
+    vals = np.zeros(8192 + 100, np.float32)
+    vals[8192 + 50] = 4.0
+    vals[7000] = 4.0
+    w, rows, cols = _f32_head(vals)
+    x = np.zeros((1, cols), np.float32)
+    x[0, 0] = 1
+    res, _ = oracle.lm_head(F32, w, rows, cols, x)
+    assert res[0].tolist() == [7000, _bits(4.0), 0]
+    vals[7000] = 3.0
+    w, rows, cols = _f32_head(vals)
+    res, _ = oracle.lm_head(F32, w, rows, cols, x)
+    assert res[0].tolist() == [8242, _bits(4.0), 0]
+
+
+def test_lm_head_q6_k_logits_are_matmul_and_index_is_first_argmax(oracle):
+    rng = np.random.default_rng(11)
+    rows, cols = 300, 512
+    w = rng.integers(0, 256, size=rows * oracle.row_bytes(Q6_K, cols), dtype=np.uint8)
+    w[208::210] = 0x00  # keep every d finite: fp16 d with a small exponent
+    w[209::210] &= 0x0F
+    x = rng.standard_normal((4, cols)).astype(np.float32)
+    res, logits = oracle.lm_head(Q6_K, w, rows, cols, x)
+    assert np.array_equal(logits, oracle.matmul(Q6_K, w, rows, cols, x))
+    for i in range(4):
+        assert res[i, 0] == np.argmax(logits[i]) and res[i, 1] == logits[i].max().view(np.uint32) and res[i, 2] == 0
