@@ -165,6 +165,10 @@ WORKLOADS = {
     "q4k_gate_up_swiglu_m8": ("gemm", "Q4_K", 17408, 5120, 8, 4),
     "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
     "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
+    "q5k_gemv_17408x5120_m1": ("gemv", "Q5_K", 17408, 5120, 1, 6),
+    "iq4xs_gemv_17408x5120_m1": ("gemv", "IQ4_XS", 17408, 5120, 1, 7),
+    "q5k_gate_up_swiglu_m512": ("gemm", "Q5_K", 17408, 5120, 512, 6),
+    "iq4xs_gate_up_swiglu_m512": ("gemm", "IQ4_XS", 17408, 5120, 512, 7),
     "upload_q4k_17408x5120": ("upload", "Q4_K", 17408, 5120, 0, 2),
     "q6k_lm_head_151936x5120_m1": ("head", "Q6_K", 151936, 5120, 1, 3),
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
@@ -367,6 +371,15 @@ def main() -> int:
         r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
         extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                             "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        for name, tn, seed in (("q5k", "Q5_K", 6), ("iq4xs", "IQ4_XS", 7)):
+            log(f"the UD pack's other formats: {tn} GEMV 17408x5120 M=1 and gate/up M=512")
+            tt = int(getattr(hl.DType, tn))
+            r = gemv_case(hl, torch, tt, 17408, 5120, 1, seed, args.steps // 2, args.warmup)
+            extra[f"{name}_gemv_17408x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                                   "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            r = gemm_case(hl, torch, tt, 17408, 5120, 512, seed, max(20, args.steps // 20), 5)
+            extra[f"{name}_gate_up_swiglu_m512"] = {"TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 2),
+                                                    "frac_bf16_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)}
         log("LM head: Q6_K 151936x5120 M=1 with the fused argmax (no logits kept)")
         r = lm_head_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
         extra["q6k_lm_head_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),

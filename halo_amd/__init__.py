@@ -1,4 +1,5 @@
-"""halo_amd: MI355X-native quantized matrix-multiply backend (GGUF Q4_0 / Q8_0 / Q4_K / Q6_K).
+"""halo_amd: MI355X-native quantized matrix-multiply backend (GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K /
+IQ4_XS).
 
 The compute path is hand-written HIP for gfx950 in ``libhalo_mi355x.so``, reached through the
 C ABI declared in ``include/halo_mi355x.h``. This package loads that library with ctypes and

@@ -24,7 +24,9 @@ class DType(enum.IntEnum):
     Q4_0 = 2
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
+    IQ4_XS = 23
 
 
 class Layout(enum.IntEnum):
@@ -58,7 +60,8 @@ class HaloError(RuntimeError):
         super().__init__(f"{self.code.name.upper()}_ERROR: {message}")
 
 
-_BLOCK = {DType.F32: (1, 4), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q4_K: (256, 144), DType.Q6_K: (256, 210)}
+_BLOCK = {DType.F32: (1, 4), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q4_K: (256, 144),
+          DType.Q5_K: (256, 176), DType.Q6_K: (256, 210), DType.IQ4_XS: (256, 136)}
 
 
 def block_elems(t: int) -> int:

@@ -60,7 +60,9 @@ const char* type_name(DType t) {
         case DType::Q4_0: return "Q4_0";
         case DType::Q8_0: return "Q8_0";
         case DType::Q4_K: return "Q4_K";
+        case DType::Q5_K: return "Q5_K";
         case DType::Q6_K: return "Q6_K";
+        case DType::IQ4_XS: return "IQ4_XS";
     }
     return "?";
 }
@@ -530,7 +532,8 @@ private:
     static std::uint64_t row_bytes(DType t, std::uint32_t cols, const char* op) {
         const std::uint64_t rb = halo_mi_row_bytes(static_cast<std::uint32_t>(t), cols);
         if (rb == 0) {
-            const bool known = t == DType::F32 || t == DType::Q4_0 || t == DType::Q8_0 || t == DType::Q4_K || t == DType::Q6_K;
+            const bool known = t == DType::F32 || t == DType::Q4_0 || t == DType::Q8_0 || t == DType::Q4_K ||
+                               t == DType::Q5_K || t == DType::Q6_K || t == DType::IQ4_XS;
             CHECK(!known, ErrorCode::Kernel, "%s: %u elements is not a multiple of the %s block size", op, cols, type_name(t));
             fail(ErrorCode::Unsupported, "%s: no kernel for weight type %u", op, static_cast<unsigned>(t));
         }

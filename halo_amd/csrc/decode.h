@@ -1,7 +1,8 @@
 // Device-side unpacking of GGUF blocks and SLAB slot records. Every weight value these
 // helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:79-90,
-// :143-151, :236-269, :302-327): all products in those expressions are exact in fp32, and the
-// one rounding step (Q4_K's `- dmin * m`) is evaluated in the same order.
+// :143-151, :236-269, :271-299, :302-327, :330-347): all products in those expressions are
+// exact in fp32, and the one rounding step (Q4_K's and Q5_K's `- dmin * m`) is evaluated in the
+// same order.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,6 +62,32 @@ __device__ __forceinline__ void q6_slot_bytes(const uint4& ql, const uint2& qh, 
     }
 }
 
+// ---- IQ4_XS ---------------------------------------------------------------------------------
+// The IQ4_NL value table of the GGUF format (ggml's kvalues_iq4nl; the reference's copy is at
+// src/tensor/ggml_tables.h:94-96), four int8 values per dword.
+constexpr uint32_t kIq4Tab[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+// The same values plus 128 (1 .. 241): unsigned bytes for the paths that bias codes.
+constexpr uint32_t kIq4TabB[4] = {0x3F2D1801u, 0x766A5D4Fu, 0xA6998D81u, 0xF1D9C5B5u};
+
+__device__ __forceinline__ int iq4_value(uint32_t nib) {
+    const uint32_t w = nib < 8 ? (nib < 4 ? kIq4Tab[0] : kIq4Tab[1]) : (nib < 12 ? kIq4Tab[2] : kIq4Tab[3]);
+    return (int)(int8_t)((w >> (8 * (nib & 3u))) & 0xFFu);
+}
+// 6-bit scale of sub-block j (quant.cpp:336): ls = (scales_l nibble j) | (scales_h bits 2j..2j+1) << 4;
+// the sub-block's multiplier is d * (ls - 32). sh = scales_h (16 bits), sl = scales_l (4 bytes).
+__device__ __forceinline__ int iq4xs_ls(uint32_t sh, uint32_t sl, uint32_t j) {
+    return (int)(((sl >> (4 * j)) & 15u) | (((sh >> (2 * j)) & 3u) << 4)) - 32;
+}
+// Four 4-bit codes in the low nibbles of q's bytes (the high nibbles are ignored) -> the
+// table's biased values (kIq4TabB) as bytes: a byte-permute over each table half with the
+// code's low 3 bits, then a third one that takes byte k from the half that bit 3 names.
+__device__ __forceinline__ uint32_t iq4_lookup4(uint32_t q) {
+    const uint32_t sel = q & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4TabB[1], kIq4TabB[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4TabB[3], kIq4TabB[2], sel);
+    return __builtin_amdgcn_perm(hi, lo, ((q >> 1) & 0x04040404u) | 0x03020100u);
+}
+
 // ---- per-element decode of a GGUF row (the reference variant; byte loads) -------------------
 // Same expressions as quant.cpp; contraction is off in every caller.
 __device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, uint32_t i) {
@@ -102,6 +129,34 @@ __device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, ui
             const uint8_t qb = blk[16 + 32 * g + l];
             const uint32_t q = hi ? (qb >> 4) : (qb & 15);
             return d1 * (float)q - m1;
+        }
+        case kQ5_K: {
+            const uint8_t* blk = row + (i / 256) * 176;
+            const uint32_t e = i % 256, g = e / 64, hi = (e % 64) / 32, l = e % 32;
+            const float d = h2f(ld_u16(blk)), dmin = h2f(ld_u16(blk + 2));
+            const uint8_t* s = blk + 4;
+            const uint32_t j = 2 * g + hi;
+            uint32_t sc, m;
+            if (j < 4) {
+                sc = s[j] & 63;
+                m = s[j + 4] & 63;
+            } else {
+                sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+            }
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            const uint8_t qb = blk[48 + 32 * g + l];
+            const uint32_t q = (hi ? (qb >> 4) : (qb & 15)) + (((blk[16 + l] >> j) & 1u) ? 16u : 0u);
+            return d1 * (float)q - m1;
+        }
+        case kIQ4_XS: {
+            const uint8_t* blk = row + (i / 256) * 136;
+            const uint32_t e = i % 256, ib = e / 32, el = e % 32;
+            const float d = h2f(ld_u16(blk));
+            const uint32_t sl = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) | ((uint32_t)blk[7] << 24);
+            const float dl = d * (float)iq4xs_ls(ld_u16(blk + 2), sl, ib);
+            const uint8_t qb = blk[8 + 16 * ib + (el & 15)];
+            return dl * (float)iq4_value(el < 16 ? (qb & 15u) : (qb >> 4));
         }
         case kQ6_K: {
             const uint8_t* blk = row + (i / 256) * 210;

@@ -145,9 +145,11 @@ void quant_q4_0(const float* x, uint8_t* blk) {
     for (int i = 0; i < 16; ++i) blk[2 + i] = static_cast<uint8_t>(q[i] | (q[i + 16] << 4));
 }
 
-// Q4_K: per 32-weight sub-block an affine fit w ~ s * q - m (q in 0..15, m >= 0); the eight
-// scales and eight mins are then quantized to 6 bits against fp16 d and dmin.
-void quant_q4_k(const float* x, uint8_t* blk) {
+// Q4_K (QMAX 15) and Q5_K (QMAX 31): per 32-weight sub-block an affine fit w ~ s * q - m
+// (q in 0..QMAX, m >= 0); the eight scales and eight mins are then quantized to 6 bits against
+// fp16 d and dmin (the 12-byte scales field both formats share).
+template <int QMAX>
+void quant_k_affine(const float* x, uint8_t* blk) {
     float scale[8], minv[8];
     for (int j = 0; j < 8; ++j) {
         float lo = x[32 * j], hi = x[32 * j];
@@ -156,7 +158,7 @@ void quant_q4_k(const float* x, uint8_t* blk) {
             hi = std::max(hi, x[32 * j + i]);
         }
         if (lo > 0.0f) lo = 0.0f;
-        scale[j] = (hi - lo) / 15.0f;
+        scale[j] = (hi - lo) / (float)QMAX;
         minv[j] = -lo;
     }
     float smax = 0.0f, mmax = 0.0f;
@@ -184,13 +186,70 @@ void quant_q4_k(const float* x, uint8_t* blk) {
         const float d1 = d * (float)sc[j], m1 = dmin * (float)mq[j];
         for (int i = 0; i < 32; ++i) {
             const int v = d1 > 0.0f ? nearest((x[32 * j + i] + m1) / d1) : 0;
-            q[32 * j + i] = static_cast<uint8_t>(std::clamp(v, 0, 15));
+            q[32 * j + i] = static_cast<uint8_t>(std::clamp(v, 0, QMAX));
         }
     }
-    // group g of 32 bytes: low nibbles = sub-block 2g, high nibbles = sub-block 2g + 1
+    // group g of 32 bytes: low nibbles = sub-block 2g, high nibbles = sub-block 2g + 1; Q5_K
+    // keeps the fifth bit of element l of sub-block j in bit j of qh[l] (bytes 16..47)
+    uint8_t* qs = blk + (QMAX == 15 ? 16 : 48);
     for (int g = 0; g < 4; ++g)
         for (int l = 0; l < 32; ++l)
-            blk[16 + 32 * g + l] = static_cast<uint8_t>(q[64 * g + l] | (q[64 * g + 32 + l] << 4));
+            qs[32 * g + l] = static_cast<uint8_t>((q[64 * g + l] & 15) | ((q[64 * g + 32 + l] & 15) << 4));
+    if constexpr (QMAX == 31) {
+        for (int l = 0; l < 32; ++l) {
+            uint8_t h = 0;
+            for (int j = 0; j < 8; ++j) h = static_cast<uint8_t>(h | ((q[32 * j + l] >> 4) << j));
+            blk[16 + l] = h;
+        }
+    }
+}
+
+// The IQ4_NL code table of the GGUF format (ggml's kvalues_iq4nl).
+constexpr int kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+// IQ4_XS: per 32-weight sub-block a scale s that maps the element of largest magnitude to the
+// table's end -127; the eight scales are quantized to 6 bits (ls - 32 in -32..31) against
+// fp16 d = -(the largest-magnitude scale) / 32; each weight takes the nearest table value.
+void quant_iq4_xs(const float* x, uint8_t* blk) {
+    float sv[8], smax = 0.0f;
+    for (int j = 0; j < 8; ++j) {
+        float vmax = 0.0f;
+        for (int i = 0; i < 32; ++i)
+            if (std::fabs(x[32 * j + i]) > std::fabs(vmax)) vmax = x[32 * j + i];
+        sv[j] = vmax / -127.0f;
+        if (std::fabs(sv[j]) > std::fabs(smax)) smax = sv[j];
+    }
+    const uint16_t dh = f32_to_f16(smax / -32.0f);
+    const float d = f16_to_f32(dh);
+    put16(blk, dh);
+    uint16_t sh = 0;
+    for (int i = 0; i < 4; ++i) blk[4 + i] = 0;
+    for (int j = 0; j < 8; ++j) {
+        const int l = d != 0.0f ? std::clamp(nearest(sv[j] / d), -32, 31) : 0;
+        const int ls = l + 32;
+        blk[4 + j / 2] = static_cast<uint8_t>(blk[4 + j / 2] | ((ls & 15) << (4 * (j % 2))));
+        sh = static_cast<uint16_t>(sh | ((ls >> 4) << (2 * j)));
+        const float dl = d * (float)l;
+        uint8_t q[32];
+        for (int i = 0; i < 32; ++i) {
+            int best = 8;
+            if (dl != 0.0f) {
+                const float t = x[32 * j + i] / dl;
+                float err = std::fabs(t - (float)kIq4Values[0]);
+                best = 0;
+                for (int k = 1; k < 16; ++k) {
+                    const float e = std::fabs(t - (float)kIq4Values[k]);
+                    if (e < err) {
+                        err = e;
+                        best = k;
+                    }
+                }
+            }
+            q[i] = static_cast<uint8_t>(best);
+        }
+        for (int i = 0; i < 16; ++i) blk[8 + 16 * j + i] = static_cast<uint8_t>(q[i] | (q[i + 16] << 4));
+    }
+    put16(blk + 2, sh);
 }
 
 // Q6_K: per 16-weight sub-block a symmetric scale s = max|x| / 31 (q in -32..31); the sixteen
@@ -348,8 +407,10 @@ int halo_mi_quantize(uint32_t type, const float* src, uint64_t n, void* dst, uin
             switch (type) {
                 case kQ4_0: quant_q4_0(x, blk); break;
                 case kQ8_0: quant_q8_0(x, blk); break;
-                case kQ4_K: quant_q4_k(x, blk); break;
+                case kQ4_K: quant_k_affine<15>(x, blk); break;
+                case kQ5_K: quant_k_affine<31>(x, blk); break;
                 case kQ6_K: quant_q6_k(x, blk); break;
+                case kIQ4_XS: quant_iq4_xs(x, blk); break;
             }
         }
     });

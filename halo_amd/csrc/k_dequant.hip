@@ -130,6 +130,37 @@ __device__ __forceinline__ void slab_slot_weights(const uint8_t* __restrict__ sl
                 w[4 * i + k] = d1 * (float)(b & 15u) - m1;
                 w[16 + 4 * i + k] = d1 * (float)(b >> 4) - m1;
             }
+    } else if constexpr (T == kQ5_K) {
+        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
+        const uint32_t qh = *reinterpret_cast<const uint32_t*>(slab + g.aux_off + ((uint64_t)s * 64 + r) * 4);
+        const uint4 hdr = *reinterpret_cast<const uint4*>(slab + g.sc_off + ((uint64_t)(s / 8) * 64 + r) * 16);
+        float d1, m1;
+        q4k_scales(hdr, s % 8, d1, m1);
+        const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = (Q[i] & 0x0F0F0F0Fu) | ((qh << (4 - i)) & 0x10101010u);
+            const uint32_t hi = ((Q[i] >> 4) & 0x0F0F0F0Fu) | ((qh >> i) & 0x10101010u);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                w[4 * i + k] = d1 * ubyte(lo, k) - m1;
+                w[16 + 4 * i + k] = d1 * ubyte(hi, k) - m1;
+            }
+        }
+    } else if constexpr (T == kIQ4_XS) {
+        const uint4 q = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
+        const uint2 hdr = *reinterpret_cast<const uint2*>(slab + g.aux_off + ((uint64_t)(s / 8) * 64 + r) * 8);
+        const float dl = h2f((uint16_t)(hdr.x & 0xFFFFu)) * (float)iq4xs_ls(hdr.x >> 16, hdr.y, s % 8);
+        const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = iq4_lookup4(Q[i]), hi = iq4_lookup4(Q[i] >> 4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                w[4 * i + k] = dl * (ubyte(lo, k) - 128.0f);
+                w[16 + 4 * i + k] = dl * (ubyte(hi, k) - 128.0f);
+            }
+        }
     } else {  // Q6_K
         const uint4 ql = *reinterpret_cast<const uint4*>(slab + g.q_off + ((uint64_t)s * 64 + r) * 16);
         const uint2 qh = *reinterpret_cast<const uint2*>(slab + g.aux_off + ((uint64_t)s * 64 + r) * 8);
@@ -202,6 +233,8 @@ int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t
         case kQ4_0: hipLaunchKernelGGL(k_dequant_slab<kQ4_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
         case kQ8_0: hipLaunchKernelGGL(k_dequant_slab<kQ8_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
         case kQ4_K: hipLaunchKernelGGL(k_dequant_slab<kQ4_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        case kQ5_K: hipLaunchKernelGGL(k_dequant_slab<kQ5_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        case kIQ4_XS: hipLaunchKernelGGL(k_dequant_slab<kIQ4_XS>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
         default: hipLaunchKernelGGL(k_dequant_slab<kQ6_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
     }
     return hip_status(hipGetLastError(), "dequant_slab launch");

@@ -145,6 +145,16 @@ struct PcW<kQ6_K> {
     uint2 ql;
     uint32_t qh, sc, d;
 };
+template <>
+struct PcW<kQ5_K> {
+    uint2 q;
+    uint32_t qh;
+    uint4 hdr;
+};
+template <>
+struct PcW<kIQ4_XS> {
+    uint2 q, hdr;
+};
 
 // Buffer resource over [base, base + bytes) for raw buffer loads (gfx9 dword 3: 32-bit data
 // format, untyped access). Offsets past `bytes` read as zero.
@@ -175,6 +185,8 @@ template <uint32_t T>
 __device__ __forceinline__ PcOff pc_offsets(uint32_t r, uint32_t h) {
     if constexpr (T == kQ4_K) return {r * 16 + 8 * h, r * 16, 0, 0};
     else if constexpr (T == kQ4_0 || T == kQ8_0) return {r * 16 + 8 * h, r * 2, 0, 0};
+    else if constexpr (T == kQ5_K) return {r * 16 + 8 * h, r * 4, r * 16, 0};
+    else if constexpr (T == kIQ4_XS) return {r * 16 + 8 * h, r * 8, 0, 0};
     else return {r * 16 + 8 * h, r * 8 + 4 * h, r * 16, r * 2};
 }
 
@@ -192,6 +204,13 @@ __device__ __forceinline__ void pc_load_w(PcW<T>& R, __amdgpu_buffer_rsrc_t slab
     } else if constexpr (T == kQ4_0) {
         R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
         R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+    } else if constexpr (T == kQ5_K) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 256));
+        R.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+    } else if constexpr (T == kIQ4_XS) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
     } else if constexpr (T == kQ8_0) {
         R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
         R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
@@ -222,6 +241,8 @@ __device__ __forceinline__ void q4k_sc_m_sel(uint32_t s0, uint32_t s1, uint32_t 
 //   Q4_0 (q - 8) d = fma(d / u, q u, -8 d)      (exact: d (q - 8) is representable)
 //   Q8_0 q d       = fma(d, q + 128, -128 d)    (q + 128 as an unsigned byte; exact)
 //   Q6_K (d sc)(q - 32) = fma(d sc, q, -32 d sc) (exact)
+//   Q5_K d1 q - m1 = fma(d1, q, -m1)             (d1 q exact: 17 x 5 bits)
+//   IQ4_XS dl v    = fma(dl, v + 128, -128 dl)   (v + 128 from the biased table; exact)
 template <uint32_t T>
 __device__ __forceinline__ void pc_dequant(const PcW<T>& R, uint32_t h, uint32_t j, float inv_unit, bf16x8& lo,
                                            bf16x8& hi) {
@@ -253,6 +274,36 @@ __device__ __forceinline__ void pc_dequant(const PcW<T>& R, uint32_t h, uint32_t
             b[4 * w + 1] = fmaf(sA, h01[1], oA);
             b[4 * w + 2] = fmaf(sA, h23[0], oA);
             b[4 * w + 3] = fmaf(sA, h23[1], oA);
+        }
+    } else if constexpr (T == kQ5_K) {
+        uint32_t sc, m;
+        q4k_sc_m_sel(R.hdr.y, R.hdr.z, R.hdr.w, j, sc, m);
+        const float d1 = h2f(R.hdr.x & 0xFFFFu) * (float)sc, o = -(h2f(R.hdr.x >> 16) * (float)m);
+        // record dword i = 2 h + w: fifth bits at (qh << (4 - i)) and (qh >> i), masked to bit 4
+        // of each byte; the shift by 2 h first (bits 0..1 of qh belong to h = 0 only)
+        const uint32_t hq = R.qh >> (2 * h);
+        const uint32_t Q[2] = {R.q.x, R.q.y};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t lc = and_or_opaque(Q[w], 0x0F0F0F0Fu, (hq << (4 - w)) & 0x10101010u);
+            const uint32_t hc = and_or_opaque(Q[w] >> 4, 0x0F0F0F0Fu, (hq >> w) & 0x10101010u);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[4 * w + k] = fmaf(d1, ubyte(lc, k), o);
+                b[4 * w + k] = fmaf(d1, ubyte(hc, k), o);
+            }
+        }
+    } else if constexpr (T == kIQ4_XS) {
+        const float dl = h2f(R.hdr.x & 0xFFFFu) * (float)iq4xs_ls(R.hdr.x >> 16, R.hdr.y, j), o = -128.0f * dl;
+        const uint32_t Q[2] = {R.q.x, R.q.y};
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t lc = iq4_lookup4(Q[w]), hc = iq4_lookup4(Q[w] >> 4);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[4 * w + k] = fmaf(dl, ubyte(lc, k), o);
+                b[4 * w + k] = fmaf(dl, ubyte(hc, k), o);
+            }
         }
     } else if constexpr (T == kQ8_0) {
         const float d = h2f(R.d), o = -128.0f * d;
@@ -777,6 +828,8 @@ void launch_gemm_lm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStrea
         case kQ4_0: hipLaunchKernelGGL((k_gemm_lm<kQ4_0, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
         case kQ8_0: hipLaunchKernelGGL((k_gemm_lm<kQ8_0, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
         case kQ4_K: hipLaunchKernelGGL((k_gemm_lm<kQ4_K, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_lm<kQ5_K, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_lm<kIQ4_XS, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
         default: hipLaunchKernelGGL((k_gemm_lm<kQ6_K, PAIR, MBW>), grid, dim3(256), 0, st, a); break;
     }
 }
@@ -787,6 +840,8 @@ void launch_gemm_pc_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStrea
         case kQ4_0: hipLaunchKernelGGL((k_gemm_pc<kQ4_0, PAIR, MB>), grid, dim3(512), 0, st, a); break;
         case kQ8_0: hipLaunchKernelGGL((k_gemm_pc<kQ8_0, PAIR, MB>), grid, dim3(512), 0, st, a); break;
         case kQ4_K: hipLaunchKernelGGL((k_gemm_pc<kQ4_K, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_pc<kQ5_K, PAIR, MB>), grid, dim3(512), 0, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_pc<kIQ4_XS, PAIR, MB>), grid, dim3(512), 0, st, a); break;
         default: hipLaunchKernelGGL((k_gemm_pc<kQ6_K, PAIR, MB>), grid, dim3(512), 0, st, a); break;
     }
 }

@@ -102,6 +102,17 @@ struct SlotGroup<kQ6_K> {
     uint32_t d;
 };
 template <>
+struct SlotGroup<kQ5_K> {
+    uint4 q[8];
+    uint32_t qh[8];
+    uint4 hdr;
+};
+template <>
+struct SlotGroup<kIQ4_XS> {
+    uint4 q[8];
+    uint2 hdr;
+};
+template <>
 struct SlotGroup<kQ4_0> {
     uint4 q[8];
     uint32_t d[8];
@@ -136,6 +147,17 @@ __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __res
     // used as soon as its own record has arrived
     if constexpr (T == kQ4_K) {
         G.hdr = ld_nt16(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+    } else if constexpr (T == kQ5_K) {
+        G.hdr = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+            G.qh[j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 4));
+        }
+    } else if constexpr (T == kIQ4_XS) {
+        G.hdr = ld_nt8(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 8);
 #pragma unroll
         for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
     } else if constexpr (T == kQ6_K) {
@@ -682,6 +704,23 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
                 mx_kstep<NV>(A, as_b(ua & 0x00FF00FFu, __builtin_amdgcn_perm(0u, ua, 0x0C030C01u)), j, i, D);
                 mx_kstep<NV>(A, as_b(ub & 0x00FF00FFu, __builtin_amdgcn_perm(0u, ub, 0x0C030C01u)), j, 4 + i, D);
             }
+        } else if constexpr (T == kQ5_K || T == kIQ4_XS) {
+            // byte codes: Q5_K's 5-bit quants (fifth bit from the qh word), IQ4_XS's table
+            // values + 128
+            const uint32_t Q[4] = {G.q[j].x, G.q[j].y, G.q[j].z, G.q[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t lo, hi;
+                if constexpr (T == kQ5_K) {
+                    lo = and_or_opaque(Q[i], 0x0F0F0F0Fu, (G.qh[j] << (4 - i)) & 0x10101010u);
+                    hi = and_or_opaque(Q[i] >> 4, 0x0F0F0F0Fu, (G.qh[j] >> i) & 0x10101010u);
+                } else {
+                    lo = iq4_lookup4(Q[i]);
+                    hi = iq4_lookup4(Q[i] >> 4);
+                }
+                mx_kstep<NV>(A, as_b(lo & 0x00FF00FFu, __builtin_amdgcn_perm(0u, lo, 0x0C030C01u)), j, i, D);
+                mx_kstep<NV>(A, as_b(hi & 0x00FF00FFu, __builtin_amdgcn_perm(0u, hi, 0x0C030C01u)), j, 4 + i, D);
+            }
         } else {  // Q6_K: the two halves have their own scales
             uint32_t lo6[4], hi6[4];
             q6_slot_bytes_gemv(G.ql[j], G.qh[j], lo6, hi6);
@@ -691,7 +730,7 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
                 mx_kstep<NV>(A, as_b(hi6[i] & 0x00FF00FFu, __builtin_amdgcn_perm(0u, hi6[i], 0x0C030C01u)), j, 4 + i, Dh);
             }
         }
-        if constexpr (T == kQ4_K) {
+        if constexpr (T == kQ4_K || T == kQ5_K) {
             uint32_t sc, m;
             q4k_sc_m(G.hdr.y, G.hdr.z, G.hdr.w, (uint32_t)j, sc, m);
             const float fsc = (float)sc, fm = (float)m;
@@ -700,6 +739,11 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
                 sa[v] = fmaf(fsc, mx_dot<NV>(D, v), sa[v]);
                 sb[v] = fmaf(fm, xsum_at(xs[v], 8 * j), sb[v]);
             }
+        } else if constexpr (T == kIQ4_XS) {
+            // dl_j = d (ls_j - 32); the codes carry + 128, taken out with the slot's x sum
+            const float fl = (float)iq4xs_ls(G.hdr.x >> 16, G.hdr.y, (uint32_t)j);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) sa[v] = fmaf(fl, fmaf(-128.0f, xsum_at(xs[v], 8 * j), mx_dot<NV>(D, v)), sa[v]);
         } else if constexpr (T == kQ4_0 || T == kQ8_0) {
             const float d = h2f(G.d[j]);
             constexpr float off = T == kQ4_0 ? -8.0f : -128.0f;
@@ -715,10 +759,14 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
             }
         }
     }
-    if constexpr (T == kQ4_K) {
+    if constexpr (T == kQ4_K || T == kQ5_K) {
         const float d = h2f(G.hdr.x & 0xFFFFu), dmin = h2f(G.hdr.x >> 16);
 #pragma unroll
         for (int v = 0; v < NV; ++v) acc[v] = fmaf(d, sa[v], -(dmin * sb[v]));
+    } else if constexpr (T == kIQ4_XS) {
+        const float d = h2f(G.hdr.x & 0xFFFFu);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = d * sa[v];
     } else if constexpr (T == kQ6_K) {
         const float d = h2f(G.d);
 #pragma unroll
@@ -727,9 +775,11 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
 }
 
 // Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
-// the Q8_0 and Q6_K loops (two register groups); the others run at most 8 waves.
+// the Q8_0, Q6_K and Q5_K loops (two register groups); the others run at most 8 waves.
 template <uint32_t T, int NV, bool ONE>
-constexpr uint32_t mx_max_threads() { return (NV == 1 && (ONE || (T != kQ8_0 && T != kQ6_K))) ? 1024u : 512u; }
+constexpr uint32_t mx_max_threads() {
+    return (NV == 1 && (ONE || (T != kQ8_0 && T != kQ6_K && T != kQ5_K))) ? 1024u : 512u;
+}
 
 // grid, split and LDS as k_gemv_slab, plus one A table per wave after the partials. ONE: every
 // wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
@@ -860,10 +910,12 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
         const char* e = std::getenv("HALO_MI_GEMV_VALU");
         return e && *e == '1';
     }();
-    if (valu) {
-        const size_t lds = (size_t)sp.nw * NV * 64 * sizeof(float);
-        hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
-        return hip_status(hipGetLastError(), "gemv_slab launch");
+    if constexpr (T != kQ5_K && T != kIQ4_XS) {  // the VALU kernel covers the first four formats
+        if (valu) {
+            const size_t lds = (size_t)sp.nw * NV * 64 * sizeof(float);
+            hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
+            return hip_status(hipGetLastError(), "gemv_slab launch");
+        }
     }
     // MFMA kernel. Below 1024 slabs it runs one slot group per wave: enough K chunks that a
     // chunk's groups fit one workgroup (at most 16 waves, 64 KB of LDS with the waves' A tables).
@@ -922,6 +974,8 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
             case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, ws, st); break;
             case kQ8_0: rc = launch_gemv_slab_nv<kQ8_0, PAIR>(c, slabs, ws, st); break;
             case kQ4_K: rc = launch_gemv_slab_nv<kQ4_K, PAIR>(c, slabs, ws, st); break;
+            case kQ5_K: rc = launch_gemv_slab_nv<kQ5_K, PAIR>(c, slabs, ws, st); break;
+            case kIQ4_XS: rc = launch_gemv_slab_nv<kIQ4_XS, PAIR>(c, slabs, ws, st); break;
             default: rc = launch_gemv_slab_nv<kQ6_K, PAIR>(c, slabs, ws, st); break;
         }
         if (rc) return rc;

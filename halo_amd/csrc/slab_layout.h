@@ -1,10 +1,12 @@
 // Block geometry and the SLAB weight layout, shared by the host repack and the device kernels.
 //
 // GGUF block formats (ggml ids; geometry as src/tensor/dtype.cpp:22-34 of the reference):
-//   Q4_0  32 weights / 18 B   { f16 d; u8 qs[16] }
-//   Q8_0  32 weights / 34 B   { f16 d; i8 qs[32] }
-//   Q4_K 256 weights / 144 B  { f16 d; f16 dmin; u8 scales[12]; u8 qs[128] }
-//   Q6_K 256 weights / 210 B  { u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d }
+//   Q4_0    32 weights / 18 B   { f16 d; u8 qs[16] }
+//   Q8_0    32 weights / 34 B   { f16 d; i8 qs[32] }
+//   Q4_K   256 weights / 144 B  { f16 d; f16 dmin; u8 scales[12]; u8 qs[128] }
+//   Q5_K   256 weights / 176 B  { f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128] }
+//   Q6_K   256 weights / 210 B  { u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d }
+//   IQ4_XS 256 weights / 136 B  { f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128] }
 //
 // SLAB layout. Rows are grouped by 64 (one wave64, one row per lane). A row of K weights is
 // cut into S = K / 32 "slots" of 32 consecutive weights. Inside a slab every plane is stored
@@ -20,6 +22,10 @@
 //   Q8_0  [ q  S x 2 x 64 x 16 (the two 16-byte halves of a block, each row-minor) ]
 //         [ d  S x 64 x 2 ]
 //   Q4_K  [ q  S x 64 x 16 ][ hdr  nb x 64 x 16 : the block's bytes 0..15 (d, dmin, scales) ]
+//   Q5_K  [ q  S x 64 x 16 : low 4 bits, as Q4_K ][ qh S x 64 x 4 : top bits, see q5_qh_word() ]
+//         [ hdr nb x 64 x 16 : the block's bytes 0..15 ]
+//   IQ4_XS [ q  S x 64 x 16 : the block's qs (already in slot order) ]
+//          [ hdr nb x 64 x 8 : the block's bytes 0..7 (d, scales_h, scales_l) ]
 //   Q6_K  [ ql S x 64 x 16 : low 4 bits, nibble order as above ]
 //         [ qh S x 64 x 8  : top 2 bits, see q6_qh_byte() ]
 //         [ sc nb x 64 x 16 : the block's int8 scales (bytes 192..207) ]
@@ -38,24 +44,36 @@
 
 namespace halo_mi {
 
-inline constexpr uint32_t kF32 = 0, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
+inline constexpr uint32_t kF32 = 0, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ4_XS = 23;
 inline constexpr uint32_t kSlabRows = 64;
 inline constexpr uint32_t kSlot = 32;  // weights per slot
 
 HALO_HD constexpr uint32_t block_elems(uint32_t t) {
-    return t == kF32 ? 1u : (t == kQ4_0 || t == kQ8_0) ? 32u : (t == kQ4_K || t == kQ6_K) ? 256u : 0u;
+    return t == kF32                                                           ? 1u
+           : (t == kQ4_0 || t == kQ8_0)                                        ? 32u
+           : (t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS) ? 256u
+                                                                               : 0u;
 }
 HALO_HD constexpr uint32_t block_bytes(uint32_t t) {
-    return t == kF32 ? 4u : t == kQ4_0 ? 18u : t == kQ8_0 ? 34u : t == kQ4_K ? 144u : t == kQ6_K ? 210u : 0u;
+    return t == kF32      ? 4u
+           : t == kQ4_0   ? 18u
+           : t == kQ8_0   ? 34u
+           : t == kQ4_K   ? 144u
+           : t == kQ5_K   ? 176u
+           : t == kQ6_K   ? 210u
+           : t == kIQ4_XS ? 136u
+                          : 0u;
 }
-HALO_HD constexpr bool is_quant(uint32_t t) { return t == kQ4_0 || t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
+HALO_HD constexpr bool is_quant(uint32_t t) {
+    return t == kQ4_0 || t == kQ8_0 || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS;
+}
 
 // Byte offsets of the planes inside one slab, for K = cols.
 struct SlabGeom {
     uint64_t slab_bytes;
     uint64_t q_off;    // 4-bit quants (ql for Q6_K), or int8 quants for Q8_0
-    uint64_t aux_off;  // Q4_0/Q8_0: d plane; Q4_K: header plane; Q6_K: qh plane
-    uint64_t sc_off;   // Q6_K scale plane
+    uint64_t aux_off;  // Q4_0/Q8_0: d plane; Q4_K, IQ4_XS: header plane; Q5_K, Q6_K: qh plane
+    uint64_t sc_off;   // Q6_K scale plane; Q5_K header plane
     uint64_t d_off;    // Q6_K d plane
 };
 
@@ -76,11 +94,20 @@ HALO_HD inline SlabGeom slab_geom(uint32_t t, uint32_t cols) {
             g.aux_off = S * 64 * 16;
             g.slab_bytes = nb * 64 * 144;
             break;
+        case kQ5_K:
+            g.aux_off = S * 64 * 16;
+            g.sc_off = g.aux_off + S * 64 * 4;
+            g.slab_bytes = nb * 64 * 176;
+            break;
         case kQ6_K:
             g.aux_off = S * 64 * 16;
             g.sc_off = g.aux_off + S * 64 * 8;
             g.d_off = g.sc_off + nb * 64 * 16;
             g.slab_bytes = nb * 64 * 210;
+            break;
+        case kIQ4_XS:
+            g.aux_off = S * 64 * 16;
+            g.slab_bytes = nb * 64 * 136;
             break;
         default:
             g.slab_bytes = 0;
@@ -111,6 +138,25 @@ HALO_HD inline uint32_t q6_hi2(const uint8_t* blk, uint32_t j, uint32_t t) {
 HALO_HD inline uint8_t q6_qh_byte(const uint32_t* h, uint32_t w, uint32_t b) {
     return static_cast<uint8_t>(h[8 * w + 4 + b] | (h[8 * w + 4 + b + 16] << 2) | (h[8 * w + b] << 4) |
                                 (h[8 * w + b + 16] << 6));
+}
+
+// Q5_K slot record top bits: h[e] (0 or 1) is the fifth bit of slot element e. Bit i + 8 b of
+// the word is element 4 i + b's (i < 4) and bit 4 + i + 8 b is element 16 + 4 i + b's, so that
+// for dword i of the 4-bit record (elements 4 i .. 4 i + 3 in its low nibbles and 16 + 4 i ..
+// in its high nibbles) one shift and the mask 0x10101010 put each bit at bit 4 of its byte:
+//   low  codes: (q & 0x0F0F0F0F) | ((word << (4 - i)) & 0x10101010)
+//   high codes: ((q >> 4) & 0x0F0F0F0F) | ((word >> i) & 0x10101010)
+HALO_HD inline uint32_t q5_qh_word(const uint32_t* h) {
+    uint32_t w = 0;
+    for (uint32_t i = 0; i < 4; ++i)
+        for (uint32_t b = 0; b < 4; ++b)
+            w |= (h[4 * i + b] << (i + 8 * b)) | (h[16 + 4 * i + b] << (4 + i + 8 * b));
+    return w;
+}
+// Its inverse for one element.
+HALO_HD inline uint32_t q5_qh_bit(uint32_t w, uint32_t e) {
+    const uint32_t up = e >> 4, i = (e & 15) >> 2, b = e & 3;
+    return (w >> ((up ? 4 + i : i) + 8 * b)) & 1u;
 }
 
 // Repack GGUF block `blk` (block index `b` of a row) of the row at lane `r` of a slab.
@@ -147,6 +193,36 @@ HALO_HD inline void slab_pack_block(uint32_t t, const uint8_t* blk, uint8_t* sla
             }
             uint8_t* hdr = slab + g.aux_off + ((uint64_t)b * 64 + r) * 16;
             for (int i = 0; i < 16; ++i) hdr[i] = blk[i];
+            break;
+        }
+        case kQ5_K: {
+            // qs group grp (64 elements): low nibbles -> slot 2 grp, high -> slot 2 grp + 1;
+            // qh[l] bit j is the top bit of element l of slot j (quant.cpp:271-299)
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint32_t grp = j / 2, hi = j % 2;
+                uint8_t* q = slab + g.q_off + (((uint64_t)b * 8 + j) * 64 + r) * 16;
+                for (uint32_t i = 0; i < 16; ++i) {
+                    const uint32_t lo = nib(blk[48 + 32 * grp + i], hi);
+                    const uint32_t up = nib(blk[48 + 32 * grp + i + 16], hi);
+                    q[i] = static_cast<uint8_t>(lo | (up << 4));
+                }
+                uint32_t h[32];
+                for (uint32_t e = 0; e < 32; ++e) h[e] = (blk[16 + e] >> j) & 1u;
+                const uint32_t w = q5_qh_word(h);
+                uint8_t* qh = slab + g.aux_off + (((uint64_t)b * 8 + j) * 64 + r) * 4;
+                for (uint32_t k = 0; k < 4; ++k) qh[k] = static_cast<uint8_t>(w >> (8 * k));
+            }
+            uint8_t* hdr = slab + g.sc_off + ((uint64_t)b * 64 + r) * 16;
+            for (int i = 0; i < 16; ++i) hdr[i] = blk[i];
+            break;
+        }
+        case kIQ4_XS: {
+            for (uint32_t j = 0; j < 8; ++j) {
+                uint8_t* q = slab + g.q_off + (((uint64_t)b * 8 + j) * 64 + r) * 16;
+                for (uint32_t i = 0; i < 16; ++i) q[i] = blk[8 + 16 * j + i];
+            }
+            uint8_t* hdr = slab + g.aux_off + ((uint64_t)b * 64 + r) * 8;
+            for (int i = 0; i < 8; ++i) hdr[i] = blk[i];
             break;
         }
         case kQ6_K: {
@@ -206,6 +282,34 @@ HALO_HD inline void slab_unpack_block(uint32_t t, const uint8_t* slab, uint8_t* 
                     blk[16 + 32 * grp + i] = static_cast<uint8_t>((qa[i] & 0x0F) | ((qb[i] & 0x0F) << 4));
                     blk[16 + 32 * grp + i + 16] = static_cast<uint8_t>((qa[i] >> 4) | (qb[i] & 0xF0));
                 }
+            }
+            break;
+        }
+        case kQ5_K: {
+            const uint8_t* hdr = slab + g.sc_off + ((uint64_t)b * 64 + r) * 16;
+            for (int i = 0; i < 16; ++i) blk[i] = hdr[i];
+            for (int i = 16; i < 48; ++i) blk[i] = 0;
+            for (uint32_t grp = 0; grp < 4; ++grp) {
+                const uint8_t* qa = slab + g.q_off + (((uint64_t)b * 8 + 2 * grp) * 64 + r) * 16;
+                const uint8_t* qb = slab + g.q_off + (((uint64_t)b * 8 + 2 * grp + 1) * 64 + r) * 16;
+                for (uint32_t i = 0; i < 16; ++i) {
+                    blk[48 + 32 * grp + i] = static_cast<uint8_t>((qa[i] & 0x0F) | ((qb[i] & 0x0F) << 4));
+                    blk[48 + 32 * grp + i + 16] = static_cast<uint8_t>((qa[i] >> 4) | (qb[i] & 0xF0));
+                }
+            }
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint8_t* qh = slab + g.aux_off + (((uint64_t)b * 8 + j) * 64 + r) * 4;
+                const uint32_t w = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+                for (uint32_t e = 0; e < 32; ++e) blk[16 + e] |= static_cast<uint8_t>(q5_qh_bit(w, e) << j);
+            }
+            break;
+        }
+        case kIQ4_XS: {
+            const uint8_t* hdr = slab + g.aux_off + ((uint64_t)b * 64 + r) * 8;
+            for (int i = 0; i < 8; ++i) blk[i] = hdr[i];
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint8_t* q = slab + g.q_off + (((uint64_t)b * 8 + j) * 64 + r) * 16;
+                for (uint32_t i = 0; i < 16; ++i) blk[8 + 16 * j + i] = q[i];
             }
             break;
         }

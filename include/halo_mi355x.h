@@ -46,7 +46,9 @@ enum {
     HALO_MI_Q4_0 = 2,
     HALO_MI_Q8_0 = 8,
     HALO_MI_Q4_K = 12,
-    HALO_MI_Q6_K = 14
+    HALO_MI_Q5_K = 13,
+    HALO_MI_Q6_K = 14,
+    HALO_MI_IQ4_XS = 23
 };
 
 /* ---- weight layouts ---------------------------------------------------------------------- */
@@ -233,7 +235,7 @@ int halo_mi_upload_slab(uint32_t type, const void* host_src, uint64_t src_stride
 /* ---- synthetic inputs (no reference counterpart: the reference has no quantizer) ----------- */
 /* Portable SplitMix64 + Box-Muller normal fill: out[i] = mean + std * N(0, 1), seed-determined. */
 void halo_mi_fill_normal(uint64_t seed, float* out, uint64_t n, float mean, float std);
-/* fp32 -> GGUF blocks for Q4_0 / Q8_0 / Q4_K / Q6_K; n must be a multiple of the block size.
+/* fp32 -> GGUF blocks for Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_XS; n must be a multiple of the block size.
  * `threads` = 0 uses all host threads. Deterministic for any thread count. */
 int halo_mi_quantize(uint32_t type, const float* src, uint64_t n, void* dst, uint32_t threads);
 

@@ -46,7 +46,7 @@ private:
 
 // ---- types (backend.h:60-314) -------------------------------------------------------------
 
-enum class DType : std::uint32_t { F32 = 0, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+enum class DType : std::uint32_t { F32 = 0, Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ4_XS = 23 };
 enum class Kind : std::uint8_t { Cpu, Hip, HipEmulation, Vulkan };
 enum class Tier : std::uint8_t { Vram, Gtt, Host };
 // How the bytes of a weight buffer are laid out (an addition of this backend).

@@ -16,7 +16,7 @@
 #include <string.h>
 #include <unistd.h>
 
-enum { T_F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
 
 /* ---- fp16 ------------------------------------------------------------------------------ */
 
@@ -53,7 +53,7 @@ uint32_t oracle_block_elems(uint32_t type) {
     switch (type) {
         case T_F32: return 1;
         case T_Q4_0: case T_Q8_0: return 32;
-        case T_Q4_K: case T_Q6_K: return 256;
+        case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: return 256;
         default: return 0;
     }
 }
@@ -64,7 +64,9 @@ uint32_t oracle_block_bytes(uint32_t type) {
         case T_Q4_0: return 18;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
+        case T_Q5_K: return 176;
         case T_Q6_K: return 210;
+        case T_IQ4_XS: return 136;
         default: return 0;
     }
 }
@@ -135,6 +137,57 @@ static void deq_q4_k(const uint8_t* blk, float* y, float* a, float* b) {
     }
 }
 
+/* quant.cpp:271-299. As Q4_K (the quants start at byte 48), with a fifth bit: bit 2g + hi of
+ * qh[l] (qh holds 32 bytes and is not advanced per group, only the tested bit moves). value
+ * (d * sc) * q - dmin * m. */
+static void deq_q5_k(const uint8_t* blk, float* y, float* a, float* b) {
+    const float d = f16_at(blk);
+    const float dmin = f16_at(blk + 2);
+    const uint8_t* scales = blk + 4;
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    for (int e = 0; e < 256; ++e) {
+        const int g = e / 64, hi = (e % 64) / 32, l = e % 32, j = 2 * g + hi;
+        int sc, m;
+        k4_scale_min(scales, j, &sc, &m);
+        const float d1 = d * (float)sc;
+        const float m1 = dmin * (float)m;
+        const uint8_t byte = qs[32 * g + l];
+        const int q = (hi ? (byte >> 4) : (byte & 0x0F)) + (((qh[l] >> j) & 1) ? 16 : 0);
+        const float t = d1 * (float)q;
+        if (y) y[e] = t - m1;
+        if (a) { a[e] = t; b[e] = m1; }
+    }
+}
+
+/* The IQ4_NL value table of the GGUF format (ggml's kvalues_iq4nl; the reference's copy is
+ * src/tensor/ggml_tables.h:94-96). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* quant.cpp:330-347. Sub-block ib of 32: 6-bit scale ls = (nibble ib of scales_l) | (bits
+ * 2ib..2ib+1 of scales_h) << 4, multiplier dl = d * fl(ls - 32); element j < 16 is the low
+ * nibble of qs[16 ib + j], j + 16 the high one, value dl * fl(table[nibble]). */
+static void deq_iq4_xs(const uint8_t* blk, float* y, float* a, float* off) {
+    const float d = f16_at(blk);
+    const unsigned sh = (unsigned)blk[2] | ((unsigned)blk[3] << 8);
+    const uint8_t* sl = blk + 4;
+    const uint8_t* qs = blk + 8;
+    for (int ib = 0; ib < 8; ++ib) {
+        const int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0x0F) | (int)(((sh >> (2 * ib)) & 3u) << 4);
+        const float dl = d * (float)(ls - 32);
+        for (int j = 0; j < 16; ++j) {
+            const uint8_t byte = qs[16 * ib + j];
+            const float lo = dl * (float)kIq4nl[byte & 0x0F], hi = dl * (float)kIq4nl[byte >> 4];
+            if (y) { y[32 * ib + j] = lo; y[32 * ib + j + 16] = hi; }
+            if (a) {
+                a[32 * ib + j] = lo;
+                a[32 * ib + j + 16] = hi;
+                off[32 * ib + j] = off[32 * ib + j + 16] = 128.0f * dl;
+            }
+        }
+    }
+}
+
 /* quant.cpp:302-327. Element e: half n = e / 128; r = e % 128; quarter k = r / 32; l = r % 32.
  * Low 4 bits: ql[64n + l + 32 (k & 1)], low nibble for k < 2 else high; top 2 bits: bits
  * 2k..2k+1 of qh[32n + l]; scale: int8 sc[8n + l / 16 + 2k]; value (d * sc) * (q - 32). */
@@ -166,7 +219,9 @@ static int dequant_blocks(uint32_t type, const uint8_t* src, float* dst, uint64_
             case T_Q4_0: deq_q4_0(blk, y); break;
             case T_Q8_0: deq_q8_0(blk, y); break;
             case T_Q4_K: deq_q4_k(blk, y, NULL, NULL); break;
+            case T_Q5_K: deq_q5_k(blk, y, NULL, NULL); break;
             case T_Q6_K: deq_q6_k(blk, y, NULL, NULL); break;
+            case T_IQ4_XS: deq_iq4_xs(blk, y, NULL, NULL); break;
             default: return ORACLE_EUNSUPPORTED;
         }
     }
@@ -200,13 +255,22 @@ int oracle_dequant_terms(uint32_t type, const uint8_t* src, float* a, float* b, 
                 break;
             }
             case T_Q8_0: {
+                const float d = f16_at(blk);
                 deq_q8_0(blk, ab);
-                for (uint32_t e = 0; e < be; ++e) { bbv[e] = 0.0f; ob[e] = 0.0f; }
+                for (uint32_t e = 0; e < be; ++e) { bbv[e] = 0.0f; ob[e] = 128.0f * d; }
                 break;
             }
             case T_Q4_K:
                 deq_q4_k(blk, NULL, ab, bbv);
                 for (uint32_t e = 0; e < be; ++e) ob[e] = 0.0f;
+                break;
+            case T_Q5_K:
+                deq_q5_k(blk, NULL, ab, bbv);
+                for (uint32_t e = 0; e < be; ++e) ob[e] = 0.0f;
+                break;
+            case T_IQ4_XS:
+                deq_iq4_xs(blk, NULL, ab, ob);
+                for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
                 break;
             case T_Q6_K:
                 deq_q6_k(blk, NULL, ab, ob);

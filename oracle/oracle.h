@@ -11,7 +11,8 @@
  * CMakeLists.txt:24-29).
  *
  * Type ids are ggml's (include/halo/tensor/dtype.h:18-49): Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
- * Q6_K = 14. F32 = 0 is accepted by the matmul (dense rows read in place).
+ * Q5_K = 13, Q6_K = 14, IQ4_XS = 23. F32 = 0 is accepted by the matmul (dense rows read in
+ * place).
  *
  * Return codes: 0 = ok, ORACLE_EMODEL (1) = bad element count / byte size (the reference's
  * Error(Model), quant.cpp:411-428), ORACLE_EUNSUPPORTED (2) = type not on this path
@@ -47,11 +48,14 @@ int oracle_dequantize_row(uint32_t type, const uint8_t* src, float* dst, int64_t
  * Test helper (no reference counterpart): splits every dequantized weight into the two
  * exactly-representable terms the reference expression subtracts, w = fl(a - b):
  *   Q4_K  a = (d*sc)*q,       b = dmin*m                     (quant.cpp:258-265)
+ *   Q5_K  a = (d*sc)*q,       b = dmin*m                     (quant.cpp:289-290)
  *   Q6_K  a = (d*sc)*(q-32),  b = 0                          (quant.cpp:318-321)
  *   Q4_0  a = (q-8)*d,        b = 0                          (quant.cpp:84-87)
  *   Q8_0  a = q*d,            b = 0                          (quant.cpp:147-148)
- * and also returns the "factored" magnitude terms the GPU kernels sum: for Q4_0 / Q6_K the
- * offset part (8*d, 32*d*sc) in off[], else 0. Used to size summation-error bounds.
+ *   IQ4_XS a = dl*table[q],   b = 0                          (quant.cpp:340-341)
+ * and also returns the "factored" magnitude terms the GPU kernels sum: the offset they take
+ * out of the quant, in off[] (Q4_0 8*d, Q6_K 32*d*sc, Q8_0 128*d, IQ4_XS 128*dl), else 0.
+ * Used to size summation-error bounds.
  */
 int oracle_dequant_terms(uint32_t type, const uint8_t* src, float* a, float* b, float* off, int64_t n);
 

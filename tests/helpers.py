@@ -5,10 +5,11 @@ import math
 
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, Q6_K, F32 = 2, 8, 12, 14, 0
-QUANT_TYPES = (Q4_K, Q6_K, Q8_0, Q4_0)
-NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
-BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, F32 = 2, 8, 12, 13, 14, 23, 0
+QUANT_TYPES = (Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, IQ4_XS)
+NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
+BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
+         IQ4_XS: (256, 136)}
 U = 2.0 ** -24  # fp32 unit roundoff
 
 
@@ -44,11 +45,13 @@ def make_weights(t: int, rows: int, cols: int, seed: int, stride_pad: int = 0, o
             sc = 2e-6 if b == 0 else rng.uniform(-0.05, 0.05)
             if t in (Q4_0, Q8_0):
                 _put16(buf, row + bb * b, sc)
-            elif t == Q4_K:
+            elif t in (Q4_K, Q5_K):
                 _put16(buf, row + bb * b, 4e-6 if b == 0 else sc)
                 _put16(buf, row + bb * b + 2, abs(rng.uniform(-0.05, 0.05)))
             elif t == Q6_K:
                 _put16(buf, row + bb * b + 208, 1e-6 if b == 0 else sc)
+            elif t == IQ4_XS:
+                _put16(buf, row + bb * b, 3e-6 if b == 0 else sc)
     return buf, stride
 
 

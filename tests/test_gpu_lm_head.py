@@ -13,7 +13,7 @@ import struct
 import numpy as np
 import pytest
 
-from helpers import F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, gemm_tol, make_weights, row_bytes, slab_gemv_tol, synth_matrix
+from helpers import F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, gemm_tol, make_weights, row_bytes, slab_gemv_tol, synth_matrix
 from test_gpu_parity import dense_of, host, say, slab_of, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +48,7 @@ def first_max(row, limit=None):
     return int(np.argmax(r)), _bits(r.max())
 
 
-@pytest.mark.parametrize("t", (Q4_K, Q6_K, Q4_0, Q8_0))
+@pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("variant", [0, 2, 3, 5])
 def test_lm_head_matches_its_logits_and_the_cpu(hl, oracle, dev, t, variant):
     rows, cols, n_vec = 1000, 512, 3

@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import (F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
+from helpers import (BLOCK, F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
                      gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 
 pytestmark = pytest.mark.gpu
@@ -105,7 +105,7 @@ def test_dequant_gguf_and_slab_bitwise(hl, oracle, dev, t, case):
 def test_repack_device_equals_host_and_unpacks(hl, dev, t, pad, off):
     import torch
 
-    rows, cols = 70, 768 if t in (Q4_K, Q6_K) else 544
+    rows, cols = 70, 768 if BLOCK[t][0] == 256 else 544
     say("repack", NAMES[t], rows, cols, pad, off)
     buf, stride = make_weights(t, rows, cols, seed=5 + t, stride_pad=pad, offset=off)
     dense = dense_of(buf, t, rows, cols, stride, off)
@@ -285,7 +285,7 @@ def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
 # ---- fused gate/up + SwiGLU ---------------------------------------------------------------
 
 
-@pytest.mark.parametrize("t", (Q4_K, Q6_K, Q4_0, Q8_0))
+@pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3), (300, 3), (17, 5), (300, 5),
                                            (600, 5)])
 def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):

@@ -7,7 +7,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import BLOCK, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, make_weights, row_bytes
+from helpers import BLOCK, IQ4_XS, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, make_weights, row_bytes
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -37,7 +37,9 @@ def test_geometry(hl):
     assert hl.row_bytes(Q4_K, 100) == 0
     assert hl.slab_bytes(Q4_K, 17408, 5120) == 17408 * 2880
     assert hl.slab_bytes(Q6_K, 65, 512) == 128 * 2 * 210  # rows rounded up to 64
-    assert hl.slab_bytes(13, 64, 256) == 0  # Q5_K: not on this path
+    assert hl.slab_bytes(Q5_K, 65, 512) == 128 * 2 * 176
+    assert hl.slab_bytes(IQ4_XS, 64, 256) == 64 * 136
+    assert hl.slab_bytes(11, 64, 256) == 0  # Q3_K: not on this path
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
@@ -118,6 +120,50 @@ def test_slab_byte_placement_q6_k(hl):
         assert np.array_equal(sc, blk[192:208]) and np.array_equal(d, blk[208:210])
 
 
+def test_slab_byte_placement_q5_k(hl):
+    """Q5_K: 4-bit records as Q4_K (quants at byte 48), a 4-byte word per (slot, row) holding
+    the fifth bits (element e's at bit i + 8 b for e = 4 i + b < 16, at bit 4 + i + 8 b for
+    e = 16 + 4 i + b), then the 16 header bytes per (block, row)."""
+    rows, cols = 3, 512
+    rng = np.random.default_rng(3)
+    w = rng.integers(0, 256, size=rows * row_bytes(Q5_K, cols), dtype=np.uint8)
+    slab = hl.repack_slab_host(Q5_K, w, rows, cols)
+    nb, S = cols // 256, cols // 32
+    for r in range(rows):
+        for b in range(nb):
+            blk = w[r * 352 + b * 176: r * 352 + (b + 1) * 176]
+            hdr = slab[S * 64 * 16 + S * 64 * 4 + (b * 64 + r) * 16:][:16]
+            assert np.array_equal(hdr, blk[:16])
+            for j in range(8):
+                g, hi = j // 2, j % 2
+                q = blk[48 + 32 * g: 48 + 32 * g + 32]
+                vals = (q >> 4) if hi else (q & 15)
+                top = (blk[16:48] >> j) & 1  # fifth bit of element l of sub-block j
+                rec = slab[((8 * b + j) * 64 + r) * 16:][:16]
+                assert np.array_equal(rec & 15, vals[:16]) and np.array_equal(rec >> 4, vals[16:])
+                word = int.from_bytes(slab[S * 64 * 16 + ((8 * b + j) * 64 + r) * 4:][:4].tobytes(), "little")
+                for e in range(32):
+                    i, bb = (e % 16) // 4, e % 4
+                    bit = (i if e < 16 else 4 + i) + 8 * bb
+                    assert (word >> bit) & 1 == top[e], (r, b, j, e)
+
+
+def test_slab_byte_placement_iq4_xs(hl):
+    """IQ4_XS: the block's 16-byte sub-block records are already slot records (element t low,
+    t + 16 high); the 8 header bytes (d, scales_h, scales_l) per (block, row) follow."""
+    rows, cols = 2, 512
+    rng = np.random.default_rng(4)
+    w = rng.integers(0, 256, size=rows * row_bytes(IQ4_XS, cols), dtype=np.uint8)
+    slab = hl.repack_slab_host(IQ4_XS, w, rows, cols)
+    nb, S = cols // 256, cols // 32
+    for r in range(rows):
+        for b in range(nb):
+            blk = w[r * 272 + b * 136: r * 272 + (b + 1) * 136]
+            assert np.array_equal(slab[S * 64 * 16 + (b * 64 + r) * 8:][:8], blk[:8])
+            for j in range(8):
+                assert np.array_equal(slab[((8 * b + j) * 64 + r) * 16:][:16], blk[8 + 16 * j: 24 + 16 * j])
+
+
 def test_fill_normal_deterministic_and_normal(hl):
     a = hl.fill_normal(0, 1_000_001)
     b = hl.fill_normal(0, 1_000_001)
@@ -144,14 +190,15 @@ def test_quantizer_round_trip_and_determinism(hl, oracle, t):
     assert np.all(np.isfinite(y))
     err = y.astype(np.float64) - x
     rel_rms = float(np.sqrt(np.mean(err ** 2)) / np.std(x))
-    limit = {Q8_0: 0.01, Q6_K: 0.04, Q4_K: 0.12, Q4_0: 0.15}[t]
+    limit = {Q8_0: 0.01, Q6_K: 0.04, Q5_K: 0.06, Q4_K: 0.12, IQ4_XS: 0.12, Q4_0: 0.15}[t]
     assert rel_rms < limit, rel_rms
 
 
 def test_quantizer_rejects(hl):
-    with pytest.raises(hl.HaloError) as e:
-        hl.quantize(13, np.zeros(256, np.float32))
-    assert e.value.code == hl.ErrorCode.Unsupported
+    for t in (11, 16):  # Q3_K, IQ2_XXS: formats the quantizer does not write
+        with pytest.raises(hl.HaloError) as e:
+            hl.quantize(t, np.zeros(256, np.float32))
+        assert e.value.code == hl.ErrorCode.Unsupported
     with pytest.raises(hl.HaloError) as e:
         hl.quantize(Q4_K, np.zeros(100, np.float32))
     assert e.value.code == hl.ErrorCode.Kernel
@@ -159,7 +206,7 @@ def test_quantizer_rejects(hl):
 
 def test_host_repack_rejects(hl):
     with pytest.raises(hl.HaloError) as e:
-        hl.repack_slab_host(13, np.zeros(176, np.uint8), 1, 256)
+        hl.repack_slab_host(11, np.zeros(110, np.uint8), 1, 256)  # Q3_K
     assert e.value.code == hl.ErrorCode.Unsupported
     with pytest.raises(hl.HaloError) as e:
         hl.repack_slab_host(Q4_K, np.zeros(144, np.uint8), 1, 100)

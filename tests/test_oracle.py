@@ -4,13 +4,15 @@ Every check here is independent of the oracle's own formulas: known-answer block
 reference's tests, literal decodings of the block formats, a library routine (numpy's fp16
 widening), closed forms, brute force in fp64, and invariants of cpu::matmul.
 """
+import json
 import math
 import struct
+from pathlib import Path
 
 import numpy as np
 import pytest
 
-from helpers import F32, Q4_0, Q4_K, Q6_K, Q8_0, U, depth_cpu
+from helpers import F32, IQ4_XS, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, U, depth_cpu
 
 
 def f16_bytes(v: float) -> bytes:
@@ -187,6 +189,109 @@ def test_q6_k_negative_scale_and_fp16_subnormal_d(oracle):
     sc = bytes([0x80] * 16)  # int8 -128
     y = oracle.dequantize_row(Q6_K, q6k_block(bytes([0xFF] * 128), bytes([0xFF] * 64), sc, d), 256)
     assert np.all(y == np.float32(d * -128 * 31))
+
+
+def q5k_block(d: float, dmin: float, scales: bytes, qh: bytes, qs: bytes) -> np.ndarray:
+    assert len(scales) == 12 and len(qh) == 32 and len(qs) == 128
+    return np.frombuffer(f16_bytes(d) + f16_bytes(dmin) + scales + qh + qs, np.uint8)
+
+
+def test_q5_k_geometry(oracle):
+    """block_q5_K {f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]} = 176 bytes per 256."""
+    assert oracle.row_bytes(Q5_K, 5120) == 20 * (2 + 2 + 12 + 32 + 128)
+    assert oracle.row_bytes(IQ4_XS, 5120) == 20 * (2 + 2 + 4 + 128)
+
+
+def test_q5_k_literal_scale_min_table_without_high_bits(oracle):
+    """qh = 0: Q5_K is Q4_K with its quants 48 bytes in (same 12-byte scales field)."""
+    qs = bytes(((15 - l % 16) << 4) | (l % 16) for g in range(4) for l in range(32))
+    y = oracle.dequantize_row(Q5_K, q5k_block(1.0, 0.5, Q4K_SCALES, bytes(32), qs), 256)
+    for e in range(256):
+        g, hi, l = e // 64, (e % 64) // 32, e % 32
+        sc, m = Q4K_SC_M[2 * g + hi]
+        q = (15 - l % 16) if hi else (l % 16)
+        assert y[e] == np.float32(sc * q - 0.5 * m), e
+
+
+@pytest.mark.parametrize("bit", range(8))
+def test_q5_k_high_bit_selects_one_subblock(oracle, bit):
+    """Only bit `bit` of every qh byte set, all nibbles 0, d = 1, dmin = 0, every sc = 1: the
+    32 elements of sub-block `bit` (group bit // 2, nibble half bit % 2) are 16, the rest 0."""
+    ones = bytes([1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1])  # sc[0..7] = 1, m[0..7] = 0
+    y = oracle.dequantize_row(Q5_K, q5k_block(1.0, 0.0, ones, bytes([1 << bit] * 32), bytes(128)), 256)
+    exp = np.zeros(256, np.float32)
+    exp[32 * bit: 32 * bit + 32] = 16.0
+    assert np.array_equal(y, exp)
+
+
+def test_q5_k_high_bit_per_lane(oracle):
+    """qh[l] = 0xFF for even l only, all nibbles 15, sc = 1, m = 1, d = 2, dmin = 0.25: element
+    (sub-block j, lane l) is 2 (15 + 16 [l even]) - 0.25."""
+    ones = bytes([1, 1, 1, 1, 1, 1, 1, 1, 0x11, 0x11, 0x11, 0x11])
+    qh = bytes(0xFF if l % 2 == 0 else 0 for l in range(32))
+    y = oracle.dequantize_row(Q5_K, q5k_block(2.0, 0.25, ones, qh, bytes([0xFF] * 128)), 256)
+    for e in range(256):
+        l = e % 32
+        assert y[e] == np.float32(2 * (15 + (16 if l % 2 == 0 else 0)) - 0.25), e
+
+
+IQ4NL = json.loads((Path(__file__).resolve().parent / "golden" / "iq4nl_table.json").read_text())["kvalues_iq4nl"]
+
+
+def iq4xs_block(d: float, scales_h: int, scales_l: bytes, qs: bytes) -> np.ndarray:
+    assert len(scales_l) == 4 and len(qs) == 128
+    return np.frombuffer(f16_bytes(d) + struct.pack("<H", scales_h) + scales_l + qs, np.uint8)
+
+
+def test_iq4_xs_table_and_nibble_order(oracle):
+    """ls = 33 everywhere (low nibble 1, high bits 2 -> 1 + 32), d = 1: dl = 1, element j of a
+    sub-block is table[low nibble of qs[j]], element j + 16 table[high nibble]; the table is the
+    reference's kvalues_iq4nl (golden fixture)."""
+    qs = bytes(((15 - j) << 4) | j for ib in range(8) for j in range(16))
+    y = oracle.dequantize_row(IQ4_XS, iq4xs_block(1.0, 0xAAAA, bytes([0x11] * 4), qs), 256)
+    for ib in range(8):
+        for j in range(16):
+            assert y[32 * ib + j] == IQ4NL[j]
+            assert y[32 * ib + j + 16] == IQ4NL[15 - j]
+
+
+def test_iq4_xs_six_bit_scales(oracle):
+    """Sub-block ib has ls = (nibble ib of scales_l) | (bits 2ib..2ib+1 of scales_h) << 4 and
+    multiplier d (ls - 32); every code 8 (table value 1): element value d (ls - 32)."""
+    ls = [0, 63, 32, 17, 48, 5, 60, 33]
+    sl = bytes((ls[2 * i] & 15) | ((ls[2 * i + 1] & 15) << 4) for i in range(4))
+    sh = sum((v >> 4) << (2 * ib) for ib, v in enumerate(ls))
+    y = oracle.dequantize_row(IQ4_XS, iq4xs_block(0.5, sh, sl, bytes([0x88] * 128)), 256)
+    for ib in range(8):
+        assert np.all(y[32 * ib: 32 * ib + 32] == np.float32(0.5 * (ls[ib] - 32) * IQ4NL[8])), ib
+
+
+def test_q5_k_and_iq4_xs_dequant_terms(oracle):
+    """a - b reproduces the dequantized weight bit for bit; Q5_K has no offset (its codes are
+    non-negative), IQ4_XS's is 128 dl with dl the sub-block multiplier d (ls - 32)."""
+    rng = np.random.default_rng(5)
+    for t, bb in ((Q5_K, 176), (IQ4_XS, 136)):
+        w = rng.integers(0, 256, size=4 * bb, dtype=np.uint8)
+        for b in range(4):
+            w[bb * b: bb * b + 2] = np.frombuffer(f16_bytes(rng.uniform(-0.05, 0.05)), np.uint8)
+            if t == Q5_K:
+                w[bb * b + 2: bb * b + 4] = np.frombuffer(f16_bytes(rng.uniform(0, 0.05)), np.uint8)
+        a, b_, off = oracle.dequant_terms(t, w, 1, 1024)
+        y = oracle.dequantize_row(t, w, 1024)
+        assert np.array_equal((a - b_).astype(np.float32)[0], y)
+        if t == Q5_K:
+            assert np.all(off == 0)
+            continue
+        assert np.all(b_ == 0)
+        for b in range(4):
+            blk = w[bb * b: bb * (b + 1)]
+            d = np.float32(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+            sh = int(blk[2]) | int(blk[3]) << 8
+            for ib in range(8):
+                ls = ((int(blk[4 + ib // 2]) >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+                dl = np.float32(d * np.float32(ls - 32))
+                seg = slice(256 * b + 32 * ib, 256 * b + 32 * ib + 32)
+                assert np.all(off[0, seg] == np.float32(128) * dl)
 
 
 def test_dequant_rejects_bad_arguments(oracle):
