@@ -97,18 +97,19 @@ def time_per_launch(torch, launch, n_copies, iters):
     return ts[len(ts) // 2], sum(ts) / len(ts)
 
 
-def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0):
+def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0, norm=False):
     wq = make_weights(hl, t, rows, cols, seed, outliers)
     copies = device_copies(hl, torch, t, wq, rows, cols)
     x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
     y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+    nw = torch.from_numpy(hl.fill_normal(seed + 2000, cols, 1.0, 0.1)).to("cuda") if norm else None
 
     def launch(i):
-        hl.gemv(t, copies[i], x, y, rows, cols, m)
+        hl.gemv(t, copies[i], x, y, rows, cols, m, norm_w=nw)
 
     ms, n = time_graph(torch, launch, len(copies), steps, warmup)
     med, mean = time_per_launch(torch, launch, len(copies), 200)
-    algo = len(wq) + 4 * m * cols + 4 * m * rows
+    algo = len(wq) + 4 * m * cols + 4 * m * rows + (4 * cols if norm else 0)
     del copies
     torch.cuda.empty_cache()
     return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9,
@@ -165,6 +166,7 @@ WORKLOADS = {
     "q4k_gate_up_swiglu_m8": ("gemm", "Q4_K", 17408, 5120, 8, 4),
     "q4k_gate_up_swiglu_m64": ("gemm", "Q4_K", 17408, 5120, 64, 4),
     "q4k_gate_up_swiglu_m512": ("gemm", "Q4_K", 17408, 5120, 512, 4),
+    "q4k_gemv_norm_17408x5120_m1": ("gemv_norm", "Q4_K", 17408, 5120, 1, 2),
     "q5k_gemv_17408x5120_m1": ("gemv", "Q5_K", 17408, 5120, 1, 6),
     "iq4xs_gemv_17408x5120_m1": ("gemv", "IQ4_XS", 17408, 5120, 1, 7),
     "q5k_gate_up_swiglu_m512": ("gemm", "Q5_K", 17408, 5120, 512, 6),
@@ -341,8 +343,8 @@ def main() -> int:
             r = lm_head_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup, outliers=0.01)
             print(json.dumps({"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}), flush=True)
             return 0
-        if kind == "gemv":
-            r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
+        if kind in ("gemv", "gemv_norm"):
+            r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup, norm=kind == "gemv_norm")
             out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
         else:
             r = gemm_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
@@ -359,6 +361,10 @@ def main() -> int:
     traffic = measured_traffic()
     extra = {}
     if not args.no_extra:
+        log("config 2 with the fused RMS-norm prologue (norm_w): Q4_K GEMV M=1")
+        r = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps // 2, args.warmup, norm=True)
+        extra["q4k_gemv_norm_17408x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("config 2: Q4_K GEMV M=4")
         r = gemv_case(hl, torch, Q4_K, 17408, 5120, 4, 2, args.steps // 2, args.warmup)
         extra["q4k_gemv_17408x5120_m4"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}

@@ -17,17 +17,20 @@ from ._lib import (  # noqa: F401
     Variant,
     ARGMAX_RESULT_BYTES,
     SLAB_ROWS,
+    STATUS_BAD_INDEX,
     block_bytes,
     block_elems,
     dequant_rows,
     fill_normal,
     gate_up_swiglu,
     gemv,
+    get_rows,
     lib,
     lm_head,
     quantize,
     repack_slab,
     repack_slab_host,
+    rms_norm,
     row_bytes,
     slab_bytes,
     swiglu,

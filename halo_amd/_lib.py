@@ -87,6 +87,8 @@ class _GemvParams(ctypes.Structure):
         ("cols", ctypes.c_uint32),
         ("n_vec", ctypes.c_uint32),
         ("variant", ctypes.c_uint32),
+        ("norm_w", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
     ]
 
 
@@ -104,6 +106,8 @@ class _GateUpParams(ctypes.Structure):
         ("cols", ctypes.c_uint32),
         ("n_vec", ctypes.c_uint32),
         ("variant", ctypes.c_uint32),
+        ("norm_w", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
     ]
 
 
@@ -119,7 +123,24 @@ class _LmHeadParams(ctypes.Structure):
     ]
 
 
+class _GetRowsParams(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("layout", ctypes.c_uint32),
+        ("table", ctypes.c_void_p),
+        ("table_stride", ctypes.c_uint64),
+        ("n_rows", ctypes.c_uint32),
+        ("cols", ctypes.c_uint32),
+        ("ids", ctypes.c_void_p),
+        ("n_ids", ctypes.c_uint32),
+        ("out", ctypes.c_void_p),
+        ("out_stride", ctypes.c_uint64),
+        ("status", ctypes.c_void_p),
+    ]
+
+
 ARGMAX_RESULT_BYTES = 12  # HALO_MI_ARGMAX_RESULT_BYTES: {index, value bits, poisoned} per vector
+STATUS_BAD_INDEX = 8  # HALO_MI_STATUS_BAD_INDEX: a GET_ROWS id outside the table
 
 
 # Every symbol include/halo_mi355x.h declares, with its ctypes signature.
@@ -131,6 +152,8 @@ SIGNATURES = {
     "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
     "halo_mi_swiglu": (_INT, [_VP, _U64, _VP, _U64, _VP, _U64, _U32, _U32, _VP]),
     "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
+    "halo_mi_get_rows": (_INT, [ctypes.POINTER(_GetRowsParams), _VP]),
+    "halo_mi_rms_norm": (_INT, [_VP, _U64, _VP, _VP, _U64, _U32, _U32, ctypes.c_float, _VP]),
     "halo_mi_row_bytes": (_U64, [_U32, _U32]),
     "halo_mi_slab_bytes": (_U64, [_U32, _U32, _U32]),
     "halo_mi_repack_slab": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP, _VP]),
@@ -253,26 +276,30 @@ def unpack_slab_host(t: int, src, rows: int, cols: int):
 
 
 def gemv(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB, w_stride: int = 0,
-         x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+         x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, norm_w=None, norm_eps: float = 1e-6,
+         stream=None) -> None:
+    """y = W x (halo_mi_gemv); with norm_w, y = W (rms_norm(x) * norm_w), eps = norm_eps."""
     p = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(y), int(y_stride),
-                    int(rows), int(cols), int(n_vec), int(variant))
+                    int(rows), int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
     _check(lib().halo_mi_gemv(ctypes.byref(p), _stream(stream)))
 
 
 def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB,
-                   x_stride: int = 0, out_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+                   x_stride: int = 0, out_stride: int = 0, variant: int = Variant.DEFAULT, norm_w=None,
+                   norm_eps: float = 1e-6, stream=None) -> None:
     p = _GateUpParams(int(t), int(layout), _ptr(w_gate), _ptr(w_up), _ptr(x), int(x_stride), _ptr(out), int(out_stride),
-                      int(rows), int(cols), int(n_vec), int(variant))
+                      int(rows), int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
     _check(lib().halo_mi_gate_up_swiglu(ctypes.byref(p), _stream(stream)))
 
 
 def lm_head(t: int, w, x, result, rows: int, cols: int, n_vec: int, *, logits=None, valid_rows: int = 0, ids=None,
             ids_slots=None, ids_scatter=None, ids_scatter_len: int = 0, layout: int = Layout.SLAB, w_stride: int = 0,
-            x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, stream=None) -> None:
+            x_stride: int = 0, y_stride: int = 0, variant: int = Variant.DEFAULT, norm_w=None, norm_eps: float = 1e-6,
+            stream=None) -> None:
     """The gemv over the vocabulary and the fused argmax (halo_mi_lm_head): result receives
     n_vec triples {index, value bits, poisoned} as uint32; logits (optional) every row."""
     g = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(logits), int(y_stride),
-                    int(rows), int(cols), int(n_vec), int(variant))
+                    int(rows), int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
     p = _LmHeadParams(g, _ptr(result), int(valid_rows), _ptr(ids), _ptr(ids_slots), _ptr(ids_scatter),
                       int(ids_scatter_len))
     _check(lib().halo_mi_lm_head(ctypes.byref(p), _stream(stream)))
@@ -289,6 +316,21 @@ def dequant_rows(t: int, layout: int, w, rows: int, cols: int, out, *, first_row
     n = rows - first_row if n_rows is None else n_rows
     _check(lib().halo_mi_dequant_rows(int(t), int(layout), _ptr(w), int(w_stride), int(rows), int(cols), int(first_row),
                                       int(n), _ptr(out), int(out_stride), _stream(stream)))
+
+
+def get_rows(t: int, layout: int, table, n_rows: int, cols: int, ids, n_ids: int, out, *, table_stride: int = 0,
+             out_stride: int = 0, status=None, stream=None) -> None:
+    """GET_ROWS (halo_mi_get_rows): out[i] = dequant(table row ids[i]); ids int32 on the device."""
+    p = _GetRowsParams(int(t), int(layout), _ptr(table), int(table_stride), int(n_rows), int(cols), _ptr(ids), int(n_ids),
+                       _ptr(out), int(out_stride), _ptr(status))
+    _check(lib().halo_mi_get_rows(ctypes.byref(p), _stream(stream)))
+
+
+def rms_norm(x, w, out, rows: int, cols: int, *, eps: float = 1e-6, x_stride: int = 0, out_stride: int = 0,
+             stream=None) -> None:
+    """RMS_NORM (halo_mi_rms_norm), bitwise cpu::rms_norm."""
+    _check(lib().halo_mi_rms_norm(_ptr(x), int(x_stride), _ptr(w), _ptr(out), int(out_stride), int(rows), int(cols),
+                                  float(eps), _stream(stream)))
 
 
 def repack_slab(t: int, src, rows: int, cols: int, dst, *, src_stride: int = 0, stream=None) -> None:

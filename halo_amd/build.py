@@ -2,6 +2,8 @@
 
 The library is compiled with hipcc for gfx950 only. Flags:
   -fno-gpu-flush-denormals-to-zero   fp16/fp32 subnormal scales must survive (bit-exact dequant)
+  -fhip-fp32-correctly-rounded-divide-sqrt   fp32 / and sqrtf correctly rounded (the RMS norm is
+                                     bitwise the CPU's); clang's default for HIP, stated here
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
   -mcode-object-version=5            loadable by the HIP runtime torch bundles (ROCm 7.0) as well
                                      as /opt/rocm's (7.2)
@@ -19,7 +21,8 @@ ROOT = PKG.parent
 LIB = PKG / "libhalo_mi355x.so"
 CSRC = PKG / "csrc"
 # the kernel files first: they take longest and are compiled in parallel with the rest
-SOURCES = [CSRC / "k_gemv.hip", CSRC / "k_gemm.hip", CSRC / "k_dequant.hip", CSRC / "k_argmax.hip", CSRC / "api.cpp",
+SOURCES = [CSRC / "k_gemv.hip", CSRC / "k_gemm.hip", CSRC / "k_dequant.hip", CSRC / "k_argmax.hip", CSRC / "k_norm.hip",
+           CSRC / "api.cpp",
            CSRC / "host_utils.cpp", CSRC / "backend.cpp"]
 OBJ_DIR = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -31,6 +34,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-pthread",
     "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",

@@ -72,6 +72,16 @@ int workspace_for(hipStream_t st, Workspace** out) {
         (void)hipFree(w.slots);
         return set_error(HALO_MI_E_MEMORY, "lm_head: cannot allocate the argmax parts");
     }
+    if (hipMalloc(&w.xn, kNormFloats * sizeof(float)) != hipSuccess ||
+        hipMalloc(&w.inv, kInvFloats * sizeof(float)) != hipSuccess) {
+        (void)hipFree(w.partials);
+        (void)hipFree(w.counters);
+        (void)hipFree(w.xb);
+        (void)hipFree(w.slots);
+        (void)hipFree(w.parts);
+        if (w.xn) (void)hipFree(w.xn);
+        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the norm buffers");
+    }
     if (launch_fill_u32(w.counters, kCounters, 0u, st) != HALO_MI_OK ||
         launch_fill_u32(reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u, st) != HALO_MI_OK)
         return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
@@ -95,6 +105,14 @@ int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, 
     return HALO_MI_OK;
 }
 
+
+// The fused norm's operand: norm_w (cols floats, 4-byte aligned) must not overlap the output.
+int check_norm(const char* op, const float* norm_w, uint32_t cols, const void* out, uint64_t out_bytes) {
+    if (!norm_w) return HALO_MI_OK;
+    if (reinterpret_cast<uintptr_t>(norm_w) % 4) return set_error(HALO_MI_E_KERNEL, "%s: norm_w must be 4-byte aligned", op);
+    if (ranges_overlap(norm_w, (uint64_t)cols * 4, out, out_bytes)) return set_error(HALO_MI_E_KERNEL, "%s: norm_w overlaps the output", op);
+    return HALO_MI_OK;
+}
 
 // The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
 uint32_t gemm_tiles(uint32_t variant) {
@@ -127,6 +145,7 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     if (!p->w) return set_error(HALO_MI_E_KERNEL, "%s: operand w is empty", op);
     auto st = static_cast<hipStream_t>(stream);
     const uint64_t yext = extent(p->n_vec, ys * 4, (uint64_t)p->rows * 4);
+    if ((code = check_norm(op, p->norm_w, p->cols, p->y, yext))) return code;
     if (variant == HALO_MI_GEMV_GGUF_REF) {
         if (p->layout != HALO_MI_LAYOUT_GGUF)
             return set_error(HALO_MI_E_CONFIG, "%s: variant %u needs the GGUF layout", op, variant);
@@ -137,8 +156,25 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
         if (p->type == kF32 && ((reinterpret_cast<uintptr_t>(p->w) | ws) % 4))
             return set_error(HALO_MI_E_KERNEL, "%s: operand w is not 4-byte aligned", op);
         if (ranges_overlap(p->y, yext, p->w, extent(p->rows, ws, rb))) return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
-        return launch_gemv_gguf_ref(p->type, static_cast<const uint8_t*>(p->w), ws, p->x, xs, p->y, ys, p->rows, p->cols,
-                                    p->n_vec, st);
+        if (!p->norm_w)
+            return launch_gemv_gguf_ref(p->type, static_cast<const uint8_t*>(p->w), ws, p->x, xs, p->y, ys, p->rows,
+                                        p->cols, p->n_vec, st);
+        // rms_norm (bitwise cpu::rms_norm) into the workspace, then the reference-order gemv,
+        // as many vectors at a time as the buffer holds
+        Workspace* wsp = nullptr;
+        if ((code = workspace_for(st, &wsp))) return code;
+        if (!wsp) return set_error(HALO_MI_E_MEMORY, "%s: the fused norm needs this stream's workspace (make one call on it before capturing)", op);
+        const uint32_t per = (uint32_t)std::min<uint64_t>(kNormFloats / p->cols, p->n_vec);
+        if (per == 0) return set_error(HALO_MI_E_UNSUPPORTED, "%s: cols %u too large for the norm buffer", op, p->cols);
+        for (uint32_t t0 = 0; t0 < p->n_vec; t0 += per) {
+            const uint32_t n = std::min(per, p->n_vec - t0);
+            if ((code = launch_rms_norm(p->x + (uint64_t)t0 * xs, xs, p->norm_w, wsp->xn, p->cols, n, p->cols, p->norm_eps, st)))
+                return code;
+            if ((code = launch_gemv_gguf_ref(p->type, static_cast<const uint8_t*>(p->w), ws, wsp->xn, p->cols,
+                                             p->y + (uint64_t)t0 * ys, ys, p->rows, p->cols, n, st)))
+                return code;
+        }
+        return HALO_MI_OK;
     }
     if (p->layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: variant %u needs the SLAB layout", op, variant);
     if (!is_quant(p->type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
@@ -149,12 +185,16 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = p->n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
     if (variant == HALO_MI_GEMV_SLAB) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
+        a.norm_w = p->norm_w;
+        a.norm_eps = p->norm_eps;
         return launch_gemv_slab<false>(p->type, a, st);
     }
     if (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
         return set_error(HALO_MI_E_KERNEL, "%s: the MFMA GEMM needs 16-byte aligned x rows", op);
     GemmArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
     a.tiles = gemm_tiles(p->variant);
+    a.norm_w = p->norm_w;
+    a.norm_eps = p->norm_eps;
     return launch_gemm_pc<false>(p->type, a, st);
 }
 
@@ -196,7 +236,8 @@ int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
                         {p->ids_scatter, p->ids_scatter ? p->ids_scatter_len * 4 : 0, "ids_scatter"}};
     for (size_t i = 0; i < 3; ++i) {
         if (ranges_overlap(outs[i].p, outs[i].n, g.x, xext) || ranges_overlap(outs[i].p, outs[i].n, g.w, wext) ||
-            ranges_overlap(outs[i].p, outs[i].n, g.y, yext) || ranges_overlap(outs[i].p, outs[i].n, p->ids_slots, p->ids_slots ? ids_bytes : 0))
+            ranges_overlap(outs[i].p, outs[i].n, g.y, yext) || ranges_overlap(outs[i].p, outs[i].n, p->ids_slots, p->ids_slots ? ids_bytes : 0) ||
+            ranges_overlap(outs[i].p, outs[i].n, g.norm_w, g.norm_w ? (uint64_t)g.cols * 4 : 0))
             return set_error(HALO_MI_E_KERNEL, "%s: %s overlaps an operand", op, outs[i].name);
         for (size_t j = 0; j < i; ++j)
             if (ranges_overlap(outs[i].p, outs[i].n, outs[j].p, outs[j].n))
@@ -224,9 +265,12 @@ int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
         if (g.w_stride != 0) return set_error(HALO_MI_E_KERNEL, "%s: a SLAB operand has no row stride", op);
         if (reinterpret_cast<uintptr_t>(g.w) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
         if (ranges_overlap(g.y, yext, g.w, wext)) return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
+        if ((code = check_norm(op, g.norm_w, g.cols, g.y, yext))) return code;
         GemvSlabArgs a{static_cast<const uint8_t*>(g.w), nullptr, g.x, xs, g.y, ys, g.rows, g.cols, g.n_vec};
         a.parts = ws->parts;
         a.valid_rows = p->valid_rows;
+        a.norm_w = g.norm_w;
+        a.norm_eps = g.norm_eps;
         if ((code = launch_gemv_slab<false>(g.type, a, st))) return code;
     } else {
         if ((code = halo_mi_gemv(&g, stream))) return code;
@@ -259,12 +303,15 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     const uint64_t oext = extent(p->n_vec, os * 4, (uint64_t)p->rows * 4);
     if (ranges_overlap(p->out, oext, p->w_gate, wbytes) || ranges_overlap(p->out, oext, p->w_up, wbytes))
         return set_error(HALO_MI_E_KERNEL, "%s: out overlaps a weight operand", op);
+    if ((code = check_norm(op, p->norm_w, p->cols, p->out, oext))) return code;
     if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
         variant = p->n_vec <= kGateUpGemvMax ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
     auto st = static_cast<hipStream_t>(stream);
     if (variant == HALO_MI_GEMV_SLAB) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                        p->rows, p->cols, p->n_vec};
+        a.norm_w = p->norm_w;
+        a.norm_eps = p->norm_eps;
         return launch_gemv_slab<true>(p->type, a, st);
     }
     if (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
@@ -272,6 +319,8 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     GemmArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                p->rows, p->cols, p->n_vec};
     a.tiles = gemm_tiles(p->variant);
+    a.norm_w = p->norm_w;
+    a.norm_eps = p->norm_eps;
     return launch_gemm_pc<true>(p->type, a, st);
 }
 
@@ -318,6 +367,75 @@ int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t
     if (layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: unknown layout %u", op, layout);
     if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, type);
     return launch_dequant_slab(type, static_cast<const uint8_t*>(w), cols, first_row, n_rows, out, out_stride, st);
+}
+
+int halo_mi_get_rows(const halo_mi_get_rows_params* p, void* stream) {
+    clear_error();
+    if (!p) return set_error(HALO_MI_E_KERNEL, "get_rows: null params");
+    const char* op = "GET_ROWS";
+    int code;
+    const uint64_t rb = row_bytes_checked(p->type, p->cols, &code, op);
+    if (code) return code;
+    if (p->n_rows > 0x7FFFFFFFu) return set_error(HALO_MI_E_KERNEL, "%s: n_rows %u exceeds int32 ids", op, p->n_rows);
+    if (p->layout != HALO_MI_LAYOUT_GGUF && p->layout != HALO_MI_LAYOUT_SLAB)
+        return set_error(HALO_MI_E_CONFIG, "%s: unknown layout %u", op, p->layout);
+    if (p->layout == HALO_MI_LAYOUT_SLAB && !is_quant(p->type))
+        return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
+    auto st = static_cast<hipStream_t>(stream);
+    if (p->status) {
+        if (reinterpret_cast<uintptr_t>(p->status) % 4) return set_error(HALO_MI_E_KERNEL, "%s: status must be 4-byte aligned", op);
+        if ((code = launch_fill_u32(p->status, 1, 0u, st))) return code;
+    }
+    if (p->n_ids == 0 || p->cols == 0) return HALO_MI_OK;
+    if (!p->table || !p->ids || !p->out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (p->n_rows == 0) return set_error(HALO_MI_E_KERNEL, "%s: the table has no rows", op);
+    const uint64_t os = p->out_stride ? p->out_stride : p->cols;
+    if (p->n_ids > 1 && os < p->cols) return set_error(HALO_MI_E_KERNEL, "%s: out stride < cols", op);
+    if ((reinterpret_cast<uintptr_t>(p->out) | reinterpret_cast<uintptr_t>(p->ids)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: out and ids must be 4-byte aligned", op);
+    uint64_t ts = p->table_stride, tbytes;
+    if (p->layout == HALO_MI_LAYOUT_GGUF) {
+        if (ts == 0) ts = rb;
+        if (p->n_rows > 1 && ts < rb) return set_error(HALO_MI_E_KERNEL, "%s: table stride < row bytes", op);
+        if (p->type == kF32 && ((reinterpret_cast<uintptr_t>(p->table) | ts) % 4))
+            return set_error(HALO_MI_E_KERNEL, "%s: an F32 table must be 4-byte aligned", op);
+        tbytes = extent(p->n_rows, ts, rb);
+    } else {
+        if (ts != 0) return set_error(HALO_MI_E_KERNEL, "%s: a SLAB operand has no row stride", op);
+        if (reinterpret_cast<uintptr_t>(p->table) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
+        tbytes = halo_mi_slab_bytes(p->type, p->n_rows, p->cols);
+    }
+    const uint64_t oext = extent(p->n_ids, os * 4, (uint64_t)p->cols * 4);
+    if (ranges_overlap(p->out, oext, p->table, tbytes) || ranges_overlap(p->out, oext, p->ids, (uint64_t)p->n_ids * 4) ||
+        ranges_overlap(p->out, oext, p->status, p->status ? 4 : 0))
+        return set_error(HALO_MI_E_KERNEL, "%s: out overlaps an operand", op);
+    if (ranges_overlap(p->status, p->status ? 4 : 0, p->table, tbytes) ||
+        ranges_overlap(p->status, p->status ? 4 : 0, p->ids, (uint64_t)p->n_ids * 4))
+        return set_error(HALO_MI_E_KERNEL, "%s: status overlaps an operand", op);
+    if (p->layout == HALO_MI_LAYOUT_GGUF)
+        return launch_dequant_gguf(p->type, static_cast<const uint8_t*>(p->table), ts, p->cols, 0, p->n_ids, p->out, os, st,
+                                   p->ids, p->n_rows, p->status);
+    return launch_dequant_slab(p->type, static_cast<const uint8_t*>(p->table), p->cols, 0, p->n_ids, p->out, os, st, p->ids,
+                               p->n_rows, p->status);
+}
+
+int halo_mi_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, uint32_t rows,
+                     uint32_t cols, float eps, void* stream) {
+    clear_error();
+    const char* op = "RMS_NORM";
+    if (rows == 0 || cols == 0) return HALO_MI_OK;
+    if (!x || !w || !out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (x_stride == 0) x_stride = cols;
+    if (out_stride == 0) out_stride = cols;
+    if (rows > 1 && (x_stride < cols || out_stride < cols)) return set_error(HALO_MI_E_KERNEL, "%s: row stride < cols", op);
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: operands must be 4-byte aligned", op);
+    const uint64_t oext = extent(rows, out_stride * 4, (uint64_t)cols * 4);
+    const bool same = out == x && out_stride == x_stride;  // in place, as cpu::rms_norm allows
+    if (!same && ranges_overlap(out, oext, x, extent(rows, x_stride * 4, (uint64_t)cols * 4)))
+        return set_error(HALO_MI_E_KERNEL, "%s: out overlaps x", op);
+    if (ranges_overlap(out, oext, w, (uint64_t)cols * 4)) return set_error(HALO_MI_E_KERNEL, "%s: out overlaps w", op);
+    return launch_rms_norm(x, x_stride, w, out, out_stride, rows, cols, eps, static_cast<hipStream_t>(stream));
 }
 
 int halo_mi_repack_slab(uint32_t type, const void* src, uint64_t src_stride, uint32_t rows, uint32_t cols, void* dst,

@@ -213,8 +213,9 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 11> kVariants{{
+constexpr std::array<VariantInfo, 12> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
+    {kRmsNorm, "rms_norm_cpu_order", OpId::RmsNorm, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
     {kGemvSlab, "gemv_slab_w64", OpId::Gemv, {}},
     {kGemmSlabBf16, "gemm_slab_bf16_mfma", OpId::Gemv, {}},
@@ -259,6 +260,7 @@ public:
         Limits l;
         l.max_n_vec = std::numeric_limits<std::uint32_t>::max();
         l.lm_head_ids = true;
+        l.max_fused_norm_cols = 4u << 20;  // the reference-order variant's normalized-x buffer
         return l;
     }
     bool lost() const noexcept override { return lost_; }
@@ -374,11 +376,56 @@ public:
                                        out.stride / kF32, st.native()));
     }
 
+    // GET_ROWS with device ids (GetRowsArgs, backend.h:254-263): the id range is checked by the
+    // kernel, which reports through the optional status word as the reference's HIP backend does.
+    void get_rows(Stream& s, const GetRowsArgs& a) override {
+        HipStream& st = stream(s, "GET_ROWS");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kDequantRows, ErrorCode::Config,
+              "GET_ROWS: unknown kernel variant id %u", a.kernel.variant_id);
+        const Resolver r(this, "GET_ROWS");
+        const auto t = static_cast<std::uint32_t>(a.type);
+        const std::uint64_t rb = row_bytes(a.type, a.cols, r.op());
+        const bool slab = !a.table.empty() && a.table.buffer->layout() == WeightLayout::Slab;
+        const Operand table = slab ? r.slab(a.table, a.type, a.n_rows, a.cols, "table")
+                                   : r.get(a.table, a.n_rows, rb, a.type == DType::F32 ? kF32 : 1, Access::Read, "table");
+        const Operand ids = r.get(a.ids, 1, mul_u64(a.n_ids, 4, r.op(), "ids"), 4, Access::Read, "ids");
+        const Operand out = r.f32(a.out, a.n_ids, a.cols, Access::Write, "out");
+        const Operand status = a.status.empty() ? Operand{} : r.get(a.status, 1, 4, 4, Access::Write, "status");
+        r.no_overlap(out, table);
+        r.no_overlap(out, ids);
+        r.no_overlap(out, status);
+        r.no_overlap(status, table);
+        r.no_overlap(status, ids);
+        halo_mi_get_rows_params p{t, slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
+                                  table.base, slab ? 0 : table.stride, a.n_rows, a.cols,
+                                  reinterpret_cast<const std::int32_t*>(ids.base), a.n_ids,
+                                  reinterpret_cast<float*>(out.base), out.stride / kF32,
+                                  reinterpret_cast<std::uint32_t*>(status.base)};
+        check_abi(halo_mi_get_rows(&p, st.native()));
+    }
+
+    // RMS_NORM (RmsNormArgs, backend.h:267-272): exact aliasing of out and x is allowed, as
+    // cpu::rms_norm's check_alias_exact_or_disjoint (backends/cpu/ops_basic.cpp:22) allows it.
+    void rms_norm(Stream& s, const RmsNormArgs& a) override {
+        HipStream& st = stream(s, "RMS_NORM");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kRmsNorm, ErrorCode::Config,
+              "RMS_NORM: unknown kernel variant id %u", a.kernel.variant_id);
+        const Resolver r(this, "RMS_NORM");
+        const Operand x = r.f32(a.x, a.rows, a.cols, Access::Read, "x");
+        const Operand w = r.f32(a.w, 1, a.cols, Access::Read, "w");
+        const Operand out = r.f32(a.out, a.rows, a.cols, Access::Write, "out");
+        if (!(out.base == x.base && out.stride == x.stride)) r.no_overlap(out, x);
+        r.no_overlap(out, w);
+        if (a.rows == 0 || a.cols == 0) return;
+        check_abi(halo_mi_rms_norm(reinterpret_cast<const float*>(x.base), x.stride / kF32,
+                                   reinterpret_cast<const float*>(w.base), reinterpret_cast<float*>(out.base),
+                                   out.stride / kF32, a.rows, a.cols, a.eps, st.native()));
+    }
+
     void gemv(Stream& s, const GemvArgs& a) override {
         HipStream& st = stream(s, "MATMUL");
         CHECK(has_variant(OpId::Gemv, a.kernel.variant_id), ErrorCode::Config, "MATMUL: unknown kernel variant id %u",
               a.kernel.variant_id);
-        CHECK(a.norm_w.empty(), ErrorCode::Unsupported, "MATMUL: a fused norm (GemvArgs::norm_w) is Vulkan-only");
         CHECK(a.gates.n_v == 0, ErrorCode::Unsupported, "MATMUL: the GDN gates epilogue (GemvArgs::gates) is Vulkan-only");
         const Resolver r(this, "MATMUL");
         const auto t = static_cast<std::uint32_t>(a.wtype);
@@ -396,6 +443,8 @@ public:
         const Operand y = r.f32(a.y, a.n_vec, a.rows, Access::Write, "y");
         r.no_overlap(y, x);
         r.no_overlap(y, w);
+        const Operand nw = a.norm_w.empty() ? Operand{} : r.f32(a.norm_w, 1, a.cols, Access::Read, "norm_w");
+        r.no_overlap(y, nw);
         if (a.n_vec == 0 || a.rows == 0) return;
         if (variant == kGemmSlabBf16 || variant == kGemmSlabBf16M512 || (variant == kGemvSlabAuto && a.n_vec > 8))
             CHECK(reinterpret_cast<std::uintptr_t>(x.base) % 16 == 0 && x.stride % 16 == 0, ErrorCode::Kernel,
@@ -405,7 +454,8 @@ public:
                               reinterpret_cast<const float*>(x.base), x.stride / kF32,
                               reinterpret_cast<float*>(y.base), y.stride / kF32,
                               a.rows, a.cols, a.n_vec,
-                              variant == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512 : variant};
+                              variant == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512 : variant,
+                              reinterpret_cast<const float*>(nw.base), a.norm_eps};
         check_abi(halo_mi_gemv(&p, st.native()));
     }
 
@@ -438,6 +488,8 @@ public:
         r.no_overlap(out, x);
         r.no_overlap(out, wg);
         r.no_overlap(out, wu);
+        const Operand nw = a.norm_w.empty() ? Operand{} : r.f32(a.norm_w, 1, a.cols, Access::Read, "norm_w");
+        r.no_overlap(out, nw);
         if (a.n_vec == 0 || a.rows == 0) return;
         const std::uint32_t variant = a.kernel.variant_id == kGateUpGemv   ? HALO_MI_GEMV_SLAB
                                       : a.kernel.variant_id == kGateUpGemm ? HALO_MI_GEMM_SLAB_BF16
@@ -446,7 +498,8 @@ public:
                                                                            : HALO_MI_GEMV_SLAB;
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,
                                  reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
-                                 out.stride / kF32, a.rows, a.cols, a.n_vec, variant};
+                                 out.stride / kF32, a.rows, a.cols, a.n_vec, variant,
+                                 reinterpret_cast<const float*>(nw.base), a.norm_eps};
         check_abi(halo_mi_gate_up_swiglu(&p, st.native()));
     }
 
@@ -485,6 +538,9 @@ public:
             r.no_overlap(*o, w);
         }
         r.no_overlap(res, y);
+        const Operand nw = g.norm_w.empty() ? Operand{} : r.f32(g.norm_w, 1, g.cols, Access::Read, "norm_w");
+        r.no_overlap(y, nw);
+        r.no_overlap(res, nw);
         Operand ids{}, slots{}, scat{};
         if (!a.ids.empty()) {
             ids = r.get(a.ids, 1, mul_u64(g.n_vec, 4, r.op(), "ids"), 4, Access::Write, "ids");
@@ -506,7 +562,8 @@ public:
                                      w.base, slab ? 0 : w.stride,
                                      reinterpret_cast<const float*>(x.base), x.stride / kF32,
                                      logits ? reinterpret_cast<float*>(y.base) : nullptr, logits ? y.stride / kF32 : 0,
-                                     g.rows, g.cols, g.n_vec, variant};
+                                     g.rows, g.cols, g.n_vec, variant,
+                                     reinterpret_cast<const float*>(nw.base), g.norm_eps};
         p.result = res.base;
         p.valid_rows = a.valid_rows;
         p.ids = reinterpret_cast<std::int32_t*>(ids.base);

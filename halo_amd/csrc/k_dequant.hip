@@ -79,13 +79,33 @@ __global__ void k_unpack_slab(uint32_t type, const uint8_t* __restrict__ src, ui
     for (uint32_t i = 0; i < block_bytes(type); ++i) d[i] = blk[i];
 }
 
+// The table row of output row r: first_row + r, or ids[r] (GET_ROWS). An id outside the table
+// returns false, and the thread of the row's first element reports it in *status.
+__device__ __forceinline__ bool table_row(const int32_t* ids, uint32_t table_rows, uint32_t first_row, uint64_t r,
+                                          bool first, uint32_t* status, uint64_t& row) {
+    if (!ids) {
+        row = first_row + r;
+        return true;
+    }
+    const int32_t id = ids[r];
+    if (id < 0 || (uint32_t)id >= table_rows) {
+        if (first && status) atomicOr(status, kStatusBadIndex);
+        return false;
+    }
+    row = (uint64_t)id;
+    return true;
+}
+
 __global__ void k_dequant_gguf(uint32_t type, const uint8_t* __restrict__ w, uint64_t w_stride, uint32_t cols,
-                               uint32_t first_row, uint32_t n_rows, float* __restrict__ out, uint64_t out_stride) {
+                               uint32_t first_row, uint32_t n_rows, float* __restrict__ out, uint64_t out_stride,
+                               const int32_t* __restrict__ ids, uint32_t table_rows, uint32_t* status) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint64_t)n_rows * cols) return;
     const uint64_t r = idx / cols;
     const uint32_t i = (uint32_t)(idx % cols);
-    out[r * out_stride + i] = gguf_elem(type, w + (first_row + r) * w_stride, i);
+    uint64_t row;
+    if (!table_row(ids, table_rows, first_row, r, i == 0, status, row)) return;
+    out[r * out_stride + i] = gguf_elem(type, w + row * w_stride, i);
 }
 
 // Exact fp32 weights of slot s of the row at lane r of `slab` (the reference's expressions).
@@ -182,13 +202,15 @@ __device__ __forceinline__ void slab_slot_weights(const uint8_t* __restrict__ sl
 
 template <uint32_t T>
 __global__ void k_dequant_slab(const uint8_t* __restrict__ w, uint32_t cols, uint32_t first_row, uint32_t n_rows,
-                               float* __restrict__ out, uint64_t out_stride) {
+                               float* __restrict__ out, uint64_t out_stride, const int32_t* __restrict__ ids,
+                               uint32_t table_rows, uint32_t* status) {
     const SlabGeom g = slab_geom(T, cols);
     const uint32_t S = cols / kSlot;
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint64_t)n_rows * S) return;
     const uint32_t s = (uint32_t)(idx % S);
-    const uint64_t row = first_row + idx / S;
+    uint64_t row;
+    if (!table_row(ids, table_rows, first_row, idx / S, s == 0, status, row)) return;
     float wv[32];
     slab_slot_weights<T>(w + (row / kSlabRows) * g.slab_bytes, g, (uint32_t)(row % kSlabRows), s, wv);
     float* o = out + (idx / S) * out_stride + (uint64_t)s * 32;
@@ -218,25 +240,28 @@ int launch_unpack_slab(uint32_t type, const uint8_t* src, uint32_t rows, uint32_
 }
 
 int launch_dequant_gguf(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t cols, uint32_t first_row,
-                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st) {
+                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st, const int32_t* ids,
+                        uint32_t table_rows, uint32_t* status) {
     const uint64_t n = (uint64_t)n_rows * cols;
     hipLaunchKernelGGL(k_dequant_gguf, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, type, w, w_stride, cols,
-                       first_row, n_rows, out, out_stride);
+                       first_row, n_rows, out, out_stride, ids, table_rows, status);
     return hip_status(hipGetLastError(), "dequant_gguf launch");
 }
 
 int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t first_row, uint32_t n_rows, float* out,
-                        uint64_t out_stride, hipStream_t st) {
+                        uint64_t out_stride, hipStream_t st, const int32_t* ids, uint32_t table_rows, uint32_t* status) {
     const uint64_t n = (uint64_t)n_rows * (cols / kSlot);
     const dim3 grid((uint32_t)((n + 255) / 256)), block(256);
+#define HALO_MI_DQ(T) hipLaunchKernelGGL(k_dequant_slab<T>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride, ids, table_rows, status)
     switch (type) {
-        case kQ4_0: hipLaunchKernelGGL(k_dequant_slab<kQ4_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
-        case kQ8_0: hipLaunchKernelGGL(k_dequant_slab<kQ8_0>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
-        case kQ4_K: hipLaunchKernelGGL(k_dequant_slab<kQ4_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
-        case kQ5_K: hipLaunchKernelGGL(k_dequant_slab<kQ5_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
-        case kIQ4_XS: hipLaunchKernelGGL(k_dequant_slab<kIQ4_XS>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
-        default: hipLaunchKernelGGL(k_dequant_slab<kQ6_K>, grid, block, 0, st, w, cols, first_row, n_rows, out, out_stride); break;
+        case kQ4_0: HALO_MI_DQ(kQ4_0); break;
+        case kQ8_0: HALO_MI_DQ(kQ8_0); break;
+        case kQ4_K: HALO_MI_DQ(kQ4_K); break;
+        case kQ5_K: HALO_MI_DQ(kQ5_K); break;
+        case kIQ4_XS: HALO_MI_DQ(kIQ4_XS); break;
+        default: HALO_MI_DQ(kQ6_K); break;
     }
+#undef HALO_MI_DQ
     return hip_status(hipGetLastError(), "dequant_slab launch");
 }
 

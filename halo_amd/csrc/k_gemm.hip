@@ -100,8 +100,12 @@ __device__ __forceinline__ V ldg(const uint8_t* ubase, uint32_t voff) {
 // k16 of the slot, 1 KB holds, for lane l, the 8 values x[32 b + l % 32][32 s + 16 k16 + 8 (l / 32) + e]
 // (the A operand of v_mfma_f32_32x32x16_bf16). Rows in [n_vec, m_pad) are zero. One thread
 // writes one lane's 16 bytes: the writes of a wave are one contiguous 1 KB.
+// With the fused norm (nw set), x is first normalized as cpu::rms_norm does, (x * inv[m]) * nw[k],
+// inv from k_rms_inv_rows: the staged values are the CPU's normalized x rounded to bf16.
 __global__ void k_x_to_frag(const float* __restrict__ x, uint64_t x_stride, uint32_t n_vec, uint32_t m_pad,
-                            uint32_t cols, __bf16* __restrict__ out) {
+                            uint32_t cols, __bf16* __restrict__ out, const float* __restrict__ inv,
+                            const float* __restrict__ nw) {
+#pragma clang fp contract(off)
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (uint64_t)m_pad * (cols / 8)) return;
     const uint32_t S = cols / kSlot;
@@ -114,7 +118,16 @@ __global__ void k_x_to_frag(const float* __restrict__ x, uint64_t x_stride, uint
     if (m < n_vec) {
         const float4 a = *reinterpret_cast<const float4*>(x + (uint64_t)m * x_stride + k);
         const float4 c = *reinterpret_cast<const float4*>(x + (uint64_t)m * x_stride + k + 4);
-        v = bf16x8{(__bf16)a.x, (__bf16)a.y, (__bf16)a.z, (__bf16)a.w, (__bf16)c.x, (__bf16)c.y, (__bf16)c.z, (__bf16)c.w};
+        float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+        if (nw) {
+            const float s = inv[m];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float t = e[i] * s;
+                e[i] = t * nw[k + i];
+            }
+        }
+        v = bf16x8{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3], (__bf16)e[4], (__bf16)e[5], (__bf16)e[6], (__bf16)e[7]};
     } else {
         v = bf16x8{};
     }
@@ -853,11 +866,16 @@ void launch_reduce(const GemmPcArgs& p, hipStream_t st) {
     hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, BM>), dim3((uint32_t)((outs + 255) / 256)), dim3(256), 0, st, p);
 }
 
-// Rows [m_start, m_start + mc) of x to bf16 fragments, zero-padded to m_pad rows.
-void stage_x(const GemmArgs& a, uint64_t m_start, uint32_t mc, uint32_t m_pad, __bf16* xb, hipStream_t st) {
+// Rows [m_start, m_start + mc) of x to bf16 fragments, zero-padded to m_pad rows; with the
+// fused norm, each row's 1 / rms first (k_rms_inv_rows into ws->inv).
+int stage_x(const GemmArgs& a, uint64_t m_start, uint32_t mc, uint32_t m_pad, Workspace* ws, hipStream_t st) {
+    const float* x = a.x + m_start * a.x_stride;
+    if (a.norm_w)
+        if (int rc = launch_rms_inv(x, a.x_stride, mc, a.cols, a.norm_eps, ws->inv, st)) return rc;
     const uint64_t n8 = (uint64_t)m_pad * (a.cols / 8);
-    hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, a.x + m_start * a.x_stride,
-                       a.x_stride, mc, m_pad, a.cols, xb);
+    hipLaunchKernelGGL(k_x_to_frag, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st, x, a.x_stride, mc, m_pad,
+                       a.cols, ws->xb, ws->inv, a.norm_w);
+    return hip_status(hipGetLastError(), "x staging launch");
 }
 
 uint32_t cu_count() {
@@ -877,14 +895,14 @@ uint32_t cu_count() {
 template <bool PAIR>
 int launch_gemm_lm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t units, hipStream_t st) {
     const uint32_t S = a.cols / kSlot, cus = cu_count();
-    const uint64_t cap_rows = kXbElems / a.cols / kLmBM * kLmBM;
+    const uint64_t cap_rows = std::min(kXbElems / a.cols, kInvFloats) / kLmBM * kLmBM;
     if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
     if ((uint64_t)kLmBM * a.cols * 2 > 0xFFFFFFFFull)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for one M tile", a.cols);
     for (uint64_t m_start = 0; m_start < a.n_vec; m_start += cap_rows) {
         const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, a.n_vec - m_start);
         const uint32_t m_tiles = (mc + kLmBM - 1) / kLmBM;
-        stage_x(a, m_start, mc, m_tiles * kLmBM, ws->xb, st);
+        if (int rc = stage_x(a, m_start, mc, m_tiles * kLmBM, ws, st)) return rc;
         const uint64_t tiles = (uint64_t)units * m_tiles;
         GemmPcArgs p{a.w0, a.w1, ws->xb, a.y + m_start * a.y_stride, a.y_stride, a.rows, a.cols, mc, units, m_tiles, 0u,
                      0u, 1u, ws->partials};
@@ -952,7 +970,7 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
                                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus))
         return launch_gemm_lm<PAIR>(type, a, ws, units, st);
     const uint32_t BM = 64u * MB;
-    const uint64_t cap_rows = kXbElems / a.cols / BM * BM;
+    const uint64_t cap_rows = std::min(kXbElems / a.cols, kInvFloats) / BM * BM;
     if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
     if ((uint64_t)BM * a.cols * 2 > 0xFFFFFFFFull)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for one M tile", a.cols);
@@ -970,7 +988,7 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     for (uint64_t m_start = 0; m_start < a.n_vec; m_start += cap_rows) {
         const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, a.n_vec - m_start);
         const uint32_t m_tiles = (mc + BM - 1) / BM;
-        stage_x(a, m_start, mc, m_tiles * BM, ws->xb, st);
+        if (int rc = stage_x(a, m_start, mc, m_tiles * BM, ws, st)) return rc;
         float* y = a.y + m_start * a.y_stride;
         // whole rounds of tiles, then the rest split over K; a matrix whose tiles cannot fill
         // half the chip is split over K altogether

@@ -325,14 +325,48 @@ __device__ __forceinline__ uint32_t gemv_ticket(const GemvSlabArgs& a, uint32_t 
     return t;
 }
 
-template <int NV, bool PAIR>
+// Cross-lane moves within rows of 16 lanes (DPP): lane ^ 1, lane ^ 2 (quad permutes), the
+// mirror inside 8 lanes (pairs the two quads) and inside 16 lanes (pairs the two halves).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the wave, wave-uniform, in a fixed order: DPP inside each row of 16 lanes (pairs,
+// quads, halves of 8, halves of 16), then (row 0 + row 1) + (row 2 + row 3).
+__device__ __forceinline__ float wave_sum(float s) {
+    s += dpp_f<kDppXor1>(s);
+    s += dpp_f<kDppXor2>(s);
+    s += dpp_f<kDppHalfMirror>(s);
+    s += dpp_f<kDppMirror>(s);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// NORM (the fused norm): ss holds each lane's sum of squares of the raw x it loaded; ss_red +
+// w * ss_stride is NV floats of LDS for wave w (its dead A table).
+template <int NV, bool PAIR, bool NORM>
 __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
                                             uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
-                                            uint32_t ticket) {
+                                            uint32_t ticket, const float (&ss)[NV], float* ss_red, uint32_t ss_stride) {
+    constexpr bool norm = NORM;
+    float sst[NV];  // the workgroup's sum of squares, then the slab's (chunk order)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) sst[v] = norm ? wave_sum(ss[v]) : 0.0f;
     // waves -> wave 0, in wave order
     if (nw > 1) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
+        if (norm && lane == 0)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) ss_red[wave * ss_stride + v] = sst[v];
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
@@ -341,6 +375,13 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
             for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
             acc0[v] = s;
         }
+        if (norm)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float s = ss_red[v];
+                for (uint32_t w = 1; w < nw; ++w) s += ss_red[w * ss_stride + v];
+                sst[v] = s;
+            }
     }
     const uint32_t row = slab * kSlabRows + lane;
     float acc1[NV];  // the up sums (PAIR)
@@ -355,24 +396,50 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
         // (bounded, with a pause) any not yet ready, adds the chunks in chunk order
         // (deterministic), and clears the words and the ticket counter for the next launch.
         uint64_t* P = a.slots + (uint64_t)slab * nch * NV * 64;
+        // the norm's sums of squares: one word per (chunk, vector) after all slabs' partials
+        uint64_t* PS = a.slots + (uint64_t)gridDim.x * NV * 64 + (uint64_t)slab * nch * NV;
         if (__builtin_amdgcn_readfirstlane(ticket) != nch - 1) {
 #pragma unroll
             for (int v = 0; v < NV; ++v)
                 __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
                                    (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
+            if (norm && lane == 0)
+#pragma unroll
+                for (int v = 0; v < NV; ++v)
+                    __hip_atomic_store(PS + (uint64_t)c * NV + v, (uint64_t)__float_as_uint(sst[v]) | (1ull << 32),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
-        float own[NV];
+        float own[NV], own_ss[NV];
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             own[v] = acc0[v];
             acc0[v] = 0.0f;
+            own_ss[v] = sst[v];
+            sst[v] = 0.0f;
         }
         // The loads of 8 chunks are issued before any is used (one memory round trip per 8
-        // chunks); past the last chunk the address is clamped and the value dropped.
+        // chunks); past the last chunk the address is clamped and the value dropped. With the
+        // norm, the chunks' sums of squares ride in the same round trip; only the gate chunks'
+        // count (the up chunks of a pair load the same x), in chunk order.
         constexpr uint32_t KB = 8;
         constexpr uint32_t kSpinLimit = 1u << 20;  // the other chunks are running: a few microseconds
+        auto ready = [&](uint64_t w, const uint64_t* addr) {
+            for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin) {
+                __builtin_amdgcn_s_sleep(2);
+                w = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
+        };
+        // the ss words of a window of 64 / NV chunks, one word per lane (lane = (k % win) NV + v)
+        constexpr uint32_t win = 64 / NV;
+        uint64_t qsl = 0;
+        auto load_window = [&](uint32_t k0) {
+            if (lane < min(nch - k0, win) * NV)
+                qsl = __hip_atomic_load(PS + (uint64_t)k0 * NV + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        if (norm) load_window(0);
         for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
             uint64_t q[KB][NV];
 #pragma unroll
@@ -388,28 +455,43 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                 if (k >= nch) break;
 #pragma unroll
                 for (int v = 0; v < NV; ++v) {
-                    float val = own[v];
-                    if (k != c) {
-                        uint64_t w = q[kk][v];
-                        for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin) {
-                            __builtin_amdgcn_s_sleep(2);
-                            w = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                        }
-                        val = (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
-                    }
+                    const float val = k == c ? own[v] : ready(q[kk][v], P + ((uint64_t)k * NV + v) * 64 + lane);
                     if (k < a.ks) acc0[v] += val;
                     else acc1[v] += val;
+                }
+                if (norm && k < a.ks) {
+                    if (k % win == 0 && k > 0) load_window(k);
+#pragma unroll
+                    for (int v = 0; v < NV; ++v) {
+                        const uint32_t idx = (k % win) * NV + v;
+                        const uint64_t w = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)qsl, idx) |
+                                           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(qsl >> 32), idx) << 32);
+                        sst[v] += k == c ? own_ss[v] : ready(w, PS + (uint64_t)k * NV + v);
+                    }
                 }
             }
         }
         for (uint32_t k = 0; k < nch; ++k)
-            if (k != c)
+            if (k != c) {
 #pragma unroll
                 for (int v = 0; v < NV; ++v)
                     __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
+                if (norm && lane == 0)
+#pragma unroll
+                    for (int v = 0; v < NV; ++v)
+                        __hip_atomic_store(PS + (uint64_t)k * NV + v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         if (lane == 0) __hip_atomic_store(&a.counters[slab], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (norm) {
+        // rms_norm's scale, applied once to the row sums (the workgroups multiplied x by norm_w)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float inv = 1.0f / sqrtf(sst[v] / (float)a.cols + a.norm_eps);
+            acc0[v] *= inv;
+            acc1[v] *= inv;
+        }
     }
     if constexpr (!PAIR) {
         // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
@@ -490,7 +572,10 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
             compute_group<T, NV>(nxt, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
         }
     }
-    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
+    float ss[NV];  // the VALU kernel has no fused norm (its launcher never passes norm_w)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) ss[v] = 0.0f;
+    gemv_finish<NV, PAIR, false>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, nullptr, 0);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -553,17 +638,6 @@ __device__ __forceinline__ void split3(float a, float b, uint32_t (&p)[3]) {
     p[2] = pack_bf16(ra - __uint_as_float(p[1] << 16), rb - __uint_as_float(p[1] & 0xFFFF0000u));
 }
 
-// Cross-lane moves within rows of 16 lanes (DPP): lane ^ 1, lane ^ 2 (quad permutes), the
-// mirror inside 8 lanes (pairs the two quads) and inside 16 lanes (pairs the two halves).
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
 // Maximum over the wave, wave-uniform (DPP inside rows, then the four row results).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = max(v, dpp_u<kDppXor1>(v));
@@ -578,9 +652,11 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // x of one slot group, lane = 8 s + r: x[slot 8 grp + s][4 r .. 4 r + 3] (zero past the end).
 // Branch-free (the address is clamped, the value selected after): a load under a branch would
 // make the compiler wait for it before the weight loads that follow are issued.
-template <int NV>
-__device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], const float* __restrict__ x, uint64_t x_stride,
-                                          uint32_t grp, uint32_t S, uint32_t lane) {
+// NORM: wr gets the same four elements of norm_w (loaded branch-free as x is).
+template <int NV, bool NORM>
+__device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], const float* __restrict__ x,
+                                          uint64_t x_stride, const float* __restrict__ norm_w, uint32_t grp, uint32_t S,
+                                          uint32_t lane) {
     const uint32_t slot = grp * 8 + (lane >> 3);
     const bool in = slot < S;
     const uint64_t e = (uint64_t)min(slot, S - 1) * 32 + 4 * (lane & 7);
@@ -591,6 +667,12 @@ __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], const float* __res
             const float t = x[(uint64_t)v * x_stride + e + i];
             xr[v][i] = in ? t : 0.0f;
         }
+    if constexpr (NORM)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float t = norm_w[e + i];
+            wr[i] = in ? t : 0.0f;
+        }
 }
 
 // Builds this wave's A table for one group from xr, reads it back as register pairs, and
@@ -599,12 +681,28 @@ __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], const float* __res
 // Q6_K, whose low-half sum is then in lane 8 s).
 // The k-step r of a slot (k-steps 0..3: slot elements 0..15, 4..7: 16..31) covers elements
 // 4 r .. 4 r + 3 in the order (0, 2, 1, 3), the order the masks below produce them.
+// With the fused norm (norm), the group's x is x * norm_w, and ss accumulates the squares of
+// the raw x.
 template <uint32_t T, int NV>
-__device__ __forceinline__ void mx_build(const float (&xr)[NV][4], uint8_t* tab, uint32_t lane,
-                                         s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV], float (&xs)[NV]) {
+__device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float (&wr)[4], bool norm, float (&ss)[NV],
+                                         uint8_t* tab, uint32_t lane, s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV],
+                                         float (&xs)[NV]) {
     constexpr int M = mx_blocks<NV>();
     constexpr int kHiShift = (T == kQ4_K || T == kQ4_0) ? 4 : 0;  // high nibbles arrive as 16 q
     const uint32_t s = lane >> 3, r = lane & 7;
+    float xr[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[v][i] = xraw[v][i];
+    if (norm)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ss[v] = fmaf(xraw[v][i], xraw[v][i], ss[v]);
+                xr[v][i] = xraw[v][i] * wr[i];
+            }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         uint32_t mb = 0;
@@ -783,8 +881,9 @@ constexpr uint32_t mx_max_threads() {
 
 // grid, split and LDS as k_gemv_slab, plus one A table per wave after the partials. ONE: every
 // wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
-template <uint32_t T, int NV, bool PAIR, bool ONE>
+template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
 __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
+    static_assert(ONE || !NORM, "the fused norm runs on the one-group kernel");
     extern __shared__ float smem[];
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     constexpr int M = mx_blocks<NV>();
@@ -803,33 +902,36 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
     float* red = smem;
     uint8_t* tab = reinterpret_cast<uint8_t*>(smem + nw * NV * 64) + wave * mx_table_bytes<NV>();
 
-    float acc0[NV];
+    float acc0[NV], ss[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
-    float xr[NV][4];
+    for (int v = 0; v < NV; ++v) acc0[v] = ss[v] = 0.0f;
+    constexpr bool norm = NORM;
+    float* ss_red = reinterpret_cast<float*>(smem + nw * NV * 64);  // wave w's A table, once it is dead
+    constexpr uint32_t ss_stride = mx_table_bytes<NV>() / 4;
+    float xr[NV][4], wr[4];
     uint32_t ticket = 0;
     if constexpr (ONE) {
         if (w0 < w1) {
             SlotGroup<T> G;
-            mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
+            mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
             load_group<T>(G, slab0, geo, lane, w0, S);
             ticket = gemv_ticket(a, slab, nch);
             s16x4 A[4 * M];
             int es[NV];
             float xs[NV];
-            mx_build<T, NV>(xr, tab, lane, A, es, xs);
+            mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
             mx_group<T, NV>(G, A, xs, min(8u, S - w0 * 8), acc0);
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
         } else {
             ticket = gemv_ticket(a, slab, nch);
         }
-        gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
+        gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
         return;
     }
     SlotGroup<T> cur, nxt;
     if (w0 < w1) {  // x first: the A table is built while the weights are on their way
-        mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
+        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, w0, S, lane);
         load_group<T>(cur, slab0, geo, lane, w0, S);
     }
     ticket = gemv_ticket(a, slab, nch);
@@ -839,9 +941,9 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
         s16x4 A[4 * M];
         int es[NV];
         float xs[NV];
-        mx_build<T, NV>(xr, tab, lane, A, es, xs);
+        mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
         const uint32_t gn = min(grp + 1, w1 - 1);
-        mx_load_x<NV>(xr, a.x, a.x_stride, gn, S, lane);
+        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, gn, S, lane);
         load_group<T>(next, slab0, geo, lane, gn, S);
         float accg[NV];
 #pragma unroll
@@ -856,7 +958,7 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
         ++grp;
         step(nxt, cur, grp);
     }
-    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
+    gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
 }
 
 // Work split of a slab-GEMV launch: ks K chunks per slab (more than one only when the slabs
@@ -866,7 +968,8 @@ struct GemvSplit {
     uint32_t ks, nw;
 };
 
-GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, bool have_ws) {
+// words: workspace words per (slab, chunk) and vector (64 partials, plus one with the norm).
+GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, bool have_ws, uint32_t words) {
     // One slot group per wave for mid-size matrices, two for large ones (measured on MI355X,
     // 17408 x 5120 and 151936 x 5120 Q4_K).
     static const uint32_t target_env = [] {
@@ -885,7 +988,7 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, boo
     // gain more from a short split-K fix-up than from more workgroups (floor of 128).
     const uint32_t target_wg = target_env ? target_env : std::clamp(4 * units, 128u, 1088u);
     if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
-    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * 64 > kSlots) --ks;
+    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * words > kSlots) --ks;
     const uint32_t gwg = (ngrp + ks - 1) / ks;
     uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
     // a wave holds the x sums of at most 4 groups (one per lane)
@@ -902,7 +1005,8 @@ template <uint32_t T, int NV, bool PAIR>
 int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_t st) {
     const uint32_t S = a.cols / kSlot;
     constexpr uint32_t MATS = PAIR ? 2 : 1;
-    const GemvSplit sp = pick_split(slabs, S, NV, MATS, ws != nullptr && slabs <= kCounters);
+    const uint32_t words = a.norm_w ? 65u : 64u;
+    const GemvSplit sp = pick_split(slabs, S, NV, MATS, ws != nullptr && slabs <= kCounters, words);
     a.ks = sp.ks;
     a.slots = ws ? ws->slots : nullptr;
     a.counters = ws ? ws->counters : nullptr;
@@ -911,7 +1015,9 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
         return e && *e == '1';
     }();
     if constexpr (T != kQ5_K && T != kIQ4_XS) {  // the VALU kernel covers the first four formats
-        if (valu) {
+        if (valu && !a.norm_w) {
+            if (a.ks * MATS > 1 && (uint64_t)slabs * a.ks * MATS * NV * 64 > kSlots)
+                return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
             const size_t lds = (size_t)sp.nw * NV * 64 * sizeof(float);
             hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
             return hip_status(hipGetLastError(), "gemv_slab launch");
@@ -923,16 +1029,28 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
     const uint32_t ngrp = (S + 7) / 8;
     uint32_t nw1 = mx_max_threads<T, NV, true>() / 64;
     while (nw1 > 1 && nw1 * per_wave > 65536) --nw1;
-    if (ws && slabs < 1024 && slabs <= kCounters) {
+    // The fused norm runs on the one-group kernel only (its registers stay out of the streaming
+    // loop), whatever the number of slabs.
+    if (ws && (slabs < 1024 || a.norm_w) && slabs <= kCounters) {
         uint32_t ks = std::max(a.ks, (ngrp + nw1 - 1) / nw1);
         ks = std::min(ks, ngrp);
-        if ((uint64_t)slabs * ks * MATS * NV * 64 <= kSlots) a.ks = ks;
+        if ((uint64_t)slabs * ks * MATS * NV * words <= kSlots) a.ks = ks;
     }
     const uint32_t gwg = (ngrp + a.ks - 1) / a.ks;  // groups of the largest chunk
+    // the chunks of a slab (or the pair's two matrices) meet in the workspace words
+    if (a.ks * MATS > 1 && (uint64_t)slabs * a.ks * MATS * NV * words > kSlots)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
     if (gwg <= nw1 && (a.ks == 1 || ws)) {
-        hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave, st, a);
+        if (a.norm_w)
+            hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave,
+                               st, a);
+        else
+            hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave, st, a);
         return hip_status(hipGetLastError(), "gemv_slab launch");
     }
+    if (a.norm_w)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: the fused norm over %u rows x %u cols needs more split-K "
+                                                "workspace than this stream has (or a workspace at all)", a.rows, a.cols);
     uint32_t nw = std::min(sp.nw, mx_max_threads<T, NV, false>() / 64);
     while (nw > 1 && nw * per_wave > 65536) --nw;
     hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), dim3(slabs * a.ks * MATS), dim3(64 * nw), nw * per_wave, st, a);

@@ -43,6 +43,12 @@ struct GemvSlabArgs {
     // at or past valid_rows (when not 0) are not ranked, but a NaN in them still counts
     ArgPart* parts = nullptr;
     uint32_t valid_rows = 0;
+    // Fused input norm: y = W (rms_norm(x) * norm_w) when norm_w is set. Each workgroup
+    // multiplies its x slots by norm_w and sums the squares of the raw x it loaded; the sums
+    // meet in the fix-up (slot words after the partials: [slabs][chunks][NV]) and the finishing
+    // workgroup scales the row sums by 1 / sqrt(sum / cols + norm_eps).
+    const float* norm_w = nullptr;
+    float norm_eps = 0.0f;
 };
 
 // M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
@@ -57,6 +63,9 @@ struct GemmArgs {
     uint64_t y_stride;
     uint32_t rows, cols, n_vec;
     uint32_t tiles = kGemmTilesAuto;  // M tile family: kGemmTiles*
+    // Fused input norm: x is normalized exactly as cpu::rms_norm while it is staged as bf16
+    const float* norm_w = nullptr;
+    float norm_eps = 0.0f;
 };
 
 // ---- split-K workspace, one per (device, stream) ------------------------------------------
@@ -69,6 +78,8 @@ constexpr uint64_t kSlots = 4ull << 20;          // GEMV split-K words: 32 MiB
 constexpr uint64_t kCounters = 1ull << 20;        // slabs (64M rows)
 constexpr uint64_t kXbElems = 16ull << 20;        // bf16 copy of x for the GEMM: 32 MiB
 constexpr uint64_t kArgParts = 1ull << 20;        // LM-head argmax parts (16 B each): 16 MiB
+constexpr uint64_t kNormFloats = 4ull << 20;      // normalized x rows (reference-order GEMV): 16 MiB
+constexpr uint64_t kInvFloats = 1ull << 20;       // per-row 1 / rms of x (GEMM staging): 4 MiB
 
 struct Workspace {
     float* partials = nullptr;
@@ -76,6 +87,8 @@ struct Workspace {
     uint32_t* counters = nullptr;
     __bf16* xb = nullptr;
     ArgPart* parts = nullptr;
+    float* xn = nullptr;
+    float* inv = nullptr;
 };
 
 // The workspace of (current device, st); *out is null when st is being captured and has none yet.
@@ -97,10 +110,16 @@ int launch_repack_slab(uint32_t type, const uint8_t* src, uint64_t src_stride, u
                        uint8_t* dst, hipStream_t st);
 int launch_unpack_slab(uint32_t type, const uint8_t* src, uint32_t rows, uint32_t cols, uint8_t* dst,
                        uint64_t dst_stride, hipStream_t st);
+// Rows [first_row, first_row + n_rows) of W, or with ids the rows ids[0 .. n_rows) (GET_ROWS):
+// an id outside [0, table_rows) leaves its output row unwritten and sets kStatusBadIndex in
+// *status (when given).
 int launch_dequant_gguf(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t cols, uint32_t first_row,
-                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st);
+                        uint32_t n_rows, float* out, uint64_t out_stride, hipStream_t st, const int32_t* ids = nullptr,
+                        uint32_t table_rows = 0, uint32_t* status = nullptr);
 int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t first_row, uint32_t n_rows, float* out,
-                        uint64_t out_stride, hipStream_t st);
+                        uint64_t out_stride, hipStream_t st, const int32_t* ids = nullptr, uint32_t table_rows = 0,
+                        uint32_t* status = nullptr);
+constexpr uint32_t kStatusBadIndex = 8u;  // the reference's status bit for a GET_ROWS id outside the table
 int launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st);
 // k_gemv.hip
 int launch_gemv_gguf_ref(uint32_t type, const uint8_t* w, uint64_t w_stride, const float* x, uint64_t x_stride, float* y,
@@ -118,5 +137,12 @@ int launch_argmax_finish(const ArgPart* parts, uint32_t n_parts, uint32_t n_vec,
                          const uint32_t* ids_slots, int32_t* ids_scatter, uint64_t scatter_len, hipStream_t st);
 int launch_swiglu(const float* g, uint64_t gs, const float* u, uint64_t us, float* out, uint64_t os, uint32_t rows,
                   uint32_t cols, hipStream_t st);
+// k_norm.hip: cpu::rms_norm, bitwise (the sum of squares in cpu::detail::dot's order). out may
+// be x itself (same stride). inv_rows: only the per-row 1 / sqrt(mean + eps), for the staging
+// of a normalized x.
+int launch_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, uint32_t rows,
+                    uint32_t cols, float eps, hipStream_t st);
+int launch_rms_inv(const float* x, uint64_t x_stride, uint32_t rows, uint32_t cols, float eps, float* inv,
+                   hipStream_t st);
 
 }  // namespace halo_mi

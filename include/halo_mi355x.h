@@ -102,6 +102,19 @@ enum {
  *      for SLAB, w_stride must be 0.
  *   x: n_vec rows of cols fp32, x_stride floats apart (0 = cols).
  *   y: n_vec rows of rows fp32, y_stride floats apart (0 = rows). y must not overlap x or w.
+ *   norm_w (optional, cols fp32): the fused input norm of GemvArgs::norm_w / norm_eps
+ *      (backend.h:292-299): y = W (rms_norm(x) * norm_w) with eps = norm_eps, x the raw rows;
+ *      rms_norm as cpu::rms_norm (backends/cpu/ops_basic.cpp:18-33). Every variant, layout and
+ *      n_vec (the reference accepts it on one Vulkan path only):
+ *        - GGUF reference variant: x is normalized first exactly as cpu::rms_norm, so y is
+ *          bitwise rms_norm then matmul;
+ *        - bf16 GEMM variants: the same normalized x, rounded to bf16 while it is staged;
+ *        - SLAB GEMV: fused into the kernel, no extra launch: each workgroup multiplies its x
+ *          slots by norm_w and sums the squares of the raw x it loads, the sums meet in the
+ *          split-K fix-up, and the row sums are scaled by 1 / sqrt(sum / cols + eps) once. The
+ *          result differs from rms_norm then gemv only by rounding (the order of the sum of
+ *          squares, and x * norm_w scaled after the dot instead of before).
+ *      norm_w must not overlap y.
  */
 typedef struct halo_mi_gemv_params {
     uint32_t type;
@@ -116,6 +129,8 @@ typedef struct halo_mi_gemv_params {
     uint32_t cols;
     uint32_t n_vec;
     uint32_t variant;
+    const float* norm_w;
+    float norm_eps;
 } halo_mi_gemv_params;
 
 int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
@@ -127,7 +142,8 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
  * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto
  * (gemv kernel for n_vec <= 4, else the GEMM, its M tiles chosen as for halo_mi_gemv), 2 = gemv
  * kernel (any n_vec, 4 vectors per pass over the weights), 3 / 5 = bf16 MFMA GEMM on 64..256 /
- * 512-row M tiles. out may not overlap x, Wg or Wu.
+ * 512-row M tiles. out may not overlap x, Wg or Wu. norm_w / norm_eps (optional): the fused
+ * input norm as for halo_mi_gemv (the FFN's post-attention norm folded into the pair).
  */
 typedef struct halo_mi_gate_up_params {
     uint32_t type;
@@ -142,6 +158,8 @@ typedef struct halo_mi_gate_up_params {
     uint32_t cols;
     uint32_t n_vec;
     uint32_t variant;
+    const float* norm_w;
+    float norm_eps;
 } halo_mi_gate_up_params;
 
 int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream);
@@ -198,6 +216,47 @@ int halo_mi_swiglu(const float* gate, uint64_t gate_stride, const float* up, uin
 int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t w_stride,
                          uint32_t rows, uint32_t cols, uint32_t first_row, uint32_t n_rows,
                          float* out, uint64_t out_stride, void* stream);
+
+/*
+ * GET_ROWS (GetRowsArgs, include/halo/backend/backend.h:254-263; CPU at
+ * src/backend/cpu_backend.cpp:284-303; the HIP status word at backends/hip/src/ops.cpp:982-1012):
+ * out[i] = dequant(table row ids[i]) for i < n_ids, bit-identical to tensor::dequantize_row.
+ *   table: n_rows rows of cols weights in `layout` (GGUF: table_stride bytes apart, 0 =
+ *          row_bytes; SLAB: table_stride 0). ids: n_ids int32 on the device.
+ *   out: n_ids rows of cols fp32, out_stride floats apart (0 = cols); must not overlap table,
+ *        ids or status.
+ *   status (optional, one uint32 on the device): cleared, then an id outside [0, n_rows) leaves
+ *        its output row unwritten and sets HALO_MI_STATUS_BAD_INDEX (the reference's
+ *        kStatusBadIndex, backends/hip/kernels/hd.h:156). Ids live on the device, so this is
+ *        where the CPU backend's Error(Kernel) shows: read the word after the stream is done.
+ */
+#define HALO_MI_STATUS_BAD_INDEX 8u
+
+typedef struct halo_mi_get_rows_params {
+    uint32_t type;
+    uint32_t layout;
+    const void* table;
+    uint64_t table_stride;
+    uint32_t n_rows;
+    uint32_t cols;
+    const int32_t* ids;
+    uint32_t n_ids;
+    float* out;
+    uint64_t out_stride;
+    uint32_t* status;
+} halo_mi_get_rows_params;
+
+int halo_mi_get_rows(const halo_mi_get_rows_params* p, void* stream);
+
+/*
+ * RMS_NORM (RmsNormArgs, backend.h:267-272; cpu::rms_norm, backends/cpu/ops_basic.cpp:18-33):
+ * out[r] = (x[r] * inv) * w with inv = 1 / sqrt(dot(x[r], x[r]) / cols + eps), bitwise equal to
+ * the CPU (the sum of squares in cpu::detail::dot's order). rows x cols fp32, strides in floats
+ * (0 = cols); out may be x itself with the same stride, or must not overlap x or w. This is the
+ * normalization halo_mi_gemv's fused norm applies for the reference and GEMM variants.
+ */
+int halo_mi_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride,
+                     uint32_t rows, uint32_t cols, float eps, void* stream);
 
 /* ---- geometry ------------------------------------------------------------------------------ */
 /* Bytes of one GGUF row of `cols` elements (src/tensor/quant.cpp:411-418); 0 on error. */

@@ -129,13 +129,40 @@ struct DequantRowsArgs {
     KernelChoice kernel{};
 };
 
+/// GET_ROWS (backend.h:254-263): out[i] = dequant(table row ids[i]), bit-identical to
+/// tensor::dequantize_row. ids: n_ids int32 in device memory. status (optional, one uint32 of
+/// device memory; the reference's StatusRef): cleared, then kStatusBadIndex when an id lies
+/// outside [0, n_rows) - that output row is not written. The CPU backend throws Error(Kernel)
+/// instead (cpu_backend.cpp:296-299); ids on the device are only known to the kernel.
+struct GetRowsArgs {
+    DType type = DType::F32;
+    TensorRef table{}, ids{}, out{};
+    std::uint32_t n_rows = 0, cols = 0, n_ids = 0;
+    KernelChoice kernel{};
+    TensorRef status{};
+};
+/// The status bit of a GET_ROWS id outside the table (backends/hip/kernels/hd.h:156).
+inline constexpr std::uint32_t kStatusBadIndex = 8u;
+
+/// RMS_NORM (backend.h:267-272; cpu::rms_norm): rows x cols; w: [cols]. out may be x itself
+/// (same stride), else must not overlap x. Bitwise equal to the CPU.
+struct RmsNormArgs {
+    TensorRef x{}, w{}, out{};
+    std::uint32_t rows = 0, cols = 0;
+    float eps = 1e-6f;
+    KernelChoice kernel{};
+};
+
 /// MATMUL / QUANT_GEMV (backend.h:283-314): y[t][n] = sum_i x[t][i] W[n][i].
 struct GemvArgs {
     DType wtype = DType::F32;
     TensorRef w{}, x{}, y{};
     std::uint32_t rows = 0, cols = 0, n_vec = 1;
     KernelChoice kernel{};
-    TensorRef norm_w{};  // Vulkan-only in the reference: rejected here
+    /// Fused input norm (backend.h:292-299): y = W (rms_norm(x) * norm_w) with eps = norm_eps,
+    /// x the raw rows; norm_w: [cols] fp32. Every variant and n_vec here (the reference takes it
+    /// on one Vulkan path); its numerics per variant are halo_mi_gemv's (include/halo_mi355x.h).
+    TensorRef norm_w{};
     float norm_eps = 1e-6f;
     /// As in the reference: off (the default), every row of y is bitwise the row an n_vec == 1 call
     /// gives, whatever n_vec (the SLAB default then runs the GEMV kernel at every n_vec). On, the
@@ -179,6 +206,8 @@ struct GateUpArgs {
     std::uint32_t rows = 0, cols = 0, n_vec = 1;
     KernelChoice kernel{};
     bool allow_gemm = false;  ///< same meaning as GemvArgs::allow_gemm
+    TensorRef norm_w{};       ///< fused input norm, as GemvArgs::norm_w
+    float norm_eps = 1e-6f;
 };
 
 class Stream {
@@ -221,6 +250,8 @@ public:
     [[nodiscard]] virtual std::span<const VariantInfo> variants(OpId op, std::string_view form = {}) const = 0;
 
     virtual void dequant_rows(Stream&, const DequantRowsArgs&) = 0;
+    virtual void get_rows(Stream&, const GetRowsArgs&) = 0;
+    virtual void rms_norm(Stream&, const RmsNormArgs&) = 0;
     virtual void gemv(Stream&, const GemvArgs&) = 0;
     virtual void swiglu(Stream&, const EltwiseArgs&) = 0;
     virtual void gate_up_swiglu(Stream&, const GateUpArgs&) = 0;
@@ -247,5 +278,6 @@ inline constexpr std::uint32_t kGateUpGemm = 8;
 inline constexpr std::uint32_t kGemmSlabBf16M512 = 9;  // == HALO_MI_GEMM_SLAB_BF16_M512 (MATMUL)
 inline constexpr std::uint32_t kGateUpGemmM512 = 10;   // GATE_UP_SWIGLU on the 512-row-tile GEMM
 inline constexpr std::uint32_t kLmHeadFused = 11;      // LM_HEAD: argmax fused into the slab gemv
+inline constexpr std::uint32_t kRmsNorm = 12;          // RMS_NORM in cpu::rms_norm's order (bitwise)
 
 }  // namespace halo_mi::backend

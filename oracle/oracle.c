@@ -443,6 +443,23 @@ void oracle_swiglu(const float* g, const float* u, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = silu(g[i]) * u[i];
 }
 
+/* backends/cpu/ops_basic.cpp:18-33. */
+void oracle_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride,
+                     uint32_t rows, uint32_t cols, float eps) {
+    if (x_stride == 0) x_stride = cols;
+    if (out_stride == 0) out_stride = cols;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float* xr = x + (uint64_t)r * x_stride;
+        float* yr = out + (uint64_t)r * out_stride;
+        const float mean = oracle_dot(xr, xr, cols) / (float)cols;
+        const float inv = 1.0f / sqrtf(mean + eps);
+        for (uint32_t i = 0; i < cols; ++i) {
+            const float t = xr[i] * inv;
+            yr[i] = t * w[i];
+        }
+    }
+}
+
 /* src/models/qwen35.cpp:789-805: gemv(gate) -> gemv(up) -> swiglu. */
 int oracle_gate_up_swiglu(uint32_t type, const uint8_t* wg, const uint8_t* wu, uint64_t w_stride,
                           uint32_t rows, uint32_t cols, const float* x, uint32_t n_vec, float* out,

@@ -81,6 +81,14 @@ int oracle_matmul(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t r
 void oracle_swiglu(const float* g, const float* u, float* out, size_t n);
 
 /*
+ * cpu::rms_norm (backends/cpu/ops_basic.cpp:18-33): per row, mean = sum_squares(x) / cols with
+ * sum_squares = dot(x, x) (kernel_common.h:29), inv = 1 / sqrt(mean + eps), out = (x * inv) * w.
+ * Strides in floats (0 = cols); out may be x itself.
+ */
+void oracle_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride,
+                     uint32_t rows, uint32_t cols, float eps);
+
+/*
  * The reference FFN composition (src/models/qwen35.cpp:789-805): gemv(gate), gemv(up),
  * swiglu -> out[t][n] = silu(Wg x_t)[n] * (Wu x_t)[n]. Both weights share type and shape.
  */

@@ -40,6 +40,7 @@ def lib() -> ctypes.CDLL:
         "oracle_vec_dot_row": (INT, [U32, VP, VP, I64, ctypes.POINTER(ctypes.c_float)]),
         "oracle_matmul": (INT, [U32, VP, U64, U32, U32, VP, U64, U32, VP, U64, U32]),
         "oracle_swiglu": (None, [VP, VP, VP, ctypes.c_size_t]),
+        "oracle_rms_norm": (None, [VP, U64, VP, VP, U64, U32, U32, ctypes.c_float]),
         "oracle_gate_up_swiglu": (INT, [U32, VP, VP, U64, U32, U32, VP, U32, VP, U32]),
         "oracle_lm_head": (INT, [U32, VP, U64, U32, U32, VP, U32, U32, VP, VP, U32]),
         "oracle_partition_range": (None, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
@@ -151,6 +152,17 @@ def swiglu(g, u) -> np.ndarray:
     out = np.empty_like(g)
     lib().oracle_swiglu(g.ctypes.data, u.ctypes.data, out.ctypes.data, g.size)
     return out
+
+
+def rms_norm(x, w, eps: float = 1e-6) -> np.ndarray:
+    """cpu::rms_norm of the rows of x (2-D) with weight w."""
+    x = _f32(x)
+    x2 = x.reshape(-1, x.shape[-1]) if x.ndim > 1 else x.reshape(1, -1)
+    w = _f32(w)
+    out = np.empty_like(x2)
+    lib().oracle_rms_norm(x2.ctypes.data, x2.shape[1], w.ctypes.data, out.ctypes.data, x2.shape[1], x2.shape[0], x2.shape[1],
+                          float(eps))
+    return out.reshape(x.shape)
 
 
 def gate_up_swiglu(t: int, wg, wu, rows: int, cols: int, x, threads: int = 0) -> np.ndarray:

@@ -48,6 +48,8 @@ const char* type_name(uint32_t t) {
         case HALO_MI_Q4_0: return "Q4_0";
         case HALO_MI_Q8_0: return "Q8_0";
         case HALO_MI_Q4_K: return "Q4_K";
+        case HALO_MI_Q5_K: return "Q5_K";
+        case HALO_MI_IQ4_XS: return "IQ4_XS";
         default: return "Q6_K";
     }
 }
@@ -249,13 +251,88 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
         check(ok2, tn + ": gate_up_swiglu variant " + std::to_string(variant) + " within the bound");
     }
 
+    // RMS_NORM and the fused norm: rms_norm bitwise; the reference-order gemv with norm_w is
+    // bitwise rms_norm then cpu::matmul; the SLAB default within the GEMV bound on the CPU's
+    // normalized x plus the norm's own rounding (half the two sums-of-squares orders' error)
+    {
+        std::vector<float> nw(cols), xn(x.size());
+        for (uint32_t i = 0; i < cols; ++i) nw[i] = 0.5f + (float)(i % 7) * 0.125f;
+        oracle_rms_norm(x.data(), 0, nw.data(), xn.data(), 0, n_vec, cols, 1e-6f);
+        auto nwb = be.allocate((size_t)cols * 4, hb::Tier::Vram);
+        auto xnb = be.allocate(x.size() * 4, hb::Tier::Vram);
+        be.upload(st, hb::TensorRef::of(*nwb), bytes_of(nw));
+        hb::RmsNormArgs rn;
+        rn.x = hb::TensorRef::of(*xb);
+        rn.w = hb::TensorRef::of(*nwb);
+        rn.out = hb::TensorRef::of(*xnb);
+        rn.rows = n_vec;
+        rn.cols = cols;
+        be.rms_norm(st, rn);
+        std::vector<float> got(x.size());
+        download_y(*xnb, got);
+        check(std::memcmp(got.data(), xn.data(), got.size() * 4) == 0, tn + ": rms_norm is bitwise cpu::rms_norm");
+        std::vector<float> nref((size_t)n_vec * rows);
+        oracle_matmul(type, wg.data(), 0, rows, cols, xn.data(), 0, n_vec, nref.data(), 0, 1);
+        hb::GemvArgs an = a;
+        an.w = hb::TensorRef::of(*w_gguf);
+        an.norm_w = hb::TensorRef::of(*nwb);
+        be.gemv(st, an);
+        download_y(*yb, y);
+        check(std::memcmp(y.data(), nref.data(), y.size() * 4) == 0, tn + ": GGUF gemv with norm_w is bitwise rms_norm + matmul");
+        an.w = hb::TensorRef::of(*w_slab);
+        be.gemv(st, an);
+        download_y(*yb, y);
+        std::vector<double> ntol = slab_bound(type, wg, rows, cols, xn, n_vec);
+        const double extra = (0.5 * (cols / 8.0 + cols / 256.0 + 30) + 11) / ((cols / 8 + 4) + (cols / 32 + 64) + 4);
+        bool okn = true;
+        for (size_t i = 0; i < y.size(); ++i) okn &= std::fabs((double)y[i] - nref[i]) <= ntol[i] * (1.0 + extra) * 1.01;
+        check(okn, tn + ": SLAB gemv with norm_w within the bound");
+        an.norm_w = hb::TensorRef::of(*yb);  // norm_w overlapping y
+        check(code_of([&] { be.gemv(st, an); }) == (int)hb::ErrorCode::Kernel, tn + ": norm_w overlapping y -> Kernel");
+    }
+
+    // GET_ROWS with device ids and the status word
+    {
+        const std::vector<int32_t> idv = {7, 0, 129, -3, 7};
+        auto idb = be.allocate(idv.size() * 4, hb::Tier::Vram);
+        auto sb = be.allocate(4, hb::Tier::Vram);
+        auto ob = be.allocate(idv.size() * cols * 4, hb::Tier::Vram);
+        be.upload(st, hb::TensorRef::of(*idb), bytes_of(idv));
+        std::vector<float> sentinel(idv.size() * cols, 999.0f), got(idv.size() * cols);
+        be.upload(st, hb::TensorRef::of(*ob), bytes_of(sentinel));
+        hb::GetRowsArgs gr;
+        gr.type = static_cast<hb::DType>(type);
+        gr.table = hb::TensorRef::of(*w_slab);
+        gr.ids = hb::TensorRef::of(*idb);
+        gr.out = hb::TensorRef::of(*ob);
+        gr.n_rows = rows;
+        gr.cols = cols;
+        gr.n_ids = (uint32_t)idv.size();
+        gr.status = hb::TensorRef::of(*sb);
+        be.get_rows(st, gr);
+        uint32_t word = 0;
+        be.download(st, hb::TensorRef::of(*sb), std::as_writable_bytes(std::span<uint32_t>(&word, 1)));
+        download_y(*ob, got);
+        std::vector<float> want(cols);
+        bool okg = word == hb::kStatusBadIndex;
+        for (size_t i = 0; i < idv.size(); ++i) {
+            if (idv[i] < 0 || idv[i] >= (int32_t)rows) {
+                for (uint32_t c = 0; c < cols; ++c) okg &= got[i * cols + c] == 999.0f;
+                continue;
+            }
+            oracle_dequantize_row(type, wg.data() + (size_t)idv[i] * halo_mi_row_bytes(type, cols), want.data(), cols);
+            okg &= std::memcmp(got.data() + i * cols, want.data(), cols * 4) == 0;
+        }
+        check(okg, tn + ": get_rows bitwise, a bad id unwritten and reported in the status word");
+    }
+
     // error mapping (backend.h:24-26)
     hb::GemvArgs bad = a;
     bad.kernel.variant_id = 99;
     check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Config, tn + ": unknown variant -> Config");
     bad = a;
-    bad.norm_w = hb::TensorRef::of(*xb);
-    check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Unsupported, tn + ": fused norm -> Unsupported");
+    bad.gates.n_v = 1;
+    check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Unsupported, tn + ": GDN gates epilogue -> Unsupported");
     bad = a;
     bad.y = hb::TensorRef::of(*xb);  // y overlaps x
     check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Kernel, tn + ": y overlapping x -> Kernel");
@@ -268,8 +345,9 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
 
 int main(int argc, char** argv) {
     if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
-        std::printf("backend_pair: gemv (GGUF ref bitwise, SLAB bound, batch invariance), gate_up_swiglu, errors; "
-                    "types Q4_0 Q8_0 Q4_K Q6_K\n");
+        std::printf("backend_pair: gemv (GGUF ref bitwise, SLAB bound, batch invariance, fused norm), rms_norm, "
+                    "get_rows, lm_head, gate_up_swiglu, errors; "
+                    "types Q4_0 Q8_0 Q4_K Q6_K Q5_K IQ4_XS\n");
         return 0;
     }
     try {
@@ -281,6 +359,7 @@ int main(int argc, char** argv) {
         // (as the reference pins its own, tests/unit/backend/test_hip_backend.cpp:925-981)
         const std::pair<hb::OpId, std::vector<std::pair<uint32_t, std::string>>> pinned[] = {
             {hb::OpId::GetRows, {{hb::kDequantRows, "dequant_rows_exact"}}},
+            {hb::OpId::RmsNorm, {{hb::kRmsNorm, "rms_norm_cpu_order"}}},
             {hb::OpId::Gemv,
              {{hb::kGemvGgufRef, "gemv_gguf_ref_b256"}, {hb::kGemvSlab, "gemv_slab_w64"},
               {hb::kGemmSlabBf16, "gemm_slab_bf16_mfma"}, {hb::kGemvSlabAuto, "gemv_slab_auto"},
@@ -302,7 +381,7 @@ int main(int argc, char** argv) {
         std::vector<std::byte> host(64);
         check(code_of([&] { (void)be->import_host(std::span<std::byte>(host)); }) == (int)hb::ErrorCode::Unsupported,
               "import_host on a device -> Unsupported");
-        for (uint32_t t : {HALO_MI_Q4_0, HALO_MI_Q8_0, HALO_MI_Q4_K, HALO_MI_Q6_K}) {
+        for (uint32_t t : {HALO_MI_Q4_0, HALO_MI_Q8_0, HALO_MI_Q4_K, HALO_MI_Q6_K, HALO_MI_Q5_K, HALO_MI_IQ4_XS}) {
             std::printf("[case] backend_pair %s\n", type_name(t));
             std::fflush(stdout);
             run_type(*be, *st, t);

@@ -1,0 +1,284 @@
+"""GPU parity of the RMS-norm prologue of the matmul (GemvArgs::norm_w / norm_eps,
+include/halo/backend/backend.h:292-299), of RMS_NORM itself (cpu::rms_norm,
+backends/cpu/ops_basic.cpp:18-33) and of GET_ROWS (GetRowsArgs, backend.h:254-263; the HIP
+status word of backends/hip/src/ops.cpp:982-1012), against the oracle, through the C ABI.
+
+Acceptance: RMS_NORM, GET_ROWS and the reference-order GEMV with the norm are bitwise the CPU's;
+the GEMM variants stage exactly the CPU's normalized x, so the GEMM bounds apply to it
+unchanged; the fused SLAB GEMV is within the GEMV bound plus the norm's own rounding
+(helpers.norm_gemv_tol).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import (F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, gemm_emulated, gemm_tol,
+                     isclose_bits, make_weights, max_ratio, norm_gemv_tol, row_bytes, swiglu_tol)
+from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, strided_xy, to_dev
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def norm_inputs(cols, n_vec, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n_vec, cols)) * 3.0).astype(np.float32)
+    w = rng.uniform(0.25, 1.75, cols).astype(np.float32)
+    return x, w
+
+
+# ---- RMS_NORM ---------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (4, 100), (2, 4097), (5, 5120), (2, 17408), (64, 256)])
+def test_rms_norm_bitwise(hl, oracle, dev, rows, cols):
+    import torch
+
+    say("rms_norm", rows, cols)
+    x, w = norm_inputs(cols, rows, 10 + cols)
+    ref = oracle.rms_norm(x, w, EPS)
+    xd, wd = to_dev(x, dev), to_dev(w, dev)
+    out = torch.full_like(xd, SENTINEL)
+    hl.rms_norm(xd, wd, out, rows, cols, eps=EPS)
+    assert isclose_bits(host(out), ref), "RMS_NORM differs from cpu::rms_norm"
+    hl.rms_norm(xd, wd, xd, rows, cols, eps=EPS)  # in place, as the CPU allows
+    assert isclose_bits(host(xd), ref), "in-place RMS_NORM differs"
+
+
+def test_rms_norm_strided_and_rejects(hl, oracle, dev):
+    import torch
+
+    rows, cols = 3, 520
+    say("rms_norm strided", rows, cols)
+    x, w = norm_inputs(cols, rows, 7)
+    xp = np.full((rows, cols + 3), 5.0, np.float32)
+    xp[:, :cols] = x
+    xd, wd = to_dev(xp, dev), to_dev(w, dev)
+    out = torch.full((rows, cols + 5), SENTINEL, dtype=torch.float32, device=dev)
+    hl.rms_norm(xd, wd, out, rows, cols, eps=EPS, x_stride=cols + 3, out_stride=cols + 5)
+    o = host(out)
+    assert isclose_bits(o[:, :cols], oracle.rms_norm(x, w, EPS))
+    assert np.all(o[:, cols:] == SENTINEL), "padding written"
+    with pytest.raises(hl.HaloError) as e:  # out overlapping x without being x
+        hl.rms_norm(xd, wd, xd.data_ptr() + 4, rows, cols, eps=EPS, x_stride=cols + 3, out_stride=cols + 3)
+    assert e.value.code == hl.ErrorCode.Kernel
+
+
+# ---- GET_ROWS ---------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES + (F32,))
+@pytest.mark.parametrize("layout", ["gguf", "slab"])
+def test_get_rows_bitwise_and_bad_ids(hl, oracle, dev, t, layout):
+    import torch
+
+    if layout == "slab" and t == F32:
+        pytest.skip("F32 has no SLAB layout")
+    rows, cols = 70, 512
+    say("get_rows", NAMES[t], layout, rows, cols)
+    pad, off = ((4, 4) if t == F32 else (3, 1)) if layout == "gguf" else (0, 0)
+    buf, stride = make_weights(t, rows, cols, seed=900 + t, stride_pad=pad, offset=off)
+    ref = oracle.dequantize_rows(t, buf[off:], rows, cols, stride)
+    if layout == "gguf":
+        wd = to_dev(buf, dev)
+        table, lay, ts = wd.data_ptr() + off, hl.Layout.GGUF, stride
+    else:
+        table, lay, ts = slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, off), rows, cols), hl.Layout.SLAB, 0
+    ids = np.array([5, 0, 69, 5, -1, 33, 70, 64, 1], np.int32)
+    idd = to_dev(ids, dev)
+    status = torch.full((1,), 0x55, dtype=torch.int32, device=dev)  # cleared by the call
+    out = torch.full((ids.size, cols + 2), SENTINEL, dtype=torch.float32, device=dev)
+    hl.get_rows(t, lay, table, rows, cols, idd, ids.size, out, table_stride=ts, out_stride=cols + 2, status=status)
+    o = host(out)
+    for i, r in enumerate(ids):
+        if 0 <= r < rows:
+            assert isclose_bits(o[i, :cols], ref[r]), f"row {i} (id {r}) differs from tensor::dequantize_row"
+        else:
+            assert np.all(o[i] == SENTINEL), f"row {i} (bad id {r}) was written"
+    assert np.all(o[:, cols:] == SENTINEL)
+    assert int(host(status)[0]) == hl.STATUS_BAD_INDEX
+    good = to_dev(np.array([3, 2, 1], np.int32), dev)
+    hl.get_rows(t, lay, table, rows, cols, good, 3, out, table_stride=ts, out_stride=cols + 2, status=status)
+    assert int(host(status)[0]) == 0, "a call with valid ids leaves the status word clear"
+    assert isclose_bits(host(out)[:3, :cols], ref[[3, 2, 1]])
+
+
+def test_get_rows_rejects(hl, dev):
+    import torch
+
+    t, rows, cols = Q4_K, 8, 256
+    buf, _ = make_weights(t, rows, cols, seed=1)
+    wd = to_dev(buf, dev)
+    ids = to_dev(np.zeros(2, np.int32), dev)
+    out = torch.zeros((2, cols), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # out overlaps the table
+        hl.get_rows(t, hl.Layout.GGUF, wd, rows, cols, ids, 2, wd)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:
+        hl.get_rows(t, 7, wd, rows, cols, ids, 2, out)
+    assert e.value.code == hl.ErrorCode.Config
+    with pytest.raises(hl.HaloError) as e:
+        hl.get_rows(11, hl.Layout.SLAB, wd, rows, cols, ids, 2, out)
+    assert e.value.code == hl.ErrorCode.Unsupported
+
+
+# ---- the fused norm in the matmul ---------------------------------------------------------
+
+
+def run_norm_gemv(hl, dev, t, w, x, nw, rows, cols, variant, layout=None, w_stride=0, x_pad=0, y_pad=0):
+    xd, xs, yd, ys = strided_xy(dev, x, rows, x_pad, y_pad)
+    hl.gemv(t, w, xd, yd, rows, cols, x.shape[0], layout=hl.Layout.SLAB if layout is None else layout, w_stride=w_stride,
+            x_stride=xs, y_stride=ys, variant=variant, norm_w=to_dev(nw, dev), norm_eps=EPS)
+    y = host(yd)
+    assert np.all(y[:, rows:] == SENTINEL), "y padding overwritten"
+    return y[:, :rows]
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES + (F32,))
+def test_gemv_norm_reference_variant_bitwise(hl, oracle, dev, t):
+    rows, cols, n_vec = 37, (100 if t == F32 else 1024), 3
+    say("gemv norm gguf_ref", NAMES[t], rows, cols, n_vec)
+    pad, off = (4, 4) if t == F32 else (3, 1)
+    buf, stride = make_weights(t, rows, cols, seed=950 + t, stride_pad=pad, offset=off)
+    x, w = norm_inputs(cols, n_vec, 951 + t)
+    ref = oracle.matmul(t, buf[off:], rows, cols, oracle.rms_norm(x, w, EPS), w_stride=stride)
+    wd = to_dev(buf, dev)
+    y = run_norm_gemv(hl, dev, t, wd.data_ptr() + off, x, w, rows, cols, hl.Variant.GGUF_REF, layout=hl.Layout.GGUF,
+                      w_stride=stride, x_pad=5, y_pad=3)
+    assert isclose_bits(y, ref), "reference-order gemv with the norm is not bitwise rms_norm + cpu::matmul"
+
+
+NORM_CASES = [(130, 1024, 1), (130, 1024, 4), (576, 5120, 1), (576, 5120, 3), (640, 17408, 1), (70, 512, 6),
+              (65600, 512, 1), (65600, 512, 4)]  # the last two: more than 1024 slabs
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("case", NORM_CASES)
+def test_gemv_norm_slab_within_bound(hl, oracle, dev, t, case):
+    rows, cols, n_vec = case
+    if rows > 10000 and t not in (Q4_K, Q6_K):
+        pytest.skip("the many-slab shapes run for Q4_K and Q6_K")
+    say("gemv norm slab", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=960 + t + rows)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    x, w = norm_inputs(cols, n_vec, 961 + cols + n_vec)
+    xn = oracle.rms_norm(x, w, EPS)
+    ref = oracle.matmul(t, dense, rows, cols, xn)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, hl.Variant.SLAB_GEMV, x_pad=1, y_pad=2)
+    tol = norm_gemv_tol(oracle, t, dense, rows, cols, xn)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    fused-norm gemv {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q6_K, IQ4_XS))
+@pytest.mark.parametrize("rows,cols", [(130, 1024), (576, 5120)])
+def test_gemv_norm_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
+    say("gemv norm batch invariance", NAMES[t], rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=970 + t + rows)
+    slab = slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, 0), rows, cols)
+    x, w = norm_inputs(cols, 9, 971)
+    singles = np.stack([run_norm_gemv(hl, dev, t, slab, x[i:i + 1], w, rows, cols, hl.Variant.SLAB_GEMV)[0]
+                        for i in range(9)])
+    for n_vec in (2, 3, 4, 5, 9):
+        y = run_norm_gemv(hl, dev, t, slab, x[:n_vec], w, rows, cols, hl.Variant.SLAB_GEMV)
+        assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("n_vec,variant", [(40, 3), (300, 3), (600, 5)])
+def test_gemm_norm_within_bounds(hl, oracle, dev, t, n_vec, variant):
+    rows, cols = 130, 1024
+    say("gemm norm", NAMES[t], rows, cols, n_vec, variant)
+    buf, stride = make_weights(t, rows, cols, seed=980 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    x, w = norm_inputs(cols, n_vec, 981 + n_vec)
+    xn = oracle.rms_norm(x, w, EPS)
+    ref = oracle.matmul(t, dense, rows, cols, xn)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, variant, x_pad=4, y_pad=1)
+    err = np.abs(y.astype(np.float64) - ref)
+    tol = gemm_tol(oracle, t, dense, rows, cols, xn)
+    print(f"    gemm+norm vs cpu: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    emu, etol = gemm_emulated(oracle, t, dense, rows, cols, xn)  # the staged x is the CPU's xn in bf16
+    assert np.all(np.abs(y.astype(np.float64) - emu) <= etol)
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q6_K, Q5_K, IQ4_XS, Q8_0, Q4_0))
+@pytest.mark.parametrize("n_vec,variant", [(1, 2), (4, 2), (17, 3), (600, 5)])
+def test_gate_up_norm(hl, oracle, dev, t, n_vec, variant):
+    import torch
+
+    rows, cols = 96, 1024
+    say("gate_up norm", NAMES[t], rows, cols, n_vec, variant)
+    bg, sg = make_weights(t, rows, cols, seed=990 + t)
+    bu, su = make_weights(t, rows, cols, seed=995 + t)
+    dg, du = dense_of(bg, t, rows, cols, sg, 0), dense_of(bu, t, rows, cols, su, 0)
+    x, w = norm_inputs(cols, n_vec, 991 + n_vec)
+    xn = oracle.rms_norm(x, w, EPS)
+    ref = oracle.gate_up_swiglu(t, dg, du, rows, cols, xn)
+    g, u = oracle.matmul(t, dg, rows, cols, xn), oracle.matmul(t, du, rows, cols, xn)
+    if variant == 2:
+        tg, tu = norm_gemv_tol(oracle, t, dg, rows, cols, xn), norm_gemv_tol(oracle, t, du, rows, cols, xn)
+    else:
+        tg, tu = gemm_tol(oracle, t, dg, rows, cols, xn), gemm_tol(oracle, t, du, rows, cols, xn)
+    tol = swiglu_tol(g, u, tg, tu, ref, fast=variant != 2)
+    out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gate_up_swiglu(t, slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols), to_dev(x, dev), out,
+                      rows, cols, n_vec, variant=variant, norm_w=to_dev(w, dev), norm_eps=EPS)
+    err = np.abs(host(out).astype(np.float64) - ref)
+    print(f"    gate_up+norm worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q6_K))
+@pytest.mark.parametrize("variant", [0, 1, 3])
+def test_lm_head_norm(hl, oracle, dev, t, variant):
+    """The LM head with the output norm folded in: the argmax is the first maximum of the GPU's
+    own logits, the logits are within the variant's bound of the CPU's (rms_norm then matmul)."""
+    import torch
+
+    rows, cols, n_vec = 1000, 512, 3
+    say("lm_head norm", NAMES[t], rows, cols, n_vec, variant)
+    buf, stride = make_weights(t, rows, cols, seed=1000 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    x, w = norm_inputs(cols, n_vec, 1001)
+    xn = oracle.rms_norm(x, w, EPS)
+    if variant == 1:
+        wt, lay = to_dev(dense, dev), hl.Layout.GGUF
+    else:
+        wt, lay = slab_of(hl, dev, t, dense, rows, cols), hl.Layout.SLAB
+    res = torch.full((n_vec, 3), 0xABCD, dtype=torch.int32, device=dev)
+    y = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.lm_head(t, wt, to_dev(x, dev), res, rows, cols, n_vec, logits=y, layout=lay, variant=variant,
+               norm_w=to_dev(w, dev), norm_eps=EPS)
+    r, yl = host(res).view(np.uint32), host(y)
+    cpu, cpu_logits = oracle.lm_head(t, dense, rows, cols, xn)
+    if variant == 1:
+        assert isclose_bits(yl, cpu_logits) and np.array_equal(r, cpu), "reference variant: not the CPU's bits"
+        return
+    tol = gemm_tol(oracle, t, dense, rows, cols, xn) if variant == 3 else norm_gemv_tol(oracle, t, dense, rows, cols, xn)
+    assert np.all(np.abs(yl.astype(np.float64) - cpu_logits) <= tol)
+    for v in range(n_vec):
+        i = int(np.argmax(yl[v]))
+        assert r[v].tolist() == [i, int(yl[v, i:i + 1].view(np.uint32)[0]), 0]
+
+
+def test_norm_rejects(hl, dev):
+    import torch
+
+    t, rows, cols = Q4_K, 64, 256
+    buf, _ = make_weights(t, rows, cols, seed=2)
+    slab = slab_of(hl, dev, t, buf[:rows * row_bytes(t, cols)], rows, cols)
+    x = to_dev(np.ones((1, cols), np.float32), dev)
+    y = torch.zeros((1, rows), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # norm_w overlapping y
+        hl.gemv(t, slab, x, y, rows, cols, 1, norm_w=y)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:  # misaligned norm_w
+        hl.gemv(t, slab, x, y, rows, cols, 1, norm_w=x.data_ptr() + 2)
+    assert e.value.code == hl.ErrorCode.Kernel

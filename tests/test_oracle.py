@@ -294,6 +294,57 @@ def test_q5_k_and_iq4_xs_dequant_terms(oracle):
                 assert np.all(off[0, seg] == np.float32(128) * dl)
 
 
+# ---- rms_norm (backends/cpu/ops_basic.cpp:18-33) ------------------------------------------
+
+
+def test_rms_norm_sum_of_squares_in_the_dot_order(oracle):
+    """x[0] = 4096 and x[1 + 8 j] = 1 for j < 8 (64 columns, eps = 0, w = 1). In the dot's 8-lane
+    order the eight ones share lane 1 (p1 = 8) and 2^24 + 8 is exact: the sum is 16777224. Added
+    one at a time to 2^24, each 1 rounds away (ties to even): 16777216. The two orders give
+    different outputs, and the oracle must give the first."""
+    x = np.zeros(64, np.float32)
+    x[0] = 4096.0
+    x[1::8] = 1.0
+    f = np.float32
+
+    def expected(ss):
+        inv = f(1.0) / np.sqrt(f(ss) / f(64))
+        return (x * inv) * f(1.0)
+
+    good, seq = expected(16777224.0), expected(16777216.0)
+    assert not np.array_equal(good, seq)
+    y = oracle.rms_norm(x, np.ones(64, np.float32), eps=0.0)
+    assert np.array_equal(y, good)
+
+
+def test_rms_norm_closed_forms(oracle):
+    w = np.random.default_rng(3).standard_normal(64).astype(np.float32)
+    # x = 0.5 everywhere, eps = 0: mean 0.25, inv 2, x * inv = 1 exactly: out = w bitwise
+    assert np.array_equal(oracle.rms_norm(np.full(64, 0.5, np.float32), w, eps=0.0), w)
+    # a zero row: inv = 1 / sqrt(eps), out = 0 (with eps = 0, 0 * inf = NaN, as on the CPU)
+    assert np.array_equal(oracle.rms_norm(np.zeros(64, np.float32), w, eps=1e-6), np.zeros(64, np.float32) * w)
+    assert np.all(np.isnan(oracle.rms_norm(np.zeros(64, np.float32), w, eps=0.0)))
+
+
+@pytest.mark.parametrize("cols", [5, 8, 100, 5120])
+def test_rms_norm_within_fp64_bound_rows_independent(oracle, cols):
+    """Against fp64: the sum of squares has relative error <= (cols/8 + 4) u (positive terms,
+    longest chain), which moves inv by half of that; mean, +eps, sqrt, 1/ and the two products
+    add at most 6 u."""
+    rng = np.random.default_rng(cols)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    w = rng.standard_normal(cols).astype(np.float32)
+    y = oracle.rms_norm(x, w, eps=1e-6)
+    x64 = x.astype(np.float64)
+    inv = 1.0 / np.sqrt((x64 * x64).sum(axis=1, keepdims=True) / cols + np.float64(np.float32(1e-6)))
+    ref = x64 * inv * w.astype(np.float64)
+    tol = (0.5 * (cols / 8 + 4) + 8) * U * np.abs(ref) + 1e-300
+    assert np.all(np.abs(y - ref) <= tol)
+    # each row on its own gives the same bits (no state across rows)
+    for r in range(3):
+        assert np.array_equal(oracle.rms_norm(x[r], w, eps=1e-6), y[r])
+
+
 def test_dequant_rejects_bad_arguments(oracle):
     """tests/unit/tensor/test_dequant.cpp:74-87."""
     src = np.zeros(210, np.uint8)
