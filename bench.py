@@ -172,6 +172,7 @@ WORKLOADS = {
     "q5k_gate_up_swiglu_m512": ("gemm", "Q5_K", 17408, 5120, 512, 6),
     "iq4xs_gate_up_swiglu_m512": ("gemm", "IQ4_XS", 17408, 5120, 512, 7),
     "upload_q4k_17408x5120": ("upload", "Q4_K", 17408, 5120, 0, 2),
+    "model_upload_64_layers": ("model_upload", None, 0, 0, 64, 9),
     "q6k_lm_head_151936x5120_m1": ("head", "Q6_K", 151936, 5120, 1, 3),
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
@@ -242,6 +243,40 @@ def upload_case(hl, torch, t, rows, cols, seed, reps=10):
     return {"bytes": nbytes, "repack_us": repack_ms * 1e3, "repack_gbs": 2 * nbytes / (repack_ms * 1e-3) / 1e9,
             "upload_ms": upload_ms, "upload_gbs": nbytes / (upload_ms * 1e-3) / 1e9,
             "pageable_ms": pageable_ms, "pageable_gbs": nbytes / (pageable_ms * 1e-3) / 1e9}
+
+
+def model_upload_case(hl, torch, layers=64, seed=9):
+    """Row (f3): a model-scale load. `layers` copies of the config-5 layer (269 MB each, so 64
+    layers are 17.2 GB) from pageable host memory into SLAB images in one device arena with one
+    halo_mi_upload_tensors call; q|k and gate|up are uploaded as row-fused projections (the
+    pair kernel takes the up half at the gate half's end). Host bytes are random: the upload
+    moves bytes and does not read them. PCIe-inclusive, so never a headline value."""
+    rng = np.random.default_rng(seed)
+    plan = [("gdn_in", ["gdn_in"]), ("gdn_out", ["gdn_out"]), ("qk", ["q", "k"]), ("v", ["v"]), ("o", ["o"]),
+            ("gate_up", ["gate_up", "gate_up"]), ("down", ["down"])]
+    spec = {name: (int(getattr(hl.DType, tn)), rows, cols) for name, tn, rows, cols in LAYER}
+    src = {name: rng.integers(0, 256, size=rows * hl.row_bytes(t, cols), dtype=np.uint8)
+           for name, (t, rows, cols) in spec.items()}
+    per_layer, offs = 0, []
+    for fused, parts in plan:
+        t, _, cols = spec[parts[0]]
+        rows = sum(spec[p][1] for p in parts)
+        offs.append((fused, t, cols, parts, per_layer))
+        per_layer += hl.slab_bytes(t, rows, cols)
+    arena = torch.empty(per_layer * layers, dtype=torch.uint8, device="cuda")
+    base = arena.data_ptr()
+    tensors = [(t, cols, [(src[p], spec[p][1]) for p in parts], base + l * per_layer + off)
+               for l in range(layers) for (fused, t, cols, parts, off) in offs]
+    nbytes = layers * sum(len(src[p]) for _, parts in plan for p in parts)
+    hl.upload_tensors(tensors[:len(plan)])  # warm-up: page-in of the sources, the first pinned buffers
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    hl.upload_tensors(tensors)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    del arena
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "s": sec, "gbs": nbytes / sec / 1e9, "tensors": len(tensors)}
 
 
 def layer_case(hl, torch, m, steps, warmup, seed=5):
@@ -333,6 +368,11 @@ def main() -> int:
             r = upload_case(hl, torch, int(getattr(hl.DType, t)), rows, cols, seed)
             print(json.dumps({"workload": args.only, **{k: round(v, 3) for k, v in r.items()}}), flush=True)
             return 0
+        if kind == "model_upload":
+            r = model_upload_case(hl, torch, m, seed)
+            print(json.dumps({"workload": args.only, "GB": round(r["bytes"] / 1e9, 2), "s": round(r["s"], 3),
+                              "GB/s": round(r["gbs"], 1)}), flush=True)
+            return 0
         if kind == "layer":
             r = layer_case(hl, torch, m, args.steps, args.warmup, seed)
             print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
@@ -399,6 +439,11 @@ def main() -> int:
         extra["q4k_17408x5120_upload_from_pageable_host"] = {"ms": round(r["pageable_ms"], 3),
                                                              "GB/s": round(r["pageable_gbs"], 1),
                                                              "note": "as from an mmap'd GGUF file"}
+        log("row (f3): model-scale upload, 64 config-5 layers (17.2 GB) with row-fused q|k and gate|up")
+        r = model_upload_case(hl, torch, 64)
+        extra["model_upload_64_layers_pageable"] = {"GB": round(r["bytes"] / 1e9, 2), "s": round(r["s"], 3),
+                                                    "GB/s": round(r["gbs"], 1), "tensors": r["tensors"],
+                                                    "note": "host -> SLAB, PCIe-inclusive, one upload_tensors call"}
         log("config 1 on the GPU: Q4_0 GEMV 4096x4096 M=1")
         r = gemv_case(hl, torch, int(hl.DType.Q4_0), 4096, 4096, 1, 0, args.steps // 2, args.warmup)
         extra["q4_0_gemv_4096x4096_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}

@@ -37,4 +37,5 @@ from ._lib import (  # noqa: F401
     unpack_slab,
     unpack_slab_host,
     upload_slab,
+    upload_tensors,
 )

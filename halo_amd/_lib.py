@@ -123,6 +123,20 @@ class _LmHeadParams(ctypes.Structure):
     ]
 
 
+class _UploadPart(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("src_stride", ctypes.c_uint64), ("rows", ctypes.c_uint32)]
+
+
+class _UploadTensor(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_uint32),
+        ("cols", ctypes.c_uint32),
+        ("parts", ctypes.POINTER(_UploadPart)),
+        ("n_parts", ctypes.c_uint32),
+        ("dst", ctypes.c_void_p),
+    ]
+
+
 class _GetRowsParams(ctypes.Structure):
     _fields_ = [
         ("type", ctypes.c_uint32),
@@ -161,6 +175,7 @@ SIGNATURES = {
     "halo_mi_repack_slab_host": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP]),
     "halo_mi_unpack_slab_host": (_INT, [_U32, _VP, _U32, _U32, _VP, _U64]),
     "halo_mi_upload_slab": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP, _U64, _VP]),
+    "halo_mi_upload_tensors": (_INT, [ctypes.POINTER(_UploadTensor), _U32, _U64, _U32, _VP]),
     "halo_mi_fill_normal": (None, [_U64, _VP, _U64, ctypes.c_float, ctypes.c_float]),
     "halo_mi_quantize": (_INT, [_U32, _VP, _U64, _VP, _U32]),
 }
@@ -339,6 +354,24 @@ def repack_slab(t: int, src, rows: int, cols: int, dst, *, src_stride: int = 0, 
 
 def unpack_slab(t: int, src, rows: int, cols: int, dst, *, dst_stride: int = 0, stream=None) -> None:
     _check(lib().halo_mi_unpack_slab(int(t), _ptr(src), int(rows), int(cols), _ptr(dst), int(dst_stride), _stream(stream)))
+
+
+def upload_tensors(tensors, *, chunk_bytes: int = 0, host_threads: int = 0, stream=None) -> None:
+    """Model-scale upload (halo_mi_upload_tensors). tensors: a list of (type, cols, parts, dst)
+    with parts a list of (host rows, rows) or (host rows, rows, src_stride); host rows are numpy
+    uint8 arrays (e.g. memmaps of the GGUF tensors) or host addresses. The parts' rows are
+    concatenated into one SLAB matrix at dst (a row-fused projection when there are several)."""
+    keep = []
+    arr = (_UploadTensor * len(tensors))()
+    for i, (t, cols, parts, dst) in enumerate(tensors):
+        pa = (_UploadPart * len(parts))()
+        for j, part in enumerate(parts):
+            src, rows = part[0], part[1]
+            stride = part[2] if len(part) > 2 else 0
+            pa[j] = _UploadPart(src if isinstance(src, int) else src.ctypes.data, int(stride), int(rows))
+        keep.append(pa)
+        arr[i] = _UploadTensor(int(t), int(cols), pa, len(parts), _ptr(dst))
+    _check(lib().halo_mi_upload_tensors(arr, len(tensors), int(chunk_bytes), int(host_threads), _stream(stream)))
 
 
 def upload_slab(t: int, host_src, rows: int, cols: int, dst, *, src_stride: int = 0, chunk_bytes: int = 0,

@@ -468,41 +468,4 @@ int halo_mi_unpack_slab(uint32_t type, const void* src, uint32_t rows, uint32_t 
                               static_cast<hipStream_t>(stream));
 }
 
-int halo_mi_upload_slab(uint32_t type, const void* host_src, uint64_t src_stride, uint32_t rows, uint32_t cols, void* dst,
-                        uint64_t chunk_bytes, void* stream) {
-    clear_error();
-    int code;
-    const uint64_t rb = row_bytes_checked(type, cols, &code, "upload_slab");
-    if (code) return code;
-    if (!is_quant(type)) return set_error(HALO_MI_E_UNSUPPORTED, "upload_slab: type %u has no SLAB layout", type);
-    if (src_stride == 0) src_stride = rb;
-    if (rows > 1 && src_stride < rb) return set_error(HALO_MI_E_KERNEL, "upload_slab: row stride < row bytes");
-    if (rows == 0 || cols == 0) return HALO_MI_OK;
-    if (chunk_bytes == 0) chunk_bytes = 64ull << 20;
-    // Chunks are whole slabs so every repack writes complete slabs.
-    uint64_t chunk_rows = std::max<uint64_t>(chunk_bytes / rb / kSlabRows, 1) * kSlabRows;
-    chunk_rows = std::min<uint64_t>(chunk_rows, (uint64_t)(rows + kSlabRows - 1) / kSlabRows * kSlabRows);
-    auto st = static_cast<hipStream_t>(stream);
-    void* staging = nullptr;
-    hipError_t e = hipMalloc(&staging, chunk_rows * rb);
-    if (e != hipSuccess) return set_error(HALO_MI_E_MEMORY, "upload_slab: cannot allocate %llu staging bytes",
-                                          (unsigned long long)(chunk_rows * rb));
-    const SlabGeom g = slab_geom(type, cols);
-    const auto* src = static_cast<const uint8_t*>(host_src);
-    int rc = HALO_MI_OK;
-    for (uint64_t r0 = 0; r0 < rows && rc == HALO_MI_OK; r0 += chunk_rows) {
-        const uint32_t n = (uint32_t)std::min<uint64_t>(chunk_rows, rows - r0);
-        if (src_stride == rb) e = hipMemcpyAsync(staging, src + r0 * rb, (uint64_t)n * rb, hipMemcpyHostToDevice, st);
-        else e = hipMemcpy2DAsync(staging, rb, src + r0 * src_stride, src_stride, rb, n, hipMemcpyHostToDevice, st);
-        if (e != hipSuccess) { rc = hip_status(e, "upload_slab copy"); break; }
-        rc = halo_mi_repack_slab(type, staging, rb, n, cols, static_cast<uint8_t*>(dst) + (r0 / kSlabRows) * g.slab_bytes, st);
-        if (rc == HALO_MI_OK) {
-            e = hipStreamSynchronize(st);  // the staging buffer is reused by the next chunk
-            if (e != hipSuccess) rc = hip_status(e, "upload_slab sync");
-        }
-    }
-    (void)hipFree(staging);
-    return rc;
-}
-
 }  // extern "C"

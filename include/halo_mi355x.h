@@ -281,12 +281,41 @@ int halo_mi_repack_slab_host(uint32_t type, const void* src, uint64_t src_stride
 int halo_mi_unpack_slab_host(uint32_t type, const void* src, uint32_t rows, uint32_t cols,
                              void* dst, uint64_t dst_stride);
 /*
- * Upload from host memory (e.g. the mmap'd GGUF tensor, GgufFile::tensor_data,
- * src/model/gguf.cpp:540-549) straight into a SLAB image on the device. Streams the rows in
- * chunks of about `chunk_bytes` (0 = 64 MiB) through one device staging buffer and repacks
- * each chunk on the device; the call returns after the last chunk has been repacked.
+ * Model-scale upload: host GGUF rows (e.g. the mmap'd file, GgufFile::tensor_data,
+ * src/model/gguf.cpp:540-549) -> SLAB images in device memory, for many tensors in one call.
  * Replaces Backend::import_host_readonly's device copy (src/backend/hip_adapter.cpp:502-515)
- * plus the loader's repack step.
+ * plus the loader's repack, and builds the row-fused projections of try_make_fused
+ * (src/models/qwen35.cpp:253-288; gate|up, q|k|v, beta|alpha) on the way: a tensor's parts are
+ * matrices of its type and cols whose rows are concatenated, in order, into one matrix.
+ *   parts[i].src: host rows, src_stride bytes apart (0 = row_bytes); any host memory.
+ *   dst: device memory of halo_mi_slab_bytes(type, sum of the parts' rows, cols) bytes,
+ *        16-byte aligned; destinations must not overlap.
+ *   chunk_bytes: rows move in chunks of about this size (0 = 64 MiB), whole slabs of one tensor;
+ *   host_threads: threads that gather a chunk into pinned memory (0 = up to 8).
+ * A three-stage pipeline over 4 chunk slots: the host gathers chunk i + 2 into pinned memory
+ * while the copy engine moves chunk i + 1 (on a stream of its own) and `stream` repacks chunk i.
+ * Returns after the last chunk has been repacked. The GGUF bytes remain recoverable
+ * (halo_mi_unpack_slab).
+ */
+typedef struct halo_mi_upload_part {
+    const void* src;
+    uint64_t src_stride;
+    uint32_t rows;
+} halo_mi_upload_part;
+
+typedef struct halo_mi_upload_tensor {
+    uint32_t type;
+    uint32_t cols;
+    const halo_mi_upload_part* parts;
+    uint32_t n_parts;
+    void* dst;
+} halo_mi_upload_tensor;
+
+int halo_mi_upload_tensors(const halo_mi_upload_tensor* tensors, uint32_t n, uint64_t chunk_bytes,
+                           uint32_t host_threads, void* stream);
+
+/*
+ * One tensor, one part: halo_mi_upload_tensors with host_threads = 0.
  */
 int halo_mi_upload_slab(uint32_t type, const void* host_src, uint64_t src_stride, uint32_t rows,
                         uint32_t cols, void* dst, uint64_t chunk_bytes, void* stream);
