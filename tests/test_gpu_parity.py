@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import (BLOCK, F32, NAMES, Q4_0, Q4_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
+from helpers import (BLOCK, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
                      gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 
 pytestmark = pytest.mark.gpu
@@ -366,6 +366,8 @@ def synth(hl, t, rows, cols, seed, outliers=0.0):
     (Q4_K, 17408, 5120, 2, 0.0),     # config 2: FFN gate/up shape
     (Q6_K, 5120, 17408, 3, 0.0),     # config 3: ffn_down
     (Q4_0, 4096, 4096, 0, 0.0),      # config 1
+    (Q5_K, 17408, 5120, 6, 0.0),     # the UD pack's other formats at the gate/up shape
+    (IQ4_XS, 17408, 5120, 7, 0.0),
 ])
 @pytest.mark.parametrize("n_vec", [1, 4])
 def test_baseline_shapes_gemv(hl, oracle, dev, t, rows, cols, seed, outliers, n_vec):
