@@ -177,6 +177,7 @@ WORKLOADS = {
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
     "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
+    "hybrid_layer_m1_qk_fused": ("layer_qk", None, 0, 0, 1, 5),
 }
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
@@ -279,12 +280,18 @@ def model_upload_case(hl, torch, layers=64, seed=9):
     return {"bytes": nbytes, "s": sec, "gbs": nbytes / sec / 1e9, "tensors": len(tensors)}
 
 
-def layer_case(hl, torch, m, steps, warmup, seed=5):
+def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False):
     """All matmuls of one config-5 layer as one step (the fused gate/up pair is one call), over
-    enough copies of the layer's weights that the MALL cannot serve repeats."""
+    enough copies of the layer's weights that the MALL cannot serve repeats. fuse_qk: q and k
+    (both Q4_K, 5120 columns) as one row-fused 7168-row matrix, one GEMV instead of two (the
+    reference's try_make_fused; v is Q6_K, so it stays apart)."""
+    layer = LAYER
+    if fuse_qk:
+        layer = [(n, tn, r, c) for n, tn, r, c in LAYER if n not in ("q", "k")]
+        layer.insert(2, ("qk", "Q4_K", 6144 + 1024, 5120))
     mats = []
     one_copy = 0
-    for i, (name, tn, rows, cols) in enumerate(LAYER):
+    for i, (name, tn, rows, cols) in enumerate(layer):
         t = int(getattr(hl.DType, tn))
         ws = [make_weights(hl, t, rows, cols, seed * 100 + 10 * i + j) for j in range(2 if name == "gate_up" else 1)]
         dev = []
@@ -373,8 +380,8 @@ def main() -> int:
             print(json.dumps({"workload": args.only, "GB": round(r["bytes"] / 1e9, 2), "s": round(r["s"], 3),
                               "GB/s": round(r["gbs"], 1)}), flush=True)
             return 0
-        if kind == "layer":
-            r = layer_case(hl, torch, m, args.steps, args.warmup, seed)
+        if kind in ("layer", "layer_qk"):
+            r = layer_case(hl, torch, m, args.steps, args.warmup, seed, fuse_qk=kind == "layer_qk")
             print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                               "TFLOP/s": round(r["tflops"], 2)}), flush=True)
             return 0
@@ -452,6 +459,11 @@ def main() -> int:
             r = layer_case(hl, torch, m, max(20, args.steps // 20), 5)
             extra[f"hybrid_layer_m{m}"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                            "TFLOP/s": round(r["tflops"], 2)}
+        for m in (1, 4):
+            log(f"config 5 with q|k row-fused (one GEMV for both) M={m}")
+            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5, fuse_qk=True)
+            extra[f"hybrid_layer_m{m}_qk_fused"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                                    "TFLOP/s": round(r["tflops"], 2)}
         for m in (2, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
             r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, max(20, args.steps // 20), 5)
