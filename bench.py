@@ -178,6 +178,8 @@ WORKLOADS = {
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
     "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
     "hybrid_layer_m1_qk_fused": ("layer_qk", None, 0, 0, 1, 5),
+    "hybrid_layer_m1_qkv_group": ("layer_qkv", None, 0, 0, 1, 5),
+    "hybrid_layer_m1_qk_fused_qkv_group": ("layer_qk_qkv", None, 0, 0, 1, 5),
 }
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
@@ -280,11 +282,12 @@ def model_upload_case(hl, torch, layers=64, seed=9):
     return {"bytes": nbytes, "s": sec, "gbs": nbytes / sec / 1e9, "tensors": len(tensors)}
 
 
-def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False):
+def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False, group_qkv=False):
     """All matmuls of one config-5 layer as one step (the fused gate/up pair is one call), over
     enough copies of the layer's weights that the MALL cannot serve repeats. fuse_qk: q and k
     (both Q4_K, 5120 columns) as one row-fused 7168-row matrix, one GEMV instead of two (the
-    reference's try_make_fused; v is Q6_K, so it stays apart)."""
+    reference's try_make_fused; v is Q6_K, so it stays apart). group_qkv: q (or q|k), k and v
+    in one halo_mi_gemv_group launch (two weight types)."""
     layer = LAYER
     if fuse_qk:
         layer = [(n, tn, r, c) for n, tn, r, c in LAYER if n not in ("q", "k")]
@@ -307,11 +310,16 @@ def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False):
     ys = {name: torch.empty((m, rows), dtype=torch.float32, device="cuda") for name, _, rows, _, _, _ in mats}
 
     def launch(i):
+        group = []
         for name, t, rows, cols, dev, _ in copies[i]:
             if name == "gate_up":
                 hl.gate_up_swiglu(t, dev[0], dev[1], xs[cols], ys[name], rows, cols, m)
+            elif group_qkv and name in ("q", "k", "qk", "v"):
+                group.append((t, dev[0], rows, ys[name]))
             else:
                 hl.gemv(t, dev[0], xs[cols], ys[name], rows, cols, m)
+        if group:
+            hl.gemv_group(group, xs[5120], 5120, m)
 
     ms, nsteps = time_graph(torch, launch, n_copies, steps, warmup)
     algo = sum(wb + 4 * m * cols + 4 * m * rows for name, _, rows, cols, _, wb in mats)
@@ -380,8 +388,9 @@ def main() -> int:
             print(json.dumps({"workload": args.only, "GB": round(r["bytes"] / 1e9, 2), "s": round(r["s"], 3),
                               "GB/s": round(r["gbs"], 1)}), flush=True)
             return 0
-        if kind in ("layer", "layer_qk"):
-            r = layer_case(hl, torch, m, args.steps, args.warmup, seed, fuse_qk=kind == "layer_qk")
+        if kind.startswith("layer"):
+            r = layer_case(hl, torch, m, args.steps, args.warmup, seed, fuse_qk="qk" in kind.split("_")[1:],
+                           group_qkv=kind.endswith("qkv"))
             print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                               "TFLOP/s": round(r["tflops"], 2)}), flush=True)
             return 0
@@ -464,6 +473,10 @@ def main() -> int:
             r = layer_case(hl, torch, m, max(20, args.steps // 20), 5, fuse_qk=True)
             extra[f"hybrid_layer_m{m}_qk_fused"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                                     "TFLOP/s": round(r["tflops"], 2)}
+            log(f"config 5 with q, k, v in one grouped launch M={m}")
+            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5, group_qkv=True)
+            extra[f"hybrid_layer_m{m}_qkv_group"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                                     "TFLOP/s": round(r["tflops"], 2)}
         for m in (2, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
             r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, max(20, args.steps // 20), 5)

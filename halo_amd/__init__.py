@@ -24,6 +24,7 @@ from ._lib import (  # noqa: F401
     fill_normal,
     gate_up_swiglu,
     gemv,
+    gemv_group,
     get_rows,
     lib,
     lm_head,

@@ -111,6 +111,24 @@ class _GateUpParams(ctypes.Structure):
     ]
 
 
+class _GemvSegment(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_uint32), ("w", ctypes.c_void_p), ("rows", ctypes.c_uint32), ("y", ctypes.c_void_p),
+                ("y_stride", ctypes.c_uint64)]
+
+
+class _GemvGroupParams(ctypes.Structure):
+    _fields_ = [
+        ("segs", ctypes.POINTER(_GemvSegment)),
+        ("n_segs", ctypes.c_uint32),
+        ("x", ctypes.c_void_p),
+        ("x_stride", ctypes.c_uint64),
+        ("cols", ctypes.c_uint32),
+        ("n_vec", ctypes.c_uint32),
+        ("norm_w", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
+    ]
+
+
 class _LmHeadParams(ctypes.Structure):
     _fields_ = [
         ("gemv", _GemvParams),
@@ -162,6 +180,7 @@ _U32, _U64, _VP, _INT = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctype
 SIGNATURES = {
     "halo_mi_last_error": (ctypes.c_char_p, []),
     "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
+    "halo_mi_gemv_group": (_INT, [ctypes.POINTER(_GemvGroupParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
     "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
     "halo_mi_swiglu": (_INT, [_VP, _U64, _VP, _U64, _VP, _U64, _U32, _U32, _VP]),
@@ -297,6 +316,18 @@ def gemv(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, layout: int = Lay
     p = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(y), int(y_stride),
                     int(rows), int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
     _check(lib().halo_mi_gemv(ctypes.byref(p), _stream(stream)))
+
+
+def gemv_group(segs, x, cols: int, n_vec: int, *, x_stride: int = 0, norm_w=None, norm_eps: float = 1e-6,
+               stream=None) -> None:
+    """Grouped GEMV (halo_mi_gemv_group): segs is a list of (type, w, rows, y) or (type, w, rows, y,
+    y_stride), SLAB matrices that share x; one launch per pair of weight types."""
+    arr = (_GemvSegment * len(segs))()
+    for i, seg in enumerate(segs):
+        t, w, rows, y = seg[:4]
+        arr[i] = _GemvSegment(int(t), _ptr(w), int(rows), _ptr(y), int(seg[4]) if len(seg) > 4 else 0)
+    p = _GemvGroupParams(arr, len(segs), _ptr(x), int(x_stride), int(cols), int(n_vec), _ptr(norm_w), float(norm_eps))
+    _check(lib().halo_mi_gemv_group(ctypes.byref(p), _stream(stream)))
 
 
 def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB,

@@ -198,6 +198,54 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     return launch_gemm_pc<false>(p->type, a, st);
 }
 
+int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream) {
+    clear_error();
+    const char* op = "MATMUL_GROUP";
+    if (!p) return set_error(HALO_MI_E_KERNEL, "%s: null params", op);
+    if (p->n_segs == 0 || p->n_vec == 0) return HALO_MI_OK;
+    if (!p->segs) return set_error(HALO_MI_E_KERNEL, "%s: null segment list", op);
+    if (p->n_segs > HALO_MI_GEMV_GROUP_MAX)
+        return set_error(HALO_MI_E_UNSUPPORTED, "%s: %u segments (at most %u)", op, p->n_segs, HALO_MI_GEMV_GROUP_MAX);
+    if (!p->x) return set_error(HALO_MI_E_KERNEL, "%s: operand x is empty", op);
+    const uint64_t xs = p->x_stride ? p->x_stride : p->cols;
+    if (p->n_vec > 1 && xs < p->cols) return set_error(HALO_MI_E_KERNEL, "%s: x row stride < cols", op);
+    if (reinterpret_cast<uintptr_t>(p->x) % 4) return set_error(HALO_MI_E_KERNEL, "%s: x must be 4-byte aligned", op);
+    const uint64_t xext = extent(p->n_vec, xs * 4, (uint64_t)p->cols * 4);
+    GroupSeg segs[HALO_MI_GEMV_GROUP_MAX];
+    uint64_t wext[HALO_MI_GEMV_GROUP_MAX], yext[HALO_MI_GEMV_GROUP_MAX];
+    for (uint32_t i = 0; i < p->n_segs; ++i) {
+        const halo_mi_gemv_segment& g = p->segs[i];
+        int code;
+        (void)row_bytes_checked(g.type, p->cols, &code, op);
+        if (code) return code;
+        if (!is_quant(g.type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: segment %u: type %u has no SLAB layout", op, i, g.type);
+        const uint64_t ys = g.y_stride ? g.y_stride : g.rows;
+        if (g.rows && (!g.w || !g.y)) return set_error(HALO_MI_E_KERNEL, "%s: segment %u: operand w or y is empty", op, i);
+        if (p->n_vec > 1 && ys < g.rows) return set_error(HALO_MI_E_KERNEL, "%s: segment %u: y row stride < rows", op, i);
+        if ((reinterpret_cast<uintptr_t>(g.w) % 16) || (reinterpret_cast<uintptr_t>(g.y) % 4))
+            return set_error(HALO_MI_E_KERNEL, "%s: segment %u: w must be 16-byte and y 4-byte aligned", op, i);
+        wext[i] = halo_mi_slab_bytes(g.type, g.rows, p->cols);
+        yext[i] = g.rows ? extent(p->n_vec, ys * 4, (uint64_t)g.rows * 4) : 0;
+        segs[i] = GroupSeg{g.type, g.w, g.rows, g.y, ys};
+    }
+    for (uint32_t i = 0; i < p->n_segs; ++i) {
+        const void* y = p->segs[i].y;
+        if (ranges_overlap(y, yext[i], p->x, xext) ||
+            ranges_overlap(y, yext[i], p->norm_w, p->norm_w ? (uint64_t)p->cols * 4 : 0))
+            return set_error(HALO_MI_E_KERNEL, "%s: segment %u: y overlaps x or norm_w", op, i);
+        for (uint32_t j = 0; j < p->n_segs; ++j) {
+            if (ranges_overlap(y, yext[i], p->segs[j].w, wext[j]))
+                return set_error(HALO_MI_E_KERNEL, "%s: segment %u: y overlaps the weights of segment %u", op, i, j);
+            if (j != i && ranges_overlap(y, yext[i], p->segs[j].y, yext[j]))
+                return set_error(HALO_MI_E_KERNEL, "%s: the outputs of segments %u and %u overlap", op, i, j);
+        }
+    }
+    if (p->norm_w && reinterpret_cast<uintptr_t>(p->norm_w) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: norm_w must be 4-byte aligned", op);
+    return launch_gemv_group(segs, p->n_segs, p->x, xs, p->cols, p->n_vec, p->norm_w, p->norm_eps,
+                             static_cast<hipStream_t>(stream));
+}
+
 int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
     clear_error();
     if (!p) return set_error(HALO_MI_E_KERNEL, "lm_head: null params");

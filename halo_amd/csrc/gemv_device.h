@@ -1,0 +1,974 @@
+// Device code of the slab GEMV kernels (k_gemv.hip: the plain launches; k_gemv_group.hip: the
+// grouped launch over several matrices that share x). Each including file gets its own copy
+// (an anonymous namespace), so the two are compiled in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+
+#include "device.h"
+#include "launch.h"
+
+namespace halo_mi {
+namespace {
+
+using namespace dev;
+
+// ==========================================================================================
+// Reference-order GEMV over GGUF rows (bitwise equal to cpu::matmul)
+// ==========================================================================================
+
+// Block of 256 threads = 32 groups of 8 lanes; group -> one W row, every x vector.
+__global__ __launch_bounds__(256) void k_gemv_gguf_ref(uint32_t type, const uint8_t* __restrict__ w, uint64_t w_stride,
+                                                       const float* __restrict__ x, uint64_t x_stride,
+                                                       float* __restrict__ y, uint64_t y_stride, uint32_t rows,
+                                                       uint32_t cols, uint32_t n_vec) {
+#pragma clang fp contract(off)
+    const uint32_t j = threadIdx.x & 7u;
+    const uint32_t n = blockIdx.x * 32u + (threadIdx.x >> 3);
+    const bool live = n < rows;
+    const uint8_t* row = w + (uint64_t)(live ? n : 0) * w_stride;
+    const uint32_t full = cols - cols % 8u;
+    for (uint32_t t = 0; t < n_vec; ++t) {
+        const float* xt = x + (uint64_t)t * x_stride;
+        float p = 0.0f;
+        if (live)
+            for (uint32_t i = j; i < full; i += 8) {
+                const float prod = xt[i] * gguf_elem(type, row, i);
+                p = p + prod;
+            }
+        // ((p0+p4)+(p1+p5)) + ((p2+p6)+(p3+p7)), then + tail, exactly as the CPU dot.
+        const float q = p + __shfl_down(p, 4, 8);   // lanes 0..3: p_j + p_{j+4}
+        const float r = q + __shfl_down(q, 1, 8);   // lane 0: left, lane 2: right
+        const float s = r + __shfl_down(r, 2, 8);   // lane 0: left + right
+        if (j == 0 && live) {
+            float tail = 0.0f;
+            for (uint32_t i = full; i < cols; ++i) {
+                const float prod = xt[i] * gguf_elem(type, row, i);
+                tail = tail + prod;
+            }
+            y[(uint64_t)t * y_stride + n] = s + tail;
+        }
+    }
+}
+
+// ==========================================================================================
+// SLAB GEMV: one row per lane; a one-wave workgroup owns a (slab, K chunk) unit
+// ==========================================================================================
+//
+// The grid is slabs x ks units (ks K chunks per slab, chosen so the chip gets many more
+// units than CUs). A unit first issues the loads of its first slot group (8 slots = 256
+// weights per row: eight contiguous 1 KB wave loads plus the group's scale records), then
+// stages its slice of x in LDS while they are in flight, and streams the remaining groups
+// with the next group's loads issued before the current group is computed. With ks > 1 the
+// per-row partials go to a workspace; the unit that finishes last for a slab (an atomic
+// counter per slab) adds the ks partials in chunk order and writes y, so the result does
+// not depend on scheduling.
+
+
+
+// Q6_K slot record -> 6-bit quants as bytes, like q6_slot_bytes (decode.h), for the GEMV.
+__device__ __forceinline__ void q6_slot_bytes_gemv(const uint4& ql, const uint2& qh, uint32_t lo[4], uint32_t hi[4]) {
+    const uint32_t L[4] = {ql.x, ql.y, ql.z, ql.w};
+    const uint32_t H[2] = {qh.x, qh.y};
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t a = L[2 * w], b = L[2 * w + 1], h = H[w];
+        lo[2 * w] = and_or_opaque(a, 0x0F0F0F0Fu, h & 0x30303030u);
+        hi[2 * w] = and_or_opaque(a >> 4, 0x0F0F0F0Fu, (h >> 2) & 0x30303030u);
+        lo[2 * w + 1] = and_or_opaque(b, 0x0F0F0F0Fu, (h << 4) & 0x30303030u);
+        hi[2 * w + 1] = and_or_opaque(b >> 4, 0x0F0F0F0Fu, (h << 2) & 0x30303030u);
+    }
+}
+
+template <uint32_t T>
+struct SlotGroup;
+
+template <>
+struct SlotGroup<kQ4_K> {
+    uint4 q[8];
+    uint4 hdr;
+};
+template <>
+struct SlotGroup<kQ6_K> {
+    uint4 ql[8];
+    uint2 qh[8];
+    uint4 sc;
+    uint32_t d;
+};
+template <>
+struct SlotGroup<kQ5_K> {
+    uint4 q[8];
+    uint32_t qh[8];
+    uint4 hdr;
+};
+template <>
+struct SlotGroup<kIQ4_XS> {
+    uint4 q[8];
+    uint2 hdr;
+};
+template <>
+struct SlotGroup<kQ4_0> {
+    uint4 q[8];
+    uint32_t d[8];
+};
+template <>
+struct SlotGroup<kQ8_0> {
+    uint4 qa[8], qb[8];
+    uint32_t d[8];
+};
+
+// The weight records are read once per launch: nontemporal loads, so the stream does not
+// displace reusable lines (x, partials) from the caches.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ld_nt16(const uint8_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_nt8(const uint8_t* p) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld_nt2(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __restrict__ slab, const SlabGeom& g,
+                                           uint32_t lane, uint32_t grp, uint32_t S) {
+    const uint32_t sb = grp * 8;
+    // scales first, then the quants in slot order: loads complete in order, so slot j can be
+    // used as soon as its own record has arrived
+    if constexpr (T == kQ4_K) {
+        G.hdr = ld_nt16(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+    } else if constexpr (T == kQ5_K) {
+        G.hdr = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+            G.qh[j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 4));
+        }
+    } else if constexpr (T == kIQ4_XS) {
+        G.hdr = ld_nt8(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+    } else if constexpr (T == kQ6_K) {
+        G.d = ld_nt2(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
+        G.sc = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+            G.qh[j] = ld_nt8(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+        }
+    } else if constexpr (T == kQ4_0) {
+        const uint32_t n = min(8u, S - sb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((uint32_t)j < n) {
+                G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+                G.d[j] = ld_nt2(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 2);
+            }
+    } else {
+        const uint32_t n = min(8u, S - sb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if ((uint32_t)j < n) {
+                G.qa[j] = ld_nt16(slab + g.q_off + (((uint64_t)(sb + j) * 2) * 64 + lane) * 16);
+                G.qb[j] = ld_nt16(slab + g.q_off + (((uint64_t)(sb + j) * 2 + 1) * 64 + lane) * 16);
+                G.d[j] = ld_nt2(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 2);
+            }
+    }
+}
+
+// x through the constant address space: wave-uniform loads become scalar loads, so x is
+// read through the scalar cache into SGPRs and fed to the FMAs as scalar operands.
+typedef __attribute__((address_space(4))) const float cfloat;
+typedef __attribute__((address_space(4))) const float4 cfloat4;
+
+// 4-bit slot record against x (SGPR): lo = sum x[t] q[t] (t < 16), hi = sum x[16 + t] q[16 + t],
+// in units of fp8_unit().
+__device__ __forceinline__ void dot_nibbles_s(const uint4& q, cfloat* xs, float& lo, float& hi) {
+    const uint32_t Q[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t a = Q[i] & 0x0F0F0F0Fu, b = (Q[i] >> 4) & 0x0F0F0F0Fu;
+        const float2v a01 = __builtin_amdgcn_cvt_pk_f32_fp8(a, false), a23 = __builtin_amdgcn_cvt_pk_f32_fp8(a, true);
+        const float2v b01 = __builtin_amdgcn_cvt_pk_f32_fp8(b, false), b23 = __builtin_amdgcn_cvt_pk_f32_fp8(b, true);
+        lo = fmaf(xs[4 * i + 0], a01[0], lo);
+        lo = fmaf(xs[4 * i + 1], a01[1], lo);
+        lo = fmaf(xs[4 * i + 2], a23[0], lo);
+        lo = fmaf(xs[4 * i + 3], a23[1], lo);
+        hi = fmaf(xs[16 + 4 * i + 0], b01[0], hi);
+        hi = fmaf(xs[16 + 4 * i + 1], b01[1], hi);
+        hi = fmaf(xs[16 + 4 * i + 2], b23[0], hi);
+        hi = fmaf(xs[16 + 4 * i + 3], b23[1], hi);
+    }
+}
+
+__device__ __forceinline__ void dot_bytes_s(const uint32_t A[4], const uint32_t B[4], cfloat* xs, float& lo, float& hi) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            lo = fmaf(xs[4 * i + k], ubyte(A[i], k), lo);
+            hi = fmaf(xs[16 + 4 * i + k], ubyte(B[i], k), hi);
+        }
+}
+
+// Half-slot sums (16 x values each) of the up-to-4 slot groups starting at group gb, held one
+// per lane: lane 16 i + h has half-slot h of group gb + i. Read back with xsum_at (readlane),
+// so the main loop never waits on memory for them.
+__device__ __forceinline__ float wave_xsums(const float* __restrict__ x, uint32_t gb, uint32_t S, uint32_t lane) {
+    const uint32_t e = gb * 256 + lane * 16;  // this lane's 16 elements
+    float s = 0.0f;
+    if (e < S * 32) {
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) s += (x[e + k] + x[e + k + 1]) + (x[e + k + 2] + x[e + k + 3]);
+    }
+    return s;
+}
+__device__ __forceinline__ float xsum_at(float xsv, uint32_t idx) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xsv), idx));
+}
+
+// One loaded group against NV vectors; x of vector v at x + v * x_stride (SGPR loads),
+// X[v][h] the group's half-slot sums.
+template <uint32_t T, int NV>
+__device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t grp, uint32_t gi, uint32_t S, cfloat* x,
+                                              uint64_t x_stride, const float (&xsv)[NV], float inv_unit,
+                                              float acc[NV]) {
+    const uint32_t sbase = grp * 8, hb = gi * 16;  // this group's half-slot sums: lanes hb .. hb + 15
+    if constexpr (T == kQ4_K) {
+        // d is scaled by 1 / fp8_unit (a power of two: exact) to undo the fp8 conversion
+        const float d = h2f(G.hdr.x & 0xFFFFu) * inv_unit, dmin = h2f(G.hdr.x >> 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sc, m;
+            q4k_sc_m(G.hdr.y, G.hdr.z, G.hdr.w, j, sc, m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_nibbles_s(G.q[j], x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(d1, lo + hi, acc[v]);
+                acc[v] = fmaf(-m1, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), acc[v]);
+            }
+        }
+    } else if constexpr (T == kQ6_K) {
+        const float d = h2f(G.d);
+        const uint32_t SC[4] = {G.sc.x, G.sc.y, G.sc.z, G.sc.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float dA = d * sbyte(SC[j >> 1], 2 * (j & 1)), dB = d * sbyte(SC[j >> 1], 2 * (j & 1) + 1);
+            uint32_t lo6[4], hi6[4];
+            q6_slot_bytes_gemv(G.ql[j], G.qh[j], lo6, hi6);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_bytes_s(lo6, hi6, x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(dA, fmaf(-32.0f, xsum_at(xsv[v], hb + 2 * j), lo), acc[v]);
+                acc[v] = fmaf(dB, fmaf(-32.0f, xsum_at(xsv[v], hb + 2 * j + 1), hi), acc[v]);
+            }
+        }
+    } else if constexpr (T == kQ4_0) {
+        const uint32_t n = min(8u, S - sbase);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if ((uint32_t)j >= n) break;
+            const float d = h2f(G.d[j]);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_nibbles_s(G.q[j], x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                const float t = fmaf(-8.0f, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), (lo + hi) * inv_unit);
+                acc[v] = fmaf(d, t, acc[v]);
+            }
+        }
+    } else {  // Q8_0
+        const uint32_t n = min(8u, S - sbase);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if ((uint32_t)j >= n) break;
+            const float d = h2f(G.d[j]);
+            // int8 q -> q + 128 as an unsigned byte; the 128 is taken back with the x sums
+            const uint32_t A[4] = {xor_opaque<0x80808080u>(G.qa[j].x), xor_opaque<0x80808080u>(G.qa[j].y),
+                                   xor_opaque<0x80808080u>(G.qa[j].z), xor_opaque<0x80808080u>(G.qa[j].w)};
+            const uint32_t B[4] = {xor_opaque<0x80808080u>(G.qb[j].x), xor_opaque<0x80808080u>(G.qb[j].y),
+                                   xor_opaque<0x80808080u>(G.qb[j].z), xor_opaque<0x80808080u>(G.qb[j].w)};
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float lo = 0.0f, hi = 0.0f;
+                dot_bytes_s(A, B, x + v * x_stride + (uint64_t)(sbase + j) * 32, lo, hi);
+                acc[v] = fmaf(d, fmaf(-128.0f, xsum_at(xsv[v], hb + 2 * j) + xsum_at(xsv[v], hb + 2 * j + 1), lo + hi), acc[v]);
+            }
+        }
+    }
+}
+
+// End of a slab-GEMV workgroup: the waves' partial sums meet in LDS in wave order, then (split
+// K) the workgroups of a slab meet in the workspace, and the result (SiLU(gate) * up for the
+// pair) is written. acc0 holds this wave's sums in fp32, rows = lanes.
+// Split-K: the workgroup's start ticket for its slab (0 .. nch - 1), taken when it starts and
+// used only at its end, so the device-scope round trip overlaps the weight stream.
+__device__ __forceinline__ uint32_t gemv_ticket(const GemvSlabArgs& a, uint32_t slab, uint32_t nch) {
+    uint32_t t = 0;
+    if (nch > 1 && threadIdx.x == 0)
+        t = __hip_atomic_fetch_add(&a.counters[a.slab0 + slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return t;
+}
+
+// Cross-lane moves within rows of 16 lanes (DPP): lane ^ 1, lane ^ 2 (quad permutes), the
+// mirror inside 8 lanes (pairs the two quads) and inside 16 lanes (pairs the two halves).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over the wave, wave-uniform, in a fixed order: DPP inside each row of 16 lanes (pairs,
+// quads, halves of 8, halves of 16), then (row 0 + row 1) + (row 2 + row 3).
+__device__ __forceinline__ float wave_sum(float s) {
+    s += dpp_f<kDppXor1>(s);
+    s += dpp_f<kDppXor2>(s);
+    s += dpp_f<kDppHalfMirror>(s);
+    s += dpp_f<kDppMirror>(s);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// NORM (the fused norm): ss holds each lane's sum of squares of the raw x it loaded; ss_red +
+// w * ss_stride is NV floats of LDS for wave w (its dead A table).
+template <int NV, bool PAIR, bool NORM>
+__device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
+                                            uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
+                                            uint32_t ticket, const float (&ss)[NV], float* ss_red, uint32_t ss_stride) {
+    constexpr bool norm = NORM;
+    float sst[NV];  // the workgroup's sum of squares, then the slab's (chunk order)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) sst[v] = norm ? wave_sum(ss[v]) : 0.0f;
+    // waves -> wave 0, in wave order
+    if (nw > 1) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
+        if (norm && lane == 0)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) ss_red[wave * ss_stride + v] = sst[v];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float s = red[v * 64 + lane];
+            for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
+            acc0[v] = s;
+        }
+        if (norm)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                float s = ss_red[v];
+                for (uint32_t w = 1; w < nw; ++w) s += ss_red[w * ss_stride + v];
+                sst[v] = s;
+            }
+    }
+    const uint32_t row = slab * kSlabRows + lane;
+    float acc1[NV];  // the up sums (PAIR)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
+    if (nch > 1) {
+        // Split-K meeting point, without cache maintenance and without a round trip at the end
+        // of most workgroups. The workgroup with the slab's last start ticket is the reducer:
+        // every other chunk of the slab started before it, so they are all running. The others
+        // store their partials as 64-bit words (fp32 bits, 1 = ready: one atomic access
+        // carries the value and its mark) and finish. The reducer loads those words, re-reads
+        // (bounded, with a pause) any not yet ready, adds the chunks in chunk order
+        // (deterministic), and clears the words and the ticket counter for the next launch.
+        // workspace words of this slab: its index among all slabs of the launch (a grouped launch
+        // covers several matrices)
+        const uint32_t gs = a.slab0 + slab;
+        uint64_t* P = a.slots + (uint64_t)gs * nch * NV * 64;
+        // the norm's sums of squares: one word per (chunk, vector) after all slabs' partials
+        const uint64_t wgs = a.wg_total ? a.wg_total : gridDim.x;
+        uint64_t* PS = a.slots + wgs * NV * 64 + (uint64_t)gs * nch * NV;
+        if (__builtin_amdgcn_readfirstlane(ticket) != nch - 1) {
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+                __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
+                                   (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (norm && lane == 0)
+#pragma unroll
+                for (int v = 0; v < NV; ++v)
+                    __hip_atomic_store(PS + (uint64_t)c * NV + v, (uint64_t)__float_as_uint(sst[v]) | (1ull << 32),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        float own[NV], own_ss[NV];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            own[v] = acc0[v];
+            acc0[v] = 0.0f;
+            own_ss[v] = sst[v];
+            sst[v] = 0.0f;
+        }
+        // The loads of 8 chunks are issued before any is used (one memory round trip per 8
+        // chunks); past the last chunk the address is clamped and the value dropped. With the
+        // norm, the chunks' sums of squares ride in the same round trip; only the gate chunks'
+        // count (the up chunks of a pair load the same x), in chunk order.
+        constexpr uint32_t KB = 8;
+        constexpr uint32_t kSpinLimit = 1u << 20;  // the other chunks are running: a few microseconds
+        auto ready = [&](uint64_t w, const uint64_t* addr) {
+            for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin) {
+                __builtin_amdgcn_s_sleep(2);
+                w = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
+        };
+        // the ss words of a window of 64 / NV chunks, one word per lane (lane = (k % win) NV + v)
+        constexpr uint32_t win = 64 / NV;
+        uint64_t qsl = 0;
+        auto load_window = [&](uint32_t k0) {
+            if (lane < min(nch - k0, win) * NV)
+                qsl = __hip_atomic_load(PS + (uint64_t)k0 * NV + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        if (norm) load_window(0);
+        for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
+            uint64_t q[KB][NV];
+#pragma unroll
+            for (uint32_t kk = 0; kk < KB; ++kk) {
+                const uint64_t* Q = P + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
+#pragma unroll
+                for (int v = 0; v < NV; ++v)
+                    q[kk][v] = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (uint32_t kk = 0; kk < KB; ++kk) {
+                const uint32_t k = k0 + kk;
+                if (k >= nch) break;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    const float val = k == c ? own[v] : ready(q[kk][v], P + ((uint64_t)k * NV + v) * 64 + lane);
+                    if (k < a.ks) acc0[v] += val;
+                    else acc1[v] += val;
+                }
+                if (norm && k < a.ks) {
+                    if (k % win == 0 && k > 0) load_window(k);
+#pragma unroll
+                    for (int v = 0; v < NV; ++v) {
+                        const uint32_t idx = (k % win) * NV + v;
+                        const uint64_t w = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)qsl, idx) |
+                                           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(qsl >> 32), idx) << 32);
+                        sst[v] += k == c ? own_ss[v] : ready(w, PS + (uint64_t)k * NV + v);
+                    }
+                }
+            }
+        }
+        for (uint32_t k = 0; k < nch; ++k)
+            if (k != c) {
+#pragma unroll
+                for (int v = 0; v < NV; ++v)
+                    __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (norm && lane == 0)
+#pragma unroll
+                    for (int v = 0; v < NV; ++v)
+                        __hip_atomic_store(PS + (uint64_t)k * NV + v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        if (lane == 0) __hip_atomic_store(&a.counters[gs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (norm) {
+        // rms_norm's scale, applied once to the row sums (the workgroups multiplied x by norm_w)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float inv = 1.0f / sqrtf(sst[v] / (float)a.cols + a.norm_eps);
+            acc0[v] *= inv;
+            acc1[v] *= inv;
+        }
+    }
+    if constexpr (!PAIR) {
+        // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
+        // lanes of wave 0 are here; rows past the matrix take no part)
+        if (a.parts) {
+            const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+            const bool live = row < a.rows;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                if ((uint32_t)v >= a.n_vec) break;
+                const bool nan = live && acc0[v] != acc0[v];
+                const bool rank = live && !nan && (a.valid_rows == 0 || row < a.valid_rows);
+                float bv;
+                uint32_t bi, any_nan;
+                wave_argmax(acc0[v], row, rank, nan, bv, bi, any_nan);
+                if (lane == 0) a.parts[(uint64_t)v * slabs + slab] = ArgPart{bv, bi, any_nan, 0u};
+            }
+        }
+    }
+    if (row >= a.rows || !a.y) return;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        if ((uint32_t)v >= a.n_vec) break;
+        a.y[(uint64_t)v * a.y_stride + row] = PAIR ? silu_f(acc0[v]) * acc1[v] : acc0[v];
+    }
+}
+
+// grid.x = slabs * ks * MATS; block = 64 * nw (nw waves). Dynamic LDS: the waves' partials
+// [nw][NV][64]. With PAIR (MATS = 2) a workgroup streams one matrix only (chunks [0, ks) the
+// gate rows, [ks, 2 ks) the up rows of the same slab) and the gate and up sums meet in the
+// split-K fix-up, which applies SiLU: the pair costs no registers over a single GEMV.
+template <uint32_t T, int NV, bool PAIR>
+__global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
+    extern __shared__ float smem[];
+    constexpr uint32_t MATS = PAIR ? 2 : 1;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
+    const uint32_t nch = a.ks * MATS;  // chunks per slab
+    const uint32_t slab = blockIdx.x / nch, c = blockIdx.x % nch;
+    const uint32_t mat = c / a.ks, cc = c % a.ks;
+    // this workgroup's groups [g0, g1), then this wave's share [w0, w1)
+    const uint32_t base = ngrp / a.ks, extra = ngrp % a.ks;
+    const uint32_t g0 = cc * base + min(cc, extra), g1 = g0 + base + (cc < extra ? 1u : 0u);
+    const uint32_t wb = (g1 - g0) / nw, we = (g1 - g0) % nw;
+    const uint32_t w0 = g0 + wave * wb + min(wave, we), w1 = w0 + wb + (wave < we ? 1u : 0u);
+    const SlabGeom geo = slab_geom(T, a.cols);
+    const uint8_t* slab0 = (mat ? a.w1 : a.w0) + (uint64_t)slab * geo.slab_bytes;
+    cfloat* xc = reinterpret_cast<cfloat*>(reinterpret_cast<uintptr_t>(a.x));
+    float* red = smem;
+
+    // 1 / fp8_unit, built from the exponent bits (exact for a power of two)
+    const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
+    float acc0[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
+    SlotGroup<T> cur0;
+    if (w0 < w1) load_group<T>(cur0, slab0, geo, lane, w0, S);
+    const uint32_t ticket = gemv_ticket(a, slab, nch);
+    float xsv[NV];  // half-slot sums of this wave's groups (at most 4), one per lane
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xsv[v] = wave_xsums(a.x + (uint64_t)v * a.x_stride, w0, S, lane);
+    for (uint32_t grp = w0; grp < w1; ++grp) {
+        if constexpr (T == kQ8_0) {
+            // a Q8_0 group is 72 registers: one buffer, the next group loaded after this one
+            compute_group<T, NV>(cur0, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+            if (grp + 1 < w1) load_group<T>(cur0, slab0, geo, lane, grp + 1, S);
+        } else {
+            // Ping-pong between two register buffers: the next group is always in flight. The
+            // prefetch is unconditional (past the last group it reloads the last one, an L2
+            // hit) so the compiler can wait for exactly the older loads (vmcnt counts in order).
+            SlotGroup<T> nxt;
+            load_group<T>(nxt, slab0, geo, lane, min(grp + 1, w1 - 1), S);
+            compute_group<T, NV>(cur0, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+            if (grp + 1 >= w1) break;
+            ++grp;
+            load_group<T>(cur0, slab0, geo, lane, min(grp + 1, w1 - 1), S);
+            compute_group<T, NV>(nxt, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
+        }
+    }
+    float ss[NV];  // the VALU kernel has no fused norm (its launcher never passes norm_w)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) ss[v] = 0.0f;
+    gemv_finish<NV, PAIR, false>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, nullptr, 0);
+}
+
+// ------------------------------------------------------------------------------------------
+// MFMA GEMV: k_gemv_mx<T, NV, PAIR>
+//
+// Same work split and SLAB stream as k_gemv_slab (one row per lane, a wave streams slot groups
+// of its 64 rows), but the multiply-adds run on v_mfma_f32_4x4x4_16b_bf16 instead of the VALU:
+//   B (per lane, its own row): four weights of one "k-step" as raw bf16 bit patterns. A code c
+//     in 0..255 held in the low bits of a bf16 is exactly c * 2^-133 (subnormal up to 127,
+//     then the first normal binade, which continues the same scale), so the quants need only
+//     masks: 4-bit records as (q & 0x000F000F), (q & 0x00F000F0) = 16 * the high nibble,
+//     6-bit and biased 8-bit codes as byte pairs.
+//   A (broadcast from one 4-lane block to all 16 with cbsz = 4): rows = x pieces. Per slot
+//     group and vector, x is scaled by 2^S (S from the group's largest |x|, so the products
+//     stay normal) and split exactly into three bf16 pieces b1 + b2 + b3 = x * 2^S. Row
+//     3 v + p holds piece p of vector v; the high-nibble k-steps carry x / 16.
+//   D (per lane, its own row): D[3 v + p] = sum_k piece_p(x_k) * q_k * 2^-133, exact products
+//     accumulated in fp32. The three pieces added give x . q for the slot in units of
+//     2^(S - 133); the slot scales (d * sc, dmin * m, offsets) are applied per row as in the
+//     VALU kernel, and each group's sum is brought back to fp32 units with ldexp.
+// The A operands of a group (8 slots x 8 k-steps x M row blocks of 4 x 4 bf16) are built by
+// the wave itself in a private LDS table and read back as 4 M register pairs; one pair feeds
+// 16 MFMAs through the broadcast block id.
+// ------------------------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// A-operand row blocks per k-step for NV vectors (3 pieces each, 4 rows per block)
+template <int NV>
+constexpr int mx_blocks() { return (3 * NV + 3) / 4; }
+// LDS bytes of one wave's A table: 8 slots x 8 k-steps x M blocks x 32 B
+template <int NV>
+constexpr uint32_t mx_table_bytes() { return 64u * mx_blocks<NV>() * 32u; }
+
+__device__ __forceinline__ f32x4 mfma4_bc(s16x4 a, s16x4 b, f32x4 c, uint32_t abid) {
+    switch (abid & 15u) {
+#define HALO_MI_BC(k) \
+    case k: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 4, k, 0);
+        HALO_MI_BC(0) HALO_MI_BC(1) HALO_MI_BC(2) HALO_MI_BC(3) HALO_MI_BC(4) HALO_MI_BC(5) HALO_MI_BC(6)
+        HALO_MI_BC(7) HALO_MI_BC(8) HALO_MI_BC(9) HALO_MI_BC(10) HALO_MI_BC(11) HALO_MI_BC(12)
+        HALO_MI_BC(13) HALO_MI_BC(14) HALO_MI_BC(15)
+#undef HALO_MI_BC
+    }
+    return c;
+}
+
+__device__ __forceinline__ s16x4 as_b(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(s16x4, u32x2_t{lo, hi});
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+// (a, b) -> three bf16 pairs whose sums are exactly a and b: each residual is exact in fp32
+// and has at most 16, then 8 significant bits, so the third piece is the residual itself.
+__device__ __forceinline__ void split3(float a, float b, uint32_t (&p)[3]) {
+    p[0] = pack_bf16(a, b);
+    const float ra = a - __uint_as_float(p[0] << 16), rb = b - __uint_as_float(p[0] & 0xFFFF0000u);
+    p[1] = pack_bf16(ra, rb);
+    p[2] = pack_bf16(ra - __uint_as_float(p[1] << 16), rb - __uint_as_float(p[1] & 0xFFFF0000u));
+}
+
+// Maximum over the wave, wave-uniform (DPP inside rows, then the four row results).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u<kDppXor1>(v));
+    v = max(v, dpp_u<kDppXor2>(v));
+    v = max(v, dpp_u<kDppHalfMirror>(v));
+    v = max(v, dpp_u<kDppMirror>(v));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+
+// x of one slot group, lane = 8 s + r: x[slot 8 grp + s][4 r .. 4 r + 3] (zero past the end).
+// Branch-free (the address is clamped, the value selected after): a load under a branch would
+// make the compiler wait for it before the weight loads that follow are issued.
+// NORM: wr gets the same four elements of norm_w (loaded branch-free as x is).
+template <int NV, bool NORM>
+__device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], const float* __restrict__ x,
+                                          uint64_t x_stride, const float* __restrict__ norm_w, uint32_t grp, uint32_t S,
+                                          uint32_t lane) {
+    const uint32_t slot = grp * 8 + (lane >> 3);
+    const bool in = slot < S;
+    const uint64_t e = (uint64_t)min(slot, S - 1) * 32 + 4 * (lane & 7);
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float t = x[(uint64_t)v * x_stride + e + i];
+            xr[v][i] = in ? t : 0.0f;
+        }
+    if constexpr (NORM)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float t = norm_w[e + i];
+            wr[i] = in ? t : 0.0f;
+        }
+}
+
+// Builds this wave's A table for one group from xr, reads it back as register pairs, and
+// returns per vector the exponent that brings the group's sums to fp32 units (es) and the x
+// sums in MFMA units (xs: lane 8 s holds slot s's sum, lane 8 s + 4 the high half's sum for
+// Q6_K, whose low-half sum is then in lane 8 s).
+// The k-step r of a slot (k-steps 0..3: slot elements 0..15, 4..7: 16..31) covers elements
+// 4 r .. 4 r + 3 in the order (0, 2, 1, 3), the order the masks below produce them.
+// With the fused norm (norm), the group's x is x * norm_w, and ss accumulates the squares of
+// the raw x.
+template <uint32_t T, int NV>
+__device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float (&wr)[4], bool norm, float (&ss)[NV],
+                                         uint8_t* tab, uint32_t lane, s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV],
+                                         float (&xs)[NV]) {
+    constexpr int M = mx_blocks<NV>();
+    constexpr int kHiShift = (T == kQ4_K || T == kQ4_0) ? 4 : 0;  // high nibbles arrive as 16 q
+    const uint32_t s = lane >> 3, r = lane & 7;
+    float xr[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[v][i] = xraw[v][i];
+    if (norm)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ss[v] = fmaf(xraw[v][i], xraw[v][i], ss[v]);
+                xr[v][i] = xraw[v][i] * wr[i];
+            }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        uint32_t mb = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mb = max(mb, __float_as_uint(xr[v][i]) & 0x7FFFFFFFu);
+        mb = wave_max_u32(mb);
+        const int e = min(max((int)(mb >> 23) - 127, -100), 127);
+        const int sx = 100 - e;  // the largest |x| * 2^sx is about 2^100
+        es[v] = 33 + e;          // 133 - sx
+        const int sh = sx - (r >= 4 ? kHiShift : 0);
+        uint32_t p01[3], p23[3];
+        split3(ldexpf(xr[v][0], sh), ldexpf(xr[v][2], sh), p01);
+        split3(ldexpf(xr[v][1], sh), ldexpf(xr[v][3], sh), p23);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+            const int rho = 3 * v + p, m = rho >> 2, row = rho & 3;
+            const uint32_t lam = (s * 8 + r) * M + m;
+            *reinterpret_cast<uint2*>(tab + (lam >> 4) * 512 + ((lam & 15) * 4 + row) * 8) = make_uint2(p01[p], p23[p]);
+        }
+        float h = (xr[v][0] + xr[v][1]) + (xr[v][2] + xr[v][3]);
+        h += dpp_f<kDppXor1>(h);
+        h += dpp_f<kDppXor2>(h);
+        if constexpr (T != kQ6_K) h += dpp_f<kDppHalfMirror>(h);
+        xs[v] = ldexpf(h, sx - 133);
+    }
+#pragma unroll
+    for (int rho = 3 * NV; rho < 4 * M; ++rho) {  // unused A rows are zero
+        const int m = rho >> 2, row = rho & 3;
+        const uint32_t lam = (s * 8 + r) * M + m;
+        *reinterpret_cast<uint2*>(tab + (lam >> 4) * 512 + ((lam & 15) * 4 + row) * 8) = make_uint2(0u, 0u);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < 4 * M; ++q) A[q] = *reinterpret_cast<const s16x4*>(tab + q * 512 + lane * 8);
+}
+
+// Sum of the three pieces of vector v from the D blocks. The last vector also adds the unused
+// rows (their A rows are zero, so they hold exactly 0 and the sum is unchanged): every row an
+// MFMA chain writes is then read after the chain. Otherwise the compiler may give a dead row's
+// register to another value a few instructions after the chain's last MFMA issues, and on
+// gfx950 a dependent MFMA (C from the previous one) can write back after that value is written
+// (seen as wrong sums, different from run to run).
+template <int NV>
+__device__ __forceinline__ float mx_dot(const f32x4 (&D)[mx_blocks<NV>()], int v) {
+    const int r0 = 3 * v, r1 = 3 * v + 1, r2 = 3 * v + 2;
+    const float s = (D[r0 >> 2][r0 & 3] + D[r1 >> 2][r1 & 3]) + D[r2 >> 2][r2 & 3];
+    if (v != NV - 1) return s;
+    float z = 0.0f;
+#pragma unroll
+    for (int r = 3 * NV; r < 4 * mx_blocks<NV>(); ++r) z += D[r >> 2][r & 3];
+    return s + z;
+}
+
+// The MFMAs of k-step r of slot j with B = b, into D (all row blocks)
+template <int NV>
+__device__ __forceinline__ void mx_kstep(const s16x4 (&A)[4 * mx_blocks<NV>()], s16x4 b, int j, int r,
+                                         f32x4 (&D)[mx_blocks<NV>()]) {
+    constexpr int M = mx_blocks<NV>();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int lam = (j * 8 + r) * M + m;
+        D[m] = mfma4_bc(A[lam >> 4], b, D[m], (uint32_t)(lam & 15));
+    }
+}
+
+// One loaded group against the A table; acc in MFMA units of this group.
+template <uint32_t T, int NV>
+__device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)[4 * mx_blocks<NV>()],
+                                         const float (&xs)[NV], uint32_t n, float (&acc)[NV]) {
+    constexpr int M = mx_blocks<NV>();
+    // Q4_K: sum_j d sc_j dot_j - dmin m_j xs_j = d sum_j sc_j dot_j - dmin sum_j m_j xs_j, the
+    // block's d and dmin applied once per group; Q6_K likewise with d.
+    float sa[NV], sb[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) sa[v] = sb[v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if constexpr (T == kQ4_0 || T == kQ8_0)
+            if ((uint32_t)j >= n) break;
+        f32x4 D[M], Dh[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) D[m] = Dh[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (T == kQ4_K || T == kQ4_0) {
+            const uint32_t Q[4] = {G.q[j].x, G.q[j].y, G.q[j].z, G.q[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t q = Q[i], q8 = q >> 8;
+                mx_kstep<NV>(A, as_b(q & 0x000F000Fu, q8 & 0x000F000Fu), j, i, D);
+                mx_kstep<NV>(A, as_b(q & 0x00F000F0u, q8 & 0x00F000F0u), j, 4 + i, D);
+            }
+        } else if constexpr (T == kQ8_0) {
+            const uint32_t Qa[4] = {G.qa[j].x, G.qa[j].y, G.qa[j].z, G.qa[j].w};
+            const uint32_t Qb[4] = {G.qb[j].x, G.qb[j].y, G.qb[j].z, G.qb[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ua = Qa[i] ^ 0x80808080u, ub = Qb[i] ^ 0x80808080u;  // q + 128
+                mx_kstep<NV>(A, as_b(ua & 0x00FF00FFu, __builtin_amdgcn_perm(0u, ua, 0x0C030C01u)), j, i, D);
+                mx_kstep<NV>(A, as_b(ub & 0x00FF00FFu, __builtin_amdgcn_perm(0u, ub, 0x0C030C01u)), j, 4 + i, D);
+            }
+        } else if constexpr (T == kQ5_K || T == kIQ4_XS) {
+            // byte codes: Q5_K's 5-bit quants (fifth bit from the qh word), IQ4_XS's table
+            // values + 128
+            const uint32_t Q[4] = {G.q[j].x, G.q[j].y, G.q[j].z, G.q[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t lo, hi;
+                if constexpr (T == kQ5_K) {
+                    lo = and_or_opaque(Q[i], 0x0F0F0F0Fu, (G.qh[j] << (4 - i)) & 0x10101010u);
+                    hi = and_or_opaque(Q[i] >> 4, 0x0F0F0F0Fu, (G.qh[j] >> i) & 0x10101010u);
+                } else {
+                    lo = iq4_lookup4(Q[i]);
+                    hi = iq4_lookup4(Q[i] >> 4);
+                }
+                mx_kstep<NV>(A, as_b(lo & 0x00FF00FFu, __builtin_amdgcn_perm(0u, lo, 0x0C030C01u)), j, i, D);
+                mx_kstep<NV>(A, as_b(hi & 0x00FF00FFu, __builtin_amdgcn_perm(0u, hi, 0x0C030C01u)), j, 4 + i, D);
+            }
+        } else {  // Q6_K: the two halves have their own scales
+            uint32_t lo6[4], hi6[4];
+            q6_slot_bytes_gemv(G.ql[j], G.qh[j], lo6, hi6);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mx_kstep<NV>(A, as_b(lo6[i] & 0x00FF00FFu, __builtin_amdgcn_perm(0u, lo6[i], 0x0C030C01u)), j, i, D);
+                mx_kstep<NV>(A, as_b(hi6[i] & 0x00FF00FFu, __builtin_amdgcn_perm(0u, hi6[i], 0x0C030C01u)), j, 4 + i, Dh);
+            }
+        }
+        if constexpr (T == kQ4_K || T == kQ5_K) {
+            uint32_t sc, m;
+            q4k_sc_m(G.hdr.y, G.hdr.z, G.hdr.w, (uint32_t)j, sc, m);
+            const float fsc = (float)sc, fm = (float)m;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                sa[v] = fmaf(fsc, mx_dot<NV>(D, v), sa[v]);
+                sb[v] = fmaf(fm, xsum_at(xs[v], 8 * j), sb[v]);
+            }
+        } else if constexpr (T == kIQ4_XS) {
+            // dl_j = d (ls_j - 32); the codes carry + 128, taken out with the slot's x sum
+            const float fl = (float)iq4xs_ls(G.hdr.x >> 16, G.hdr.y, (uint32_t)j);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) sa[v] = fmaf(fl, fmaf(-128.0f, xsum_at(xs[v], 8 * j), mx_dot<NV>(D, v)), sa[v]);
+        } else if constexpr (T == kQ4_0 || T == kQ8_0) {
+            const float d = h2f(G.d[j]);
+            constexpr float off = T == kQ4_0 ? -8.0f : -128.0f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) acc[v] = fmaf(d, fmaf(off, xsum_at(xs[v], 8 * j), mx_dot<NV>(D, v)), acc[v]);
+        } else {
+            const uint32_t SC[4] = {G.sc.x, G.sc.y, G.sc.z, G.sc.w};
+            const float sA = sbyte(SC[j >> 1], 2 * (j & 1)), sB = sbyte(SC[j >> 1], 2 * (j & 1) + 1);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                sa[v] = fmaf(sA, fmaf(-32.0f, xsum_at(xs[v], 8 * j), mx_dot<NV>(D, v)), sa[v]);
+                sa[v] = fmaf(sB, fmaf(-32.0f, xsum_at(xs[v], 8 * j + 4), mx_dot<NV>(Dh, v)), sa[v]);
+            }
+        }
+    }
+    if constexpr (T == kQ4_K || T == kQ5_K) {
+        const float d = h2f(G.hdr.x & 0xFFFFu), dmin = h2f(G.hdr.x >> 16);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = fmaf(d, sa[v], -(dmin * sb[v]));
+    } else if constexpr (T == kIQ4_XS) {
+        const float d = h2f(G.hdr.x & 0xFFFFu);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = d * sa[v];
+    } else if constexpr (T == kQ6_K) {
+        const float d = h2f(G.d);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = d * sa[v];
+    }
+}
+
+// Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
+// the Q8_0, Q6_K and Q5_K loops (two register groups); the others run at most 8 waves.
+template <uint32_t T, int NV, bool ONE>
+constexpr uint32_t mx_max_threads() {
+    return (NV == 1 && (ONE || (T != kQ8_0 && T != kQ6_K && T != kQ5_K))) ? 1024u : 512u;
+}
+
+// grid, split and LDS as k_gemv_slab, plus one A table per wave after the partials. ONE: every
+// wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
+// The body of workgroup `bid` of a k_gemv_mx launch over the matrix of `a` (also one segment of a
+// grouped launch, k_gemv_mx_group).
+template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM>
+__device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid) {
+    static_assert(ONE || !NORM, "the fused norm runs on the one-group kernel");
+    extern __shared__ float smem[];
+    constexpr uint32_t MATS = PAIR ? 2 : 1;
+    constexpr int M = mx_blocks<NV>();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
+    const uint32_t nch = a.ks * MATS;
+    const uint32_t slab = bid / nch, c = bid % nch;
+    const uint32_t mat = c / a.ks, cc = c % a.ks;
+    const uint32_t base = ngrp / a.ks, extra = ngrp % a.ks;
+    const uint32_t g0 = cc * base + min(cc, extra), g1 = g0 + base + (cc < extra ? 1u : 0u);
+    const uint32_t wb = (g1 - g0) / nw, we = (g1 - g0) % nw;
+    const uint32_t w0 = g0 + wave * wb + min(wave, we), w1 = w0 + wb + (wave < we ? 1u : 0u);
+    const SlabGeom geo = slab_geom(T, a.cols);
+    const uint8_t* slab0 = (mat ? a.w1 : a.w0) + (uint64_t)slab * geo.slab_bytes;
+    float* red = smem;
+    uint8_t* tab = reinterpret_cast<uint8_t*>(smem + nw * NV * 64) + wave * mx_table_bytes<NV>();
+
+    float acc0[NV], ss[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc0[v] = ss[v] = 0.0f;
+    constexpr bool norm = NORM;
+    float* ss_red = reinterpret_cast<float*>(smem + nw * NV * 64);  // wave w's A table, once it is dead
+    constexpr uint32_t ss_stride = mx_table_bytes<NV>() / 4;
+    float xr[NV][4], wr[4];
+    uint32_t ticket = 0;
+    if constexpr (ONE) {
+        if (w0 < w1) {
+            SlotGroup<T> G;
+            mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
+            load_group<T>(G, slab0, geo, lane, w0, S);
+            ticket = gemv_ticket(a, slab, nch);
+            s16x4 A[4 * M];
+            int es[NV];
+            float xs[NV];
+            mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
+            mx_group<T, NV>(G, A, xs, min(8u, S - w0 * 8), acc0);
+#pragma unroll
+            for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
+        } else {
+            ticket = gemv_ticket(a, slab, nch);
+        }
+        gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
+        return;
+    }
+    SlotGroup<T> cur, nxt;
+    if (w0 < w1) {  // x first: the A table is built while the weights are on their way
+        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, w0, S, lane);
+        load_group<T>(cur, slab0, geo, lane, w0, S);
+    }
+    ticket = gemv_ticket(a, slab, nch);
+    // One group: build its A table from xr, prefetch x and the weights of the next group (past
+    // the last group: the last one again, an L2 hit, so the loop stays branch-free), multiply.
+    auto step = [&](const SlotGroup<T>& G, SlotGroup<T>& next, uint32_t grp) {
+        s16x4 A[4 * M];
+        int es[NV];
+        float xs[NV];
+        mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
+        const uint32_t gn = min(grp + 1, w1 - 1);
+        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, gn, S, lane);
+        load_group<T>(next, slab0, geo, lane, gn, S);
+        float accg[NV];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) accg[v] = 0.0f;
+        mx_group<T, NV>(G, A, xs, min(8u, S - grp * 8), accg);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc0[v] += ldexpf(accg[v], es[v]);
+    };
+    for (uint32_t grp = w0; grp < w1; ++grp) {
+        step(cur, nxt, grp);
+        if (grp + 1 >= w1) break;
+        ++grp;
+        step(nxt, cur, grp);
+    }
+    gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
+}
+
+template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
+__global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
+    gemv_mx_body<T, NV, PAIR, ONE, NORM>(a, blockIdx.x);
+}
+
+}  // namespace
+}  // namespace halo_mi

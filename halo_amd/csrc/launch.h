@@ -49,6 +49,10 @@ struct GemvSlabArgs {
     // workgroup scales the row sums by 1 / sqrt(sum / cols + norm_eps).
     const float* norm_w = nullptr;
     float norm_eps = 0.0f;
+    // Workspace indexing in a grouped launch (k_gemv_mx_group): this matrix's first slab among
+    // the launch's slabs, and the launch's workgroups (0: a launch of its own).
+    uint32_t slab0 = 0;
+    uint32_t wg_total = 0;
 };
 
 // M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
@@ -126,6 +130,16 @@ int launch_gemv_gguf_ref(uint32_t type, const uint8_t* w, uint64_t w_stride, con
                          uint64_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_vec, hipStream_t st);
 template <bool PAIR>
 int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st);
+// k_gemv_group.hip: SLAB matrices sharing x in one launch per pair of weight types
+struct GroupSeg {
+    uint32_t type;
+    const void* w;
+    uint32_t rows;
+    float* y;
+    uint64_t y_stride;  // floats, already resolved (not 0)
+};
+int launch_gemv_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t x_stride, uint32_t cols, uint32_t n_vec,
+                      const float* norm_w, float eps, hipStream_t st);
 // k_gemm.hip
 template <bool PAIR>
 int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st);

@@ -136,6 +136,44 @@ typedef struct halo_mi_gemv_params {
 int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
 
 /*
+ * Grouped GEMV: several SLAB matrices that share x, in one launch per pair of weight types,
+ * e.g. a layer's q, k and v projections (Q4_K q and k, Q6_K v) after the same input norm. The
+ * reference issues them one by one on one stream (Qwen35::Impl::gemv,
+ * src/models/qwen35.cpp:486-498), and each small projection then pays a whole launch's ramp and
+ * drain; row-fusing them into one matrix (halo_mi_upload_tensors) needs equal types.
+ *   segs[i]: the segment's weight type, SLAB image (16-byte aligned), rows, and output y_i
+ *            (n_vec rows of rows floats, y_stride apart, 0 = rows): y_i = W_i x (with the fused
+ *            norm: W_i (rms_norm(x) * norm_w), as halo_mi_gemv).
+ *   x, x_stride, cols, n_vec, norm_w, norm_eps: shared, with halo_mi_gemv's meaning.
+ * Numerics: halo_mi_gemv's SLAB GEMV bound per output (the K split follows the group's total
+ * slabs, so a row may round differently from a call of its own; rows stay independent of n_vec).
+ * No output may overlap x, norm_w, any segment's weights or another output.
+ * n_segs <= HALO_MI_GEMV_GROUP_MAX; more than two weight types take one launch per pair.
+ */
+#define HALO_MI_GEMV_GROUP_MAX 4u
+
+typedef struct halo_mi_gemv_segment {
+    uint32_t type;
+    const void* w;
+    uint32_t rows;
+    float* y;
+    uint64_t y_stride;
+} halo_mi_gemv_segment;
+
+typedef struct halo_mi_gemv_group_params {
+    const halo_mi_gemv_segment* segs;
+    uint32_t n_segs;
+    const float* x;
+    uint64_t x_stride;
+    uint32_t cols;
+    uint32_t n_vec;
+    const float* norm_w;
+    float norm_eps;
+} halo_mi_gemv_group_params;
+
+int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream);
+
+/*
  * Fused FFN gate/up: out[t][n] = silu((Wg x_t)[n]) * (Wu x_t)[n], silu(v) = v / (1 + exp(-v)).
  * The reference composes it as gemv(gate), gemv(up), swiglu (src/models/qwen35.cpp:789-805;
  * backends/cpu/ops_basic.cpp:165-167); here both matmuls and the epilogue are one launch.

@@ -1,7 +1,8 @@
 """GPU parity of the RMS-norm prologue of the matmul (GemvArgs::norm_w / norm_eps,
 include/halo/backend/backend.h:292-299), of RMS_NORM itself (cpu::rms_norm,
-backends/cpu/ops_basic.cpp:18-33) and of GET_ROWS (GetRowsArgs, backend.h:254-263; the HIP
-status word of backends/hip/src/ops.cpp:982-1012), against the oracle, through the C ABI.
+backends/cpu/ops_basic.cpp:18-33), of GET_ROWS (GetRowsArgs, backend.h:254-263; the HIP
+status word of backends/hip/src/ops.cpp:982-1012) and of the grouped GEMV over matrices that
+share x, against the oracle, through the C ABI.
 
 Acceptance: RMS_NORM, GET_ROWS and the reference-order GEMV with the norm are bitwise the CPU's;
 the GEMM variants stage exactly the CPU's normalized x, so the GEMM bounds apply to it
@@ -14,7 +15,7 @@ import numpy as np
 import pytest
 
 from helpers import (F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, gemm_emulated, gemm_tol,
-                     isclose_bits, make_weights, max_ratio, norm_gemv_tol, row_bytes, swiglu_tol)
+                     isclose_bits, make_weights, max_ratio, norm_gemv_tol, row_bytes, slab_gemv_tol, swiglu_tol)
 from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, strided_xy, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -282,3 +283,80 @@ def test_norm_rejects(hl, dev):
     with pytest.raises(hl.HaloError) as e:  # misaligned norm_w
         hl.gemv(t, slab, x, y, rows, cols, 1, norm_w=x.data_ptr() + 2)
     assert e.value.code == hl.ErrorCode.Kernel
+
+
+# ---- grouped GEMV (halo_mi_gemv_group) ------------------------------------------------------
+
+
+GROUPS = [
+    [(Q4_K, 640), (Q4_K, 128), (Q6_K, 128)],             # q, k, v: two types, one launch
+    [(Q5_K, 200), (IQ4_XS, 70), (Q6_K, 64), (Q8_0, 33)],  # four types: two launches
+    [(Q4_K, 1088)],                                      # one segment
+]
+
+
+@pytest.mark.parametrize("g", range(len(GROUPS)))
+@pytest.mark.parametrize("n_vec,norm", [(1, False), (3, False), (1, True), (6, True)])
+def test_gemv_group_within_bounds(hl, oracle, dev, g, n_vec, norm):
+    import torch
+
+    cols = 1024
+    say("gemv_group", g, n_vec, norm)
+    x, w = norm_inputs(cols, n_vec, 1200 + g)
+    xn = oracle.rms_norm(x, w, EPS) if norm else x
+    segs, refs = [], []
+    for i, (t, rows) in enumerate(GROUPS[g]):
+        buf, stride = make_weights(t, rows, cols, seed=1210 + 10 * g + i)
+        dense = dense_of(buf, t, rows, cols, stride, 0)
+        y = torch.full((n_vec, rows + 3), SENTINEL, dtype=torch.float32, device=dev)
+        segs.append((t, slab_of(hl, dev, t, dense, rows, cols), rows, y, rows + 3))
+        tol = norm_gemv_tol(oracle, t, dense, rows, cols, xn) if norm else slab_gemv_tol(oracle, t, dense, rows, cols, xn)
+        refs.append((oracle.matmul(t, dense, rows, cols, xn), tol))
+    xd = to_dev(x, dev)
+    for rep in range(2):  # twice: the workspace words and counters are left clean
+        hl.gemv_group(segs, xd, cols, n_vec, norm_w=to_dev(w, dev) if norm else None, norm_eps=EPS)
+        for (t, _, rows, y, _), (ref, tol) in zip(segs, refs):
+            out = host(y)
+            assert np.all(out[:, rows:] == SENTINEL), "y padding written"
+            err = np.abs(out[:, :rows].astype(np.float64) - ref)
+            assert np.all(err <= tol), f"{NAMES[t]}: worst |d|/bound = {max_ratio(err, tol):.3f}"
+
+
+def test_gemv_group_rows_do_not_depend_on_the_batch(hl, dev):
+    import torch
+
+    cols = 1024
+    x, _ = norm_inputs(cols, 5, 1300)
+    segs = []
+    for i, (t, rows) in enumerate(GROUPS[0]):
+        buf, stride = make_weights(t, rows, cols, seed=1310 + i)
+        segs.append((t, slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, 0), rows, cols), rows))
+
+    def run(xs):
+        ys = [torch.zeros((xs.shape[0], rows), dtype=torch.float32, device=dev) for _, _, rows in segs]
+        hl.gemv_group([(t, w, rows, y) for (t, w, rows), y in zip(segs, ys)], to_dev(xs, dev), cols, xs.shape[0])
+        return [host(y) for y in ys]
+
+    singles = [run(x[i:i + 1]) for i in range(5)]
+    batch = run(x)
+    for k in range(len(segs)):
+        assert isclose_bits(batch[k], np.concatenate([s[k] for s in singles])), f"segment {k}: a row changed with n_vec"
+
+
+def test_gemv_group_rejects(hl, dev):
+    import torch
+
+    cols = 256
+    buf, _ = make_weights(Q4_K, 64, cols, seed=3)
+    w = slab_of(hl, dev, Q4_K, buf[:64 * row_bytes(Q4_K, cols)], 64, cols)
+    x = to_dev(np.ones((1, cols), np.float32), dev)
+    y = torch.zeros((1, 128), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # two outputs overlapping
+        hl.gemv_group([(Q4_K, w, 64, y), (Q4_K, w, 64, y.data_ptr() + 128)], x, cols, 1)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:  # an output inside x
+        hl.gemv_group([(Q4_K, w, 64, x)], x, cols, 1)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:
+        hl.gemv_group([(Q4_K, w, 64, y)] * 5, x, cols, 1)
+    assert e.value.code == hl.ErrorCode.Unsupported
