@@ -620,9 +620,9 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
 //     in iteration i - 1, complete since the barrier that ended it), stage i + 2 dequantized
 //     (its records were loaded four iterations ago) and that half's x fragments reloaded with
 //     stage i + 2 in between;
-//   region B: the second K half's MFMAs, with stage i + 2 written to buffer (i + 2) % 3, stage
-//     i + 6's records loaded into the freed ring slot and the second half's x fragments
-//     reloaded in between; then the barrier (after this wave's LDS accesses complete).
+//   region B: the second K half's MFMAs, with stage i + 2 written to buffer (i + 2) % 3, the
+//     second half's x fragments reloaded and stage i + 6's records loaded into the freed ring
+//     slot in between; then the barrier (after this wave's LDS accesses complete).
 // Buffer (i + 2) % 3 was last read in iteration i - 2, which every wave finished before the
 // barrier that ended it. The next stage's first MFMAs need nothing from LDS, so the barrier's
 // latency and the LDS round trip overlap the MFMA pipe. Both regions interleave the other
@@ -769,13 +769,15 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
             // apart (the scheduler would otherwise issue a dependent pair back to back).
             __builtin_amdgcn_sched_barrier(0);
             // Region B: the second K half's MFMAs with the LDS writes of stage i + 2 and the loads
-            // of stage i + 6's W records and stage i + 2's x fragments in between.
+            // of stage i + 2's x fragments and stage i + 6's W records in between.
             mma(xb, 1, Bc[1]);
             __bf16* dst = lds + bufw * STAGE + wdst;
             *reinterpret_cast<bf16x8*>(dst) = lo;
             *reinterpret_cast<bf16x8*>(dst + 16) = hi;
-            load_w(ws, s_begin + i0 + q + 2 + kLmWDepth);
+            // x before W: vmcnt counts in order, so the wait for these x fragments (two stages
+            // on) then covers only W records issued a stage earlier, which have come from HBM
             load_a(xb, 1, s_begin + i0 + q + 2);
+            load_w(ws, s_begin + i0 + q + 2 + kLmWDepth);
             if constexpr (MBW == 4) {
 #pragma unroll
                 for (int k = 0; k < 16; ++k) {
