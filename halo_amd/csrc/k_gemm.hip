@@ -521,9 +521,11 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     }
 
     // ---------------- producers ----------------
-    const uint32_t pt = tid - 256;
-    const uint32_t mat = __builtin_amdgcn_readfirstlane(pt >> 7);  // one matrix per wave
-    const uint32_t r = (pt >> 1) & 63u, h = pt & 1u;
+    const uint32_t pw = wave - 4;
+    const uint32_t mat = pw >> 1;  // two waves per matrix
+    // lane -> (row, half): 32 consecutive rows per half-wave, so the 8 lanes of a ds_write_b128
+    // group hit 8 distinct bank quads (80-byte row pitch); the record loads stay one 512-byte run
+    const uint32_t r = 32 * (pw & 1u) + (lane & 31u), h = lane >> 5;
     const uint8_t* slab_ptr;
     if constexpr (PAIR) {
         slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)u * g.slab_bytes;
