@@ -839,6 +839,87 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
         }
 }
 
+// ------------------------------------------------------------------------------------------
+// Small-M GEMM: k_gemm_sm<T, PAIR> (at most 32 x rows)
+//
+// A workgroup owns W unit u (PAIR: the gate and up rows of slab u; else slabs 2u and 2u + 1)
+// over K chunk `chunk` (whole super-blocks) and all 32 x rows of the staged buffer. Wave w takes
+// matrix w / 2 and row block w % 2 (32 W rows). Lane l dequantizes row l % 32, half l / 32 of
+// each slot record, which is exactly its B operand of v_mfma_f32_32x32x16_bf16 for the slot's
+// two K halves: no LDS, no barrier, every wave streams on its own with kSmDepth slots of
+// weight records and x fragments in flight (the four waves read the same x fragments: L1
+// hits). Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128]
+// (columns 64 * matrix + 32 * block), and k_gemm_pc_reduce adds the chunks in order and applies
+// the epilogue. Per slot and lane: one exact dequantization and two MFMAs, so the kernel is
+// bound by the dequantization's VALU work instead of a per-stage barrier chain.
+// ------------------------------------------------------------------------------------------
+constexpr int kSmDepth = 8;  // slots in flight per wave (also the loop unroll: ring slot static)
+constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
+
+template <uint32_t T, bool PAIR>
+__global__ __launch_bounds__(256) void k_gemm_sm(GemmPcArgs a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t S = a.cols / kSlot;
+    const SlabGeom g = slab_geom(T, a.cols);
+    const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
+    const uint32_t u = blockIdx.x / a.kchunks, chunk = blockIdx.x % a.kchunks;
+    const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
+    const uint32_t g0 = chunk * base + min(chunk, extra);
+    const uint32_t s_begin = 8 * g0, s_end = 8 * (g0 + base + (chunk < extra ? 1u : 0u));
+    const uint32_t mat = wave >> 1, rb = wave & 1u;
+    const uint32_t r = lane & 31u, h = lane >> 5;
+    const uint8_t* slab_ptr;
+    if constexpr (PAIR) {
+        slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)u * g.slab_bytes;
+    } else {
+        // a missing second slab reads the last one again: its outputs are never stored
+        slab_ptr = a.w0 + (uint64_t)min(2 * u + mat, slabs - 1) * g.slab_bytes;
+    }
+    const __amdgpu_buffer_rsrc_t wres = make_rsrc(slab_ptr, (uint32_t)g.slab_bytes);
+    const PcOff off = pc_offsets<T>(32 * rb + r, h);
+    const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
+    const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf, (uint32_t)((uint64_t)kSmRows * a.cols * 2));
+    const uint32_t xlane = lane * 16;
+    PcW<T> R[kSmDepth];
+    uint4 X[kSmDepth][2];
+    // slot s of this chunk into ring slot q; slots past the chunk read zeros (out of range)
+    auto load = [&](int q, uint32_t s) {
+        const bool live = s < s_end;
+        pc_load_w<T>(R[q], wres, g, off, s, live);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) X[q][k] = bld128(xres, xlane, live ? (s * 2 + k) * 1024 : kPcOob);
+    };
+#pragma unroll
+    for (int q = 0; q < kSmDepth; ++q) load(q, s_begin + q);
+    floatx16 acc = floatx16{};
+    for (uint32_t i0 = s_begin; i0 < s_end; i0 += kSmDepth) {
+#pragma unroll
+        for (int q = 0; q < kSmDepth; ++q) {
+            bf16x8 lo, hi;
+            pc_dequant<T>(R[q], h, q % 8, inv_unit, lo, hi);  // s_begin and i0: multiples of 8
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[q][0]), lo, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[q][1]), hi, acc, 0, 0, 0);
+            load(q, i0 + q + kSmDepth);
+        }
+    }
+    float* P = a.partials + ((uint64_t)u * a.kchunks + chunk) * kSmRows * kPcW + 64 * mat + 32 * rb + r;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) P[mfma32_row(e, lane) * kPcW] = acc[e];
+}
+
+template <bool PAIR>
+void launch_gemm_sm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
+    switch (type) {
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_sm<kQ4_0, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_sm<kQ8_0, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_sm<kQ4_K, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_sm<kQ5_K, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sm<kIQ4_XS, PAIR>), grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_sm<kQ6_K, PAIR>), grid, dim3(256), 0, st, a); break;
+    }
+}
+
 template <bool PAIR, int MBW>
 void launch_gemm_lm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
     switch (type) {
@@ -950,10 +1031,35 @@ int launch_gemm_lm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
     return HALO_MI_OK;
 }
 
+// The k_gemm_sm path (at most 32 x rows, K in whole super-blocks): x staged as one 32-row
+// block, every unit split over K into about four workgroups per CU (three are resident at the
+// kernel's registers, so the last round is short), then the chunk-order reduce.
+template <bool PAIR>
+int launch_gemm_sm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t units, hipStream_t st) {
+    const uint32_t S = a.cols / kSlot, cus = cu_count();
+    if ((uint64_t)kSmRows * a.cols > kXbElems || (uint64_t)kSmRows * a.cols * 2 > 0xFFFFFFFFull)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
+    static const uint32_t kc_env = [] {  // tuning knob: K chunks per unit
+        const char* e = std::getenv("HALO_MI_GEMM_SM_KC");
+        return e ? (uint32_t)std::max(1, std::atoi(e)) : 0u;
+    }();
+    uint32_t kc = std::clamp<uint32_t>(kc_env ? kc_env : (4 * cus + units - 1) / units, 1u, S / 8);
+    while (kc > 1 && (uint64_t)units * kc * kSmRows * kPcW > kPartialFloats) --kc;
+    if ((uint64_t)units * kc * kSmRows * kPcW > kPartialFloats)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm: %u rows exceed the small-M partials workspace", a.rows);
+    if (int rc = stage_x(a, 0, a.n_vec, kSmRows, ws, st)) return rc;
+    GemmPcArgs p{a.w0, a.w1, ws->xb, a.y, a.y_stride, a.rows, a.cols, a.n_vec, 0u, 1u, 0u, units, kc, ws->partials};
+    p.split_unit0 = 0;
+    launch_gemm_sm_type<PAIR>(type, p, dim3(units * kc), st);
+    launch_reduce<PAIR, kSmRows>(p, st);
+    return hip_status(hipGetLastError(), "gemm_sm launch");
+}
+
 }  // namespace
 
-// x -> bf16 staging (in chunks of rows that fit the workspace), then the GEMM: k_gemm_lm for
-// large M (launch_gemm_lm), else the producer/consumer k_gemm_pc. When k_gemm_pc's tiles do not
+// x -> bf16 staging (in chunks of rows that fit the workspace), then the GEMM: k_gemm_sm for at
+// most 32 x rows and k_gemm_lm for large M when the variant leaves the choice to the shape
+// (launch_gemm_sm, launch_gemm_lm), else the producer/consumer k_gemm_pc. When k_gemm_pc's tiles do not
 // fill whole rounds of the chip (e.g. 272 slabs on 256 CUs), the tiles past the last whole round
 // are split over K so that the last round is spread over all CUs: their fp32 partials go to the
 // workspace and k_gemm_pc_reduce adds them in a fixed order.
@@ -973,6 +1079,14 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     if (a.tiles == kGemmTilesLm || (a.tiles == kGemmTilesAuto && a.n_vec > kLmMinRows &&
                                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus))
         return launch_gemm_lm<PAIR>(type, a, ws, units, st);
+    // the small-M kernel: about 1.5x k_gemm_pc's rate at M = 8 (no per-stage barrier chain)
+    static const bool sm_off = [] {  // HALO_MI_GEMM_SM=0: k_gemm_pc instead (for comparison)
+        const char* e = std::getenv("HALO_MI_GEMM_SM");
+        return e && *e == '0';
+    }();
+    const uint64_t sm_floats = (uint64_t)units * kSmRows * kPcW;  // partials at one K chunk
+    if (!sm_off && a.tiles == kGemmTilesAuto && a.n_vec <= kSmRows && S % 8 == 0 && sm_floats <= kPartialFloats)
+        return launch_gemm_sm<PAIR>(type, a, ws, units, st);
     const uint32_t BM = 64u * MB;
     const uint64_t cap_rows = std::min(kXbElems / a.cols, kInvFloats) / BM * BM;
     if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);

@@ -80,8 +80,10 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *   3 HALO_MI_GEMM_SLAB_BF16 SLAB layout, bf16 MFMA GEMM (dequantized W and x rounded to
  *                            bf16, fp32 accumulate) on M tiles of 64 / 128 / 256 rows by n_vec;
  *                            any n_vec.
- *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8; else 5 when n_vec > 256 and its
- *                            tiles fill the GPU, else 3.
+ *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8; else the small-M bf16 GEMM
+ *                            (same numerics as 3, no LDS stage) for n_vec <= 32 when cols is a
+ *                            multiple of 256; else 5 when n_vec > 256 and its tiles fill the
+ *                            GPU, else 3.
  *   5 HALO_MI_GEMM_SLAB_BF16_M512  the bf16 MFMA GEMM on 512-row M tiles (every wave both
  *                            dequantizes and multiplies; same numerics as 3); any n_vec.
  */

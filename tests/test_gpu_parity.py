@@ -237,6 +237,36 @@ def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case, variant):
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("case", [(37, 5120, 17, 0, 0, 5, 3), (130, 1024, 9, 0, 0, 4, 1), (200, 768, 32, 0, 0, 0, 0),
+                                  (64, 256, 12, 0, 0, 0, 0)])
+def test_gemm_small_m_within_bounds(hl, oracle, dev, t, case):
+    """The auto variant at 9..32 x rows runs the small-M GEMM (k_gemm_sm: every wave dequantizes
+    its own MFMA B fragments, no LDS; K chunks added in order by the reduce): the same bf16
+    bounds as the other GEMM tile families, against the CPU and the bf16-exact products, and a
+    second call is bitwise the first."""
+    rows, cols, n_vec, pad, off, xp, yp = case
+    say("gemm_small_m", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=320 + t + rows, stride_pad=pad, offset=off)
+    dense = dense_of(buf, t, rows, cols, stride, off)
+    x = np.random.default_rng(3200 + t + n_vec).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    if xp % 4:
+        xp += 4 - xp % 4
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, 4, xp, yp)
+    err = np.abs(y.astype(np.float64) - ref)
+    tol = gemm_tol(oracle, t, dense, rows, cols, x)
+    print(f"    gemm vs cpu: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    emu, etol = gemm_emulated(oracle, t, dense, rows, cols, x)
+    eerr = np.abs(y.astype(np.float64) - emu)
+    print(f"    gemm vs bf16-exact products: worst |d|/bound = {max_ratio(eerr, etol):.4f}")
+    assert np.all(eerr <= etol)
+    y2 = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, 4, xp, yp)
+    assert isclose_bits(y2, y), "a second small-M GEMM call gave different bits"
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("pair", [False, True])
 @pytest.mark.parametrize("kind", ["one", "many"])
 def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
@@ -287,7 +317,7 @@ def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3), (300, 3), (17, 5), (300, 5),
-                                           (600, 5)])
+                                           (600, 5), (5, 4), (8, 4), (17, 4), (32, 4)])
 def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
     import torch
 
