@@ -847,17 +847,18 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 // matrix w / 2 and row block w % 2 (32 W rows). Lane l dequantizes row l % 32, half l / 32 of
 // each slot record, which is exactly its B operand of v_mfma_f32_32x32x16_bf16 for the slot's
 // two K halves: no LDS, no barrier, every wave streams on its own with kSmDepth slots of
-// weight records and x fragments in flight (the four waves read the same x fragments: L1
-// hits). Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128]
+// weight records and kSmXDepth slots of x fragments in flight (the four waves read the same x
+// fragments: L1 hits). Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128]
 // (columns 64 * matrix + 32 * block), and k_gemm_pc_reduce adds the chunks in order and applies
 // the epilogue. Per slot and lane: one exact dequantization and two MFMAs, so the kernel is
 // bound by the dequantization's VALU work instead of a per-stage barrier chain.
 // ------------------------------------------------------------------------------------------
-constexpr int kSmDepth = 8;  // slots in flight per wave (also the loop unroll: ring slot static)
+constexpr int kSmDepth = 16;  // slots of weight records in flight per wave (two half-rounds of 8)
+constexpr int kSmXDepth = 2;  // slots of x fragments in flight per wave
 constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
 
 template <uint32_t T, bool PAIR>
-__global__ __launch_bounds__(256) void k_gemm_sm(GemmPcArgs a) {
+__global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = a.cols / kSlot;
@@ -881,27 +882,36 @@ __global__ __launch_bounds__(256) void k_gemm_sm(GemmPcArgs a) {
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
     const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf, (uint32_t)((uint64_t)kSmRows * a.cols * 2));
     const uint32_t xlane = lane * 16;
+    // weight records kSmDepth slots ahead (HBM), x fragments kSmXDepth slots ahead (L2)
     PcW<T> R[kSmDepth];
-    uint4 X[kSmDepth][2];
-    // slot s of this chunk into ring slot q; slots past the chunk read zeros (out of range)
-    auto load = [&](int q, uint32_t s) {
-        const bool live = s < s_end;
-        pc_load_w<T>(R[q], wres, g, off, s, live);
+    uint4 X[kSmXDepth][2];
+    auto load_w = [&](int q, uint32_t s) { pc_load_w<T>(R[q], wres, g, off, s, s < s_end); };
+    auto load_x = [&](int q, uint32_t s) {
 #pragma unroll
-        for (int k = 0; k < 2; ++k) X[q][k] = bld128(xres, xlane, live ? (s * 2 + k) * 1024 : kPcOob);
+        for (int k = 0; k < 2; ++k) X[q][k] = bld128(xres, xlane, s < s_end ? (s * 2 + k) * 1024 : kPcOob);
     };
 #pragma unroll
-    for (int q = 0; q < kSmDepth; ++q) load(q, s_begin + q);
+    for (int q = 0; q < kSmXDepth; ++q) load_x(q, s_begin + q);
+#pragma unroll
+    for (int q = 0; q < kSmDepth; ++q) load_w(q, s_begin + q);
     floatx16 acc = floatx16{};
+    // slot s: ring slots s % kSmDepth and s % kSmXDepth, static in the unrolled half-rounds;
+    // chunks are whole super-blocks, so the loop may end after either half
+    auto step = [&](int q, uint32_t s) {
+        bf16x8 lo, hi;
+        pc_dequant<T>(R[q], h, q % 8, inv_unit, lo, hi);  // s_begin: a multiple of 8
+        const int qx = q % kSmXDepth;
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[qx][0]), lo, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[qx][1]), hi, acc, 0, 0, 0);
+        load_x(qx, s + kSmXDepth);
+        load_w(q, s + kSmDepth);
+    };
     for (uint32_t i0 = s_begin; i0 < s_end; i0 += kSmDepth) {
 #pragma unroll
-        for (int q = 0; q < kSmDepth; ++q) {
-            bf16x8 lo, hi;
-            pc_dequant<T>(R[q], h, q % 8, inv_unit, lo, hi);  // s_begin and i0: multiples of 8
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[q][0]), lo, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[q][1]), hi, acc, 0, 0, 0);
-            load(q, i0 + q + kSmDepth);
-        }
+        for (int q = 0; q < 8; ++q) step(q, i0 + q);
+        if (i0 + 8 >= s_end) break;
+#pragma unroll
+        for (int q = 8; q < kSmDepth; ++q) step(q, i0 + q);
     }
     float* P = a.partials + ((uint64_t)u * a.kchunks + chunk) * kSmRows * kPcW + 64 * mat + 32 * rb + r;
 #pragma unroll
