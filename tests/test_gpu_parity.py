@@ -238,10 +238,11 @@ def test_gemm_bf16_within_bounds(hl, oracle, dev, t, case, variant):
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("case", [(37, 5120, 17, 0, 0, 5, 3), (130, 1024, 9, 0, 0, 4, 1), (200, 768, 32, 0, 0, 0, 0),
-                                  (64, 256, 12, 0, 0, 0, 0)])
+                                  (64, 256, 12, 0, 0, 0, 0), (130, 1024, 40, 0, 0, 4, 1), (37, 768, 64, 0, 0, 0, 0)])
 def test_gemm_small_m_within_bounds(hl, oracle, dev, t, case):
     """The auto variant at 9..32 x rows runs the small-M GEMM (k_gemm_sm: every wave dequantizes
-    its own MFMA B fragments, no LDS; K chunks added in order by the reduce): the same bf16
+    its own MFMA B fragments, no LDS; K chunks added in order by the reduce), at 40 and 64 rows
+    the 64-row tiles of k_gemm_pc: the same bf16
     bounds as the other GEMM tile families, against the CPU and the bf16-exact products, and a
     second call is bitwise the first."""
     rows, cols, n_vec, pad, off, xp, yp = case
@@ -317,7 +318,7 @@ def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("n_vec,variant", [(1, 2), (2, 2), (4, 2), (5, 2), (8, 3), (17, 3), (300, 3), (17, 5), (300, 5),
-                                           (600, 5), (5, 4), (8, 4), (17, 4), (32, 4)])
+                                           (600, 5), (5, 4), (8, 4), (17, 4), (32, 4), (48, 4), (64, 4)])
 def test_gate_up_swiglu(hl, oracle, dev, t, n_vec, variant):
     import torch
 
