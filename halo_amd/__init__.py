@@ -18,10 +18,13 @@ from ._lib import (  # noqa: F401
     ARGMAX_RESULT_BYTES,
     SLAB_ROWS,
     STATUS_BAD_INDEX,
+    STATUS_SPLITK_TIMEOUT,
+    argmax,
     block_bytes,
     block_elems,
     dequant_rows,
     fill_normal,
+    force_splitk_timeout,
     gate_up_swiglu,
     gemv,
     gemv_group,
@@ -34,6 +37,8 @@ from ._lib import (  # noqa: F401
     rms_norm,
     row_bytes,
     slab_bytes,
+    stream_check,
+    stream_release,
     swiglu,
     unpack_slab,
     unpack_slab_host,

@@ -41,6 +41,8 @@ class Variant(enum.IntEnum):
     SLAB_GEMM_BF16 = 3
     SLAB_AUTO = 4
     SLAB_GEMM_BF16_M512 = 5
+    SLAB_GEMV_VALU = 6
+    SLAB_GEMM_BF16_SMALL_M = 7
 
 
 class ErrorCode(enum.IntEnum):
@@ -168,11 +170,13 @@ class _GetRowsParams(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("out_stride", ctypes.c_uint64),
         ("status", ctypes.c_void_p),
+        ("status_keep", ctypes.c_uint32),
     ]
 
 
 ARGMAX_RESULT_BYTES = 12  # HALO_MI_ARGMAX_RESULT_BYTES: {index, value bits, poisoned} per vector
 STATUS_BAD_INDEX = 8  # HALO_MI_STATUS_BAD_INDEX: a GET_ROWS id outside the table
+STATUS_SPLITK_TIMEOUT = 0x100  # HALO_MI_STATUS_SPLITK_TIMEOUT: a split-K reduction gave up waiting
 
 
 # Every symbol include/halo_mi355x.h declares, with its ctypes signature.
@@ -183,10 +187,14 @@ SIGNATURES = {
     "halo_mi_gemv_group": (_INT, [ctypes.POINTER(_GemvGroupParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
     "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
+    "halo_mi_argmax": (_INT, [_VP, _U64, _U32, _U32, _VP, _VP]),
     "halo_mi_swiglu": (_INT, [_VP, _U64, _VP, _U64, _VP, _U64, _U32, _U32, _VP]),
     "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
     "halo_mi_get_rows": (_INT, [ctypes.POINTER(_GetRowsParams), _VP]),
     "halo_mi_rms_norm": (_INT, [_VP, _U64, _VP, _VP, _U64, _U32, _U32, ctypes.c_float, _VP]),
+    "halo_mi_stream_check": (_INT, [_VP]),
+    "halo_mi_stream_release": (_INT, [_VP]),
+    "halo_mi_test_splitk_timeout": (_INT, [_U32, _INT]),
     "halo_mi_row_bytes": (_U64, [_U32, _U32]),
     "halo_mi_slab_bytes": (_U64, [_U32, _U32, _U32]),
     "halo_mi_repack_slab": (_INT, [_U32, _VP, _U64, _U32, _U32, _VP, _VP]),
@@ -351,6 +359,11 @@ def lm_head(t: int, w, x, result, rows: int, cols: int, n_vec: int, *, logits=No
     _check(lib().halo_mi_lm_head(ctypes.byref(p), _stream(stream)))
 
 
+def argmax(logits, result, n: int, n_vec: int, *, logits_stride: int = 0, stream=None) -> None:
+    """ARGMAX (halo_mi_argmax): result receives n_vec triples {index, value bits, poisoned}."""
+    _check(lib().halo_mi_argmax(_ptr(logits), int(logits_stride), int(n), int(n_vec), _ptr(result), _stream(stream)))
+
+
 def swiglu(gate, up, out, rows: int, cols: int, *, gate_stride: int = 0, up_stride: int = 0, out_stride: int = 0,
            stream=None) -> None:
     _check(lib().halo_mi_swiglu(_ptr(gate), int(gate_stride), _ptr(up), int(up_stride), _ptr(out), int(out_stride),
@@ -365,10 +378,10 @@ def dequant_rows(t: int, layout: int, w, rows: int, cols: int, out, *, first_row
 
 
 def get_rows(t: int, layout: int, table, n_rows: int, cols: int, ids, n_ids: int, out, *, table_stride: int = 0,
-             out_stride: int = 0, status=None, stream=None) -> None:
+             out_stride: int = 0, status=None, status_keep: bool = False, stream=None) -> None:
     """GET_ROWS (halo_mi_get_rows): out[i] = dequant(table row ids[i]); ids int32 on the device."""
     p = _GetRowsParams(int(t), int(layout), _ptr(table), int(table_stride), int(n_rows), int(cols), _ptr(ids), int(n_ids),
-                       _ptr(out), int(out_stride), _ptr(status))
+                       _ptr(out), int(out_stride), _ptr(status), 1 if status_keep else 0)
     _check(lib().halo_mi_get_rows(ctypes.byref(p), _stream(stream)))
 
 
@@ -377,6 +390,23 @@ def rms_norm(x, w, out, rows: int, cols: int, *, eps: float = 1e-6, x_stride: in
     """RMS_NORM (halo_mi_rms_norm), bitwise cpu::rms_norm."""
     _check(lib().halo_mi_rms_norm(_ptr(x), int(x_stride), _ptr(w), _ptr(out), int(out_stride), int(rows), int(cols),
                                   float(eps), _stream(stream)))
+
+
+def stream_check(stream=None) -> None:
+    """Synchronizes the stream and raises HaloError(Device) when a kernel marked its status word
+    (a split-K reduction that gave up waiting) since the last check (halo_mi_stream_check)."""
+    _check(lib().halo_mi_stream_check(_stream(stream)))
+
+
+def stream_release(stream=None) -> None:
+    """Frees the stream's workspace on the current device (halo_mi_stream_release)."""
+    _check(lib().halo_mi_stream_release(_stream(stream)))
+
+
+def force_splitk_timeout(spin_limit: int, force: bool) -> None:
+    """Failure-path test hook (halo_mi_test_splitk_timeout): force every split-K reduction to give
+    up after spin_limit rounds; force=False restores normal operation."""
+    _check(lib().halo_mi_test_splitk_timeout(int(spin_limit), 1 if force else 0))
 
 
 def repack_slab(t: int, src, rows: int, cols: int, dst, *, src_stride: int = 0, stream=None) -> None:

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -31,7 +32,31 @@ uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes) { return row
 namespace {
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+// halo_mi_test_splitk_timeout's setting (0 / false: the kernels' own defaults)
+std::atomic<uint32_t> g_test_spin_limit{0};
+std::atomic<bool> g_test_flip{false};
+
+void free_workspace(Workspace& w) {
+    void* bufs[] = {w.status, w.partials, w.slots, w.counters, w.xb, w.parts, w.xn, w.inv};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    w = Workspace{};
+}
+
+// Clears the counters, the split-K words and the status word (fill kernels on st, never a memset).
+int clear_workspace(const Workspace& w, hipStream_t st) {
+    if (launch_fill_u32(w.counters, kCounters, 0u, st) != HALO_MI_OK ||
+        launch_fill_u32(reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u, st) != HALO_MI_OK ||
+        launch_fill_u32(w.status, 1, 0u, st) != HALO_MI_OK)
+        return set_error(HALO_MI_E_DEVICE, "workspace: clearing failed");
+    return HALO_MI_OK;
+}
 }  // namespace
+
+void apply_test_hooks(GemvSlabArgs& a) {
+    a.spin_limit = g_test_spin_limit.load(std::memory_order_relaxed);
+    a.tag_flip = g_test_flip.load(std::memory_order_relaxed) ? (1ull << 63) : 0ull;
+}
 
 int workspace_for(hipStream_t st, Workspace** out) {
     int dev = 0;
@@ -48,47 +73,34 @@ int workspace_for(hipStream_t st, Workspace** out) {
         return HALO_MI_OK;
     }
     Workspace w;
-    if (hipMalloc(&w.partials, kPartialFloats * sizeof(float)) != hipSuccess)
-        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K workspace");
-    if (hipMalloc(&w.counters, kCounters * sizeof(uint32_t)) != hipSuccess) {
-        (void)hipFree(w.partials);
-        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K counters");
+    struct Alloc {
+        void** p;
+        uint64_t bytes;
+        const char* what;
+    };
+    const Alloc allocs[] = {
+        {reinterpret_cast<void**>(&w.status), 256, "the status word"},
+        {reinterpret_cast<void**>(&w.partials), kPartialFloats * sizeof(float), "the GEMM partials"},
+        {reinterpret_cast<void**>(&w.counters), kCounters * sizeof(uint32_t), "the split-K counters"},
+        {reinterpret_cast<void**>(&w.xb), kXbElems * sizeof(__bf16), "the bf16 staging buffer for x"},
+        {reinterpret_cast<void**>(&w.slots), kSlots * sizeof(uint64_t), "the split-K words"},
+        {reinterpret_cast<void**>(&w.parts), kArgParts * sizeof(ArgPart), "the argmax parts"},
+        {reinterpret_cast<void**>(&w.xn), kNormFloats * sizeof(float), "the normalized x rows"},
+        {reinterpret_cast<void**>(&w.inv), kInvFloats * sizeof(float), "the norm scales"},
+    };
+    for (const Alloc& al : allocs)
+        if (hipMalloc(al.p, al.bytes) != hipSuccess) {
+            free_workspace(w);
+            return set_error(HALO_MI_E_MEMORY, "workspace: cannot allocate %s", al.what);
+        }
+    if (clear_workspace(w, st) != HALO_MI_OK) {
+        (void)hipStreamSynchronize(st);
+        free_workspace(w);
+        return set_error(HALO_MI_E_DEVICE, "workspace: init failed");
     }
-    if (hipMalloc(&w.xb, kXbElems * sizeof(__bf16)) != hipSuccess) {
-        (void)hipFree(w.partials);
-        (void)hipFree(w.counters);
-        return set_error(HALO_MI_E_MEMORY, "gemm: cannot allocate the bf16 staging buffer for x");
-    }
-    if (hipMalloc(&w.slots, kSlots * sizeof(uint64_t)) != hipSuccess) {
-        (void)hipFree(w.partials);
-        (void)hipFree(w.counters);
-        (void)hipFree(w.xb);
-        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the split-K slots");
-    }
-    if (hipMalloc(&w.parts, kArgParts * sizeof(ArgPart)) != hipSuccess) {
-        (void)hipFree(w.partials);
-        (void)hipFree(w.counters);
-        (void)hipFree(w.xb);
-        (void)hipFree(w.slots);
-        return set_error(HALO_MI_E_MEMORY, "lm_head: cannot allocate the argmax parts");
-    }
-    if (hipMalloc(&w.xn, kNormFloats * sizeof(float)) != hipSuccess ||
-        hipMalloc(&w.inv, kInvFloats * sizeof(float)) != hipSuccess) {
-        (void)hipFree(w.partials);
-        (void)hipFree(w.counters);
-        (void)hipFree(w.xb);
-        (void)hipFree(w.slots);
-        (void)hipFree(w.parts);
-        if (w.xn) (void)hipFree(w.xn);
-        return set_error(HALO_MI_E_MEMORY, "gemv: cannot allocate the norm buffers");
-    }
-    if (launch_fill_u32(w.counters, kCounters, 0u, st) != HALO_MI_OK ||
-        launch_fill_u32(reinterpret_cast<uint32_t*>(w.slots), 2 * kSlots, 0u, st) != HALO_MI_OK)
-        return set_error(HALO_MI_E_DEVICE, "gemv: workspace init failed");
     *out = &(g_ws[{dev, st}] = w);
     return HALO_MI_OK;
 }
-
 
 int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, uint64_t y_stride, uint32_t rows,
              uint32_t cols, uint32_t n_vec) {
@@ -116,8 +128,12 @@ int check_norm(const char* op, const float* norm_w, uint32_t cols, const void* o
 
 // The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
 uint32_t gemm_tiles(uint32_t variant) {
-    return variant == HALO_MI_GEMM_SLAB_BF16 ? kGemmTilesPc : variant == HALO_MI_GEMM_SLAB_BF16_M512 ? kGemmTilesLm
-                                                                                                   : kGemmTilesAuto;
+    switch (variant) {
+        case HALO_MI_GEMM_SLAB_BF16: return kGemmTilesPc;
+        case HALO_MI_GEMM_SLAB_BF16_M512: return kGemmTilesLm;
+        case HALO_MI_GEMM_SLAB_BF16_SMALL_M: return kGemmTilesSm;
+        default: return kGemmTilesAuto;
+    }
 }
 
 }  // namespace halo_mi
@@ -134,7 +150,7 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     const uint64_t rb = row_bytes_checked(p->type, p->cols, &code, op);
     if (code) return code;
     uint32_t variant = p->variant;
-    if (variant > HALO_MI_GEMM_SLAB_BF16_M512)
+    if (variant > HALO_MI_GEMV_VARIANT_LAST)
         return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
     if (variant == HALO_MI_GEMV_DEFAULT)
         variant = p->layout == HALO_MI_LAYOUT_SLAB ? HALO_MI_GEMV_SLAB_AUTO : HALO_MI_GEMV_GGUF_REF;
@@ -183,10 +199,11 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     if (ranges_overlap(p->y, yext, p->w, halo_mi_slab_bytes(p->type, p->rows, p->cols)))
         return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
     if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = p->n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
-    if (variant == HALO_MI_GEMV_SLAB) {
+    if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
         a.norm_w = p->norm_w;
         a.norm_eps = p->norm_eps;
+        a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<false>(p->type, a, st);
     }
     if (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
@@ -255,11 +272,11 @@ int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
     const uint64_t rb = row_bytes_checked(g.type, g.cols, &code, op);
     if (code) return code;
     uint32_t variant = g.variant;
-    if (variant > HALO_MI_GEMM_SLAB_BF16_M512)
+    if (variant > HALO_MI_GEMV_VARIANT_LAST)
         return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
     const bool slab = g.layout == HALO_MI_LAYOUT_SLAB;
     const bool fused = slab && (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB ||
-                                variant == HALO_MI_GEMV_SLAB_AUTO);
+                                variant == HALO_MI_GEMV_SLAB_AUTO || variant == HALO_MI_GEMV_SLAB_VALU);
     if (!fused && !g.y) return set_error(HALO_MI_E_KERNEL, "%s: variant %u ranks the logits: gemv.y is needed", op, variant);
     if ((p->ids_slots == nullptr) != (p->ids_scatter == nullptr) || (p->ids_scatter && !p->ids))
         return set_error(HALO_MI_E_KERNEL, "%s: ids_slots and ids_scatter go together, and only with ids", op);
@@ -319,6 +336,7 @@ int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream) {
         a.valid_rows = p->valid_rows;
         a.norm_w = g.norm_w;
         a.norm_eps = g.norm_eps;
+        a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         if ((code = launch_gemv_slab<false>(g.type, a, st))) return code;
     } else {
         if ((code = halo_mi_gemv(&g, stream))) return code;
@@ -338,7 +356,7 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     if (p->layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: needs the SLAB layout", op);
     if (!is_quant(p->type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
     uint32_t variant = p->variant;
-    if (variant == HALO_MI_GEMV_GGUF_REF || variant > HALO_MI_GEMM_SLAB_BF16_M512)
+    if (variant == HALO_MI_GEMV_GGUF_REF || variant > HALO_MI_GEMV_VARIANT_LAST)
         return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, variant);
     const uint64_t xs = p->x_stride ? p->x_stride : p->cols;
     const uint64_t os = p->out_stride ? p->out_stride : p->rows;
@@ -355,11 +373,12 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
         variant = p->n_vec <= kGateUpGemvMax ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
     auto st = static_cast<hipStream_t>(stream);
-    if (variant == HALO_MI_GEMV_SLAB) {
+    if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                        p->rows, p->cols, p->n_vec};
         a.norm_w = p->norm_w;
         a.norm_eps = p->norm_eps;
+        a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<true>(p->type, a, st);
     }
     if (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
@@ -370,6 +389,32 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     a.norm_w = p->norm_w;
     a.norm_eps = p->norm_eps;
     return launch_gemm_pc<true>(p->type, a, st);
+}
+
+int halo_mi_argmax(const float* logits, uint64_t logits_stride, uint32_t n, uint32_t n_vec, void* result, void* stream) {
+    clear_error();
+    const char* op = "ARGMAX_FUSED";
+    if (n_vec == 0) return HALO_MI_OK;
+    if (n == 0) return set_error(HALO_MI_E_KERNEL, "%s: empty row", op);
+    if (!logits || !result) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    const uint64_t ls = logits_stride ? logits_stride : n;
+    if (n_vec > 1 && ls < n) return set_error(HALO_MI_E_KERNEL, "%s: logits row stride < n", op);
+    if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(result)) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: operands must be 4-byte aligned", op);
+    if (ranges_overlap(result, (uint64_t)n_vec * HALO_MI_ARGMAX_RESULT_BYTES, logits, extent(n_vec, ls * 4, (uint64_t)n * 4)))
+        return set_error(HALO_MI_E_KERNEL, "%s: result overlaps logits", op);
+    auto st = static_cast<hipStream_t>(stream);
+    Workspace* ws = nullptr;
+    int code;
+    if ((code = workspace_for(st, &ws))) return code;
+    if (!ws)
+        return set_error(HALO_MI_E_MEMORY, "%s: this stream is being captured and has no workspace yet "
+                                           "(make one call on it before capturing)", op);
+    const uint32_t n_parts = (n + kSlabRows - 1) / kSlabRows;
+    if ((uint64_t)n_parts * n_vec > kArgParts)
+        return set_error(HALO_MI_E_UNSUPPORTED, "%s: %u rows of %u exceed the argmax workspace", op, n_vec, n);
+    if ((code = launch_argmax_parts(logits, ls, n, n_vec, 0, ws->parts, st))) return code;
+    return launch_argmax_finish(ws->parts, n_parts, n_vec, static_cast<uint32_t*>(result), nullptr, nullptr, nullptr, 0, st);
 }
 
 int halo_mi_swiglu(const float* gate, uint64_t gate_stride, const float* up, uint64_t up_stride, float* out,
@@ -432,7 +477,7 @@ int halo_mi_get_rows(const halo_mi_get_rows_params* p, void* stream) {
     auto st = static_cast<hipStream_t>(stream);
     if (p->status) {
         if (reinterpret_cast<uintptr_t>(p->status) % 4) return set_error(HALO_MI_E_KERNEL, "%s: status must be 4-byte aligned", op);
-        if ((code = launch_fill_u32(p->status, 1, 0u, st))) return code;
+        if (!p->status_keep && (code = launch_fill_u32(p->status, 1, 0u, st))) return code;
     }
     if (p->n_ids == 0 || p->cols == 0) return HALO_MI_OK;
     if (!p->table || !p->ids || !p->out) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
@@ -514,6 +559,51 @@ int halo_mi_unpack_slab(uint32_t type, const void* src, uint32_t rows, uint32_t 
     if (rows == 0 || cols == 0) return HALO_MI_OK;
     return launch_unpack_slab(type, static_cast<const uint8_t*>(src), rows, cols, static_cast<uint8_t*>(dst), dst_stride,
                               static_cast<hipStream_t>(stream));
+}
+
+int halo_mi_stream_check(void* stream) {
+    clear_error();
+    auto st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "stream_check: hipGetDevice failed");
+    Workspace w;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        auto it = g_ws.find({dev, st});
+        if (it == g_ws.end()) return hip_status(hipStreamSynchronize(st), "stream_check");
+        w = it->second;
+    }
+    uint32_t word = 0;
+    if (int rc = hip_status(hipMemcpyAsync(&word, w.status, sizeof(word), hipMemcpyDeviceToHost, st), "stream_check"))
+        return rc;
+    if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
+    if (word == 0) return HALO_MI_OK;
+    // the words and counters of a wait that gave up are in an unknown state: start again clean
+    if (int rc = clear_workspace(w, st)) return rc;
+    if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
+    return set_error(HALO_MI_E_DEVICE, "stream_check: a split-K reduction gave up waiting for partial sums "
+                                       "(status 0x%x); outputs written since the last check hold NaN", word);
+}
+
+int halo_mi_stream_release(void* stream) {
+    clear_error();
+    auto st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "stream_release: hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = g_ws.find({dev, st});
+    if (it == g_ws.end()) return HALO_MI_OK;
+    const int rc = hip_status(hipStreamSynchronize(st), "stream_release");
+    free_workspace(it->second);
+    g_ws.erase(it);
+    return rc;
+}
+
+int halo_mi_test_splitk_timeout(uint32_t spin_limit, int force) {
+    clear_error();
+    g_test_spin_limit.store(spin_limit, std::memory_order_relaxed);
+    g_test_flip.store(force != 0, std::memory_order_relaxed);
+    return HALO_MI_OK;
 }
 
 }  // extern "C"

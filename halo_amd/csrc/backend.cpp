@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <array>
+#include <bit>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -57,14 +58,18 @@ std::uint64_t mul_u64(std::uint64_t a, std::uint64_t b, const char* op, const ch
 const char* type_name(DType t) {
     switch (t) {
         case DType::F32: return "F32";
+        case DType::F16: return "F16";
         case DType::Q4_0: return "Q4_0";
         case DType::Q8_0: return "Q8_0";
+        case DType::Q3_K: return "Q3_K";
         case DType::Q4_K: return "Q4_K";
         case DType::Q5_K: return "Q5_K";
         case DType::Q6_K: return "Q6_K";
+        case DType::IQ4_NL: return "IQ4_NL";
+        case DType::IQ3_S: return "IQ3_S";
         case DType::IQ4_XS: return "IQ4_XS";
+        default: return "?";
     }
-    return "?";
 }
 
 // ---- buffers --------------------------------------------------------------------------------
@@ -74,7 +79,7 @@ struct SlabMeta {
     std::uint32_t rows = 0, cols = 0;
 };
 
-class DeviceBuffer final : public Buffer {
+class DeviceBuffer final : public MiBuffer {
 public:
     DeviceBuffer(const Backend* owner, void* mem, std::uint64_t bytes, Tier tier, bool writable, bool host, WeightLayout layout,
                  SlabMeta meta)
@@ -105,21 +110,35 @@ private:
 
 // ---- streams --------------------------------------------------------------------------------
 
-class MiBackend;
+class Mi355xBackend;
 
-class HipStream final : public Stream {
+// A stream owns its hipStream_t and one device word for the GET_ROWS status bits of the ops
+// enqueued since the last wait(); the library's per-stream workspace is released with it.
+class HipStream final : public MiStream {
 public:
-    HipStream(MiBackend* owner, hipStream_t s) : owner_(owner), s_(s) {}
-    ~HipStream() override { (void)hipStreamDestroy(s_); }
+    HipStream(Mi355xBackend* owner, hipStream_t s, std::uint32_t* status) : owner_(owner), s_(s), status_(status) {}
+    ~HipStream() override {
+        (void)hipStreamSynchronize(s_);
+        (void)halo_mi_stream_release(s_);
+        (void)hipFree(status_);
+        (void)hipStreamDestroy(s_);
+    }
     void submit() override {}
     void wait() override;
     void abort() noexcept override { (void)hipStreamSynchronize(s_); }
     void* native() const noexcept override { return s_; }
-    const MiBackend* owner() const noexcept { return owner_; }
+    const Mi355xBackend* owner() const noexcept { return owner_; }
+    // the GET_ROWS status word, marked as used until the next wait()
+    std::uint32_t* get_rows_status() noexcept {
+        status_used_ = true;
+        return status_;
+    }
 
 private:
-    MiBackend* owner_;
+    Mi355xBackend* owner_;
     hipStream_t s_;
+    std::uint32_t* status_;
+    bool status_used_ = false;
 };
 
 // ---- operand resolution ---------------------------------------------------------------------
@@ -213,7 +232,7 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 12> kVariants{{
+constexpr std::array<VariantInfo, 17> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
     {kRmsNorm, "rms_norm_cpu_order", OpId::RmsNorm, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
@@ -221,11 +240,16 @@ constexpr std::array<VariantInfo, 12> kVariants{{
     {kGemmSlabBf16, "gemm_slab_bf16_mfma", OpId::Gemv, {}},
     {kGemvSlabAuto, "gemv_slab_auto", OpId::Gemv, {}},
     {kGemmSlabBf16M512, "gemm_slab_bf16_mfma_m512", OpId::Gemv, {}},
+    {kGemvSlabValu, "gemv_slab_valu_w64", OpId::Gemv, {}},
+    {kGemmSlabBf16SmallM, "gemm_slab_bf16_mfma_small_m", OpId::Gemv, {}},
     {kSwiglu, "swiglu_b256", OpId::Swiglu, {}},
+    {kLmHeadFused, "lm_head_argmax_parts", OpId::LmHead, {}},
+    {kArgmax, "argmax_parts_b256", OpId::Argmax, {}},
+    {kCopy, "copy_async", OpId::Copy, {}},
     {kGateUpGemv, "gate_up_gemv_w64", OpId::GateUpSwiglu, {}},
     {kGateUpGemm, "gate_up_gemm_bf16_mfma", OpId::GateUpSwiglu, {}},
     {kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512", OpId::GateUpSwiglu, {}},
-    {kLmHeadFused, "lm_head_slab_argmax", OpId::LmHead, {}},
+    {kGateUpGemmSmallM, "gate_up_gemm_bf16_mfma_small_m", OpId::GateUpSwiglu, {}},
 }};
 
 bool has_variant(OpId op, std::uint32_t id) {
@@ -233,11 +257,18 @@ bool has_variant(OpId op, std::uint32_t id) {
     return std::any_of(kVariants.begin(), kVariants.end(), [&](const VariantInfo& v) { return v.op == op && v.id == id; });
 }
 
+// MATMUL registry id -> the C ABI's variant id (the two lists are in the same order)
+std::uint32_t abi_gemv_variant(std::uint32_t id) { return id == 0 ? HALO_MI_GEMV_DEFAULT : id - kGemvGgufRef + 1; }
+
+void check_no_status(const StatusRef& st, const char* op) {
+    CHECK(st.empty(), ErrorCode::Unsupported, "%s: per-sequence status words are not implemented (WS-BI-1)", op);
+}
+
 // ---- the backend ----------------------------------------------------------------------------
 
-class MiBackend final : public Backend {
+class Mi355xBackend final : public MiBackend {
 public:
-    explicit MiBackend(int device) : device_(device) {
+    explicit Mi355xBackend(int device) : device_(device) {
         int n = 0;
         CHECK(hipGetDeviceCount(&n) == hipSuccess && device >= 0 && device < n, ErrorCode::Device,
               "mi355x backend: no HIP device %d (%d visible)", device, n);
@@ -258,9 +289,10 @@ public:
     }
     Limits limits() const noexcept override {
         Limits l;
-        l.max_n_vec = std::numeric_limits<std::uint32_t>::max();
         l.lm_head_ids = true;
-        l.max_fused_norm_cols = 4u << 20;  // the reference-order variant's normalized-x buffer
+        // Every variant's fused norm is bitwise rms_norm then the same variant unfused; the
+        // reference-order variant normalizes a vector at a time into a 4 Mi-float buffer.
+        l.max_fused_norm_cols = 4u << 20;
         return l;
     }
     bool lost() const noexcept override { return lost_; }
@@ -309,8 +341,8 @@ public:
         check_alive("import_weights");
         const auto t = static_cast<std::uint32_t>(type);
         const std::uint64_t rb = halo_mi_row_bytes(t, cols);
-        CHECK(type != DType::F32 && rb != 0, ErrorCode::Unsupported, "import_weights: %s x %u has no SLAB layout", type_name(type),
-              cols);
+        CHECK(type != DType::F32 && rb != 0 && halo_mi_slab_bytes(t, 1, cols) != 0, ErrorCode::Unsupported,
+              "import_weights: %s x %u has no SLAB layout", type_name(type), cols);
         const std::uint64_t stride = row_stride ? row_stride : rb;
         CHECK(rows == 0 || gguf.size() >= (rows - 1) * stride + rb, ErrorCode::Kernel,
               "import_weights: %zu bytes hold fewer than %u rows", gguf.size(), rows);
@@ -329,7 +361,17 @@ public:
         hipStream_t s = nullptr;
         CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess, ErrorCode::Device,
               "mi355x backend: cannot create a stream");
-        return std::make_unique<HipStream>(this, s);
+        void* status = nullptr;
+        if (hipMalloc(&status, 256) != hipSuccess) {
+            (void)hipStreamDestroy(s);
+            fail(ErrorCode::Memory, "mi355x backend: cannot allocate a stream's status word");
+        }
+        if (hipMemsetAsync(status, 0, 4, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+            (void)hipFree(status);
+            (void)hipStreamDestroy(s);
+            fail(ErrorCode::Device, "mi355x backend: cannot clear a stream's status word");
+        }
+        return std::make_unique<HipStream>(this, s, static_cast<std::uint32_t*>(status));
     }
 
     void upload(Stream& s, TensorRef dst, std::span<const std::byte> src) override {
@@ -365,7 +407,7 @@ public:
         const std::uint64_t rb = row_bytes(a.type, a.cols, r.op());
         CHECK(a.first_row <= a.n_rows_table && a.n_rows <= a.n_rows_table - a.first_row, ErrorCode::Kernel,
               "GET_ROWS: rows [%u, %u) out of %u", a.first_row, a.first_row + a.n_rows, a.n_rows_table);
-        const bool slab = !a.table.empty() && a.table.buffer->layout() == WeightLayout::Slab;
+        const bool slab = is_slab(a.table);
         const Operand table = slab ? r.slab(a.table, a.type, a.n_rows_table, a.cols, "table")
                                    : r.get(a.table, a.n_rows_table, rb, a.type == DType::F32 ? kF32 : 1, Access::Read, "table");
         const Operand out = r.f32(a.out, a.n_rows, a.cols, Access::Write, "out");
@@ -377,30 +419,28 @@ public:
     }
 
     // GET_ROWS with device ids (GetRowsArgs, backend.h:254-263): the id range is checked by the
-    // kernel, which reports through the optional status word as the reference's HIP backend does.
+    // kernel, which sets the stream's status word as the reference's HIP backend does
+    // (backends/hip/src/ops.cpp:982-1012); the stream's wait() reports it as Error(Kernel).
     void get_rows(Stream& s, const GetRowsArgs& a) override {
         HipStream& st = stream(s, "GET_ROWS");
         CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kDequantRows, ErrorCode::Config,
               "GET_ROWS: unknown kernel variant id %u", a.kernel.variant_id);
+        check_no_status(a.status, "GET_ROWS");
         const Resolver r(this, "GET_ROWS");
         const auto t = static_cast<std::uint32_t>(a.type);
         const std::uint64_t rb = row_bytes(a.type, a.cols, r.op());
-        const bool slab = !a.table.empty() && a.table.buffer->layout() == WeightLayout::Slab;
+        const bool slab = is_slab(a.table);
         const Operand table = slab ? r.slab(a.table, a.type, a.n_rows, a.cols, "table")
                                    : r.get(a.table, a.n_rows, rb, a.type == DType::F32 ? kF32 : 1, Access::Read, "table");
         const Operand ids = r.get(a.ids, 1, mul_u64(a.n_ids, 4, r.op(), "ids"), 4, Access::Read, "ids");
         const Operand out = r.f32(a.out, a.n_ids, a.cols, Access::Write, "out");
-        const Operand status = a.status.empty() ? Operand{} : r.get(a.status, 1, 4, 4, Access::Write, "status");
         r.no_overlap(out, table);
         r.no_overlap(out, ids);
-        r.no_overlap(out, status);
-        r.no_overlap(status, table);
-        r.no_overlap(status, ids);
+        if (a.n_ids == 0 || a.cols == 0) return;
         halo_mi_get_rows_params p{t, slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
                                   table.base, slab ? 0 : table.stride, a.n_rows, a.cols,
                                   reinterpret_cast<const std::int32_t*>(ids.base), a.n_ids,
-                                  reinterpret_cast<float*>(out.base), out.stride / kF32,
-                                  reinterpret_cast<std::uint32_t*>(status.base)};
+                                  reinterpret_cast<float*>(out.base), out.stride / kF32, st.get_rows_status(), 1u};
         check_abi(halo_mi_get_rows(&p, st.native()));
     }
 
@@ -430,7 +470,7 @@ public:
         const Resolver r(this, "MATMUL");
         const auto t = static_cast<std::uint32_t>(a.wtype);
         const std::uint64_t rb = row_bytes(a.wtype, a.cols, r.op());
-        const bool slab = !a.w.empty() && a.w.buffer->layout() == WeightLayout::Slab;
+        const bool slab = is_slab(a.w);
         std::uint32_t variant = a.kernel.variant_id;
         if (variant == 0) variant = slab ? kGemvSlabAuto : kGemvGgufRef;
         // rows must not depend on the batch unless the caller accepts the GEMM's numerics
@@ -446,15 +486,16 @@ public:
         const Operand nw = a.norm_w.empty() ? Operand{} : r.f32(a.norm_w, 1, a.cols, Access::Read, "norm_w");
         r.no_overlap(y, nw);
         if (a.n_vec == 0 || a.rows == 0) return;
-        if (variant == kGemmSlabBf16 || variant == kGemmSlabBf16M512 || (variant == kGemvSlabAuto && a.n_vec > 8))
+        const bool gemm = variant == kGemmSlabBf16 || variant == kGemmSlabBf16M512 || variant == kGemmSlabBf16SmallM ||
+                          (variant == kGemvSlabAuto && a.n_vec > 8);
+        if (gemm)
             CHECK(reinterpret_cast<std::uintptr_t>(x.base) % 16 == 0 && x.stride % 16 == 0, ErrorCode::Kernel,
                   "MATMUL: the MFMA GEMM needs 16-byte aligned x rows");
         halo_mi_gemv_params p{t,      slab ? (std::uint32_t)HALO_MI_LAYOUT_SLAB : (std::uint32_t)HALO_MI_LAYOUT_GGUF,
                               w.base, slab ? 0 : w.stride,
                               reinterpret_cast<const float*>(x.base), x.stride / kF32,
                               reinterpret_cast<float*>(y.base), y.stride / kF32,
-                              a.rows, a.cols, a.n_vec,
-                              variant == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512 : variant,
+                              a.rows, a.cols, a.n_vec, abi_gemv_variant(variant),
                               reinterpret_cast<const float*>(nw.base), a.norm_eps};
         check_abi(halo_mi_gemv(&p, st.native()));
     }
@@ -491,11 +532,13 @@ public:
         const Operand nw = a.norm_w.empty() ? Operand{} : r.f32(a.norm_w, 1, a.cols, Access::Read, "norm_w");
         r.no_overlap(out, nw);
         if (a.n_vec == 0 || a.rows == 0) return;
-        const std::uint32_t variant = a.kernel.variant_id == kGateUpGemv   ? HALO_MI_GEMV_SLAB
-                                      : a.kernel.variant_id == kGateUpGemm ? HALO_MI_GEMM_SLAB_BF16
-                                      : a.kernel.variant_id == kGateUpGemmM512 ? HALO_MI_GEMM_SLAB_BF16_M512
-                                      : a.allow_gemm                       ? HALO_MI_GEMV_SLAB_AUTO
-                                                                           : HALO_MI_GEMV_SLAB;
+        const std::uint32_t id = a.kernel.variant_id;
+        const std::uint32_t variant = id == kGateUpGemv         ? HALO_MI_GEMV_SLAB
+                                      : id == kGateUpGemm       ? HALO_MI_GEMM_SLAB_BF16
+                                      : id == kGateUpGemmM512   ? HALO_MI_GEMM_SLAB_BF16_M512
+                                      : id == kGateUpGemmSmallM ? HALO_MI_GEMM_SLAB_BF16_SMALL_M
+                                      : a.allow_gemm            ? HALO_MI_GEMV_SLAB_AUTO
+                                                                : HALO_MI_GEMV_SLAB;
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,
                                  reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
                                  out.stride / kF32, a.rows, a.cols, a.n_vec, variant,
@@ -512,6 +555,7 @@ public:
         HipStream& st = stream(s, "LM_HEAD");
         CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kLmHeadFused, ErrorCode::Config,
               "LM_HEAD: unknown kernel variant id %u", a.kernel.variant_id);
+        check_no_status(a.status, "LM_HEAD");
         const GemvArgs& g = a.gemv;
         CHECK(has_variant(OpId::Gemv, g.kernel.variant_id), ErrorCode::Config, "LM_HEAD: unknown gemv variant id %u",
               g.kernel.variant_id);
@@ -520,10 +564,9 @@ public:
         const Resolver r(this, "LM_HEAD");
         const auto t = static_cast<std::uint32_t>(g.wtype);
         const std::uint64_t rb = row_bytes(g.wtype, g.cols, r.op());
-        const bool slab = !g.w.empty() && g.w.buffer->layout() == WeightLayout::Slab;
-        std::uint32_t variant = g.kernel.variant_id == kGemmSlabBf16M512 ? (std::uint32_t)HALO_MI_GEMM_SLAB_BF16_M512
-                                                                          : g.kernel.variant_id;
-        if (variant == 0) variant = slab ? HALO_MI_GEMV_SLAB : HALO_MI_GEMV_GGUF_REF;
+        const bool slab = is_slab(g.w);
+        std::uint32_t variant = g.kernel.variant_id;
+        if (variant == 0) variant = slab ? kGemvSlab : kGemvGgufRef;
         CHECK(slab == (variant != kGemvGgufRef), ErrorCode::Config, "LM_HEAD: variant %u does not read the %s layout",
               variant, slab ? "SLAB" : "GGUF");
         const Operand w = slab ? r.slab(g.w, g.wtype, g.rows, g.cols, "w")
@@ -562,7 +605,7 @@ public:
                                      w.base, slab ? 0 : w.stride,
                                      reinterpret_cast<const float*>(x.base), x.stride / kF32,
                                      logits ? reinterpret_cast<float*>(y.base) : nullptr, logits ? y.stride / kF32 : 0,
-                                     g.rows, g.cols, g.n_vec, variant,
+                                     g.rows, g.cols, g.n_vec, abi_gemv_variant(variant),
                                      reinterpret_cast<const float*>(nw.base), g.norm_eps};
         p.result = res.base;
         p.valid_rows = a.valid_rows;
@@ -573,7 +616,61 @@ public:
         check_abi(halo_mi_lm_head(&p, st.native()));
     }
 
+    // ARGMAX (CpuBackend::argmax, src/backend/cpu_backend.cpp:772-783): the result words of each
+    // vector; a NaN logit poisons its vector's words (the reference HIP backend's device form of
+    // the CPU's Error(Kernel); decode_argmax reports it).
+    void argmax(Stream& s, const ArgmaxArgs& a) override {
+        HipStream& st = stream(s, "ARGMAX_FUSED");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kArgmax, ErrorCode::Config,
+              "ARGMAX_FUSED: unknown kernel variant id %u", a.kernel.variant_id);
+        check_no_status(a.status, "ARGMAX_FUSED");
+        const Resolver r(this, "ARGMAX_FUSED");
+        const Operand l = r.f32(a.logits, a.n_vec, a.n, Access::Read, "logits");
+        const Operand res = r.get(a.result, 1, mul_u64(a.n_vec, kArgmaxResultBytes, r.op(), "result"), 4, Access::Write, "result");
+        r.no_overlap(res, l);
+        if (a.n_vec == 0) return;
+        CHECK(a.n > 0, ErrorCode::Kernel, "ARGMAX_FUSED: empty row");
+        check_abi(halo_mi_argmax(reinterpret_cast<const float*>(l.base), l.stride / kF32, a.n, a.n_vec, res.base, st.native()));
+    }
+
+    // COPY (CpuBackend::copy): bytes from src to dst, in stream order; the ranges must not overlap.
+    void copy(Stream& s, const CopyArgs& a) override {
+        HipStream& st = stream(s, "COPY");
+        CHECK(a.kernel.variant_id == 0 || a.kernel.variant_id == kCopy, ErrorCode::Config, "COPY: unknown kernel variant id %u",
+              a.kernel.variant_id);
+        const Resolver r(this, "COPY");
+        const Operand src = r.get(a.src, 1, a.bytes, 1, Access::Read, "src");
+        const Operand dst = r.get(a.dst, 1, a.bytes, 1, Access::Write, "dst");
+        r.no_overlap(dst, src);
+        if (a.bytes == 0) return;
+        CHECK(hipMemcpyAsync(dst.base, src.base, a.bytes, hipMemcpyDeviceToDevice, (hipStream_t)st.native()) == hipSuccess,
+              ErrorCode::Device, "COPY: hipMemcpyAsync failed");
+    }
+
+    // The ops of the reference interface outside this path.
+    void add_rms_norm(Stream&, const AddRmsNormArgs&) override { unsupported(OpId::AddRmsNorm); }
+    void gdn_gates(Stream&, const GdnGateArgs&) override { unsupported(OpId::GdnGates); }
+    void conv1d_silu(Stream&, const Conv1dArgs&) override { unsupported(OpId::Conv1dSilu); }
+    void gated_delta_rule(Stream&, const GdnArgs&) override { unsupported(OpId::GatedDeltaRule); }
+    void gated_rms_norm(Stream&, const GatedNormArgs&) override { unsupported(OpId::GatedRmsNorm); }
+    void partial_rope(Stream&, const RopeArgs&) override { unsupported(OpId::PartialRope); }
+    void kv_write(Stream&, const KvWriteArgs&) override { unsupported(OpId::KvWrite); }
+    void attention(Stream&, const AttentionArgs&) override { unsupported(OpId::Attention); }
+    void mul_sigmoid(Stream&, const EltwiseArgs&) override { unsupported(OpId::MulSigmoid); }
+    void add(Stream&, const EltwiseArgs&) override { unsupported(OpId::Add); }
+    void top_k(Stream&, const TopKArgs&) override { unsupported(OpId::TopK); }
+
 private:
+    [[noreturn]] static void unsupported(OpId op) {
+        fail(ErrorCode::Unsupported, "%.*s is not implemented by the mi355x backend (quantized matmul path only)",
+             (int)op_name(op).size(), op_name(op).data());
+    }
+
+    static bool is_slab(const TensorRef& t) {
+        const auto* b = dynamic_cast<const DeviceBuffer*>(t.buffer);
+        return b != nullptr && b->layout() == WeightLayout::Slab;
+    }
+
     void check_alive(const char* op) const {
         CHECK(!lost_, ErrorCode::Device, "%s: the device behind this backend is lost", op);
         CHECK(!poisoned_, ErrorCode::Kernel, "%s: a previous kernel fault poisoned this backend", op);
@@ -589,9 +686,8 @@ private:
     static std::uint64_t row_bytes(DType t, std::uint32_t cols, const char* op) {
         const std::uint64_t rb = halo_mi_row_bytes(static_cast<std::uint32_t>(t), cols);
         if (rb == 0) {
-            const bool known = t == DType::F32 || t == DType::Q4_0 || t == DType::Q8_0 || t == DType::Q4_K ||
-                               t == DType::Q5_K || t == DType::Q6_K || t == DType::IQ4_XS;
-            CHECK(!known, ErrorCode::Kernel, "%s: %u elements is not a multiple of the %s block size", op, cols, type_name(t));
+            const std::uint64_t one = halo_mi_row_bytes(static_cast<std::uint32_t>(t), 256);
+            CHECK(one == 0, ErrorCode::Kernel, "%s: %u elements is not a multiple of the %s block size", op, cols, type_name(t));
             fail(ErrorCode::Unsupported, "%s: no kernel for weight type %u", op, static_cast<unsigned>(t));
         }
         return rb;
@@ -605,10 +701,25 @@ private:
 
 void HipStream::wait() {
     const hipError_t e = hipStreamSynchronize(s_);
-    if (e == hipSuccess) return;
-    const bool kernel_fault = e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorAssert;
-    owner_->poison(kernel_fault);
-    throw Error(kernel_fault ? ErrorCode::Kernel : ErrorCode::Device, std::string("stream wait: ") + hipGetErrorString(e));
+    if (e != hipSuccess) {
+        const bool kernel_fault = e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorAssert;
+        owner_->poison(kernel_fault);
+        throw Error(kernel_fault ? ErrorCode::Kernel : ErrorCode::Device, std::string("stream wait: ") + hipGetErrorString(e));
+    }
+    // a split-K reduction that gave up waiting: the device did not finish its work in the wait budget
+    if (halo_mi_stream_check(s_) != HALO_MI_OK) {
+        owner_->poison(false);
+        throw Error(ErrorCode::Device, std::string("stream wait: ") + halo_mi_last_error());
+    }
+    if (!status_used_) return;
+    status_used_ = false;
+    std::uint32_t word = 0;
+    if (hipMemcpy(&word, status_, 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        (word != 0 && hipMemsetAsync(status_, 0, 4, s_) != hipSuccess) || hipStreamSynchronize(s_) != hipSuccess) {
+        owner_->poison(false);
+        throw Error(ErrorCode::Device, "stream wait: cannot read the status word");
+    }
+    CHECK(!(word & kStatusBadIndex), ErrorCode::Kernel, "GET_ROWS: an id lies outside the table (status 0x%x)", word);
 }
 
 }  // namespace
@@ -632,10 +743,103 @@ std::string_view to_string(ErrorCode c) noexcept {
 Error::Error(ErrorCode code, const std::string& message)
     : std::runtime_error(std::string(to_string(code)) + ": " + message), code_(code) {}
 
-void Backend::unsupported(OpId op) const {
-    fail(ErrorCode::Unsupported, "op %u is not implemented by the mi355x backend", static_cast<unsigned>(op));
+std::string_view to_string(Kind k) noexcept {
+    switch (k) {
+        case Kind::Cpu: return "cpu";
+        case Kind::Hip: return "hip";
+        case Kind::HipEmulation: return "hip-emulation";
+        case Kind::Vulkan: return "vulkan";
+    }
+    return "unknown";
 }
 
-std::unique_ptr<Backend> make_mi355x_backend(int device) { return std::make_unique<MiBackend>(device); }
+// The op names of the reference's registry (src/backend/backend.cpp:22-46).
+std::string_view op_name(OpId op) noexcept {
+    switch (op) {
+        case OpId::GetRows: return "GET_ROWS";
+        case OpId::RmsNorm: return "RMS_NORM";
+        case OpId::AddRmsNorm: return "ADD_RMS_NORM";
+        case OpId::Gemv: return "MATMUL";
+        case OpId::GdnGates: return "GDN_GATE";
+        case OpId::Conv1dSilu: return "CONV1D_SHORT";
+        case OpId::GatedDeltaRule: return "GATED_DELTANET";
+        case OpId::GatedRmsNorm: return "GATED_NORM";
+        case OpId::PartialRope: return "PARTIAL_ROPE";
+        case OpId::KvWrite: return "KV_WRITE";
+        case OpId::Attention: return "ATTENTION";
+        case OpId::Swiglu: return "SWIGLU";
+        case OpId::MulSigmoid: return "MUL_SIGMOID";
+        case OpId::Add: return "ADD";
+        case OpId::LmHead: return "LM_HEAD";
+        case OpId::Argmax: return "ARGMAX_FUSED";
+        case OpId::TopK: return "TOP_K";
+        case OpId::Copy: return "COPY";
+        case OpId::GateUpSwiglu: return "GATE_UP_SWIGLU";
+    }
+    return "UNKNOWN";
+}
+
+TensorRef TensorRef::shifted(std::uint64_t delta) const {
+    CHECK(bytes == 0 || delta < bytes, ErrorCode::Kernel, "TensorRef::shifted: %llu bytes past a %llu-byte view",
+          (unsigned long long)delta, (unsigned long long)bytes);
+    CHECK(offset <= std::numeric_limits<std::uint64_t>::max() - delta, ErrorCode::Kernel, "TensorRef::shifted: offset overflow");
+    return {buffer, offset + delta, bytes == 0 ? 0 : bytes - delta, row_stride};
+}
+
+namespace {
+template <class A>
+const A& args_of(const OpInvocation& inv) {
+    const A* a = std::get_if<A>(&inv.args);
+    if (a == nullptr) {
+        const std::string_view n = op_name(inv.op);
+        fail(ErrorCode::Api, "run_op: %.*s called with the args of another op", (int)n.size(), n.data());
+    }
+    return *a;
+}
+}  // namespace
+
+// Backend::run_op (src/backend/backend.cpp:57-81 of the reference): the typed method of inv.op.
+void Backend::run_op(Stream& s, const OpInvocation& inv) {
+    switch (inv.op) {
+        case OpId::GetRows: return get_rows(s, args_of<GetRowsArgs>(inv));
+        case OpId::RmsNorm: return rms_norm(s, args_of<RmsNormArgs>(inv));
+        case OpId::AddRmsNorm: return add_rms_norm(s, args_of<AddRmsNormArgs>(inv));
+        case OpId::Gemv: return gemv(s, args_of<GemvArgs>(inv));
+        case OpId::GdnGates: return gdn_gates(s, args_of<GdnGateArgs>(inv));
+        case OpId::Conv1dSilu: return conv1d_silu(s, args_of<Conv1dArgs>(inv));
+        case OpId::GatedDeltaRule: return gated_delta_rule(s, args_of<GdnArgs>(inv));
+        case OpId::GatedRmsNorm: return gated_rms_norm(s, args_of<GatedNormArgs>(inv));
+        case OpId::PartialRope: return partial_rope(s, args_of<RopeArgs>(inv));
+        case OpId::KvWrite: return kv_write(s, args_of<KvWriteArgs>(inv));
+        case OpId::Attention: return attention(s, args_of<AttentionArgs>(inv));
+        case OpId::Swiglu: return swiglu(s, args_of<EltwiseArgs>(inv));
+        case OpId::MulSigmoid: return mul_sigmoid(s, args_of<EltwiseArgs>(inv));
+        case OpId::Add: return add(s, args_of<EltwiseArgs>(inv));
+        case OpId::LmHead: return lm_head(s, args_of<LmHeadArgs>(inv));
+        case OpId::Argmax: return argmax(s, args_of<ArgmaxArgs>(inv));
+        case OpId::TopK: return top_k(s, args_of<TopKArgs>(inv));
+        case OpId::Copy: return copy(s, args_of<CopyArgs>(inv));
+        case OpId::GateUpSwiglu: break;  // an addition with no args type in OpInvocation
+    }
+    fail(ErrorCode::Api, "run_op: unknown op id %u", static_cast<unsigned>(inv.op));
+}
+
+// decode_argmax (src/backend/backend.cpp:83-99 of the reference): a poisoned vector decodes as
+// {-1, NaN} and does not stop the others.
+std::vector<ArgmaxResult> decode_argmax(std::span<const std::byte> words) {
+    CHECK(words.size() % kArgmaxResultBytes == 0, ErrorCode::Kernel, "decode_argmax: %zu bytes is not a multiple of %u",
+          words.size(), kArgmaxResultBytes);
+    const std::size_t n = words.size() / kArgmaxResultBytes;
+    std::vector<ArgmaxResult> out(n);
+    for (std::size_t i = 0; i < n; ++i) {
+        std::array<std::uint32_t, 3> w{};
+        std::memcpy(w.data(), words.data() + i * kArgmaxResultBytes, sizeof(w));
+        out[i] = w[2] != 0 ? ArgmaxResult{-1, std::numeric_limits<float>::quiet_NaN()}
+                           : ArgmaxResult{static_cast<std::int32_t>(w[0]), std::bit_cast<float>(w[1])};
+    }
+    return out;
+}
+
+std::unique_ptr<MiBackend> make_mi355x_backend(int device) { return std::make_unique<Mi355xBackend>(device); }
 
 }  // namespace halo_mi::backend

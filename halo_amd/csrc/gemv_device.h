@@ -314,8 +314,10 @@ __device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t gr
 // End of a slab-GEMV workgroup: the waves' partial sums meet in LDS in wave order, then (split
 // K) the workgroups of a slab meet in the workspace, and the result (SiLU(gate) * up for the
 // pair) is written. acc0 holds this wave's sums in fp32, rows = lanes.
-// Split-K: the workgroup's start ticket for its slab (0 .. nch - 1), taken when it starts and
-// used only at its end, so the device-scope round trip overlaps the weight stream.
+// Split-K: the workgroup's start ticket for its slab, taken when it starts and used only at its
+// end, so the device-scope round trip overlaps the weight stream. A slab's counter holds the
+// arrivals of the running launch in its low kTicketBits bits and the slab's launch generation
+// above them (kept across launches: the reducer moves it on by one and clears the arrivals).
 __device__ __forceinline__ uint32_t gemv_ticket(const GemvSlabArgs& a, uint32_t slab, uint32_t nch) {
     uint32_t t = 0;
     if (nch > 1 && threadIdx.x == 0)
@@ -348,23 +350,14 @@ __device__ __forceinline__ float wave_sum(float s) {
     return (r0 + r1) + (r2 + r3);
 }
 
-// NORM (the fused norm): ss holds each lane's sum of squares of the raw x it loaded; ss_red +
-// w * ss_stride is NV floats of LDS for wave w (its dead A table).
-template <int NV, bool PAIR, bool NORM>
+template <int NV, bool PAIR>
 __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
                                             uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
-                                            uint32_t ticket, const float (&ss)[NV], float* ss_red, uint32_t ss_stride) {
-    constexpr bool norm = NORM;
-    float sst[NV];  // the workgroup's sum of squares, then the slab's (chunk order)
-#pragma unroll
-    for (int v = 0; v < NV; ++v) sst[v] = norm ? wave_sum(ss[v]) : 0.0f;
+                                            uint32_t ticket) {
     // waves -> wave 0, in wave order
     if (nw > 1) {
 #pragma unroll
         for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
-        if (norm && lane == 0)
-#pragma unroll
-            for (int v = 0; v < NV; ++v) ss_red[wave * ss_stride + v] = sst[v];
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
@@ -373,13 +366,6 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
             for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
             acc0[v] = s;
         }
-        if (norm)
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                float s = ss_red[v];
-                for (uint32_t w = 1; w < nw; ++w) s += ss_red[w * ss_stride + v];
-                sst[v] = s;
-            }
     }
     const uint32_t row = slab * kSlabRows + lane;
     float acc1[NV];  // the up sums (PAIR)
@@ -389,59 +375,51 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
         // Split-K meeting point, without cache maintenance and without a round trip at the end
         // of most workgroups. The workgroup with the slab's last start ticket is the reducer:
         // every other chunk of the slab started before it, so they are all running. The others
-        // store their partials as 64-bit words (fp32 bits, 1 = ready: one atomic access
-        // carries the value and its mark) and finish. The reducer loads those words, re-reads
-        // (bounded, with a pause) any not yet ready, adds the chunks in chunk order
-        // (deterministic), and clears the words and the ticket counter for the next launch.
+        // store their partials as 64-bit words (fp32 bits and this launch's tag: one atomic
+        // access carries the value and its mark) and finish. The reducer loads those words,
+        // re-reads (bounded, with a pause) any not yet ready, adds the chunks in chunk order
+        // (deterministic), and clears the words and the arrivals for the next launch.
         // workspace words of this slab: its index among all slabs of the launch (a grouped launch
         // covers several matrices)
         const uint32_t gs = a.slab0 + slab;
         uint64_t* P = a.slots + (uint64_t)gs * nch * NV * 64;
-        // the norm's sums of squares: one word per (chunk, vector) after all slabs' partials
-        const uint64_t wgs = a.wg_total ? a.wg_total : gridDim.x;
-        uint64_t* PS = a.slots + wgs * NV * 64 + (uint64_t)gs * nch * NV;
-        if (__builtin_amdgcn_readfirstlane(ticket) != nch - 1) {
+        // A word is ready when its high half holds this launch's tag (the slab's generation,
+        // never 0): a word left over from an earlier launch (one that arrived after its reducer
+        // gave up waiting) is never taken for this launch's.
+        const uint32_t tk = __builtin_amdgcn_readfirstlane(ticket);
+        const uint32_t gen = tk >> kTicketBits;
+        const uint64_t tag = (uint64_t)((gen & kTagMask) | (kTagMask + 1)) << 32;
+        if ((tk & kArrivalMask) != nch - 1) {
 #pragma unroll
             for (int v = 0; v < NV; ++v)
-                __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane,
-                                   (uint64_t)__float_as_uint(acc0[v]) | (1ull << 32), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            if (norm && lane == 0)
-#pragma unroll
-                for (int v = 0; v < NV; ++v)
-                    __hip_atomic_store(PS + (uint64_t)c * NV + v, (uint64_t)__float_as_uint(sst[v]) | (1ull << 32),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane, (uint64_t)__float_as_uint(acc0[v]) | tag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
-        float own[NV], own_ss[NV];
+        float own[NV];
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             own[v] = acc0[v];
             acc0[v] = 0.0f;
-            own_ss[v] = sst[v];
-            sst[v] = 0.0f;
         }
         // The loads of 8 chunks are issued before any is used (one memory round trip per 8
-        // chunks); past the last chunk the address is clamped and the value dropped. With the
-        // norm, the chunks' sums of squares ride in the same round trip; only the gate chunks'
-        // count (the up chunks of a pair load the same x), in chunk order.
+        // chunks); past the last chunk the address is clamped and the value dropped.
         constexpr uint32_t KB = 8;
-        constexpr uint32_t kSpinLimit = 1u << 20;  // the other chunks are running: a few microseconds
+        // The other chunks are running, so a word is a few microseconds away at most. A wait
+        // that gives up marks the stream's status word (the host reports it as a device error
+        // at its next check) and leaves NaN in the output.
+        constexpr uint32_t kSpinLimit = 1u << 20;
+        const uint32_t spin_limit = a.spin_limit ? a.spin_limit : kSpinLimit;
+        const uint64_t want = tag ^ a.tag_flip;  // tag_flip: the host's forced-timeout test only
         auto ready = [&](uint64_t w, const uint64_t* addr) {
-            for (uint32_t spin = 0; (w >> 32) == 0 && spin < kSpinLimit; ++spin) {
+            for (uint32_t spin = 0; (w & ~0xFFFFFFFFull) != want && spin < spin_limit; ++spin) {
                 __builtin_amdgcn_s_sleep(2);
                 w = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            return (w >> 32) ? __uint_as_float((uint32_t)w) : __builtin_nanf("");
+            if ((w & ~0xFFFFFFFFull) == want) return __uint_as_float((uint32_t)w);
+            if (a.status) __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return __builtin_nanf("");
         };
-        // the ss words of a window of 64 / NV chunks, one word per lane (lane = (k % win) NV + v)
-        constexpr uint32_t win = 64 / NV;
-        uint64_t qsl = 0;
-        auto load_window = [&](uint32_t k0) {
-            if (lane < min(nch - k0, win) * NV)
-                qsl = __hip_atomic_load(PS + (uint64_t)k0 * NV + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        };
-        if (norm) load_window(0);
         for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
             uint64_t q[KB][NV];
 #pragma unroll
@@ -461,16 +439,6 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                     if (k < a.ks) acc0[v] += val;
                     else acc1[v] += val;
                 }
-                if (norm && k < a.ks) {
-                    if (k % win == 0 && k > 0) load_window(k);
-#pragma unroll
-                    for (int v = 0; v < NV; ++v) {
-                        const uint32_t idx = (k % win) * NV + v;
-                        const uint64_t w = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)qsl, idx) |
-                                           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(qsl >> 32), idx) << 32);
-                        sst[v] += k == c ? own_ss[v] : ready(w, PS + (uint64_t)k * NV + v);
-                    }
-                }
             }
         }
         for (uint32_t k = 0; k < nch; ++k)
@@ -479,21 +447,9 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                 for (int v = 0; v < NV; ++v)
                     __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-                if (norm && lane == 0)
-#pragma unroll
-                    for (int v = 0; v < NV; ++v)
-                        __hip_atomic_store(PS + (uint64_t)k * NV + v, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-        if (lane == 0) __hip_atomic_store(&a.counters[gs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (norm) {
-        // rms_norm's scale, applied once to the row sums (the workgroups multiplied x by norm_w)
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const float inv = 1.0f / sqrtf(sst[v] / (float)a.cols + a.norm_eps);
-            acc0[v] *= inv;
-            acc1[v] *= inv;
-        }
+        if (lane == 0)
+            __hip_atomic_store(&a.counters[gs], (gen + 1) << kTicketBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if constexpr (!PAIR) {
         // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
@@ -574,10 +530,7 @@ __global__ __launch_bounds__(1024, 4) void k_gemv_slab(GemvSlabArgs a) {
             compute_group<T, NV>(nxt, grp, grp - w0, S, xc, a.x_stride, xsv, inv_unit, acc0);
         }
     }
-    float ss[NV];  // the VALU kernel has no fused norm (its launcher never passes norm_w)
-#pragma unroll
-    for (int v = 0; v < NV; ++v) ss[v] = 0.0f;
-    gemv_finish<NV, PAIR, false>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, nullptr, 0);
+    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -683,12 +636,13 @@ __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], co
 // Q6_K, whose low-half sum is then in lane 8 s).
 // The k-step r of a slot (k-steps 0..3: slot elements 0..15, 4..7: 16..31) covers elements
 // 4 r .. 4 r + 3 in the order (0, 2, 1, 3), the order the masks below produce them.
-// With the fused norm (norm), the group's x is x * norm_w, and ss accumulates the squares of
-// the raw x.
-template <uint32_t T, int NV>
-__device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float (&wr)[4], bool norm, float (&ss)[NV],
+// With the fused norm (NORM), the group's x is (x * inv) * norm_w, rounded as cpu::rms_norm
+// rounds it (backends/cpu/ops_basic.cpp:29 of the reference): exactly the normalized x.
+template <uint32_t T, int NV, bool NORM>
+__device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float (&wr)[4], const float (&inv)[NV],
                                          uint8_t* tab, uint32_t lane, s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV],
                                          float (&xs)[NV]) {
+#pragma clang fp contract(off)
     constexpr int M = mx_blocks<NV>();
     constexpr int kHiShift = (T == kQ4_K || T == kQ4_0) ? 4 : 0;  // high nibbles arrive as 16 q
     const uint32_t s = lane >> 3, r = lane & 7;
@@ -696,15 +650,14 @@ __device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float
 #pragma unroll
     for (int v = 0; v < NV; ++v)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[v][i] = xraw[v][i];
-    if (norm)
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                ss[v] = fmaf(xraw[v][i], xraw[v][i], ss[v]);
-                xr[v][i] = xraw[v][i] * wr[i];
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (NORM) {
+                const float t = xraw[v][i] * inv[v];
+                xr[v][i] = t * wr[i];
+            } else {
+                xr[v][i] = xraw[v][i];
             }
+        }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         uint32_t mb = 0;
@@ -874,6 +827,69 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
     }
 }
 
+// The fused norm's prologue: 1 / rms of each vector's raw x row, bitwise cpu::rms_norm's
+// (backends/cpu/ops_basic.cpp:26-27 of the reference: mean = dot(x, x) / cols, inv =
+// 1 / sqrt(mean + eps), the sum of squares in cpu::detail::dot's order), for the whole
+// workgroup. Wave 0 stages the rows through LDS (stage: kNormPiece floats per vector) in
+// pieces, lanes 8 v + j run the dot's interleaved sequential sums j = 0..7 of vector v, and the
+// combine ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)) follows (cols is a multiple of 32: no tail).
+// The result goes through inv_lds (NV floats that nothing else writes) to every wave. Every
+// wave of the workgroup must call it (it ends with a barrier). The normalized x the kernels then
+// build is exactly rms_norm's output, so the fused GEMV is bitwise rms_norm then the GEMV.
+constexpr uint32_t kNormPiece = 512;
+
+template <int NV>
+__device__ __forceinline__ void gemv_norm_inv(const GemvSlabArgs& a, float* stage, float* inv_lds, uint32_t wave,
+                                              uint32_t lane, float (&inv)[NV]) {
+#pragma clang fp contract(off)
+    if (wave == 0) {
+        const uint32_t v_l = lane >> 3, j = lane & 7;
+        float p = 0.0f;
+        for (uint32_t c0 = 0; c0 < a.cols; c0 += kNormPiece) {
+            const uint32_t n = min(kNormPiece, a.cols - c0);
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+                if ((uint32_t)v < a.n_vec)
+                    for (uint32_t i = lane; i < n; i += 64) stage[v * kNormPiece + i] = a.x[(uint64_t)v * a.x_stride + c0 + i];
+            __builtin_amdgcn_wave_barrier();
+            if (v_l < min((uint32_t)NV, a.n_vec)) {
+                const float* sv = stage + v_l * kNormPiece;
+#pragma unroll 8
+                for (uint32_t i = j; i < n; i += 8) {
+                    const float t = sv[i];
+                    const float q = t * t;
+                    p = p + q;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // lanes 8 v .. 8 v + 7 hold p0..p7 of vector v
+        const float q = p + __shfl_down(p, 4, 8);  // j < 4: p_j + p_{j+4}
+        const float r = q + __shfl_down(q, 1, 8);  // j = 0: left pair, j = 2: right pair
+        const float t = r + __shfl_down(r, 2, 8);  // j = 0: the sum
+        if (j == 0 && v_l < (uint32_t)NV) {
+            const float mean = t / (float)a.cols;
+            inv_lds[v_l] = 1.0f / sqrtf(mean + a.norm_eps);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < NV; ++v) inv[v] = inv_lds[v];
+}
+
+// Dynamic LDS floats of a k_gemv_mx workgroup of nw waves: the waves' partials and A tables, and
+// with the fused norm the prologue's stage (which they overlay) and its NV results after them.
+template <int NV>
+constexpr uint32_t mx_wave_floats() { return NV * 64 + mx_table_bytes<NV>() / 4; }
+template <int NV>
+__host__ __device__ constexpr uint32_t mx_norm_inv_offset(uint32_t nw) {
+    return nw * mx_wave_floats<NV>() > NV * kNormPiece ? nw * mx_wave_floats<NV>() : NV * kNormPiece;
+}
+template <int NV>
+__host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw, bool norm) {
+    return norm ? (size_t)(mx_norm_inv_offset<NV>(nw) + NV) * 4 : (size_t)nw * mx_wave_floats<NV>() * 4;
+}
+
 // Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
 // the Q8_0, Q6_K and Q5_K loops (two register groups); the others run at most 8 waves.
 template <uint32_t T, int NV, bool ONE>
@@ -887,7 +903,6 @@ constexpr uint32_t mx_max_threads() {
 // grouped launch, k_gemv_mx_group).
 template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM>
 __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid) {
-    static_assert(ONE || !NORM, "the fused norm runs on the one-group kernel");
     extern __shared__ float smem[];
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     constexpr int M = mx_blocks<NV>();
@@ -906,48 +921,64 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     float* red = smem;
     uint8_t* tab = reinterpret_cast<uint8_t*>(smem + nw * NV * 64) + wave * mx_table_bytes<NV>();
 
-    float acc0[NV], ss[NV];
+    float acc0[NV], inv[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc0[v] = ss[v] = 0.0f;
-    constexpr bool norm = NORM;
-    float* ss_red = reinterpret_cast<float*>(smem + nw * NV * 64);  // wave w's A table, once it is dead
-    constexpr uint32_t ss_stride = mx_table_bytes<NV>() / 4;
+    for (int v = 0; v < NV; ++v) acc0[v] = inv[v] = 0.0f;
     float xr[NV][4], wr[4];
     uint32_t ticket = 0;
+    // Loads are waited for in issue order (vmcnt), so x comes first (the A table is built while
+    // the weights are on their way). With the fused norm, wave 0 runs the norm's prologue before
+    // it issues its own loads (its staging loads would otherwise wait behind its weights); the
+    // other waves issue theirs first and meet it at the prologue's barrier.
+    const bool early = !NORM || wave != 0;
     if constexpr (ONE) {
-        if (w0 < w1) {
-            SlotGroup<T> G;
+        SlotGroup<T> G;
+        if (early && w0 < w1) {
             mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
             load_group<T>(G, slab0, geo, lane, w0, S);
-            ticket = gemv_ticket(a, slab, nch);
+        }
+        ticket = gemv_ticket(a, slab, nch);
+        if constexpr (NORM) {
+            gemv_norm_inv<NV>(a, smem, smem + mx_norm_inv_offset<NV>(nw), wave, lane, inv);
+            if (!early && w0 < w1) {
+                mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
+                load_group<T>(G, slab0, geo, lane, w0, S);
+            }
+        }
+        if (w0 < w1) {
             s16x4 A[4 * M];
             int es[NV];
             float xs[NV];
-            mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
+            mx_build<T, NV, NORM>(xr, wr, inv, tab, lane, A, es, xs);
             mx_group<T, NV>(G, A, xs, min(8u, S - w0 * 8), acc0);
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
-        } else {
-            ticket = gemv_ticket(a, slab, nch);
         }
-        gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
+        gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
         return;
     }
     SlotGroup<T> cur, nxt;
-    if (w0 < w1) {  // x first: the A table is built while the weights are on their way
-        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, w0, S, lane);
+    if (early && w0 < w1) {
+        mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
         load_group<T>(cur, slab0, geo, lane, w0, S);
     }
     ticket = gemv_ticket(a, slab, nch);
+    if constexpr (NORM) {
+        gemv_norm_inv<NV>(a, smem, smem + mx_norm_inv_offset<NV>(nw), wave, lane, inv);
+        if (!early && w0 < w1) {
+            mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
+            load_group<T>(cur, slab0, geo, lane, w0, S);
+        }
+    }
     // One group: build its A table from xr, prefetch x and the weights of the next group (past
     // the last group: the last one again, an L2 hit, so the loop stays branch-free), multiply.
     auto step = [&](const SlotGroup<T>& G, SlotGroup<T>& next, uint32_t grp) {
         s16x4 A[4 * M];
         int es[NV];
         float xs[NV];
-        mx_build<T, NV>(xr, wr, norm, ss, tab, lane, A, es, xs);
+        mx_build<T, NV, NORM>(xr, wr, inv, tab, lane, A, es, xs);
         const uint32_t gn = min(grp + 1, w1 - 1);
-        mx_load_x<NV, false>(xr, wr, a.x, a.x_stride, nullptr, gn, S, lane);
+        mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, gn, S, lane);
         load_group<T>(next, slab0, geo, lane, gn, S);
         float accg[NV];
 #pragma unroll
@@ -962,7 +993,7 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
         ++grp;
         step(nxt, cur, grp);
     }
-    gemv_finish<NV, PAIR, NORM>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket, ss, ss_red, ss_stride);
+    gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
 template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>

@@ -1049,11 +1049,7 @@ int launch_gemm_sm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
     const uint32_t S = a.cols / kSlot, cus = cu_count();
     if ((uint64_t)kSmRows * a.cols > kXbElems || (uint64_t)kSmRows * a.cols * 2 > 0xFFFFFFFFull)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
-    static const uint32_t kc_env = [] {  // tuning knob: K chunks per unit
-        const char* e = std::getenv("HALO_MI_GEMM_SM_KC");
-        return e ? (uint32_t)std::max(1, std::atoi(e)) : 0u;
-    }();
-    uint32_t kc = std::clamp<uint32_t>(kc_env ? kc_env : (4 * cus + units - 1) / units, 1u, S / 8);
+    uint32_t kc = std::clamp<uint32_t>((4 * cus + units - 1) / units, 1u, S / 8);
     while (kc > 1 && (uint64_t)units * kc * kSmRows * kPcW > kPartialFloats) --kc;
     if ((uint64_t)units * kc * kSmRows * kPcW > kPartialFloats)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: %u rows exceed the small-M partials workspace", a.rows);
@@ -1090,12 +1086,13 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
                                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus))
         return launch_gemm_lm<PAIR>(type, a, ws, units, st);
     // the small-M kernel: about 1.5x k_gemm_pc's rate at M = 8 (no per-stage barrier chain)
-    static const bool sm_off = [] {  // HALO_MI_GEMM_SM=0: k_gemm_pc instead (for comparison)
-        const char* e = std::getenv("HALO_MI_GEMM_SM");
-        return e && *e == '0';
-    }();
     const uint64_t sm_floats = (uint64_t)units * kSmRows * kPcW;  // partials at one K chunk
-    if (!sm_off && a.tiles == kGemmTilesAuto && a.n_vec <= kSmRows && S % 8 == 0 && sm_floats <= kPartialFloats)
+    const bool sm_fits = a.n_vec <= kSmRows && S % 8 == 0 && sm_floats <= kPartialFloats;
+    if (a.tiles == kGemmTilesSm && !sm_fits)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm: the small-M kernel takes at most %u x rows, cols a multiple of "
+                                                "256 and at most %llu rows", kSmRows,
+                         (unsigned long long)(kPartialFloats / (kSmRows * kPcW) * (PAIR ? 64 : 128)));
+    if ((a.tiles == kGemmTilesAuto || a.tiles == kGemmTilesSm) && sm_fits)
         return launch_gemm_sm<PAIR>(type, a, ws, units, st);
     const uint32_t BM = 64u * MB;
     const uint64_t cap_rows = std::min(kXbElems / a.cols, kInvFloats) / BM * BM;

@@ -9,7 +9,6 @@
 
 #include <algorithm>
 #include <cstdint>
-#include <cstdlib>
 
 #include "gemv_device.h"
 
@@ -19,34 +18,45 @@ namespace {
 using namespace dev;
 
 // Work split of a slab-GEMV launch: ks K chunks per slab (more than one only when the slabs
-// alone cannot fill the chip; the chunks then meet in the workspace), nw waves per workgroup
-// (about two slot groups per wave, so each wave streams with one group in flight).
+// alone cannot fill the chip; the chunks then meet in the workspace), nw waves per workgroup.
+//
+// Every quantity here is chosen as for the widest launch (kMaxGemvVec vectors), never from the
+// launch's own vector count: the K chunks and the waves of a chunk fix the order in which a
+// row's sum is added up, so a row of an n_vec > 1 call is bitwise the row of its n_vec == 1
+// call (GemvArgs::allow_gemm off, include/halo/backend/backend.h:298-302 of the reference).
 struct GemvSplit {
     uint32_t ks, nw;
+    bool one;  // one slot group per wave (k_gemv_mx's ONE form)
 };
 
-// words: workspace words per (slab, chunk) and vector (64 partials, plus one with the norm).
-GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, bool have_ws, uint32_t words) {
+template <uint32_t T>
+GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
+    constexpr uint32_t NVW = kMaxGemvVec;
     // One slot group per wave for mid-size matrices, two for large ones (measured on MI355X,
     // 17408 x 5120 and 151936 x 5120 Q4_K).
-    static const uint32_t target_env = [] {
-        const char* e = std::getenv("HALO_MI_GEMV_WGS");  // tuning knob: min workgroups per launch
-        return e ? (uint32_t)std::max(1, std::atoi(e)) : 0u;
-    }();
-    static const int gpw_env = [] {
-        const char* e = std::getenv("HALO_MI_GEMV_GPW");  // tuning knob: slot groups per wave
-        return e ? std::max(1, std::atoi(e)) : 0;
-    }();
-    const uint32_t groups_per_wave = gpw_env ? (uint32_t)gpw_env : (slabs >= 1024 ? 2u : 1u);
+    const uint32_t groups_per_wave = slabs >= 1024 ? 2u : 1u;
     const uint32_t ngrp = (S + 7) / 8;
-    uint32_t ks = 1;
     const uint32_t units = std::max(slabs, 1u) * mats;
+    auto fits = [&](uint32_t k) {
+        return k * mats <= kMaxChunks && (uint64_t)slabs * k * mats * NVW * 64 <= kSlots;
+    };
+    uint32_t ks = 1;
     // Measured on MI355X: about 4 workgroups per slab up to 1088 per launch; small matrices
     // gain more from a short split-K fix-up than from more workgroups (floor of 128).
-    const uint32_t target_wg = target_env ? target_env : std::clamp(4 * units, 128u, 1088u);
+    const uint32_t target_wg = std::clamp(4 * units, 128u, 1088u);
     if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
-    while (ks > 1 && (uint64_t)slabs * ks * mats * nv * words > kSlots) --ks;
-    const uint32_t gwg = (ngrp + ks - 1) / ks;
+    while (ks > 1 && !fits(ks)) --ks;
+    // The one-group form (below 1024 slabs): enough K chunks that a chunk's groups fit one
+    // workgroup (LDS: the waves' partials and A tables).
+    const size_t per_wave = NVW * 64 * sizeof(float) + mx_table_bytes<NVW>();
+    uint32_t nw1 = mx_max_threads<T, NVW, true>() / 64;
+    while (nw1 > 1 && nw1 * per_wave > 65536) --nw1;
+    if (have_ws && slabs < 1024) {
+        const uint32_t k1 = std::min(std::max(ks, (ngrp + nw1 - 1) / nw1), ngrp);
+        if (fits(k1)) ks = k1;
+    }
+    const uint32_t gwg = (ngrp + ks - 1) / ks;  // groups of the largest chunk
+    if (gwg <= nw1 && (ks == 1 || have_ws)) return {ks, gwg, true};
     uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
     // a wave holds the x sums of at most 4 groups (one per lane)
     while (ks < ngrp && (gwg + nw - 1) / nw > 4) {
@@ -55,62 +65,46 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t nv, uint32_t mats, boo
         const uint32_t g2 = (ngrp + ks - 1) / ks;
         if ((g2 + nw - 1) / nw <= 4) break;
     }
-    return {ks, nw};
+    nw = std::min(nw, mx_max_threads<T, NVW, false>() / 64);
+    while (nw > 1 && nw * per_wave > 65536) --nw;
+    return {ks, nw, false};
 }
 
 template <uint32_t T, int NV, bool PAIR>
 int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_t st) {
     const uint32_t S = a.cols / kSlot;
     constexpr uint32_t MATS = PAIR ? 2 : 1;
-    const uint32_t words = a.norm_w ? 65u : 64u;
-    const GemvSplit sp = pick_split(slabs, S, NV, MATS, ws != nullptr && slabs <= kCounters, words);
+    const bool have_ws = ws != nullptr && slabs <= kCounters;
+    // the fused norm takes the plain launch's split: its result is bitwise rms_norm then this GEMV
+    const GemvSplit sp = pick_split<T>(slabs, S, MATS, have_ws);
     a.ks = sp.ks;
     a.slots = ws ? ws->slots : nullptr;
     a.counters = ws ? ws->counters : nullptr;
-    static const bool valu = [] {
-        const char* e = std::getenv("HALO_MI_GEMV_VALU");
-        return e && *e == '1';
-    }();
-    if constexpr (T != kQ5_K && T != kIQ4_XS) {  // the VALU kernel covers the first four formats
-        if (valu && !a.norm_w) {
-            if (a.ks * MATS > 1 && (uint64_t)slabs * a.ks * MATS * NV * 64 > kSlots)
-                return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
-            const size_t lds = (size_t)sp.nw * NV * 64 * sizeof(float);
-            hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw), lds, st, a);
+    a.status = ws ? ws->status : nullptr;
+    apply_test_hooks(a);
+    // the chunks of a slab (or the pair's two matrices) meet in the workspace words
+    if (a.ks * MATS > 1 && (!have_ws || (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64 > kSlots))
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
+    const bool norm = a.norm_w != nullptr;
+    const size_t lds = mx_lds_bytes<NV>(sp.nw, norm);
+    if (a.valu) {  // the VALU kernel (variant HALO_MI_GEMV_SLAB_VALU): first four formats, no norm
+        if constexpr (T != kQ5_K && T != kIQ4_XS) {
+            if (a.norm_w) return set_error(HALO_MI_E_UNSUPPORTED, "gemv: the VALU slab kernel has no fused norm");
+            hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw),
+                               (size_t)sp.nw * NV * 64 * sizeof(float), st, a);
             return hip_status(hipGetLastError(), "gemv_slab launch");
+        } else {
+            return set_error(HALO_MI_E_UNSUPPORTED, "gemv: the VALU slab kernel covers Q4_0, Q8_0, Q4_K and Q6_K only");
         }
     }
-    // MFMA kernel. Below 1024 slabs it runs one slot group per wave: enough K chunks that a
-    // chunk's groups fit one workgroup (at most 16 waves, 64 KB of LDS with the waves' A tables).
-    const size_t per_wave = NV * 64 * sizeof(float) + mx_table_bytes<NV>();
-    const uint32_t ngrp = (S + 7) / 8;
-    uint32_t nw1 = mx_max_threads<T, NV, true>() / 64;
-    while (nw1 > 1 && nw1 * per_wave > 65536) --nw1;
-    // The fused norm runs on the one-group kernel only (its registers stay out of the streaming
-    // loop), whatever the number of slabs.
-    if (ws && (slabs < 1024 || a.norm_w) && slabs <= kCounters) {
-        uint32_t ks = std::max(a.ks, (ngrp + nw1 - 1) / nw1);
-        ks = std::min(ks, ngrp);
-        if ((uint64_t)slabs * ks * MATS * NV * words <= kSlots) a.ks = ks;
+    const dim3 grid(slabs * a.ks * MATS), block(64 * sp.nw);
+    if (sp.one) {
+        if (norm) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true, true>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), grid, block, lds, st, a);
+    } else {
+        if (norm) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false, true>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), grid, block, lds, st, a);
     }
-    const uint32_t gwg = (ngrp + a.ks - 1) / a.ks;  // groups of the largest chunk
-    // the chunks of a slab (or the pair's two matrices) meet in the workspace words
-    if (a.ks * MATS > 1 && (uint64_t)slabs * a.ks * MATS * NV * words > kSlots)
-        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
-    if (gwg <= nw1 && (a.ks == 1 || ws)) {
-        if (a.norm_w)
-            hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave,
-                               st, a);
-        else
-            hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), dim3(slabs * a.ks * MATS), dim3(64 * gwg), gwg * per_wave, st, a);
-        return hip_status(hipGetLastError(), "gemv_slab launch");
-    }
-    if (a.norm_w)
-        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: the fused norm over %u rows x %u cols needs more split-K "
-                                                "workspace than this stream has (or a workspace at all)", a.rows, a.cols);
-    uint32_t nw = std::min(sp.nw, mx_max_threads<T, NV, false>() / 64);
-    while (nw > 1 && nw * per_wave > 65536) --nw;
-    hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), dim3(slabs * a.ks * MATS), dim3(64 * nw), nw * per_wave, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
 }
 

@@ -67,7 +67,9 @@ int type_index(uint32_t t) {
 }
 
 // The one-group waves a workgroup of the pair's kernel may hold (at most 16 waves and 64 KB of
-// LDS, as for a single matrix).
+// LDS, as for a single matrix). Taken for the widest launch (kMaxGemvVec vectors) whatever the
+// launch's own: the waves of a chunk fix the order of a row's sum, so rows stay bitwise
+// independent of n_vec.
 template <int NV>
 uint32_t group_waves(uint32_t ta, uint32_t tb) {
     auto max_threads = [](uint32_t t) -> uint32_t {
@@ -88,18 +90,17 @@ template <int NV>
 int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, const float* x, uint64_t x_stride,
                     uint32_t cols, const float* norm_w, float eps, Workspace* ws, hipStream_t st) {
     const uint32_t S = cols / kSlot, ngrp = (S + 7) / 8;
-    const uint32_t words = norm_w ? 65u : 64u;
     uint64_t slabs = 0;
     for (uint32_t i = 0; i < n; ++i) slabs += (segs[i].rows + kSlabRows - 1) / kSlabRows;
     if (slabs == 0) return HALO_MI_OK;
     if (slabs > kCounters) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: %llu slabs exceed the workspace", (unsigned long long)slabs);
     // K split: a chip's worth of workgroups (as a single matrix of all the slabs would take), and
     // at least enough chunks that a chunk's slot groups fit one workgroup of one-group waves
-    const uint32_t nw1 = group_waves<NV>(ta, tb);
+    const uint32_t nw1 = group_waves<kMaxGemvVec>(ta, tb);
     const uint32_t target = std::clamp<uint32_t>(4 * (uint32_t)slabs, 128u, 1088u);
     uint32_t ks = std::min<uint32_t>((target + (uint32_t)slabs - 1) / (uint32_t)slabs, ngrp);
     ks = std::min(std::max(ks, (ngrp + nw1 - 1) / nw1), ngrp);
-    if (ks > 1 && slabs * ks * NV * words > kSlots)
+    if (ks > 1 && (ks > kMaxChunks || slabs * ks * kMaxGemvVec * 64 > kSlots))
         return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: %llu slabs exceed the split-K workspace", (unsigned long long)slabs);
     const uint32_t gwg = (ngrp + ks - 1) / ks;
     if (gwg > nw1) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: cols %u too large for one workgroup per chunk", cols);
@@ -116,6 +117,8 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         a.norm_w = norm_w;
         a.norm_eps = eps;
         a.slab0 = slab0;
+        a.status = ws->status;
+        apply_test_hooks(a);
         g.seg[i] = a;
         g.type[i] = segs[i].type;
         slab0 += sl;
@@ -123,7 +126,7 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         g.wg_end[i] = wg;
     }
     for (uint32_t i = 0; i < n; ++i) g.seg[i].wg_total = wg;
-    const size_t lds = gwg * (NV * 64 * sizeof(float) + mx_table_bytes<NV>());
+    const size_t lds = mx_lds_bytes<NV>(gwg, norm_w != nullptr);
     const bool ok = norm_w ? launch_types<NV, true>(ta, tb, g, dim3(wg), dim3(64 * gwg), lds, st)
                            : launch_types<NV, false>(ta, tb, g, dim3(wg), dim3(64 * gwg), lds, st);
     if (!ok) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: no kernel for types %u and %u", ta, tb);

@@ -53,10 +53,31 @@ struct GemvSlabArgs {
     // the launch's slabs, and the launch's workgroups (0: a launch of its own).
     uint32_t slab0 = 0;
     uint32_t wg_total = 0;
+    // The stream's status word: a split-K wait that gives up sets kStatusSplitKTimeout.
+    uint32_t* status = nullptr;
+    // Test hooks, set only by halo_mi_test_splitk_timeout: the reducer's wait bound (0 = the
+    // default) and a mask that makes it wait for a tag no chunk writes (a forced timeout).
+    uint32_t spin_limit = 0;
+    uint64_t tag_flip = 0;
+    // The VALU slab kernel (k_gemv_slab) instead of the MFMA one (variant HALO_MI_GEMV_SLAB_VALU).
+    bool valu = false;
 };
 
+// Sets a's test hooks from halo_mi_test_splitk_timeout's process-wide setting (no-op otherwise).
+void apply_test_hooks(GemvSlabArgs& a);
+
+// Split-K tickets and words. A slab's counter holds the arrivals of the running launch in its low
+// kTicketBits bits and the slab's launch generation above them; a partial's word carries the
+// generation (kTagMask bits of it, plus a bit that makes the tag non-zero) in its high half.
+constexpr uint32_t kTicketBits = 12;
+constexpr uint32_t kArrivalMask = (1u << kTicketBits) - 1;
+constexpr uint32_t kMaxChunks = kArrivalMask;  // K chunks x matrices of one slab
+constexpr uint32_t kTagMask = 0x7FFFFu;
+// Status word bits (the stream's, read and cleared by halo_mi_stream_check).
+constexpr uint32_t kStatusSplitKTimeout = 0x100u;
+
 // M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
-constexpr uint32_t kGemmTilesAuto = 0, kGemmTilesPc = 1, kGemmTilesLm = 2;
+constexpr uint32_t kGemmTilesAuto = 0, kGemmTilesPc = 1, kGemmTilesLm = 2, kGemmTilesSm = 3;
 
 struct GemmArgs {
     const uint8_t* w0;
@@ -86,6 +107,7 @@ constexpr uint64_t kNormFloats = 4ull << 20;      // normalized x rows (referenc
 constexpr uint64_t kInvFloats = 1ull << 20;       // per-row 1 / rms of x (GEMM staging): 4 MiB
 
 struct Workspace {
+    uint32_t* status = nullptr;  // one word: kStatus* bits set by the kernels since the last check
     float* partials = nullptr;
     uint64_t* slots = nullptr;
     uint32_t* counters = nullptr;

@@ -69,7 +69,9 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
 /* ---- gemv variants (append-only ids; 0 = default for the layout) ------------------------ */
 /*
  * Counterpart of the reference's KernelChoice registry (backend.h:173-176, ids pinned by
- * tests/unit/backend/test_hip_backend.cpp:925-981).
+ * tests/unit/backend/test_hip_backend.cpp:925-981). These are this library's own ids; the
+ * reference registry ids they take behind its HIP backend are listed with the C++ backend
+ * (include/halo_mi355x_backend.hpp).
  *   0 HALO_MI_GEMV_DEFAULT   GGUF layout -> gemv_gguf_ref; SLAB layout -> gemv_slab_auto.
  *   1 HALO_MI_GEMV_GGUF_REF  GGUF layout, 8 lanes per output in cpu::detail::dot's order:
  *                            bit-identical to the CPU backend.
@@ -86,6 +88,12 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *                            GPU, else 3.
  *   5 HALO_MI_GEMM_SLAB_BF16_M512  the bf16 MFMA GEMM on 512-row M tiles (every wave both
  *                            dequantizes and multiplies; same numerics as 3); any n_vec.
+ *   6 HALO_MI_GEMV_SLAB_VALU the SLAB GEMV with its multiply-adds on the VALU instead of the
+ *                            matrix core (Q4_0, Q8_0, Q4_K, Q6_K; no fused norm); the same
+ *                            split and bound as 2.
+ *   7 HALO_MI_GEMM_SLAB_BF16_SMALL_M  the bf16 MFMA GEMM's small-M kernel (no LDS stage; waves
+ *                            dequantize their own MFMA operands): n_vec <= 32, cols a multiple
+ *                            of 256; same numerics as 3.
  */
 enum {
     HALO_MI_GEMV_DEFAULT = 0,
@@ -93,7 +101,10 @@ enum {
     HALO_MI_GEMV_SLAB = 2,
     HALO_MI_GEMM_SLAB_BF16 = 3,
     HALO_MI_GEMV_SLAB_AUTO = 4,
-    HALO_MI_GEMM_SLAB_BF16_M512 = 5
+    HALO_MI_GEMM_SLAB_BF16_M512 = 5,
+    HALO_MI_GEMV_SLAB_VALU = 6,
+    HALO_MI_GEMM_SLAB_BF16_SMALL_M = 7,
+    HALO_MI_GEMV_VARIANT_LAST = 7
 };
 
 /*
@@ -111,11 +122,10 @@ enum {
  *        - GGUF reference variant: x is normalized first exactly as cpu::rms_norm, so y is
  *          bitwise rms_norm then matmul;
  *        - bf16 GEMM variants: the same normalized x, rounded to bf16 while it is staged;
- *        - SLAB GEMV: fused into the kernel, no extra launch: each workgroup multiplies its x
- *          slots by norm_w and sums the squares of the raw x it loads, the sums meet in the
- *          split-K fix-up, and the row sums are scaled by 1 / sqrt(sum / cols + eps) once. The
- *          result differs from rms_norm then gemv only by rounding (the order of the sum of
- *          squares, and x * norm_w scaled after the dot instead of before).
+ *        - SLAB GEMV (2, 4, 6 and the GEMV legs of the auto variants): fused into the kernel,
+ *          no extra launch: each workgroup computes 1 / sqrt(dot(x, x) / cols + eps) in
+ *          cpu::detail::dot's order and builds (x * inv) * norm_w, exactly rms_norm's output, so
+ *          y is bitwise halo_mi_rms_norm then the same variant without the norm, at any n_vec.
  *      norm_w must not overlap y.
  */
 typedef struct halo_mi_gemv_params {
@@ -240,6 +250,15 @@ typedef struct halo_mi_lm_head_params {
 int halo_mi_lm_head(const halo_mi_lm_head_params* p, void* stream);
 
 /*
+ * ARGMAX (ArgmaxArgs, backend.h:463-468; CpuBackend::argmax, src/backend/cpu_backend.cpp:772-783):
+ * for each of n_vec rows of n fp32 logits (logits_stride floats apart, 0 = n) the result words
+ * {index, value bits, poisoned} of halo_mi_lm_head: the highest value, ties to the lowest index;
+ * a NaN poisons its row's words (the CPU backend's Error(Kernel) for it). n >= 1. result may not
+ * overlap logits.
+ */
+int halo_mi_argmax(const float* logits, uint64_t logits_stride, uint32_t n, uint32_t n_vec, void* result, void* stream);
+
+/*
  * SWIGLU: out[r][c] = silu(gate[r][c]) * up[r][c] for rows x cols fp32 (strides in floats,
  * 0 = cols). The reference's op (backends/cpu/ops_basic.cpp:165-167, EltwiseArgs at
  * include/halo/backend/backend.h:420-427). out may not overlap gate or up.
@@ -265,10 +284,13 @@ int halo_mi_dequant_rows(uint32_t type, uint32_t layout, const void* w, uint64_t
  *          row_bytes; SLAB: table_stride 0). ids: n_ids int32 on the device.
  *   out: n_ids rows of cols fp32, out_stride floats apart (0 = cols); must not overlap table,
  *        ids or status.
- *   status (optional, one uint32 on the device): cleared, then an id outside [0, n_rows) leaves
- *        its output row unwritten and sets HALO_MI_STATUS_BAD_INDEX (the reference's
- *        kStatusBadIndex, backends/hip/kernels/hd.h:156). Ids live on the device, so this is
- *        where the CPU backend's Error(Kernel) shows: read the word after the stream is done.
+ *   status (optional, one uint32 on the device): an id outside [0, n_rows) leaves its output
+ *        row unwritten and sets HALO_MI_STATUS_BAD_INDEX (the reference's kStatusBadIndex,
+ *        backends/hip/kernels/hd.h:156) in it. Ids live on the device, so this is where the CPU
+ *        backend's Error(Kernel) shows: read the word after the stream is done.
+ *   status_keep: 0 = the call clears the word first (it reports this call only); otherwise the
+ *        bits accumulate over calls until the caller clears the word (a stream's report up to
+ *        its next wait).
  */
 #define HALO_MI_STATUS_BAD_INDEX 8u
 
@@ -284,6 +306,7 @@ typedef struct halo_mi_get_rows_params {
     float* out;
     uint64_t out_stride;
     uint32_t* status;
+    uint32_t status_keep;
 } halo_mi_get_rows_params;
 
 int halo_mi_get_rows(const halo_mi_get_rows_params* p, void* stream);
@@ -297,6 +320,35 @@ int halo_mi_get_rows(const halo_mi_get_rows_params* p, void* stream);
  */
 int halo_mi_rms_norm(const float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride,
                      uint32_t rows, uint32_t cols, float eps, void* stream);
+
+/* ---- stream state --------------------------------------------------------------------------- */
+/*
+ * The kernels' own failures cannot be returned by the call that enqueued them. A split-K
+ * reduction of the SLAB GEMV waits for the partial sums of the slab's other workgroups for a
+ * bounded time; if it gives up, the output holds NaN and the stream's status word gets
+ * HALO_MI_STATUS_SPLITK_TIMEOUT. halo_mi_stream_check() synchronizes `stream`, reads and clears
+ * the word and returns HALO_MI_E_DEVICE when it was set (the reference's device-loss path,
+ * Stream::wait() -> Error(Device), backend.h:495-506); the workspace is then reset.
+ */
+#define HALO_MI_STATUS_SPLITK_TIMEOUT 0x100u
+int halo_mi_stream_check(void* stream);
+
+/*
+ * Every (device, stream) pair that runs a gemv-family call gets a workspace of device memory
+ * (split-K words, GEMM partials and staging, argmax parts: about 116 MiB), allocated on the
+ * first call. halo_mi_stream_release() synchronizes `stream` and frees its workspace on the
+ * current device; call it before destroying the stream. A later call on the stream allocates
+ * a new one.
+ */
+int halo_mi_stream_release(void* stream);
+
+/*
+ * Test hook, no counterpart in the reference: with force != 0 every split-K reduction of the
+ * SLAB GEMV waits for a tag no partial carries, for spin_limit rounds (0 = the default bound),
+ * then gives up as above; force = 0 restores normal operation. The kernels still exit
+ * normally. Process-wide; for the failure-path tests only.
+ */
+int halo_mi_test_splitk_timeout(uint32_t spin_limit, int force);
 
 /* ---- geometry ------------------------------------------------------------------------------ */
 /* Bytes of one GGUF row of `cols` elements (src/tensor/quant.cpp:411-418); 0 on error. */

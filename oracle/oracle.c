@@ -533,3 +533,20 @@ int oracle_lm_head(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t 
     free(buf), free(bi), free(bv), free(poisoned);
     return err;
 }
+
+void oracle_argmax_words(const float* logits, uint32_t n, uint32_t n_vec, uint32_t* result) {
+    for (uint32_t i = 0; i < n_vec; ++i) {
+        const float* row = logits + (size_t)i * n;
+        uint32_t best = 0, nan = 0;
+        for (uint32_t c = 0; c < n; ++c) {
+            if (isnan(row[c])) nan = 1;
+            else if (!isnan(row[best]) ? row[c] > row[best] : 1) best = c;
+        }
+        float v = nan ? nanf("") : row[best];
+        uint32_t vb;
+        memcpy(&vb, &v, 4);
+        result[3 * i] = nan ? 0xFFFFFFFFu : best;
+        result[3 * i + 1] = vb;
+        result[3 * i + 2] = nan;
+    }
+}

@@ -106,6 +106,14 @@ int oracle_gate_up_swiglu(uint32_t type, const uint8_t* wg, const uint8_t* wu, u
 int oracle_lm_head(uint32_t type, const uint8_t* w, uint64_t w_stride, uint32_t rows, uint32_t cols, const float* x,
                    uint32_t n_vec, uint32_t valid_rows, float* logits, uint32_t* result, uint32_t threads);
 
+/*
+ * cpu::argmax per row (backends/cpu/matmul.cpp:61-72: the first maximum, a row replacing the best
+ * only when strictly greater) as result words {index, value bits, poisoned}; a NaN in the row
+ * (the CPU's Error(Kernel)) gives the poisoned words {0xFFFFFFFF, quiet NaN, 1}, as LM_HEAD's
+ * (src/backend/cpu_backend.cpp:745-747, :825-833). logits: n_vec rows of n floats, dense.
+ */
+void oracle_argmax_words(const float* logits, uint32_t n, uint32_t n_vec, uint32_t* result);
+
 /* include/halo/backends/cpu/thread_pool.h:58-64: part i of [0, n) split into `parts`. */
 void oracle_partition_range(size_t n, size_t parts, size_t i, size_t* begin, size_t* end);
 

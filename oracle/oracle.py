@@ -43,6 +43,7 @@ def lib() -> ctypes.CDLL:
         "oracle_rms_norm": (None, [VP, U64, VP, VP, U64, U32, U32, ctypes.c_float]),
         "oracle_gate_up_swiglu": (INT, [U32, VP, VP, U64, U32, U32, VP, U32, VP, U32]),
         "oracle_lm_head": (INT, [U32, VP, U64, U32, U32, VP, U32, U32, VP, VP, U32]),
+        "oracle_argmax_words": (None, [VP, U32, U32, VP]),
         "oracle_partition_range": (None, [ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                           ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
         "oracle_default_threads": (U32, []),
@@ -145,6 +146,15 @@ def lm_head(t: int, w, rows: int, cols: int, x, *, valid_rows: int = 0, w_stride
     _chk(lib().oracle_lm_head(int(t), w.ctypes.data, int(w_stride), int(rows), int(cols), x.ctypes.data, n,
                               int(valid_rows), logits.ctypes.data, res.ctypes.data, int(th)), "lm_head")
     return res, logits
+
+
+def argmax_words(logits) -> np.ndarray:
+    """Result words [n_vec, 3] of cpu::argmax per row (poisoned words for a row with a NaN)."""
+    lg = _f32(logits)
+    lg = lg.reshape(-1, lg.shape[-1]) if lg.ndim > 1 else lg.reshape(1, -1)
+    res = np.empty((lg.shape[0], 3), dtype=np.uint32)
+    lib().oracle_argmax_words(lg.ctypes.data, lg.shape[1], lg.shape[0], res.ctypes.data)
+    return res
 
 
 def swiglu(g, u) -> np.ndarray:

@@ -110,7 +110,7 @@ std::vector<double> gemm_bound(uint32_t type, const std::vector<uint8_t>& w, uin
 
 double silu(double v) { return v / (1.0 + std::exp(-v)); }
 
-void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
+void run_type(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
     const std::string tn = type_name(type);
     const uint32_t rows = 130, cols = 1024, n_vec = 3;  // two full slabs and a ragged one
     const std::vector<uint8_t> wg = make_weights(type, rows, cols, 11 + type);
@@ -121,7 +121,8 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
     auto w_gguf = be.import_host_readonly(bytes_of(wg));
     auto w_slab = be.import_weights(bytes_of(wg), static_cast<hb::DType>(type), rows, cols);
     auto u_slab = be.import_weights(bytes_of(wu), static_cast<hb::DType>(type), rows, cols);
-    check(w_gguf->layout() == hb::WeightLayout::Gguf && w_slab->layout() == hb::WeightLayout::Slab,
+    check(dynamic_cast<const hb::MiBuffer&>(*w_gguf).layout() == hb::WeightLayout::Gguf &&
+              dynamic_cast<const hb::MiBuffer&>(*w_slab).layout() == hb::WeightLayout::Slab,
           tn + ": buffer layouts");
     auto xb = be.allocate(x.size() * 4, hb::Tier::Vram);
     auto yb = be.allocate((size_t)n_vec * rows * 4, hb::Tier::Vram);
@@ -221,7 +222,7 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
     // fused gate/up (GEMV pair and bf16 GEMM variants) against the oracle's composition
     const std::vector<double> tu = slab_bound(type, wu, rows, cols, x, n_vec);
     const std::vector<double> gg = gemm_bound(type, wg, rows, cols, x, n_vec), gu = gemm_bound(type, wu, rows, cols, x, n_vec);
-    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512}) {
+    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512, hb::kGateUpGemmSmallM}) {
         hb::GateUpArgs g;
         g.wtype = static_cast<hb::DType>(type);
         g.w_gate = hb::TensorRef::of(*w_slab);
@@ -251,9 +252,9 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
         check(ok2, tn + ": gate_up_swiglu variant " + std::to_string(variant) + " within the bound");
     }
 
-    // RMS_NORM and the fused norm: rms_norm bitwise; the reference-order gemv with norm_w is
-    // bitwise rms_norm then cpu::matmul; the SLAB default within the GEMV bound on the CPU's
-    // normalized x plus the norm's own rounding (half the two sums-of-squares orders' error)
+    // RMS_NORM and the fused norm: rms_norm bitwise; every gemv with norm_w is bitwise rms_norm
+    // then the same gemv (Limits::max_fused_norm_cols), so the reference-order one is bitwise
+    // rms_norm then cpu::matmul
     {
         std::vector<float> nw(cols), xn(x.size());
         for (uint32_t i = 0; i < cols; ++i) nw[i] = 0.5f + (float)(i % 7) * 0.125f;
@@ -279,23 +280,33 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
         be.gemv(st, an);
         download_y(*yb, y);
         check(std::memcmp(y.data(), nref.data(), y.size() * 4) == 0, tn + ": GGUF gemv with norm_w is bitwise rms_norm + matmul");
+        check(be.limits().max_fused_norm_cols >= cols, tn + ": max_fused_norm_cols covers the test's cols");
+        hb::GemvArgs plain = a;  // the SLAB default on the normalized x
+        plain.w = hb::TensorRef::of(*w_slab);
+        plain.x = hb::TensorRef::of(*xnb);
+        auto y2b = be.allocate((size_t)n_vec * rows * 4, hb::Tier::Vram);
+        plain.y = hb::TensorRef::of(*y2b);
+        be.gemv(st, plain);
+        std::vector<float> y2(y.size());
+        download_y(*y2b, y2);
         an.w = hb::TensorRef::of(*w_slab);
-        be.gemv(st, an);
-        download_y(*yb, y);
-        std::vector<double> ntol = slab_bound(type, wg, rows, cols, xn, n_vec);
-        const double extra = (0.5 * (cols / 8.0 + cols / 256.0 + 30) + 11) / ((cols / 8 + 4) + (cols / 32 + 64) + 4);
-        bool okn = true;
-        for (size_t i = 0; i < y.size(); ++i) okn &= std::fabs((double)y[i] - nref[i]) <= ntol[i] * (1.0 + extra) * 1.01;
-        check(okn, tn + ": SLAB gemv with norm_w within the bound");
+        for (uint32_t nv : {n_vec, 1u}) {  // R > 1 verify rows and the R == 1 decode row
+            an.n_vec = nv;
+            be.gemv(st, an);
+            download_y(*yb, y);
+            check(std::memcmp(y.data(), y2.data(), (size_t)nv * rows * 4) == 0,
+                  tn + ": SLAB gemv with norm_w (n_vec " + std::to_string(nv) + ") is bitwise rms_norm then the SLAB gemv");
+        }
+        an.n_vec = n_vec;
         an.norm_w = hb::TensorRef::of(*yb);  // norm_w overlapping y
         check(code_of([&] { be.gemv(st, an); }) == (int)hb::ErrorCode::Kernel, tn + ": norm_w overlapping y -> Kernel");
     }
 
-    // GET_ROWS with device ids and the status word
+    // GET_ROWS with device ids: an id outside the table fails the stream's next wait() with
+    // Error(Kernel), leaves its row unwritten, and the rows of the good ids are bitwise
     {
         const std::vector<int32_t> idv = {7, 0, 129, -3, 7};
         auto idb = be.allocate(idv.size() * 4, hb::Tier::Vram);
-        auto sb = be.allocate(4, hb::Tier::Vram);
         auto ob = be.allocate(idv.size() * cols * 4, hb::Tier::Vram);
         be.upload(st, hb::TensorRef::of(*idb), bytes_of(idv));
         std::vector<float> sentinel(idv.size() * cols, 999.0f), got(idv.size() * cols);
@@ -308,13 +319,12 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
         gr.n_rows = rows;
         gr.cols = cols;
         gr.n_ids = (uint32_t)idv.size();
-        gr.status = hb::TensorRef::of(*sb);
         be.get_rows(st, gr);
-        uint32_t word = 0;
-        be.download(st, hb::TensorRef::of(*sb), std::as_writable_bytes(std::span<uint32_t>(&word, 1)));
-        download_y(*ob, got);
+        be.download(st, hb::TensorRef::of(*ob), std::as_writable_bytes(std::span<float>(got)));
+        check(code_of([&] { st.wait(); }) == (int)hb::ErrorCode::Kernel, tn + ": get_rows with a bad id -> Kernel at wait()");
+        check(code_of([&] { st.wait(); }) == -1, tn + ": the next wait() is clean");
         std::vector<float> want(cols);
-        bool okg = word == hb::kStatusBadIndex;
+        bool okg = true;
         for (size_t i = 0; i < idv.size(); ++i) {
             if (idv[i] < 0 || idv[i] >= (int32_t)rows) {
                 for (uint32_t c = 0; c < cols; ++c) okg &= got[i * cols + c] == 999.0f;
@@ -323,7 +333,9 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
             oracle_dequantize_row(type, wg.data() + (size_t)idv[i] * halo_mi_row_bytes(type, cols), want.data(), cols);
             okg &= std::memcmp(got.data() + i * cols, want.data(), cols * 4) == 0;
         }
-        check(okg, tn + ": get_rows bitwise, a bad id unwritten and reported in the status word");
+        check(okg, tn + ": get_rows bitwise, a bad id's row unwritten");
+        gr.status.word = 0;
+        check(code_of([&] { be.get_rows(st, gr); }) == (int)hb::ErrorCode::Unsupported, tn + ": a StatusRef -> Unsupported");
     }
 
     // error mapping (backend.h:24-26)
@@ -339,6 +351,71 @@ void run_type(hb::Backend& be, hb::Stream& st, uint32_t type) {
     bad = a;
     bad.kernel.variant_id = hb::kGemvGgufRef;  // a GGUF-only kernel on a SLAB buffer
     check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Config, tn + ": layout/variant mismatch -> Config");
+}
+
+// The reference interface outside the path: every op virtual exists, the ones this backend does
+// not run throw Error(Unsupported); run_op dispatches by OpId and rejects mismatched args with
+// Error(Api); ARGMAX and COPY run; decode_argmax reads poisoned vectors as {-1, NaN}.
+void run_interface(hb::MiBackend& be, hb::Stream& st) {
+    hb::Backend& b = be;
+    const int U = (int)hb::ErrorCode::Unsupported;
+    check(code_of([&] { b.add_rms_norm(st, hb::AddRmsNormArgs{}); }) == U, "add_rms_norm -> Unsupported");
+    check(code_of([&] { b.gdn_gates(st, hb::GdnGateArgs{}); }) == U, "gdn_gates -> Unsupported");
+    check(code_of([&] { b.conv1d_silu(st, hb::Conv1dArgs{}); }) == U, "conv1d_silu -> Unsupported");
+    check(code_of([&] { b.gated_delta_rule(st, hb::GdnArgs{}); }) == U, "gated_delta_rule -> Unsupported");
+    check(code_of([&] { b.gated_rms_norm(st, hb::GatedNormArgs{}); }) == U, "gated_rms_norm -> Unsupported");
+    check(code_of([&] { b.partial_rope(st, hb::RopeArgs{}); }) == U, "partial_rope -> Unsupported");
+    check(code_of([&] { b.kv_write(st, hb::KvWriteArgs{}); }) == U, "kv_write -> Unsupported");
+    check(code_of([&] { b.attention(st, hb::AttentionArgs{}); }) == U, "attention -> Unsupported");
+    check(code_of([&] { b.mul_sigmoid(st, hb::EltwiseArgs{}); }) == U, "mul_sigmoid -> Unsupported");
+    check(code_of([&] { b.add(st, hb::EltwiseArgs{}); }) == U, "add -> Unsupported");
+    check(code_of([&] { b.top_k(st, hb::TopKArgs{}); }) == U, "top_k -> Unsupported");
+    hb::OpInvocation inv;
+    inv.op = hb::OpId::TopK;
+    inv.args = hb::TopKArgs{};
+    check(code_of([&] { b.run_op(st, inv); }) == U, "run_op(TOP_K) reaches top_k");
+    inv.op = hb::OpId::Gemv;  // the args of another op
+    check(code_of([&] { b.run_op(st, inv); }) == (int)hb::ErrorCode::Api, "run_op with mismatched args -> Api");
+    check(b.limits().max_fused_norm_cols > 0 && b.limits().lm_head_ids, "limits");
+    check(b.variants(hb::OpId::Attention).empty(), "no variants for an op this backend does not run");
+
+    // ARGMAX and COPY through run_op
+    const uint32_t n = 300, nv = 3;
+    std::vector<float> logits((size_t)n * nv);
+    halo_mi_fill_normal(77, logits.data(), logits.size(), 0.0f, 1.0f);
+    logits[5] = logits[250] = 9.0f;                 // vector 0: a tie, the lower index wins
+    logits[n + 17] = std::nanf("");                // vector 1: poisoned
+    auto lb = be.allocate(logits.size() * 4, hb::Tier::Vram), lc = be.allocate(logits.size() * 4, hb::Tier::Vram);
+    auto rb = be.allocate(nv * hb::kArgmaxResultBytes, hb::Tier::Vram);
+    be.upload(st, hb::TensorRef::of(*lb), bytes_of(logits));
+    hb::CopyArgs c;
+    c.src = hb::TensorRef::of(*lb);
+    c.dst = hb::TensorRef::of(*lc);
+    c.bytes = logits.size() * 4;
+    inv.op = hb::OpId::Copy;
+    inv.args = c;
+    b.run_op(st, inv);
+    hb::ArgmaxArgs am;
+    am.logits = hb::TensorRef::of(*lc);
+    am.result = hb::TensorRef::of(*rb);
+    am.n = n;
+    am.n_vec = nv;
+    inv.op = hb::OpId::Argmax;
+    inv.args = am;
+    b.run_op(st, inv);
+    std::vector<std::byte> words(nv * hb::kArgmaxResultBytes);
+    b.download(st, hb::TensorRef::of(*rb), words);
+    st.submit();
+    st.wait();
+    std::vector<uint32_t> cpu((size_t)nv * 3);
+    oracle_argmax_words(logits.data(), n, nv, cpu.data());
+    check(std::memcmp(cpu.data(), words.data(), words.size()) == 0, "argmax words equal the oracle's");
+    const std::vector<hb::ArgmaxResult> dec = hb::decode_argmax(words);
+    check(dec.size() == nv && dec[0].index == 5 && dec[1].index == -1 && std::isnan(dec[1].value), "decode_argmax");
+    c.dst = hb::TensorRef::of(*lb);  // overlapping ranges
+    c.src = hb::TensorRef{lb.get(), 4, 0, 0};
+    c.bytes = 64;
+    check(code_of([&] { b.copy(st, c); }) == (int)hb::ErrorCode::Kernel, "copy with overlapping ranges -> Kernel");
 }
 
 }  // namespace
@@ -358,17 +435,18 @@ int main(int argc, char** argv) {
         // the registry's id -> name map is pinned: ids are append-only and never reused
         // (as the reference pins its own, tests/unit/backend/test_hip_backend.cpp:925-981)
         const std::pair<hb::OpId, std::vector<std::pair<uint32_t, std::string>>> pinned[] = {
-            {hb::OpId::GetRows, {{hb::kDequantRows, "dequant_rows_exact"}}},
-            {hb::OpId::RmsNorm, {{hb::kRmsNorm, "rms_norm_cpu_order"}}},
+            {hb::OpId::GetRows, {{37, "dequant_rows_exact"}}},
+            {hb::OpId::RmsNorm, {{38, "rms_norm_cpu_order"}}},
             {hb::OpId::Gemv,
-             {{hb::kGemvGgufRef, "gemv_gguf_ref_b256"}, {hb::kGemvSlab, "gemv_slab_w64"},
-              {hb::kGemmSlabBf16, "gemm_slab_bf16_mfma"}, {hb::kGemvSlabAuto, "gemv_slab_auto"},
-              {hb::kGemmSlabBf16M512, "gemm_slab_bf16_mfma_m512"}}},
-            {hb::OpId::Swiglu, {{hb::kSwiglu, "swiglu_b256"}}},
+             {{30, "gemv_gguf_ref_b256"}, {31, "gemv_slab_w64"}, {32, "gemm_slab_bf16_mfma"}, {33, "gemv_slab_auto"},
+              {34, "gemm_slab_bf16_mfma_m512"}, {35, "gemv_slab_valu_w64"}, {36, "gemm_slab_bf16_mfma_small_m"}}},
+            {hb::OpId::Swiglu, {{39, "swiglu_b256"}}},
+            {hb::OpId::LmHead, {{40, "lm_head_argmax_parts"}}},
+            {hb::OpId::Argmax, {{41, "argmax_parts_b256"}}},
+            {hb::OpId::Copy, {{42, "copy_async"}}},
             {hb::OpId::GateUpSwiglu,
-             {{hb::kGateUpGemv, "gate_up_gemv_w64"}, {hb::kGateUpGemm, "gate_up_gemm_bf16_mfma"},
-              {hb::kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512"}}},
-            {hb::OpId::LmHead, {{hb::kLmHeadFused, "lm_head_slab_argmax"}}},
+             {{43, "gate_up_gemv_w64"}, {44, "gate_up_gemm_bf16_mfma"}, {45, "gate_up_gemm_bf16_mfma_m512"},
+              {46, "gate_up_gemm_bf16_mfma_small_m"}}},
         };
         for (const auto& [op, want] : pinned) {
             const auto got = be->variants(op);
@@ -378,6 +456,7 @@ int main(int argc, char** argv) {
             check(same, "variant registry of op " + std::to_string((int)op) + " is the pinned id -> name map");
         }
         auto st = be->create_stream();
+        run_interface(*be, *st);
         std::vector<std::byte> host(64);
         check(code_of([&] { (void)be->import_host(std::span<std::byte>(host)); }) == (int)hb::ErrorCode::Unsupported,
               "import_host on a device -> Unsupported");

@@ -112,19 +112,6 @@ def slab_gemv_tol(oracle, t, wbytes, rows, cols, x):
     return (depth_cpu(cols) + depth_slab_gemv(cols) + 4) * U * mag * (1 + 1e-3) + 1e-30
 
 
-def norm_gemv_tol(oracle, t, wbytes, rows, cols, xn):
-    """The SLAB GEMV with the fused norm against rms_norm then matmul on the CPU (xn: the CPU's
-    normalized x). The kernel sums the squares of x in another order (per lane over its 4
-    elements, a 64-lane butterfly, at most 16 waves and cols/256 chunks: against the dot's
-    cols/8 + 4), which moves inv by half the two orders' relative errors; it multiplies x by
-    norm_w once and scales the row sums by inv once (3 roundings against the CPU's 2), and
-    mean, + eps, sqrt and 1/ round on both sides. So on top of the GEMV's own bound (taken on
-    xn), (0.5 (cols/8 + cols/256 + 30) + 11) u times the magnitude."""
-    mag = gemv_mag(oracle, t, wbytes, rows, cols, xn)
-    rel = depth_cpu(cols) + depth_slab_gemv(cols) + 4 + 0.5 * (cols / 8 + cols / 256 + 30) + 11
-    return rel * U * mag * (1 + 1e-2) + 1e-30
-
-
 def bf16_round(a: np.ndarray) -> np.ndarray:
     """Round fp32 to bf16 (nearest even), returned as fp32."""
     u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)

@@ -5,9 +5,9 @@ status word of backends/hip/src/ops.cpp:982-1012) and of the grouped GEMV over m
 share x, against the oracle, through the C ABI.
 
 Acceptance: RMS_NORM, GET_ROWS and the reference-order GEMV with the norm are bitwise the CPU's;
-the GEMM variants stage exactly the CPU's normalized x, so the GEMM bounds apply to it
-unchanged; the fused SLAB GEMV is within the GEMV bound plus the norm's own rounding
-(helpers.norm_gemv_tol).
+every variant with the fused norm is bitwise RMS_NORM then the same variant without it (the
+reference's Limits::max_fused_norm_cols contract, backend.h:236-242: an R == 1 decode must stay
+bitwise the unfused R > 1 verify forward), so the unfused bounds apply to the CPU's normalized x.
 """
 from __future__ import annotations
 
@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from helpers import (F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, gemm_emulated, gemm_tol,
-                     isclose_bits, make_weights, max_ratio, norm_gemv_tol, row_bytes, slab_gemv_tol, swiglu_tol)
+                     isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, strided_xy, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -91,6 +91,10 @@ def test_get_rows_bitwise_and_bad_ids(hl, oracle, dev, t, layout):
     idd = to_dev(ids, dev)
     status = torch.full((1,), 0x55, dtype=torch.int32, device=dev)  # cleared by the call
     out = torch.full((ids.size, cols + 2), SENTINEL, dtype=torch.float32, device=dev)
+    keep = torch.full((1,), 0x40, dtype=torch.int32, device=dev)  # status_keep: bits accumulate
+    hl.get_rows(t, lay, table, rows, cols, idd, ids.size, out, table_stride=ts, out_stride=cols + 2, status=keep,
+                status_keep=True)
+    assert int(host(keep)[0]) == 0x40 | hl.STATUS_BAD_INDEX
     hl.get_rows(t, lay, table, rows, cols, idd, ids.size, out, table_stride=ts, out_stride=cols + 2, status=status)
     o = host(out)
     for i, r in enumerate(ids):
@@ -155,9 +159,18 @@ NORM_CASES = [(130, 1024, 1), (130, 1024, 4), (576, 5120, 1), (576, 5120, 3), (6
               (65600, 512, 1), (65600, 512, 4)]  # the last two: more than 1024 slabs
 
 
+def unfused_gemv(hl, dev, t, w, xn, rows, cols, variant):
+    """The same variant without the norm, on RMS_NORM's output computed on the GPU."""
+    import torch
+
+    yd = torch.full((xn.shape[0], rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gemv(t, w, to_dev(xn, dev), yd, rows, cols, xn.shape[0], variant=variant)
+    return host(yd)
+
+
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("case", NORM_CASES)
-def test_gemv_norm_slab_within_bound(hl, oracle, dev, t, case):
+def test_gemv_norm_slab_bitwise(hl, oracle, dev, t, case):
     rows, cols, n_vec = case
     if rows > 10000 and t not in (Q4_K, Q6_K):
         pytest.skip("the many-slab shapes run for Q4_K and Q6_K")
@@ -166,10 +179,13 @@ def test_gemv_norm_slab_within_bound(hl, oracle, dev, t, case):
     dense = dense_of(buf, t, rows, cols, stride, 0)
     x, w = norm_inputs(cols, n_vec, 961 + cols + n_vec)
     xn = oracle.rms_norm(x, w, EPS)
-    ref = oracle.matmul(t, dense, rows, cols, xn)
     slab = slab_of(hl, dev, t, dense, rows, cols)
-    y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, hl.Variant.SLAB_GEMV, x_pad=1, y_pad=2)
-    tol = norm_gemv_tol(oracle, t, dense, rows, cols, xn)
+    for variant in (hl.Variant.SLAB_GEMV, hl.Variant.SLAB_AUTO):
+        y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, variant, x_pad=1, y_pad=2)
+        assert isclose_bits(y, unfused_gemv(hl, dev, t, slab, xn, rows, cols, variant)), \
+            f"variant {int(variant)}: the fused norm is not bitwise rms_norm then the gemv"
+    ref = oracle.matmul(t, dense, rows, cols, xn)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, xn)
     err = np.abs(y.astype(np.float64) - ref)
     print(f"    fused-norm gemv {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
@@ -201,6 +217,8 @@ def test_gemm_norm_within_bounds(hl, oracle, dev, t, n_vec, variant):
     ref = oracle.matmul(t, dense, rows, cols, xn)
     slab = slab_of(hl, dev, t, dense, rows, cols)
     y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, variant, x_pad=4, y_pad=1)
+    assert isclose_bits(y, unfused_gemv(hl, dev, t, slab, xn, rows, cols, variant)), \
+        "the GEMM's fused norm is not bitwise rms_norm then the GEMM"
     err = np.abs(y.astype(np.float64) - ref)
     tol = gemm_tol(oracle, t, dense, rows, cols, xn)
     print(f"    gemm+norm vs cpu: worst |d|/bound = {max_ratio(err, tol):.4f}")
@@ -224,13 +242,17 @@ def test_gate_up_norm(hl, oracle, dev, t, n_vec, variant):
     ref = oracle.gate_up_swiglu(t, dg, du, rows, cols, xn)
     g, u = oracle.matmul(t, dg, rows, cols, xn), oracle.matmul(t, du, rows, cols, xn)
     if variant == 2:
-        tg, tu = norm_gemv_tol(oracle, t, dg, rows, cols, xn), norm_gemv_tol(oracle, t, du, rows, cols, xn)
+        tg, tu = slab_gemv_tol(oracle, t, dg, rows, cols, xn), slab_gemv_tol(oracle, t, du, rows, cols, xn)
     else:
         tg, tu = gemm_tol(oracle, t, dg, rows, cols, xn), gemm_tol(oracle, t, du, rows, cols, xn)
     tol = swiglu_tol(g, u, tg, tu, ref, fast=variant != 2)
     out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
-    hl.gate_up_swiglu(t, slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols), to_dev(x, dev), out,
-                      rows, cols, n_vec, variant=variant, norm_w=to_dev(w, dev), norm_eps=EPS)
+    sg, su = slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols)
+    hl.gate_up_swiglu(t, sg, su, to_dev(x, dev), out, rows, cols, n_vec, variant=variant, norm_w=to_dev(w, dev),
+                      norm_eps=EPS)
+    plain = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gate_up_swiglu(t, sg, su, to_dev(xn, dev), plain, rows, cols, n_vec, variant=variant)
+    assert isclose_bits(host(out), host(plain)), "the fused norm is not bitwise rms_norm then gate_up"
     err = np.abs(host(out).astype(np.float64) - ref)
     print(f"    gate_up+norm worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
@@ -262,8 +284,9 @@ def test_lm_head_norm(hl, oracle, dev, t, variant):
     if variant == 1:
         assert isclose_bits(yl, cpu_logits) and np.array_equal(r, cpu), "reference variant: not the CPU's bits"
         return
-    tol = gemm_tol(oracle, t, dense, rows, cols, xn) if variant == 3 else norm_gemv_tol(oracle, t, dense, rows, cols, xn)
+    tol = gemm_tol(oracle, t, dense, rows, cols, xn) if variant == 3 else slab_gemv_tol(oracle, t, dense, rows, cols, xn)
     assert np.all(np.abs(yl.astype(np.float64) - cpu_logits) <= tol)
+    assert isclose_bits(yl, unfused_gemv(hl, dev, t, wt, xn, rows, cols, variant)), "logits: the fused norm is not bitwise"
     for v in range(n_vec):
         i = int(np.argmax(yl[v]))
         assert r[v].tolist() == [i, int(yl[v, i:i + 1].view(np.uint32)[0]), 0]
@@ -310,16 +333,22 @@ def test_gemv_group_within_bounds(hl, oracle, dev, g, n_vec, norm):
         dense = dense_of(buf, t, rows, cols, stride, 0)
         y = torch.full((n_vec, rows + 3), SENTINEL, dtype=torch.float32, device=dev)
         segs.append((t, slab_of(hl, dev, t, dense, rows, cols), rows, y, rows + 3))
-        tol = norm_gemv_tol(oracle, t, dense, rows, cols, xn) if norm else slab_gemv_tol(oracle, t, dense, rows, cols, xn)
+        tol = slab_gemv_tol(oracle, t, dense, rows, cols, xn)
         refs.append((oracle.matmul(t, dense, rows, cols, xn), tol))
     xd = to_dev(x, dev)
+    plain = None
+    if norm:  # the fused norm is bitwise rms_norm then the same group
+        plain = [torch.zeros((n_vec, rows), dtype=torch.float32, device=dev) for (_, _, rows, _, _) in segs]
+        hl.gemv_group([(t, wt, rows, p) for (t, wt, rows, _, _), p in zip(segs, plain)], to_dev(xn, dev), cols, n_vec)
     for rep in range(2):  # twice: the workspace words and counters are left clean
         hl.gemv_group(segs, xd, cols, n_vec, norm_w=to_dev(w, dev) if norm else None, norm_eps=EPS)
-        for (t, _, rows, y, _), (ref, tol) in zip(segs, refs):
+        for k, ((t, _, rows, y, _), (ref, tol)) in enumerate(zip(segs, refs)):
             out = host(y)
             assert np.all(out[:, rows:] == SENTINEL), "y padding written"
             err = np.abs(out[:, :rows].astype(np.float64) - ref)
             assert np.all(err <= tol), f"{NAMES[t]}: worst |d|/bound = {max_ratio(err, tol):.3f}"
+            if plain is not None:
+                assert isclose_bits(out[:, :rows], host(plain[k])), f"{NAMES[t]}: fused norm not bitwise"
 
 
 def test_gemv_group_rows_do_not_depend_on_the_batch(hl, dev):

@@ -1,0 +1,243 @@
+"""GPU parity of the path's smaller ops and of the stream state, through the C ABI:
+
+- SWIGLU (EltwiseArgs, include/halo/backend/backend.h:420-427; cpu::swiglu,
+  backends/cpu/ops_basic.cpp:165-167) against oracle_swiglu, with strided views;
+- ARGMAX (ArgmaxArgs, backend.h:463-468; cpu::argmax, backends/cpu/matmul.cpp:61-72) against the
+  oracle's result words: ties to the lowest index, NaN poisoning per vector;
+- the kernel variants chosen by id only (the VALU slab GEMV, the small-M GEMM);
+- the split-K reduction's failure path, forced from the host (every kernel still exits): the
+  stream's status word turns into a Device error at halo_mi_stream_check, and the workspace is
+  clean afterwards; halo_mi_stream_release frees a stream's workspace.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import (NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, gemm_emulated, gemm_tol, isclose_bits,
+                     make_weights, max_ratio, slab_gemv_tol)
+from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+# ---- SWIGLU -------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,cols,pads", [(1, 1, (0, 0, 0)), (3, 1000, (2, 5, 1)), (64, 17408, (0, 0, 0)),
+                                            (7, 333, (1, 0, 4))])
+def test_swiglu_against_oracle(hl, oracle, dev, rows, cols, pads):
+    """silu(g) u with g, u and out at their own row strides; padding untouched. The kernel's
+    silu is v / (1 + expf(-v)): within a few ulp of the CPU's libm form, so the bound is 8 ulp of
+    |out| plus the propagated exp error."""
+    import torch
+
+    say("swiglu", rows, cols, pads)
+    rng = np.random.default_rng(rows * 31 + cols)
+    g = (rng.standard_normal((rows, cols)) * 6).astype(np.float32)
+    u = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    g.flat[:4] = [0.0, -0.0, 88.0, -104.0][: min(4, g.size)]  # zero, overflow of exp(-v) to inf
+    ref = oracle.swiglu(g, u)
+    pg, pu, po = pads
+
+    def padded(a, p, fill):
+        h = np.full((rows, cols + p), fill, np.float32)
+        h[:, :cols] = a
+        return to_dev(h, dev)
+
+    gd, ud = padded(g, pg, 7.0), padded(u, pu, 9.0)
+    out = torch.full((rows, cols + po), SENTINEL, dtype=torch.float32, device=dev)
+    hl.swiglu(gd, ud, out, rows, cols, gate_stride=cols + pg, up_stride=cols + pu, out_stride=cols + po)
+    o = host(out)
+    assert np.all(o[:, cols:] == SENTINEL), "padding written"
+    err = np.abs(o[:, :cols].astype(np.float64) - ref)
+    tol = 8 * U * np.abs(ref.astype(np.float64)) + 1e-38
+    print(f"    swiglu worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+
+
+def test_swiglu_rejects(hl, dev):
+    import torch
+
+    a = torch.zeros((4, 64), dtype=torch.float32, device=dev)
+    b = torch.zeros((4, 64), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # out overlaps gate
+        hl.swiglu(a, b, a.data_ptr() + 64, 4, 64)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:  # stride below cols
+        hl.swiglu(a, b, torch.zeros_like(a), 4, 64, gate_stride=32)
+    assert e.value.code == hl.ErrorCode.Kernel
+
+
+# ---- ARGMAX -------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n,n_vec", [(1, 1), (300, 5), (151936, 3), (64, 2), (65, 4)])
+def test_argmax_words_against_oracle(hl, oracle, dev, n, n_vec):
+    import torch
+
+    say("argmax", n, n_vec)
+    rng = np.random.default_rng(n + n_vec)
+    lg = rng.standard_normal((n_vec, n)).astype(np.float32)
+    if n > 64:
+        lg[0, [n // 2, n - 1]] = 50.0  # a tie across 64-row parts: the lower index wins
+    if n_vec > 1:
+        lg[1, n // 3] = np.nan         # poisons vector 1 only
+    if n_vec > 2:
+        lg[2, :] = -np.inf
+    ref = oracle.argmax_words(lg)
+    ld = torch.full((n_vec, n + 3), -7.0, dtype=torch.float32, device=dev)
+    ld[:, :n] = to_dev(lg, dev)
+    res = torch.full((n_vec, 3), 0x5A5A, dtype=torch.int32, device=dev)
+    hl.argmax(ld, res, n, n_vec, logits_stride=n + 3)
+    got = host(res).view(np.uint32)
+    for v in range(n_vec):
+        if ref[v, 2]:
+            assert got[v, 0] == 0xFFFFFFFF and got[v, 2] == 1 and np.isnan(got[v, 1:2].view(np.float32)[0]), v
+        else:
+            assert np.array_equal(got[v], ref[v]), (v, got[v], ref[v])
+
+
+def test_argmax_rejects(hl, dev):
+    import torch
+
+    lg = torch.zeros((2, 10), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # result inside the logits
+        hl.argmax(lg, lg, 10, 2)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:  # empty row
+        hl.argmax(lg, torch.zeros(6, dtype=torch.int32, device=dev), 0, 2)
+    assert e.value.code == hl.ErrorCode.Kernel
+
+
+# ---- variants chosen by id ------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("t", (Q4_0, Q8_0, Q4_K, Q6_K))
+@pytest.mark.parametrize("n_vec", [1, 3, 6])
+def test_gemv_slab_valu_variant(hl, oracle, dev, t, n_vec):
+    """HALO_MI_GEMV_SLAB_VALU: the VALU slab kernel, within the SLAB GEMV bound, rows bitwise
+    independent of n_vec (the same split as the MFMA kernel)."""
+    import torch
+
+    rows, cols = 576, 5120
+    say("gemv valu", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=1500 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(1501).standard_normal((n_vec, cols)).astype(np.float32)
+    y = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMV_VALU)
+    yh = host(y)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
+    err = np.abs(yh.astype(np.float64) - ref)
+    print(f"    valu {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    y1 = torch.full((1, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gemv(t, slab, to_dev(x[-1:], dev), y1, rows, cols, 1, variant=hl.Variant.SLAB_GEMV_VALU)
+    assert isclose_bits(host(y1)[0], yh[-1]), "the VALU kernel's rows depend on n_vec"
+
+
+def test_gemv_slab_valu_rejects_other_formats(hl, dev):
+    import torch
+
+    t, rows, cols = Q5_K, 64, 256
+    buf, stride = make_weights(t, rows, cols, seed=3)
+    slab = slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, 0), rows, cols)
+    y = torch.zeros((1, rows), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:
+        hl.gemv(t, slab, to_dev(np.ones((1, cols), np.float32), dev), y, rows, cols, 1,
+                variant=hl.Variant.SLAB_GEMV_VALU)
+    assert e.value.code == hl.ErrorCode.Unsupported
+    with pytest.raises(hl.HaloError) as e:  # past the last id
+        hl.gemv(t, slab, to_dev(np.ones((1, cols), np.float32), dev), y, rows, cols, 1, variant=8)
+    assert e.value.code == hl.ErrorCode.Config
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("n_vec", [2, 9, 32])
+def test_gemm_small_m_variant(hl, oracle, dev, t, n_vec):
+    """HALO_MI_GEMM_SLAB_BF16_SMALL_M: the small-M kernel by id, within the bf16 GEMM bounds; more
+    than 32 vectors or cols not a multiple of 256 is Unsupported."""
+    import torch
+
+    rows, cols = 130, 1024
+    say("gemm small-M", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=1600 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(1601 + n_vec).standard_normal((n_vec, cols)).astype(np.float32)
+    y = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMM_BF16_SMALL_M)
+    yh = host(y).astype(np.float64)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    assert np.all(np.abs(yh - ref) <= gemm_tol(oracle, t, dense, rows, cols, x))
+    emu, etol = gemm_emulated(oracle, t, dense, rows, cols, x)
+    assert np.all(np.abs(yh - emu) <= etol)
+    x33 = to_dev(np.ones((33, cols), np.float32), dev)
+    with pytest.raises(hl.HaloError) as e:
+        hl.gemv(t, slab, x33, torch.zeros((33, rows), dtype=torch.float32, device=dev), rows, cols, 33,
+                variant=hl.Variant.SLAB_GEMM_BF16_SMALL_M)
+    assert e.value.code == hl.ErrorCode.Unsupported
+
+
+# ---- split-K failure path and the stream's workspace ------------------------------------------
+
+
+def test_split_k_timeout_is_reported_and_the_workspace_recovers(hl, oracle, dev):
+    """Forced from the host: every split-K reduction waits for a tag no partial carries (a
+    bounded wait of 64 rounds), gives up, writes NaN and marks the status word. The kernels
+    exit normally; halo_mi_stream_check reports a Device error once, and the next call on the
+    stream is correct again."""
+    import torch
+
+    t, rows, cols = Q4_K, 576, 5120  # 9 slabs: split over K, every slab has a reducer
+    say("split-K forced timeout", rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=1700)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(1701).standard_normal((1, cols)).astype(np.float32)
+    xd = to_dev(x, dev)
+    y = torch.full((1, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.stream_check()  # clean before
+    try:
+        hl.force_splitk_timeout(64, True)
+        hl.gemv(t, slab, xd, y, rows, cols, 1, variant=hl.Variant.SLAB_GEMV)
+    finally:
+        hl.force_splitk_timeout(0, False)
+    with pytest.raises(hl.HaloError) as e:
+        hl.stream_check()
+    assert e.value.code == hl.ErrorCode.Device
+    assert np.all(np.isnan(host(y))), "a reduction that gave up must not write a plausible value"
+    hl.stream_check()  # reported once
+    hl.gemv(t, slab, xd, y, rows, cols, 1, variant=hl.Variant.SLAB_GEMV)
+    hl.stream_check()
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    assert np.all(np.abs(host(y).astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dense, rows, cols, x))
+
+
+def test_stream_release_frees_and_reallocates(hl, oracle, dev):
+    import torch
+
+    t, rows, cols = Q6_K, 640, 5120
+    say("stream release", rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=1800)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(1801).standard_normal((2, cols)).astype(np.float32)
+    s = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            y = torch.full((2, rows), SENTINEL, dtype=torch.float32, device=dev)
+            hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, 2)
+            hl.stream_check()
+            outs.append(host(y))
+            free_before = torch.cuda.mem_get_info()[0]
+            hl.stream_release()
+            assert torch.cuda.mem_get_info()[0] >= free_before + (100 << 20), "the workspace was not freed"
+    hl.stream_release(s.cuda_stream)  # releasing a stream without a workspace is a no-op
+    assert isclose_bits(outs[0], outs[1])
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    assert np.all(np.abs(outs[0].astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dense, rows, cols, x))

@@ -183,6 +183,36 @@ def test_gemv_slab_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
         assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
 
 
+@pytest.mark.parametrize("t,rows,cols,pair", [(Q4_K, 17408, 5120, False), (Q4_K, 17408, 5120, True),
+                                               (Q6_K, 5120, 17408, False), (Q6_K, 151936, 5120, False)])
+def test_gemv_rows_do_not_depend_on_the_batch_at_baseline_shapes(hl, dev, t, rows, cols, pair):
+    """The same invariance at the BASELINE shapes, where the K split and the waves per chunk are
+    largest (the gate/up pair streams two matrices; 151936 rows takes the multi-group kernel)."""
+    import torch
+
+    say("gemv batch invariance", NAMES[t], rows, cols, "pair" if pair else "")
+    if rows == 151936:
+        _, slab = head_weights(hl, dev)
+    else:
+        slab = slab_of(hl, dev, t, synth(hl, t, rows, cols, 90 + rows), rows, cols)
+    slab_u = slab_of(hl, dev, t, synth(hl, t, rows, cols, 91 + rows), rows, cols) if pair else None
+    x = np.random.default_rng(9000 + rows).standard_normal((9, cols)).astype(np.float32)
+    xd = to_dev(x, dev)
+
+    def run(n0, n):
+        y = torch.full((n, rows), SENTINEL, dtype=torch.float32, device=dev)
+        xv = xd[n0:n0 + n]
+        if pair:
+            hl.gate_up_swiglu(t, slab, slab_u, xv, y, rows, cols, n, variant=hl.Variant.SLAB_GEMV)
+        else:
+            hl.gemv(t, slab, xv, y, rows, cols, n, variant=hl.Variant.SLAB_GEMV)
+        return host(y)
+
+    singles = np.concatenate([run(i, 1) for i in range(9)])
+    for n_vec in (2, 3, 4, 5, 9):
+        assert isclose_bits(run(0, n_vec), singles[:n_vec]), f"n_vec={n_vec} changed a row"
+
+
 @pytest.mark.parametrize("t", (Q4_K, Q6_K))
 def test_gemv_split_k_state_is_clean_between_calls(hl, oracle, dev, t):
     """Split-K calls of different shapes share the stream's workspace (arrival counters and
@@ -415,30 +445,40 @@ def test_baseline_shapes_gemv(hl, oracle, dev, t, rows, cols, seed, outliers, n_
     assert np.all(err <= tol)
 
 
-def test_baseline_q6_k_head(hl, oracle, dev):
-    """config 3b: 151936 x 5120 Q6_K with 1% of the columns scaled x8."""
+_HEAD = {}
+
+
+def head_weights(hl, dev):
+    """config 3b's head (151936 x 5120 Q6_K, 1% of the columns x8), quantized and uploaded once."""
+    if "w" not in _HEAD:
+        t, rows, cols = Q6_K, 151936, 5120
+        wq = synth(hl, t, rows, cols, 3, 0.01)
+        _HEAD["w"] = (wq, slab_of(hl, dev, t, wq, rows, cols))
+    return _HEAD["w"]
+
+
+@pytest.mark.parametrize("n_vec", [1, 2, 3, 4])
+def test_baseline_q6_k_head(hl, oracle, dev, n_vec):
+    """config 3b: 151936 x 5120 Q6_K with 1% of the columns scaled x8, M = 1..4, whole output."""
     t, rows, cols = Q6_K, 151936, 5120
-    say("baseline head", rows, cols)
-    wq = synth(hl, t, rows, cols, 3, 0.01)
-    x = hl.fill_normal(1003, cols).reshape(1, cols)
+    say("baseline head", rows, cols, n_vec)
+    wq, slab = head_weights(hl, dev)
+    x = hl.fill_normal(1003 + n_vec, n_vec * cols).reshape(n_vec, cols)
     ref = oracle.matmul(t, wq, rows, cols, x)
-    slab = slab_of(hl, dev, t, wq, rows, cols)
     y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.DEFAULT)
     tol = slab_gemv_tol(oracle, t, wq, rows, cols, x)
     err = np.abs(y.astype(np.float64) - ref)
-    print(f"    head worst |d|/bound = {max_ratio(err, tol):.4f}")
+    print(f"    head M={n_vec} worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
-    assert int(np.argmax(y[0])) == int(np.argmax(ref[0])) or abs(float(y[0].max() - ref[0].max())) <= tol.max()
 
 
 GATE_UP_GEMV_MAX = 4  # kGateUpGemvMax: the gate/up auto choice runs the GEMV pair up to 4 vectors
 
 
-@pytest.mark.parametrize("n_vec", [2, 8, 64, 512])
+@pytest.mark.parametrize("n_vec", [2, 4, 8, 64, 512])
 def test_baseline_gate_up(hl, oracle, dev, n_vec):
-    """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices; the oracle checks the
-    first 512 and the last 1088 output columns (rows of W are independent; at M = 512 the last
-    17 slabs are the K-split tiles of the GEMM launch)."""
+    """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices (and config 5's FFN pair
+    at M = 4); the oracle checks every output."""
     import torch
 
     t, rows, cols = Q4_K, 17408, 5120
@@ -454,12 +494,12 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
     # the split-K partial sums are added in a fixed order: a second call is bitwise identical
     hl.gate_up_swiglu(t, sg, su, xd, out, rows, cols, n_vec)
     assert isclose_bits(host(out), yall), "gate/up result changed between two identical calls"
-    for c0, c1 in ((0, 512), (rows - 1088, rows)):
+    for c0, c1 in ((0, rows),):
         n = c1 - c0
         wg_c, wu_c = wg[c0 * rb:c1 * rb], wu[c0 * rb:c1 * rb]
-        ref = oracle.gate_up_swiglu(t, wg_c, wu_c, n, cols, x)
         g = oracle.matmul(t, wg_c, n, cols, x)
         u = oracle.matmul(t, wu_c, n, cols, x)
+        ref = oracle.swiglu(g, u)  # oracle.gate_up_swiglu's composition (pinned in test_oracle)
         y = yall[:, c0:c1]
         gemv = n_vec <= GATE_UP_GEMV_MAX  # the auto choice: the GEMV pair up to 4 vectors, then the GEMM
         if gemv:
@@ -480,24 +520,21 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
 @pytest.mark.parametrize("name,t,rows,cols", [
     ("gdn_in", Q4_K, 12288, 5120), ("gdn_out", Q4_K, 5120, 6144), ("q", Q4_K, 6144, 5120),
     ("k", Q4_K, 1024, 5120), ("v", Q6_K, 1024, 5120), ("down", Q6_K, 5120, 17408)])
-def test_baseline_hybrid_layer_shapes(hl, oracle, dev, name, t, rows, cols):
-    """Each projection of the config-5 layer at M = 1 (GEMV) and M = 512 (bf16 GEMM, the
-    default for more than 8 vectors), checked on its first and last 256 rows."""
+@pytest.mark.parametrize("n_vec", [1, 4, 512])
+def test_baseline_hybrid_layer_shapes(hl, oracle, dev, name, t, rows, cols, n_vec):
+    """Each projection of the config-5 layer at M = 1 and 4 (GEMV) and M = 512 (bf16 GEMM, the
+    default for more than 8 vectors), every output checked."""
     import torch
 
-    say("hybrid layer", name, NAMES[t], rows, cols)
+    say("hybrid layer", name, NAMES[t], rows, cols, n_vec)
     wq = synth(hl, t, rows, cols, 500 + rows + cols)
-    rb = row_bytes(t, cols)
     slab = slab_of(hl, dev, t, wq, rows, cols)
-    for n_vec in (1, 512):
-        x = hl.fill_normal(600 + n_vec, n_vec * cols).reshape(n_vec, cols)
-        y = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
-        hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, n_vec)
-        yh = host(y)
-        for r0 in (0, rows - 256):
-            part = wq[r0 * rb:(r0 + 256) * rb]
-            ref = oracle.matmul(t, part, 256, cols, x)
-            tol = slab_gemv_tol(oracle, t, part, 256, cols, x) if n_vec == 1 else gemm_tol(oracle, t, part, 256, cols, x)
-            err = np.abs(yh[:, r0:r0 + 256].astype(np.float64) - ref)
-            print(f"    {name} M={n_vec} rows [{r0}, {r0 + 256}): worst |d|/bound = {max_ratio(err, tol):.4f}")
-            assert np.all(err <= tol)
+    x = hl.fill_normal(600 + n_vec, n_vec * cols).reshape(n_vec, cols)
+    y = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
+    hl.gemv(t, slab, to_dev(x, dev), y, rows, cols, n_vec)
+    yh = host(y)
+    ref = oracle.matmul(t, wq, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, wq, rows, cols, x) if n_vec <= 8 else gemm_tol(oracle, t, wq, rows, cols, x)
+    err = np.abs(yh.astype(np.float64) - ref)
+    print(f"    {name} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)

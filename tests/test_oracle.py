@@ -294,6 +294,119 @@ def test_q5_k_and_iq4_xs_dequant_terms(oracle):
                 assert np.all(off[0, seg] == np.float32(128) * dl)
 
 
+def _f16(blk, i):
+    return np.float32(np.frombuffer(bytes(blk[i:i + 2]), np.float16)[0])
+
+
+def _random_blocks(rng, t, bb, n):
+    """n blocks of random bytes with finite fp16 scales (the d / dmin words)."""
+    w = rng.integers(0, 256, size=n * bb, dtype=np.uint8)
+    for b in range(n):
+        base = bb * b + (208 if t == Q6_K else 0)
+        w[base: base + 2] = np.frombuffer(f16_bytes(rng.uniform(-0.05, 0.05)), np.uint8)
+        if t in (Q4_K, Q5_K):
+            w[bb * b + 2: bb * b + 4] = np.frombuffer(f16_bytes(rng.uniform(0, 0.05)), np.uint8)
+    # an fp16-subnormal scale in the first block
+    w[(208 if t == Q6_K else 0): (208 if t == Q6_K else 0) + 2] = np.frombuffer(bytes([0x07, 0x00]), np.uint8)
+    return w
+
+
+@pytest.mark.parametrize("t,bb,be", [(Q4_0, 18, 32), (Q8_0, 34, 32)])
+def test_q4_0_q8_0_dequant_terms(oracle, t, bb, be):
+    """Q4_0: w = q d - 8 d, so off = 8 d (quant.cpp:79-90); Q8_0: codes are read as unsigned
+    bytes by the kernels, so off = 128 d (quant.cpp:143-151). a is the dequantized weight,
+    b = 0. With every code at its lowest value (nibble 0 / int8 -128), w = -off exactly."""
+    rng = np.random.default_rng(11)
+    n = 8
+    w = _random_blocks(rng, t, bb, n)
+    a, b_, off = oracle.dequant_terms(t, w, 1, n * be)
+    y = oracle.dequantize_row(t, w, n * be)
+    assert np.array_equal((a - b_).astype(np.float32)[0], y)
+    assert np.all(b_ == 0)
+    k = 8 if t == Q4_0 else 128
+    for b in range(n):
+        d = _f16(w[bb * b: bb * (b + 1)], 0)
+        assert np.all(off[0, be * b: be * (b + 1)] == np.float32(k) * d), b
+    low = w.copy()
+    for b in range(n):
+        low[bb * b + 2: bb * (b + 1)] = 0x00 if t == Q4_0 else 0x80
+    a2, b2, off2 = oracle.dequant_terms(t, low, 1, n * be)
+    y2 = oracle.dequantize_row(t, low, n * be)
+    assert isbits(off2[0], -y2) and isbits(a2[0], y2)
+
+
+def _k4_scale_min(s: bytes, j: int):
+    """ggml's get_scale_min_k4 written from the 12-byte layout: 6-bit (sc, m) pairs, the first
+    four whole in bytes 0..3 / 4..7, the last four split into low nibbles of bytes 8..11 and
+    the top two bits of bytes 0..7."""
+    if j < 4:
+        return s[j] & 63, s[j + 4] & 63
+    return (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4), (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+
+
+def test_q4_k_dequant_terms(oracle):
+    """Q4_K: a = (d sc) q, b = dmin m, off = 0 (quant.cpp:247-269); recomputed here from the
+    block bytes with an independent reading of the scale/min table."""
+    rng = np.random.default_rng(12)
+    n = 6
+    w = _random_blocks(rng, Q4_K, 144, n)
+    a, b_, off = oracle.dequant_terms(Q4_K, w, 1, n * 256)
+    y = oracle.dequantize_row(Q4_K, w, n * 256)
+    assert np.array_equal((a - b_).astype(np.float32)[0], y)
+    assert np.all(off == 0)
+    for b in range(n):
+        blk = bytes(w[144 * b: 144 * (b + 1)])
+        d, dmin = _f16(blk, 0), _f16(blk, 2)
+        for e in range(256):
+            g, hi, l = e // 64, (e % 64) // 32, e % 32
+            sc, m = _k4_scale_min(blk[4:16], 2 * g + hi)
+            byte = blk[16 + 32 * g + l]
+            q = (byte >> 4) if hi else (byte & 15)
+            assert a[0, 256 * b + e] == np.float32(np.float32(d * np.float32(sc)) * np.float32(q)), (b, e)
+            assert b_[0, 256 * b + e] == np.float32(dmin * np.float32(m)), (b, e)
+
+
+def test_q6_k_dequant_terms(oracle):
+    """Q6_K: a is the dequantized weight, b = 0, off = 32 (d sc) with sc the int8 scale of the
+    element's 16-weight sub-block (quant.cpp:302-327). Every code 0 gives w = -32 (d sc), so
+    off = -w exactly there; on random blocks off is constant over each 16-weight run and is 32
+    times one of the block's 16 products d sc."""
+    rng = np.random.default_rng(13)
+    n = 5
+    w = _random_blocks(rng, Q6_K, 210, n)
+    a, b_, off = oracle.dequant_terms(Q6_K, w, 1, n * 256)
+    y = oracle.dequantize_row(Q6_K, w, n * 256)
+    assert np.array_equal((a - b_).astype(np.float32)[0], y)
+    assert np.all(b_ == 0)
+    for b in range(n):
+        blk = w[210 * b: 210 * (b + 1)]
+        d = _f16(blk, 208)
+        allowed = {float(np.float32(32) * np.float32(d * np.float32(s))) for s in blk[192:208].view(np.int8)}
+        ob = off[0, 256 * b: 256 * (b + 1)].reshape(16, 16)
+        assert np.all(ob == ob[:, :1])
+        assert {float(v) for v in ob[:, 0]} <= allowed
+    zero = w.copy()
+    for b in range(n):
+        zero[210 * b: 210 * b + 192] = 0
+    a2, _, off2 = oracle.dequant_terms(Q6_K, zero, 1, n * 256)
+    y2 = oracle.dequantize_row(Q6_K, zero, n * 256)
+    assert isbits(off2[0], -y2) and isbits(a2[0], y2)
+    # one scale per sub-block: scale s_j alone non-zero moves exactly the 16 weights of run j
+    for j in range(16):
+        one = zero[:210].copy()
+        one[192:208] = 0
+        one[192 + j] = 3
+        _, _, o1 = oracle.dequant_terms(Q6_K, one, 1, 256)
+        nz = np.nonzero(o1[0])[0]
+        y1 = oracle.dequantize_row(Q6_K, one, 256)
+        assert np.array_equal(nz, np.nonzero(y1)[0]) and len(nz) == 16, j
+
+
+def isbits(a, b) -> bool:
+    return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32),
+                          np.ascontiguousarray(b, np.float32).view(np.uint32))
+
+
 # ---- rms_norm (backends/cpu/ops_basic.cpp:18-33) ------------------------------------------
 
 
@@ -590,3 +703,28 @@ def test_lm_head_q6_k_logits_are_matmul_and_index_is_first_argmax(oracle):
     assert np.array_equal(logits, oracle.matmul(Q6_K, w, rows, cols, x))
     for i in range(4):
         assert res[i, 0] == np.argmax(logits[i]) and res[i, 1] == logits[i].max().view(np.uint32) and res[i, 2] == 0
+
+
+# ---- argmax (backends/cpu/matmul.cpp:61-72) -------------------------------------------------
+
+
+def test_argmax_words_first_maximum_and_poison(oracle):
+    """The index is numpy's first maximum (ties to the lowest index), the value its bits; a row
+    with a NaN anywhere gives the poisoned words {0xFFFFFFFF, NaN, 1}."""
+    rng = np.random.default_rng(21)
+    lg = rng.standard_normal((6, 777)).astype(np.float32)
+    lg[0, [3, 500]] = 7.0                      # tie
+    lg[1, :] = -np.inf                         # all -inf: index 0
+    lg[2, 0] = np.nan                          # NaN first
+    lg[3, 776] = np.nan                        # NaN last
+    lg[4, :] = 0.0
+    lg[4, 9] = -0.0                            # -0 == +0: the first zero stays
+    res = oracle.argmax_words(lg)
+    for i in range(6):
+        if np.isnan(lg[i]).any():
+            assert res[i, 0] == 0xFFFFFFFF and res[i, 2] == 1 and np.isnan(res[i, 1:2].view(np.float32)[0]), i
+            continue
+        j = int(np.argmax(lg[i]))
+        assert res[i, 0] == j and res[i, 2] == 0, i
+        assert res[i, 1] == lg[i, j:j + 1].view(np.uint32)[0], i
+    assert res[0, 0] == 3 and res[1, 0] == 0 and res[4, 0] == 0
