@@ -126,6 +126,26 @@ int check_norm(const char* op, const float* norm_w, uint32_t cols, const void* o
     return HALO_MI_OK;
 }
 
+int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t* xs, uint64_t* ys) {
+    int code;
+    (void)row_bytes_checked(p->type, p->cols, &code, op);
+    if (code) return code;
+    *xs = p->x_stride ? p->x_stride : p->cols;
+    *ys = p->y_stride ? p->y_stride : p->rows;
+    if ((code = check_xy(op, p->x, *xs, p->y, *ys, p->rows, p->cols, p->n_vec))) return code;
+    if (p->n_vec == 0 || p->rows == 0) return HALO_MI_OK;
+    if (!p->w) return set_error(HALO_MI_E_KERNEL, "%s: operand w is empty", op);
+    const uint64_t yext = extent(p->n_vec, *ys * 4, (uint64_t)p->rows * 4);
+    if ((code = check_norm(op, p->norm_w, p->cols, p->y, yext))) return code;
+    if (p->layout != HALO_MI_LAYOUT_SLAB) return set_error(HALO_MI_E_CONFIG, "%s: needs the SLAB layout", op);
+    if (!is_quant(p->type)) return set_error(HALO_MI_E_UNSUPPORTED, "%s: type %u has no SLAB layout", op, p->type);
+    if (p->w_stride != 0) return set_error(HALO_MI_E_KERNEL, "%s: a SLAB operand has no row stride", op);
+    if (reinterpret_cast<uintptr_t>(p->w) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
+    if (ranges_overlap(p->y, yext, p->w, halo_mi_slab_bytes(p->type, p->rows, p->cols)))
+        return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
+    return HALO_MI_OK;
+}
+
 // The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
 uint32_t gemm_tiles(uint32_t variant) {
     switch (variant) {

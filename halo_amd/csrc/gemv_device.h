@@ -607,11 +607,9 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // x of one slot group, lane = 8 s + r: x[slot 8 grp + s][4 r .. 4 r + 3] (zero past the end).
 // Branch-free (the address is clamped, the value selected after): a load under a branch would
 // make the compiler wait for it before the weight loads that follow are issued.
-// NORM: wr gets the same four elements of norm_w (loaded branch-free as x is).
-template <int NV, bool NORM>
-__device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], const float* __restrict__ x,
-                                          uint64_t x_stride, const float* __restrict__ norm_w, uint32_t grp, uint32_t S,
-                                          uint32_t lane) {
+template <int NV>
+__device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], const float* __restrict__ x, uint64_t x_stride, uint32_t grp,
+                                          uint32_t S, uint32_t lane) {
     const uint32_t slot = grp * 8 + (lane >> 3);
     const bool in = slot < S;
     const uint64_t e = (uint64_t)min(slot, S - 1) * 32 + 4 * (lane & 7);
@@ -622,12 +620,6 @@ __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], co
             const float t = x[(uint64_t)v * x_stride + e + i];
             xr[v][i] = in ? t : 0.0f;
         }
-    if constexpr (NORM)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float t = norm_w[e + i];
-            wr[i] = in ? t : 0.0f;
-        }
 }
 
 // Builds this wave's A table for one group from xr, reads it back as register pairs, and
@@ -636,28 +628,12 @@ __device__ __forceinline__ void mx_load_x(float (&xr)[NV][4], float (&wr)[4], co
 // Q6_K, whose low-half sum is then in lane 8 s).
 // The k-step r of a slot (k-steps 0..3: slot elements 0..15, 4..7: 16..31) covers elements
 // 4 r .. 4 r + 3 in the order (0, 2, 1, 3), the order the masks below produce them.
-// With the fused norm (NORM), the group's x is (x * inv) * norm_w, rounded as cpu::rms_norm
-// rounds it (backends/cpu/ops_basic.cpp:29 of the reference): exactly the normalized x.
-template <uint32_t T, int NV, bool NORM>
-__device__ __forceinline__ void mx_build(const float (&xraw)[NV][4], const float (&wr)[4], const float (&inv)[NV],
-                                         uint8_t* tab, uint32_t lane, s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV],
-                                         float (&xs)[NV]) {
-#pragma clang fp contract(off)
+template <uint32_t T, int NV>
+__device__ __forceinline__ void mx_build(const float (&xr)[NV][4], uint8_t* tab, uint32_t lane,
+                                         s16x4 (&A)[4 * mx_blocks<NV>()], int (&es)[NV], float (&xs)[NV]) {
     constexpr int M = mx_blocks<NV>();
     constexpr int kHiShift = (T == kQ4_K || T == kQ4_0) ? 4 : 0;  // high nibbles arrive as 16 q
     const uint32_t s = lane >> 3, r = lane & 7;
-    float xr[NV][4];
-#pragma unroll
-    for (int v = 0; v < NV; ++v)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (NORM) {
-                const float t = xraw[v][i] * inv[v];
-                xr[v][i] = t * wr[i];
-            } else {
-                xr[v][i] = xraw[v][i];
-            }
-        }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         uint32_t mb = 0;
@@ -827,67 +803,10 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
     }
 }
 
-// The fused norm's prologue: 1 / rms of each vector's raw x row, bitwise cpu::rms_norm's
-// (backends/cpu/ops_basic.cpp:26-27 of the reference: mean = dot(x, x) / cols, inv =
-// 1 / sqrt(mean + eps), the sum of squares in cpu::detail::dot's order), for the whole
-// workgroup. Wave 0 stages the rows through LDS (stage: kNormPiece floats per vector) in
-// pieces, lanes 8 v + j run the dot's interleaved sequential sums j = 0..7 of vector v, and the
-// combine ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)) follows (cols is a multiple of 32: no tail).
-// The result goes through inv_lds (NV floats that nothing else writes) to every wave. Every
-// wave of the workgroup must call it (it ends with a barrier). The normalized x the kernels then
-// build is exactly rms_norm's output, so the fused GEMV is bitwise rms_norm then the GEMV.
-constexpr uint32_t kNormPiece = 512;
-
+// Dynamic LDS bytes of a k_gemv_mx workgroup of nw waves: the waves' partials and A tables.
 template <int NV>
-__device__ __forceinline__ void gemv_norm_inv(const GemvSlabArgs& a, float* stage, float* inv_lds, uint32_t wave,
-                                              uint32_t lane, float (&inv)[NV]) {
-#pragma clang fp contract(off)
-    if (wave == 0) {
-        const uint32_t v_l = lane >> 3, j = lane & 7;
-        float p = 0.0f;
-        for (uint32_t c0 = 0; c0 < a.cols; c0 += kNormPiece) {
-            const uint32_t n = min(kNormPiece, a.cols - c0);
-#pragma unroll
-            for (int v = 0; v < NV; ++v)
-                if ((uint32_t)v < a.n_vec)
-                    for (uint32_t i = lane; i < n; i += 64) stage[v * kNormPiece + i] = a.x[(uint64_t)v * a.x_stride + c0 + i];
-            __builtin_amdgcn_wave_barrier();
-            if (v_l < min((uint32_t)NV, a.n_vec)) {
-                const float* sv = stage + v_l * kNormPiece;
-#pragma unroll 8
-                for (uint32_t i = j; i < n; i += 8) {
-                    const float t = sv[i];
-                    const float q = t * t;
-                    p = p + q;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-        }
-        // lanes 8 v .. 8 v + 7 hold p0..p7 of vector v
-        const float q = p + __shfl_down(p, 4, 8);  // j < 4: p_j + p_{j+4}
-        const float r = q + __shfl_down(q, 1, 8);  // j = 0: left pair, j = 2: right pair
-        const float t = r + __shfl_down(r, 2, 8);  // j = 0: the sum
-        if (j == 0 && v_l < (uint32_t)NV) {
-            const float mean = t / (float)a.cols;
-            inv_lds[v_l] = 1.0f / sqrtf(mean + a.norm_eps);
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int v = 0; v < NV; ++v) inv[v] = inv_lds[v];
-}
-
-// Dynamic LDS floats of a k_gemv_mx workgroup of nw waves: the waves' partials and A tables, and
-// with the fused norm the prologue's stage (which they overlay) and its NV results after them.
-template <int NV>
-constexpr uint32_t mx_wave_floats() { return NV * 64 + mx_table_bytes<NV>() / 4; }
-template <int NV>
-__host__ __device__ constexpr uint32_t mx_norm_inv_offset(uint32_t nw) {
-    return nw * mx_wave_floats<NV>() > NV * kNormPiece ? nw * mx_wave_floats<NV>() : NV * kNormPiece;
-}
-template <int NV>
-__host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw, bool norm) {
-    return norm ? (size_t)(mx_norm_inv_offset<NV>(nw) + NV) * 4 : (size_t)nw * mx_wave_floats<NV>() * 4;
+__host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw) {
+    return (size_t)nw * (NV * 64 * sizeof(float) + mx_table_bytes<NV>());
 }
 
 // Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
@@ -901,7 +820,7 @@ constexpr uint32_t mx_max_threads() {
 // wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
 // The body of workgroup `bid` of a k_gemv_mx launch over the matrix of `a` (also one segment of a
 // grouped launch, k_gemv_mx_group).
-template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM>
+template <uint32_t T, int NV, bool PAIR, bool ONE>
 __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid) {
     extern __shared__ float smem[];
     constexpr uint32_t MATS = PAIR ? 2 : 1;
@@ -921,64 +840,47 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     float* red = smem;
     uint8_t* tab = reinterpret_cast<uint8_t*>(smem + nw * NV * 64) + wave * mx_table_bytes<NV>();
 
-    float acc0[NV], inv[NV];
+    float acc0[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc0[v] = inv[v] = 0.0f;
-    float xr[NV][4], wr[4];
+    for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
+    float xr[NV][4];
     uint32_t ticket = 0;
-    // Loads are waited for in issue order (vmcnt), so x comes first (the A table is built while
-    // the weights are on their way). With the fused norm, wave 0 runs the norm's prologue before
-    // it issues its own loads (its staging loads would otherwise wait behind its weights); the
-    // other waves issue theirs first and meet it at the prologue's barrier.
-    const bool early = !NORM || wave != 0;
     if constexpr (ONE) {
-        SlotGroup<T> G;
-        if (early && w0 < w1) {
-            mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
-            load_group<T>(G, slab0, geo, lane, w0, S);
-        }
-        ticket = gemv_ticket(a, slab, nch);
-        if constexpr (NORM) {
-            gemv_norm_inv<NV>(a, smem, smem + mx_norm_inv_offset<NV>(nw), wave, lane, inv);
-            if (!early && w0 < w1) {
-                mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
-                load_group<T>(G, slab0, geo, lane, w0, S);
-            }
-        }
         if (w0 < w1) {
+            SlotGroup<T> G;
+            // x first: the A table is built while the weights are on their way (loads are waited
+            // for in issue order)
+            mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
+            load_group<T>(G, slab0, geo, lane, w0, S);
+            ticket = gemv_ticket(a, slab, nch);
             s16x4 A[4 * M];
             int es[NV];
             float xs[NV];
-            mx_build<T, NV, NORM>(xr, wr, inv, tab, lane, A, es, xs);
+            mx_build<T, NV>(xr, tab, lane, A, es, xs);
             mx_group<T, NV>(G, A, xs, min(8u, S - w0 * 8), acc0);
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
+        } else {
+            ticket = gemv_ticket(a, slab, nch);
         }
         gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
         return;
     }
     SlotGroup<T> cur, nxt;
-    if (early && w0 < w1) {
-        mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
+    if (w0 < w1) {  // x first: the A table is built while the weights are on their way
+        mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
         load_group<T>(cur, slab0, geo, lane, w0, S);
     }
     ticket = gemv_ticket(a, slab, nch);
-    if constexpr (NORM) {
-        gemv_norm_inv<NV>(a, smem, smem + mx_norm_inv_offset<NV>(nw), wave, lane, inv);
-        if (!early && w0 < w1) {
-            mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, w0, S, lane);
-            load_group<T>(cur, slab0, geo, lane, w0, S);
-        }
-    }
     // One group: build its A table from xr, prefetch x and the weights of the next group (past
     // the last group: the last one again, an L2 hit, so the loop stays branch-free), multiply.
     auto step = [&](const SlotGroup<T>& G, SlotGroup<T>& next, uint32_t grp) {
         s16x4 A[4 * M];
         int es[NV];
         float xs[NV];
-        mx_build<T, NV, NORM>(xr, wr, inv, tab, lane, A, es, xs);
+        mx_build<T, NV>(xr, tab, lane, A, es, xs);
         const uint32_t gn = min(grp + 1, w1 - 1);
-        mx_load_x<NV, NORM>(xr, wr, a.x, a.x_stride, a.norm_w, gn, S, lane);
+        mx_load_x<NV>(xr, a.x, a.x_stride, gn, S, lane);
         load_group<T>(next, slab0, geo, lane, gn, S);
         float accg[NV];
 #pragma unroll
@@ -996,9 +898,9 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
-template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
+template <uint32_t T, int NV, bool PAIR, bool ONE>
 __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
-    gemv_mx_body<T, NV, PAIR, ONE, NORM>(a, blockIdx.x);
+    gemv_mx_body<T, NV, PAIR, ONE>(a, blockIdx.x);
 }
 
 }  // namespace

@@ -70,12 +70,15 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     return {ks, nw, false};
 }
 
+// slots_cap / counters_cap: the split-K words and slab counters the workspace holds. The split is
+// always chosen for the allocated workspace's capacity (kSlots, kCounters), so a smaller workspace
+// gives the same bits or refuses the shape.
 template <uint32_t T, int NV, bool PAIR>
-int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_t st) {
+int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t slots_cap, uint64_t counters_cap,
+                       hipStream_t st) {
     const uint32_t S = a.cols / kSlot;
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     const bool have_ws = ws != nullptr && slabs <= kCounters;
-    // the fused norm takes the plain launch's split: its result is bitwise rms_norm then this GEMV
     const GemvSplit sp = pick_split<T>(slabs, S, MATS, have_ws);
     a.ks = sp.ks;
     a.slots = ws ? ws->slots : nullptr;
@@ -83,13 +86,13 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
     a.status = ws ? ws->status : nullptr;
     apply_test_hooks(a);
     // the chunks of a slab (or the pair's two matrices) meet in the workspace words
-    if (a.ks * MATS > 1 && (!have_ws || (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64 > kSlots))
-        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows exceed the split-K workspace", a.rows);
-    const bool norm = a.norm_w != nullptr;
-    const size_t lds = mx_lds_bytes<NV>(sp.nw, norm);
-    if (a.valu) {  // the VALU kernel (variant HALO_MI_GEMV_SLAB_VALU): first four formats, no norm
+    if (a.ks * MATS > 1 &&
+        (!have_ws || (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64 > slots_cap || slabs > counters_cap))
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows x %u cols exceed the split-K workspace (%llu words, %llu slabs)",
+                         a.rows, a.cols, (unsigned long long)slots_cap, (unsigned long long)counters_cap);
+    const size_t lds = mx_lds_bytes<NV>(sp.nw);
+    if (a.valu) {  // the VALU kernel (variant HALO_MI_GEMV_SLAB_VALU): the first four formats
         if constexpr (T != kQ5_K && T != kIQ4_XS) {
-            if (a.norm_w) return set_error(HALO_MI_E_UNSUPPORTED, "gemv: the VALU slab kernel has no fused norm");
             hipLaunchKernelGGL((k_gemv_slab<T, NV, PAIR>), dim3(slabs * a.ks * MATS), dim3(64 * sp.nw),
                                (size_t)sp.nw * NV * 64 * sizeof(float), st, a);
             return hip_status(hipGetLastError(), "gemv_slab launch");
@@ -98,62 +101,92 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, hipStream_
         }
     }
     const dim3 grid(slabs * a.ks * MATS), block(64 * sp.nw);
-    if (sp.one) {
-        if (norm) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true, true>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), grid, block, lds, st, a);
-    } else {
-        if (norm) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false, true>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), grid, block, lds, st, a);
-    }
+    if (sp.one) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), grid, block, lds, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
 }
 
 template <uint32_t T, bool PAIR>
-int launch_gemv_slab_nv(const GemvSlabArgs& a, uint32_t slabs, Workspace* ws, hipStream_t st) {
+int launch_gemv_slab_nv(const GemvSlabArgs& a, uint32_t slabs, Workspace* ws, uint64_t slots_cap, uint64_t counters_cap,
+                        hipStream_t st) {
     switch (a.n_vec) {
-        case 1: return launch_gemv_slab_t<T, 1, PAIR>(a, slabs, ws, st);
-        case 2: return launch_gemv_slab_t<T, 2, PAIR>(a, slabs, ws, st);
-        case 3: return launch_gemv_slab_t<T, 3, PAIR>(a, slabs, ws, st);
-        default: return launch_gemv_slab_t<T, 4, PAIR>(a, slabs, ws, st);
+        case 1: return launch_gemv_slab_t<T, 1, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+        case 2: return launch_gemv_slab_t<T, 2, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+        case 3: return launch_gemv_slab_t<T, 3, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+        default: return launch_gemv_slab_t<T, 4, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
     }
 }
 
-
-}  // namespace
-
+// The slab GEMV over a given workspace (vectors in launches of at most kMaxGemvVec). With the
+// fused norm, as many rows of x as ws->xn holds (xn_cap floats) are normalized into it first by
+// the RMS_NORM kernel (bitwise cpu::rms_norm), and the GEMV reads them: the result is bitwise
+// RMS_NORM then the same GEMV.
 template <bool PAIR>
-int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
+int launch_gemv_slab_in(uint32_t type, GemvSlabArgs a, Workspace* ws, uint64_t slots_cap, uint64_t counters_cap,
+                        uint64_t xn_cap, hipStream_t st) {
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
-    Workspace* ws = nullptr;
-    if (int rc = workspace_for(st, &ws)) return rc;
     // the pair's gate and up sums always meet in the workspace
     if (PAIR && !ws)
         return set_error(HALO_MI_E_MEMORY, "gate_up: this stream is being captured and has no workspace yet "
                                            "(make one call on it before capturing)");
-    if (PAIR && slabs > kCounters) return set_error(HALO_MI_E_UNSUPPORTED, "gate_up: %u rows exceed the workspace", a.rows);
+    if (PAIR && slabs > counters_cap) return set_error(HALO_MI_E_UNSUPPORTED, "gate_up: %u rows exceed the workspace", a.rows);
+    uint32_t per_norm = 0;  // vectors normalized at a time (a multiple of kMaxGemvVec)
+    if (a.norm_w) {
+        if (!ws || !ws->xn)
+            return set_error(HALO_MI_E_MEMORY, "gemv: the fused norm needs this stream's workspace (make one call on it "
+                                               "before capturing)");
+        per_norm = (uint32_t)std::min<uint64_t>(xn_cap / a.cols / kMaxGemvVec * kMaxGemvVec, 1u << 30);
+        if (per_norm == 0)
+            return set_error(HALO_MI_E_UNSUPPORTED, "gemv: cols %u too large for the fused norm's buffer (%llu floats)", a.cols,
+                             (unsigned long long)xn_cap);
+    }
     const uint32_t total = a.n_vec;
     for (uint32_t t0 = 0; t0 < total; t0 += kMaxGemvVec) {
         GemvSlabArgs c = a;
         c.n_vec = std::min(kMaxGemvVec, total - t0);
         c.x = a.x + (uint64_t)t0 * a.x_stride;
+        if (a.norm_w) {
+            const uint32_t k = t0 % per_norm;  // this chunk's row in the normalized block
+            if (k == 0) {
+                const uint32_t nb = std::min(per_norm, total - t0);
+                if (int rc = launch_rms_norm(c.x, a.x_stride, a.norm_w, ws->xn, a.cols, nb, a.cols, a.norm_eps, st))
+                    return rc;
+            }
+            c.x = ws->xn + (uint64_t)k * a.cols;
+            c.x_stride = a.cols;
+            c.norm_w = nullptr;
+        }
         c.y = a.y ? a.y + (uint64_t)t0 * a.y_stride : nullptr;
         if (a.parts) c.parts = a.parts + (uint64_t)t0 * slabs;
         int rc;
         switch (type) {
-            case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, ws, st); break;
-            case kQ8_0: rc = launch_gemv_slab_nv<kQ8_0, PAIR>(c, slabs, ws, st); break;
-            case kQ4_K: rc = launch_gemv_slab_nv<kQ4_K, PAIR>(c, slabs, ws, st); break;
-            case kQ5_K: rc = launch_gemv_slab_nv<kQ5_K, PAIR>(c, slabs, ws, st); break;
-            case kIQ4_XS: rc = launch_gemv_slab_nv<kIQ4_XS, PAIR>(c, slabs, ws, st); break;
-            default: rc = launch_gemv_slab_nv<kQ6_K, PAIR>(c, slabs, ws, st); break;
+            case kQ4_0: rc = launch_gemv_slab_nv<kQ4_0, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
+            case kQ8_0: rc = launch_gemv_slab_nv<kQ8_0, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
+            case kQ4_K: rc = launch_gemv_slab_nv<kQ4_K, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
+            case kQ5_K: rc = launch_gemv_slab_nv<kQ5_K, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
+            case kIQ4_XS: rc = launch_gemv_slab_nv<kIQ4_XS, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
+            default: rc = launch_gemv_slab_nv<kQ6_K, PAIR>(c, slabs, ws, slots_cap, counters_cap, st); break;
         }
         if (rc) return rc;
     }
     return HALO_MI_OK;
 }
 
+}  // namespace
+
+template <bool PAIR>
+int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
+    Workspace* ws = nullptr;
+    if (int rc = workspace_for(st, &ws)) return rc;
+    return launch_gemv_slab_in<PAIR>(type, a, ws, kSlots, kCounters, kNormFloats, st);
+}
+
 template int launch_gemv_slab<false>(uint32_t, GemvSlabArgs, hipStream_t);
 template int launch_gemv_slab<true>(uint32_t, GemvSlabArgs, hipStream_t);
+
+}  // namespace halo_mi
+
+namespace halo_mi {
 
 int launch_gemv_gguf_ref(uint32_t type, const uint8_t* w, uint64_t w_stride, const float* x, uint64_t x_stride, float* y,
                          uint64_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_vec, hipStream_t st) {

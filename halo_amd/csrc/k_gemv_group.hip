@@ -3,10 +3,10 @@
 // The reference issues them one by one (Qwen35::Impl::gemv, src/models/qwen35.cpp:486-498), so
 // each small projection pays a whole launch's ramp and drain.
 //
-// k_gemv_mx_group<TA, TB, NV, NORM>: the workgroups of segment s are the range
-// [wg_end[s - 1], wg_end[s]) of the grid; each runs the one-group kernel body of its segment's
-// weight type (TA or TB). All segments share the K split (so the workgroup size), x, n_vec and
-// the fused norm; their slabs take consecutive places in the workspace's counters and words.
+// k_gemv_mx_group<TA, TB, NV>: the workgroups of segment s are the range [wg_end[s - 1],
+// wg_end[s]) of the grid; each runs the one-group kernel body of its segment's weight type (TA or
+// TB). All segments share the K split (so the workgroup size), x and n_vec; their slabs take
+// consecutive places in the workspace's counters and words.
 #include "gemv_device.h"
 
 namespace halo_mi {
@@ -26,32 +26,32 @@ constexpr uint32_t group_max_threads() {
     return std::min(mx_max_threads<TA, NV, true>(), mx_max_threads<TB, NV, true>());
 }
 
-template <uint32_t TA, uint32_t TB, int NV, bool NORM>
+template <uint32_t TA, uint32_t TB, int NV>
 __global__ __launch_bounds__((group_max_threads<TA, TB, NV>())) void k_gemv_mx_group(GemvGroupArgs g) {
     uint32_t s = 0;
     while (s + 1 < g.n && blockIdx.x >= g.wg_end[s]) ++s;
     const uint32_t bid = blockIdx.x - (s ? g.wg_end[s - 1] : 0u);
     if (g.type[s] == TA) {
-        gemv_mx_body<TA, NV, false, true, NORM>(g.seg[s], bid);
+        gemv_mx_body<TA, NV, false, true>(g.seg[s], bid);
     } else {
-        if constexpr (TB != TA) gemv_mx_body<TB, NV, false, true, NORM>(g.seg[s], bid);
+        if constexpr (TB != TA) gemv_mx_body<TB, NV, false, true>(g.seg[s], bid);
     }
 }
 
 constexpr uint32_t kTypes[6] = {kQ4_0, kQ8_0, kQ4_K, kQ5_K, kQ6_K, kIQ4_XS};
 
-template <int NV, bool NORM, int IA, int IB>
+template <int NV, int IA, int IB>
 bool launch_pair(uint32_t ta, uint32_t tb, const GemvGroupArgs& g, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
     constexpr uint32_t TA = kTypes[IA], TB = kTypes[IB];
     if (ta != TA || tb != TB) return false;
-    hipLaunchKernelGGL((k_gemv_mx_group<TA, TB, NV, NORM>), grid, block, lds, st, g);
+    hipLaunchKernelGGL((k_gemv_mx_group<TA, TB, NV>), grid, block, lds, st, g);
     return true;
 }
 
 // (ta, tb) with ta's index <= tb's in kTypes
-template <int NV, bool NORM>
+template <int NV>
 bool launch_types(uint32_t ta, uint32_t tb, const GemvGroupArgs& g, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
-#define HALO_MI_PAIR(A, B) launch_pair<NV, NORM, A, B>(ta, tb, g, grid, block, lds, st)
+#define HALO_MI_PAIR(A, B) launch_pair<NV, A, B>(ta, tb, g, grid, block, lds, st)
     return HALO_MI_PAIR(0, 0) || HALO_MI_PAIR(0, 1) || HALO_MI_PAIR(0, 2) || HALO_MI_PAIR(0, 3) || HALO_MI_PAIR(0, 4) ||
            HALO_MI_PAIR(0, 5) || HALO_MI_PAIR(1, 1) || HALO_MI_PAIR(1, 2) || HALO_MI_PAIR(1, 3) || HALO_MI_PAIR(1, 4) ||
            HALO_MI_PAIR(1, 5) || HALO_MI_PAIR(2, 2) || HALO_MI_PAIR(2, 3) || HALO_MI_PAIR(2, 4) || HALO_MI_PAIR(2, 5) ||
@@ -88,7 +88,7 @@ uint32_t group_waves(uint32_t ta, uint32_t tb) {
 
 template <int NV>
 int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, const float* x, uint64_t x_stride,
-                    uint32_t cols, const float* norm_w, float eps, Workspace* ws, hipStream_t st) {
+                    uint32_t cols, Workspace* ws, hipStream_t st) {
     const uint32_t S = cols / kSlot, ngrp = (S + 7) / 8;
     uint64_t slabs = 0;
     for (uint32_t i = 0; i < n; ++i) slabs += (segs[i].rows + kSlabRows - 1) / kSlabRows;
@@ -114,8 +114,6 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         a.ks = ks;
         a.slots = ws->slots;
         a.counters = ws->counters;
-        a.norm_w = norm_w;
-        a.norm_eps = eps;
         a.slab0 = slab0;
         a.status = ws->status;
         apply_test_hooks(a);
@@ -126,15 +124,16 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         g.wg_end[i] = wg;
     }
     for (uint32_t i = 0; i < n; ++i) g.seg[i].wg_total = wg;
-    const size_t lds = mx_lds_bytes<NV>(gwg, norm_w != nullptr);
-    const bool ok = norm_w ? launch_types<NV, true>(ta, tb, g, dim3(wg), dim3(64 * gwg), lds, st)
-                           : launch_types<NV, false>(ta, tb, g, dim3(wg), dim3(64 * gwg), lds, st);
-    if (!ok) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: no kernel for types %u and %u", ta, tb);
+    if (!launch_types<NV>(ta, tb, g, dim3(wg), dim3(64 * gwg), mx_lds_bytes<NV>(gwg), st))
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: no kernel for types %u and %u", ta, tb);
     return hip_status(hipGetLastError(), "gemv_group launch");
 }
 
 }  // namespace
 
+// With the fused norm, blocks of x rows are normalized into the workspace first by the RMS_NORM
+// kernel (bitwise cpu::rms_norm) and the group reads them: the result is bitwise RMS_NORM then
+// the same group.
 int launch_gemv_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t x_stride, uint32_t cols, uint32_t n_vec,
                       const float* norm_w, float eps, hipStream_t st) {
     Workspace* ws = nullptr;
@@ -149,29 +148,44 @@ int launch_gemv_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t
         for (uint32_t k = 0; k < nt; ++k) seen |= types[k] == segs[i].type;
         if (!seen) types[nt++] = segs[i].type;
     }
-    for (uint32_t k0 = 0; k0 < nt; k0 += 2) {
-        uint32_t ta = types[k0], tb = k0 + 1 < nt ? types[k0 + 1] : types[k0];
-        if (type_index(ta) > type_index(tb)) std::swap(ta, tb);
-        GroupSeg part[HALO_MI_GEMV_GROUP_MAX];
-        uint32_t np = 0;
-        for (uint32_t i = 0; i < n; ++i)
-            if (segs[i].type == ta || segs[i].type == tb) part[np++] = segs[i];
-        for (uint32_t t0 = 0; t0 < n_vec; t0 += kMaxGemvVec) {
-            const uint32_t nv = std::min(kMaxGemvVec, n_vec - t0);
-            GroupSeg chunk[HALO_MI_GEMV_GROUP_MAX];
-            for (uint32_t i = 0; i < np; ++i) {
-                chunk[i] = part[i];
-                chunk[i].y = part[i].y + (uint64_t)t0 * part[i].y_stride;
+    uint32_t per = n_vec;  // vectors per normalized block
+    if (norm_w) {
+        per = (uint32_t)std::min<uint64_t>(kNormFloats / cols / kMaxGemvVec * kMaxGemvVec, n_vec);
+        if (per == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: cols %u too large for the fused norm's buffer", cols);
+    }
+    for (uint32_t b0 = 0; b0 < n_vec; b0 += per) {
+        const uint32_t nb = std::min(per, n_vec - b0);
+        const float* xb = x + (uint64_t)b0 * x_stride;
+        uint64_t xbs = x_stride;
+        if (norm_w) {
+            if (int rc = launch_rms_norm(xb, x_stride, norm_w, ws->xn, cols, nb, cols, eps, st)) return rc;
+            xb = ws->xn;
+            xbs = cols;
+        }
+        for (uint32_t k0 = 0; k0 < nt; k0 += 2) {
+            uint32_t ta = types[k0], tb = k0 + 1 < nt ? types[k0 + 1] : types[k0];
+            if (type_index(ta) > type_index(tb)) std::swap(ta, tb);
+            GroupSeg part[HALO_MI_GEMV_GROUP_MAX];
+            uint32_t np = 0;
+            for (uint32_t i = 0; i < n; ++i)
+                if (segs[i].type == ta || segs[i].type == tb) part[np++] = segs[i];
+            for (uint32_t t0 = 0; t0 < nb; t0 += kMaxGemvVec) {
+                const uint32_t nv = std::min(kMaxGemvVec, nb - t0);
+                GroupSeg chunk[HALO_MI_GEMV_GROUP_MAX];
+                for (uint32_t i = 0; i < np; ++i) {
+                    chunk[i] = part[i];
+                    chunk[i].y = part[i].y + (uint64_t)(b0 + t0) * part[i].y_stride;
+                }
+                const float* xc = xb + (uint64_t)t0 * xbs;
+                int rc;
+                switch (nv) {
+                    case 1: rc = launch_group_nv<1>(chunk, np, ta, tb, xc, xbs, cols, ws, st); break;
+                    case 2: rc = launch_group_nv<2>(chunk, np, ta, tb, xc, xbs, cols, ws, st); break;
+                    case 3: rc = launch_group_nv<3>(chunk, np, ta, tb, xc, xbs, cols, ws, st); break;
+                    default: rc = launch_group_nv<4>(chunk, np, ta, tb, xc, xbs, cols, ws, st); break;
+                }
+                if (rc) return rc;
             }
-            const float* xc = x + (uint64_t)t0 * x_stride;
-            int rc;
-            switch (nv) {
-                case 1: rc = launch_group_nv<1>(chunk, np, ta, tb, xc, x_stride, cols, norm_w, eps, ws, st); break;
-                case 2: rc = launch_group_nv<2>(chunk, np, ta, tb, xc, x_stride, cols, norm_w, eps, ws, st); break;
-                case 3: rc = launch_group_nv<3>(chunk, np, ta, tb, xc, x_stride, cols, norm_w, eps, ws, st); break;
-                default: rc = launch_group_nv<4>(chunk, np, ta, tb, xc, x_stride, cols, norm_w, eps, ws, st); break;
-            }
-            if (rc) return rc;
         }
     }
     return HALO_MI_OK;

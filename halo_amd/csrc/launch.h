@@ -43,10 +43,9 @@ struct GemvSlabArgs {
     // at or past valid_rows (when not 0) are not ranked, but a NaN in them still counts
     ArgPart* parts = nullptr;
     uint32_t valid_rows = 0;
-    // Fused input norm: y = W (rms_norm(x) * norm_w) when norm_w is set. Each workgroup
-    // multiplies its x slots by norm_w and sums the squares of the raw x it loaded; the sums
-    // meet in the fix-up (slot words after the partials: [slabs][chunks][NV]) and the finishing
-    // workgroup scales the row sums by 1 / sqrt(sum / cols + norm_eps).
+    // Fused input norm: y = W (rms_norm(x) * norm_w) when norm_w is set. The launcher normalizes
+    // x into the workspace first (the RMS_NORM kernel, bitwise cpu::rms_norm); the kernels see
+    // only the normalized rows.
     const float* norm_w = nullptr;
     float norm_eps = 0.0f;
     // Workspace indexing in a grouped launch (k_gemv_mx_group): this matrix's first slab among
@@ -129,6 +128,10 @@ uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes);
 // Common checks for the x / y operands of a gemv-shaped call.
 int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, uint64_t y_stride, uint32_t rows,
              uint32_t cols, uint32_t n_vec);
+
+// The checks halo_mi_gemv makes on a SLAB-layout call, bar the variant id: shapes, strides,
+// alignment, overlap and the fused norm's operand. xs / ys receive the resolved strides (floats).
+int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t* xs, uint64_t* ys);
 
 // ---- launchers (arguments already validated; they return a status) ---------------------------
 // k_dequant.hip

@@ -122,10 +122,10 @@ enum {
  *        - GGUF reference variant: x is normalized first exactly as cpu::rms_norm, so y is
  *          bitwise rms_norm then matmul;
  *        - bf16 GEMM variants: the same normalized x, rounded to bf16 while it is staged;
- *        - SLAB GEMV (2, 4, 6 and the GEMV legs of the auto variants): fused into the kernel,
- *          no extra launch: each workgroup computes 1 / sqrt(dot(x, x) / cols + eps) in
- *          cpu::detail::dot's order and builds (x * inv) * norm_w, exactly rms_norm's output, so
- *          y is bitwise halo_mi_rms_norm then the same variant without the norm, at any n_vec.
+ *        - SLAB GEMV (2, 6 and the GEMV legs of the auto variants): x is normalized into the
+ *          stream's workspace by the RMS_NORM kernel, then the GEMV runs on it.
+ *      So y is bitwise halo_mi_rms_norm then the same variant without the norm, at any n_vec
+ *      (the reference's Limits::max_fused_norm_cols contract, backend.h:236-242).
  *      norm_w must not overlap y.
  */
 typedef struct halo_mi_gemv_params {
