@@ -28,6 +28,7 @@ from ._lib import (  # noqa: F401
     gate_up_swiglu,
     gemv,
     gemv_group,
+    gemv_noalloc,
     get_rows,
     lib,
     lm_head,

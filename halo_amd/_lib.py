@@ -184,6 +184,7 @@ _U32, _U64, _VP, _INT = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_void_p, ctype
 SIGNATURES = {
     "halo_mi_last_error": (ctypes.c_char_p, []),
     "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
+    "halo_mi_gemv_noalloc": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
     "halo_mi_gemv_group": (_INT, [ctypes.POINTER(_GemvGroupParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
     "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
@@ -324,6 +325,14 @@ def gemv(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, layout: int = Lay
     p = _GemvParams(int(t), int(layout), _ptr(w), int(w_stride), _ptr(x), int(x_stride), _ptr(y), int(y_stride),
                     int(rows), int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
     _check(lib().halo_mi_gemv(ctypes.byref(p), _stream(stream)))
+
+
+def gemv_noalloc(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, x_stride: int = 0, y_stride: int = 0,
+                 variant: int = Variant.DEFAULT, norm_w=None, norm_eps: float = 1e-6, stream=None) -> None:
+    """halo_mi_gemv_noalloc: the SLAB GEMV over the library's device-resident scratch (no allocation)."""
+    p = _GemvParams(int(t), int(Layout.SLAB), _ptr(w), 0, _ptr(x), int(x_stride), _ptr(y), int(y_stride), int(rows),
+                    int(cols), int(n_vec), int(variant), _ptr(norm_w), float(norm_eps))
+    _check(lib().halo_mi_gemv_noalloc(ctypes.byref(p), _stream(stream)))
 
 
 def gemv_group(segs, x, cols: int, n_vec: int, *, x_stride: int = 0, norm_w=None, norm_eps: float = 1e-6,

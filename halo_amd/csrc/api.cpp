@@ -586,6 +586,11 @@ int halo_mi_stream_check(void* stream) {
     auto st = static_cast<hipStream_t>(stream);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "stream_check: hipGetDevice failed");
+    uint32_t na_word = 0;
+    if (int rc = noalloc_status_take(st, &na_word)) return rc;
+    if (na_word != 0)
+        return set_error(HALO_MI_E_DEVICE, "stream_check: a split-K reduction of halo_mi_gemv_noalloc gave up waiting for "
+                                           "partial sums (status 0x%x); outputs written since the last check hold NaN", na_word);
     Workspace w;
     {
         std::lock_guard<std::mutex> lock(g_ws_mu);

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "gemv_device.h"
 
@@ -72,7 +73,7 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
 
 // slots_cap / counters_cap: the split-K words and slab counters the workspace holds. The split is
 // always chosen for the allocated workspace's capacity (kSlots, kCounters), so a smaller workspace
-// gives the same bits or refuses the shape.
+// (halo_mi_gemv_noalloc's scratch) gives the same bits or refuses the shape.
 template <uint32_t T, int NV, bool PAIR>
 int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t slots_cap, uint64_t counters_cap,
                        hipStream_t st) {
@@ -184,7 +185,103 @@ int launch_gemv_slab(uint32_t type, GemvSlabArgs a, hipStream_t st) {
 template int launch_gemv_slab<false>(uint32_t, GemvSlabArgs, hipStream_t);
 template int launch_gemv_slab<true>(uint32_t, GemvSlabArgs, hipStream_t);
 
+// ---- halo_mi_gemv_noalloc: the slab GEMV over a device-resident scratch array ---------------
+// Layout of `scratch`: the status word (256 B), the slab counters, the split-K words. Its size is
+// fixed at build time; every GPU the library runs on holds its own copy until the process ends.
+constexpr uint64_t kNaStatusBytes = 256;
+constexpr uint64_t kNaCounters = 1ull << 16;   // slabs: 4 Mi rows
+constexpr uint64_t kNaSlots = 1ull << 20;      // split-K words: 8 MiB
+constexpr uint64_t kNaNormFloats = 1ull << 18;  // normalized x rows of the fused norm: 1 MiB
+constexpr uint64_t kNaSlotsOff = kNaStatusBytes + kNaCounters * sizeof(uint32_t);
+constexpr uint64_t kNaNormOff = kNaSlotsOff + kNaSlots * sizeof(uint64_t);
+constexpr uint64_t kNaBytes = kNaNormOff + kNaNormFloats * sizeof(float);
+static_assert(kNaSlotsOff % 256 == 0 && kNaNormOff % 256 == 0, "scratch regions 256-byte aligned");
+
 }  // namespace halo_mi
+
+static __device__ __align__(256) unsigned char scratch[halo_mi::kNaBytes];
+
+namespace halo_mi {
+namespace {
+
+constexpr int kNaMaxDevices = 64;
+std::mutex g_na_mu;
+unsigned char* g_na_ptr[kNaMaxDevices];  // the device address of `scratch` on each device, once set up
+
+// The device's scratch address: hipGetSymbolAddress once per device (with that device current);
+// the array's host-side name is never used as a device address.
+int noalloc_scratch(int dev, unsigned char** out) {
+    std::lock_guard<std::mutex> lock(g_na_mu);
+    if (dev < 0 || dev >= kNaMaxDevices) return set_error(HALO_MI_E_DEVICE, "gemv_noalloc: device %d out of range", dev);
+    if (!g_na_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(HALO_MI_E_DEVICE, "gemv_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        g_na_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    *out = g_na_ptr[dev];
+    return HALO_MI_OK;
+}
+
+}  // namespace
+
+int noalloc_status_take(hipStream_t st, uint32_t* word) {
+    *word = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNaMaxDevices) return HALO_MI_OK;
+    unsigned char* base;
+    {
+        std::lock_guard<std::mutex> lock(g_na_mu);
+        base = g_na_ptr[dev];
+    }
+    if (!base) return HALO_MI_OK;  // never used on this device
+    uint32_t* status = reinterpret_cast<uint32_t*>(base);
+    if (int rc = hip_status(hipMemcpyAsync(word, status, sizeof(uint32_t), hipMemcpyDeviceToHost, st), "stream_check"))
+        return rc;
+    if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
+    if (*word == 0) return HALO_MI_OK;
+    // start again clean: the words and counters of a reduction that gave up are in an unknown state
+    if (launch_fill_u32(status, 1, 0u, st) || launch_fill_u32(reinterpret_cast<uint32_t*>(base + kNaStatusBytes), kNaCounters, 0u, st) ||
+        launch_fill_u32(reinterpret_cast<uint32_t*>(base + kNaSlotsOff), 2 * kNaSlots, 0u, st))
+        return set_error(HALO_MI_E_DEVICE, "stream_check: clearing the no-alloc scratch failed");
+    return hip_status(hipStreamSynchronize(st), "stream_check");
+}
+
+}  // namespace halo_mi
+
+extern "C" int halo_mi_gemv_noalloc(const halo_mi_gemv_params* p, void* stream) {
+    using namespace halo_mi;
+    clear_error();
+    const char* op = "MATMUL";
+    if (!p) return set_error(HALO_MI_E_KERNEL, "gemv_noalloc: null params");
+    if (p->variant > HALO_MI_GEMV_VARIANT_LAST)
+        return set_error(HALO_MI_E_CONFIG, "%s: unknown kernel variant id %u", op, p->variant);
+    uint64_t xs = 0, ys = 0;
+    if (int rc = check_gemv_slab_call(p, op, &xs, &ys)) return rc;
+    if (p->n_vec == 0 || p->rows == 0) return HALO_MI_OK;
+    const uint32_t v = p->variant;
+    const bool gemv_leg = v == HALO_MI_GEMV_SLAB || v == HALO_MI_GEMV_SLAB_VALU ||
+                          ((v == HALO_MI_GEMV_DEFAULT || v == HALO_MI_GEMV_SLAB_AUTO) && p->n_vec <= 8);
+    if (!gemv_leg)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv_noalloc: variant %u at n_vec %u runs the GEMM, whose staging does not "
+                                                "fit the scratch (the slab GEMV variants 0/4 up to 8 vectors, 2 and 6 only)",
+                         v, p->n_vec);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv_noalloc: hipGetDevice failed");
+    unsigned char* base = nullptr;
+    if (int rc = noalloc_scratch(dev, &base)) return rc;
+    Workspace ws;
+    ws.status = reinterpret_cast<uint32_t*>(base);
+    ws.counters = reinterpret_cast<uint32_t*>(base + kNaStatusBytes);
+    ws.slots = reinterpret_cast<uint64_t*>(base + kNaSlotsOff);
+    ws.xn = reinterpret_cast<float*>(base + kNaNormOff);
+    GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
+    a.norm_w = p->norm_w;
+    a.norm_eps = p->norm_eps;
+    a.valu = v == HALO_MI_GEMV_SLAB_VALU;
+    return launch_gemv_slab_in<false>(p->type, a, &ws, kNaSlots, kNaCounters, kNaNormFloats, static_cast<hipStream_t>(stream));
+}
 
 namespace halo_mi {
 

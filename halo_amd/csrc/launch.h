@@ -129,6 +129,10 @@ uint64_t extent(uint64_t rows, uint64_t stride, uint64_t row_bytes);
 int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, uint64_t y_stride, uint32_t rows,
              uint32_t cols, uint32_t n_vec);
 
+// The no-alloc scratch's status word on the current device (0 when halo_mi_gemv_noalloc never ran
+// here), read on st and cleared with the scratch's words and counters when set.
+int noalloc_status_take(hipStream_t st, uint32_t* word);
+
 // The checks halo_mi_gemv makes on a SLAB-layout call, bar the variant id: shapes, strides,
 // alignment, overlap and the fused norm's operand. xs / ys receive the resolved strides (floats).
 int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t* xs, uint64_t* ys);

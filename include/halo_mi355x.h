@@ -148,6 +148,21 @@ typedef struct halo_mi_gemv_params {
 int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
 
 /*
+ * halo_mi_gemv without any allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same operands, checks and results as halo_mi_gemv (bitwise) for the
+ * SLAB GEMV variants: 2 and 6 at any n_vec, 0 and 4 up to 8 vectors; other variants return
+ * HALO_MI_E_UNSUPPORTED. The split-K words, slab counters and status word live in a fixed
+ * device array of this library (about 8.3 MiB per GPU, held until the process ends), not in a
+ * per-stream workspace: a shape whose split needs more than 65536 slabs of counters or 2^20
+ * words (e.g. the 17408 x 5120 headline needs 2^18.1) returns HALO_MI_E_UNSUPPORTED. Every call
+ * on one GPU shares that array, so calls that overlap in time on one GPU (other streams, other
+ * threads) race and give wrong results: order them. halo_mi_stream_check also reports this
+ * array's status word.
+ */
+int halo_mi_gemv_noalloc(const halo_mi_gemv_params* p, void* stream);
+
+/*
  * Grouped GEMV: several SLAB matrices that share x, in one launch per pair of weight types,
  * e.g. a layer's q, k and v projections (Q4_K q and k, Q6_K v) after the same input norm. The
  * reference issues them one by one on one stream (Qwen35::Impl::gemv,
