@@ -53,33 +53,67 @@ def device_copies(hl, torch, t, wq, rows, cols, min_bytes=MALL_BYTES):
     return copies
 
 
-def time_graph(torch, launch, n_copies, steps, warmup):
-    """Capture one pass over the weight copies into a HIP graph, replay it; returns
-    (ms per step from events around the whole timed region, total steps run)."""
+WINDOW_MS = 150.0  # wall time each extra workload is replayed for, split into SAMPLES samples
+SAMPLES = 5
+
+
+def _warm_graph(torch, launch, indices):
+    """Eager warm-up over the weight copies on a side stream (also loads the code objects and
+    creates the library's per-stream workspace there), then a HIP graph of launch(i) for i in
+    indices captured on that stream."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for i in range(n_copies):  # eager warm-up (also loads the code objects)
+        for i in sorted(set(indices)):
             launch(i)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    # capture on the warmed-up stream: the library's per-stream split-K workspace exists there
     with torch.cuda.graph(g, stream=s):
-        for i in range(n_copies):
+        for i in indices:
             launch(i)
-    reps_w = max(1, math.ceil(warmup / n_copies))
-    reps = max(1, math.ceil(steps / n_copies))
-    for _ in range(reps_w):
-        g.replay()
+    return g
+
+
+def time_exact(torch, launch, n_copies, steps, warmup):
+    """The headline's timing: `warmup` untimed steps, then exactly `steps` steps (one launch
+    over the next weight copy each) in one graph replay, bracketed by a synchronize and HIP
+    events on the stream the graph replays on. Returns ms per step."""
+    gk = _warm_graph(torch, launch, [i % n_copies for i in range(steps)])
+    if warmup > 0:
+        gw = _warm_graph(torch, launch, [i % n_copies for i in range(warmup)])
+        gw.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        g.replay()
+    gk.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * n_copies), reps * n_copies
+    return e0.elapsed_time(e1) / steps
+
+
+def time_window(torch, launch, n_copies, min_ms=WINDOW_MS, samples=SAMPLES):
+    """Replays of one pass over the weight copies for at least min_ms of GPU time, in `samples`
+    samples bracketed by HIP events; returns (median ms per step, the samples, steps timed)."""
+    g = _warm_graph(torch, launch, list(range(n_copies)))
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    pass_ms = max(e0.elapsed_time(e1), 1e-3)
+    reps = max(1, math.ceil(min_ms / samples / pass_ms))
+    per = []
+    for _ in range(samples):
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) / (reps * n_copies))
+    return sorted(per)[len(per) // 2], per, samples * reps * n_copies
 
 
 def time_per_launch(torch, launch, n_copies, iters):
@@ -97,7 +131,7 @@ def time_per_launch(torch, launch, n_copies, iters):
     return ts[len(ts) // 2], sum(ts) / len(ts)
 
 
-def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0, norm=False):
+def gemv_case(hl, torch, t, rows, cols, m, seed, steps=0, warmup=0, outliers=0.0, norm=False, exact_steps=False):
     wq = make_weights(hl, t, rows, cols, seed, outliers)
     copies = device_copies(hl, torch, t, wq, rows, cols)
     x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
@@ -107,16 +141,20 @@ def gemv_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0, no
     def launch(i):
         hl.gemv(t, copies[i], x, y, rows, cols, m, norm_w=nw)
 
-    ms, n = time_graph(torch, launch, len(copies), steps, warmup)
-    med, mean = time_per_launch(torch, launch, len(copies), 200)
+    ms, samples, n = time_window(torch, launch, len(copies))
+    r = {"ms": ms, "samples_us": [round(v * 1e3, 3) for v in samples], "steps": n}
+    if exact_steps:  # the headline: exactly `steps` timed steps after `warmup`
+        r["exact_ms"] = time_exact(torch, launch, len(copies), steps, warmup)
+        med, mean = time_per_launch(torch, launch, len(copies), 200)
+        r.update(event_median_us=med * 1e3, event_mean_us=mean * 1e3)
     algo = len(wq) + 4 * m * cols + 4 * m * rows + (4 * cols if norm else 0)
     del copies
     torch.cuda.empty_cache()
-    return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9,
-            "event_median_us": med * 1e3, "event_mean_us": mean * 1e3, "wq": wq, "x": x.cpu().numpy()}
+    r.update(bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, wq=wq, x=x.cpu().numpy())
+    return r
 
 
-def lm_head_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0):
+def lm_head_case(hl, torch, t, rows, cols, m, seed, outliers=0.0):
     """The LM head (halo_mi_lm_head): the gemv over the vocabulary with the argmax fused into
     its epilogue, the logits not kept. Same bytes as the plain GEMV plus 12 B of result words
     per vector."""
@@ -128,14 +166,14 @@ def lm_head_case(hl, torch, t, rows, cols, m, seed, steps, warmup, outliers=0.0)
     def launch(i):
         hl.lm_head(t, copies[i], x, res, rows, cols, m)
 
-    ms, n = time_graph(torch, launch, len(copies), steps, warmup)
+    ms, samples, n = time_window(torch, launch, len(copies))
     algo = len(wq) + 4 * m * cols + 12 * m
     del copies
     torch.cuda.empty_cache()
     return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9}
 
 
-def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
+def gemm_case(hl, torch, t, rows, cols, m, seed):
     wg = make_weights(hl, t, rows, cols, seed)
     wu = make_weights(hl, t, rows, cols, seed + 40)
     cg = device_copies(hl, torch, t, wg, rows, cols, MALL_BYTES // 2)
@@ -147,13 +185,12 @@ def gemm_case(hl, torch, t, rows, cols, m, seed, steps, warmup):
     def launch(i):
         hl.gate_up_swiglu(t, cg[i], cu[i], x, out, rows, cols, m)
 
-    ms, nsteps = time_graph(torch, launch, n, steps, warmup)
-    med, mean = time_per_launch(torch, launch, n, 50)
+    ms, samples, nsteps = time_window(torch, launch, n)
     flops = 4.0 * m * rows * cols
     del cg, cu
     torch.cuda.empty_cache()
     return {"flops": flops, "ms": ms, "steps": nsteps, "tflops": flops / (ms * 1e-3) / 1e12,
-            "event_median_us": med * 1e3, "event_mean_us": mean * 1e3}
+            "samples_us": [round(v * 1e3, 3) for v in samples]}
 
 
 # name -> (kind, type, rows, cols, M, seed): the workloads of the extra figures
@@ -180,6 +217,10 @@ WORKLOADS = {
     "hybrid_layer_m1_qk_fused": ("layer_qk", None, 0, 0, 1, 5),
     "hybrid_layer_m1_qkv_group": ("layer_qkv", None, 0, 0, 1, 5),
     "hybrid_layer_m1_qk_fused_qkv_group": ("layer_qk_qkv", None, 0, 0, 1, 5),
+    "q6k_gemv_151936x5120_m1": ("gemv", "Q6_K", 151936, 5120, 1, 3),
+    "q4k_gate_up_swiglu_m4": ("gemm", "Q4_K", 17408, 5120, 4, 4),
+    "read_floor_50MB": ("read_floor", None, 17408 * 2880, 0, 0, 0),
+    "read_floor_73MB": ("read_floor", None, 5120 * 14280, 0, 0, 0),
 }
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_17408x5120_m1_traffic.json")
@@ -282,7 +323,7 @@ def model_upload_case(hl, torch, layers=64, seed=9):
     return {"bytes": nbytes, "s": sec, "gbs": nbytes / sec / 1e9, "tensors": len(tensors)}
 
 
-def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False, group_qkv=False):
+def layer_case(hl, torch, m, seed=5, fuse_qk=False, group_qkv=False):
     """All matmuls of one config-5 layer as one step (the fused gate/up pair is one call), over
     enough copies of the layer's weights that the MALL cannot serve repeats. fuse_qk: q and k
     (both Q4_K, 5120 columns) as one row-fused 7168-row matrix, one GEMV instead of two (the
@@ -321,7 +362,7 @@ def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False, group_qkv=Fal
         if group:
             hl.gemv_group(group, xs[5120], 5120, m)
 
-    ms, nsteps = time_graph(torch, launch, n_copies, steps, warmup)
+    ms, samples, nsteps = time_window(torch, launch, n_copies)
     algo = sum(wb + 4 * m * cols + 4 * m * rows for name, _, rows, cols, _, wb in mats)
     flops = sum((4.0 if name == "gate_up" else 2.0) * m * rows * cols for name, _, rows, cols, _, _ in mats)
     del copies, mats
@@ -329,12 +370,38 @@ def layer_case(hl, torch, m, steps, warmup, seed=5, fuse_qk=False, group_qkv=Fal
     return {"ms": ms, "steps": nsteps, "bytes": algo, "gbs": algo / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
-def cpu_baseline(t, wq, rows, cols, x, seconds):
-    """The oracle (a C port of the reference's cpu::matmul) on all host cores, best of N
-    after one warm-up, for about `seconds` of CPU time."""
+def read_floor_case(hl, torch, nbytes, min_bytes=MALL_BYTES):
+    """The single-launch read floor of `nbytes`: halo_mi_stream_read (a plain read-only stream,
+    nothing computed or written) over enough copies that the MALL cannot serve repeats; the
+    best of a sweep of launch shapes (workgroups per CU x loads in flight per thread)."""
+    n = max(2, math.ceil(min_bytes / nbytes) + 1)
+    bufs = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(n)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(cus * 64 * 256, dtype=torch.int32, device="cuda")
+    best = None
+    for per_cu in (4, 8, 16, 32):
+        for unroll in (4, 8, 16):
+            wgs = cus * per_cu
+
+            def launch(i, wgs=wgs, unroll=unroll):
+                hl.stream_read(bufs[i], nbytes, wgs, unroll, sink)
+
+            ms, _, _ = time_window(torch, launch, n, min_ms=30.0, samples=3)
+            if best is None or ms < best[0]:
+                best = (ms, per_cu, unroll, launch)
+    ms, samples, _ = time_window(torch, best[3], n)
+    del bufs
+    torch.cuda.empty_cache()
+    return {"us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9, "workgroups_per_cu": best[1], "loads_in_flight": best[2],
+            "samples_us": [round(v * 1e3, 3) for v in samples]}
+
+
+def cpu_baseline(t, wq, rows, cols, x, seconds, threads=0):
+    """The oracle (a C port of the reference's cpu::matmul) on `threads` host cores (0 = all),
+    best of N after one warm-up, for about `seconds` of CPU time."""
     from oracle import oracle as orc
 
-    threads = orc.default_threads()
+    threads = threads or orc.default_threads()
     orc.matmul(t, wq, rows, cols, x, threads=threads)
     best, spent, runs = float("inf"), 0.0, 0
     while runs == 0 or (spent < seconds and runs < 1000):
@@ -352,8 +419,8 @@ def cpu_baseline(t, wq, rows, cols, x, seconds):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=2000, help="timed steps of the headline workload (exactly)")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed steps before them")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--only", choices=sorted(WORKLOADS),
@@ -365,6 +432,9 @@ def main() -> int:
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1).",
               file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         return 2
 
     import torch
@@ -388,62 +458,69 @@ def main() -> int:
             print(json.dumps({"workload": args.only, "GB": round(r["bytes"] / 1e9, 2), "s": round(r["s"], 3),
                               "GB/s": round(r["gbs"], 1)}), flush=True)
             return 0
+        if kind == "read_floor":
+            r = read_floor_case(hl, torch, rows)
+            print(json.dumps({"workload": args.only, **{k: v for k, v in r.items()}}), flush=True)
+            return 0
         if kind.startswith("layer"):
-            r = layer_case(hl, torch, m, args.steps, args.warmup, seed, fuse_qk="qk" in kind.split("_")[1:],
-                           group_qkv=kind.endswith("qkv"))
+            r = layer_case(hl, torch, m, seed, fuse_qk="qk" in kind.split("_")[1:], group_qkv=kind.endswith("qkv"))
             print(json.dumps({"workload": args.only, "us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                               "TFLOP/s": round(r["tflops"], 2)}), flush=True)
             return 0
         t = int(getattr(hl.DType, t))
         if kind == "head":
-            r = lm_head_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup, outliers=0.01)
+            r = lm_head_case(hl, torch, t, rows, cols, m, seed, outliers=0.01)
             print(json.dumps({"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}), flush=True)
             return 0
         if kind in ("gemv", "gemv_norm"):
-            r = gemv_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup, norm=kind == "gemv_norm")
+            r = gemv_case(hl, torch, t, rows, cols, m, seed, norm=kind == "gemv_norm",
+                          outliers=0.01 if rows == 151936 else 0.0)
             out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
         else:
-            r = gemm_case(hl, torch, t, rows, cols, m, seed, args.steps, args.warmup)
+            r = gemm_case(hl, torch, t, rows, cols, m, seed)
             out = {"workload": args.only, "TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 3)}
         print(json.dumps(out), flush=True)
         return 0
 
-    log("config 2: Q4_K GEMV 17408x5120 M=1")
-    head = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps, args.warmup)
-    # average launch duration: HIP events around the timed region (graph replays on the current
-    # stream, the stream the kernels are launched on) divided by the launches in it
-    kernel_us = head["ms"] * 1e3
+    def gemv_fig(r):
+        return {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+
+    def gemm_fig(r):
+        return {"TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 2),
+                "frac_bf16_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)}
+
+    log(f"config 2: Q4_K GEMV 17408x5120 M=1 ({args.warmup} warm-up steps, {args.steps} timed steps)")
+    head = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps, args.warmup, exact_steps=True)
+    # average launch duration: HIP events around the timed region, on the stream the graph (and
+    # so the kernels) runs on, divided by the launches in it
+    kernel_us = head["exact_ms"] * 1e3
     achieved = head["bytes"] / (kernel_us * 1e-6) / 1e9
     traffic = measured_traffic()
-    extra = {}
+    log("read floor: one read-only stream over the headline's 50 MB of weights")
+    floor = read_floor_case(hl, torch, hl.slab_bytes(Q4_K, 17408, 5120))
+    extra = {"q4k_gemv_17408x5120_m1_window": {**gemv_fig(head), "samples_us": head["samples_us"],
+                                                "note": f"median of {SAMPLES} samples over {WINDOW_MS:.0f} ms of replays"}}
     if not args.no_extra:
+        log("read floor of the 73 MB Q6_K 5120x17408 matrix")
+        r = read_floor_case(hl, torch, hl.slab_bytes(Q6_K, 5120, 17408))
+        extra["read_floor_73MB"] = {"us": round(r["us"], 2), "GB/s": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("config 2 with the fused RMS-norm prologue (norm_w): Q4_K GEMV M=1")
-        r = gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, args.steps // 2, args.warmup, norm=True)
-        extra["q4k_gemv_norm_17408x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
-                                                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        extra["q4k_gemv_norm_17408x5120_m1"] = gemv_fig(gemv_case(hl, torch, Q4_K, 17408, 5120, 1, 2, norm=True))
         log("config 2: Q4_K GEMV M=4")
-        r = gemv_case(hl, torch, Q4_K, 17408, 5120, 4, 2, args.steps // 2, args.warmup)
-        extra["q4k_gemv_17408x5120_m4"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}
-        for m in (1, 4):
+        extra["q4k_gemv_17408x5120_m4"] = gemv_fig(gemv_case(hl, torch, Q4_K, 17408, 5120, 4, 2))
+        for m in (1, 2, 3, 4):
             log(f"config 3: Q6_K GEMV 5120x17408 M={m}")
-            r = gemv_case(hl, torch, Q6_K, 5120, 17408, m, 3, args.steps // 2, args.warmup)
-            extra[f"q6k_gemv_5120x17408_m{m}"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
-                                                  "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
-        log("config 3: Q6_K GEMV 151936x5120 M=1 (1% outlier columns)")
-        r = gemv_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
-        extra["q6k_gemv_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
-                                            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            extra[f"q6k_gemv_5120x17408_m{m}"] = gemv_fig(gemv_case(hl, torch, Q6_K, 5120, 17408, m, 3))
+        for m in (1, 4):
+            log(f"config 3: Q6_K GEMV 151936x5120 M={m} (1% outlier columns)")
+            extra[f"q6k_gemv_151936x5120_m{m}"] = gemv_fig(gemv_case(hl, torch, Q6_K, 151936, 5120, m, 3, outliers=0.01))
         for name, tn, seed in (("q5k", "Q5_K", 6), ("iq4xs", "IQ4_XS", 7)):
             log(f"the UD pack's other formats: {tn} GEMV 17408x5120 M=1 and gate/up M=512")
             tt = int(getattr(hl.DType, tn))
-            r = gemv_case(hl, torch, tt, 17408, 5120, 1, seed, args.steps // 2, args.warmup)
-            extra[f"{name}_gemv_17408x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
-                                                   "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
-            r = gemm_case(hl, torch, tt, 17408, 5120, 512, seed, max(20, args.steps // 20), 5)
-            extra[f"{name}_gate_up_swiglu_m512"] = {"TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 2),
-                                                    "frac_bf16_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)}
+            extra[f"{name}_gemv_17408x5120_m1"] = gemv_fig(gemv_case(hl, torch, tt, 17408, 5120, 1, seed))
+            extra[f"{name}_gate_up_swiglu_m512"] = gemm_fig(gemm_case(hl, torch, tt, 17408, 5120, 512, seed))
         log("LM head: Q6_K 151936x5120 M=1 with the fused argmax (no logits kept)")
-        r = lm_head_case(hl, torch, Q6_K, 151936, 5120, 1, 3, max(50, args.steps // 20), 10, outliers=0.01)
+        r = lm_head_case(hl, torch, Q6_K, 151936, 5120, 1, 3, outliers=0.01)
         extra["q6k_lm_head_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("part (c): GGUF -> SLAB repack and host upload, Q4_K 17408x5120")
@@ -461,50 +538,57 @@ def main() -> int:
                                                     "GB/s": round(r["gbs"], 1), "tensors": r["tensors"],
                                                     "note": "host -> SLAB, PCIe-inclusive, one upload_tensors call"}
         log("config 1 on the GPU: Q4_0 GEMV 4096x4096 M=1")
-        r = gemv_case(hl, torch, int(hl.DType.Q4_0), 4096, 4096, 1, 0, args.steps // 2, args.warmup)
-        extra["q4_0_gemv_4096x4096_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2)}
+        extra["q4_0_gemv_4096x4096_m1"] = gemv_fig(gemv_case(hl, torch, int(hl.DType.Q4_0), 4096, 4096, 1, 0))
         for m in (1, 4, 512):
             log(f"config 5: hybrid layer (8 matmuls, 269 MB of weights) M={m}")
-            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5)
+            r = layer_case(hl, torch, m)
             extra[f"hybrid_layer_m{m}"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                            "TFLOP/s": round(r["tflops"], 2)}
         for m in (1, 4):
             log(f"config 5 with q|k row-fused (one GEMV for both) M={m}")
-            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5, fuse_qk=True)
+            r = layer_case(hl, torch, m, fuse_qk=True)
             extra[f"hybrid_layer_m{m}_qk_fused"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                                     "TFLOP/s": round(r["tflops"], 2)}
             log(f"config 5 with q, k, v in one grouped launch M={m}")
-            r = layer_case(hl, torch, m, max(20, args.steps // 20), 5, group_qkv=True)
+            r = layer_case(hl, torch, m, group_qkv=True)
             extra[f"hybrid_layer_m{m}_qkv_group"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                                      "TFLOP/s": round(r["tflops"], 2)}
-        for m in (2, 8, 64, 512):
+        for m in (2, 4, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
-            r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, max(20, args.steps // 20), 5)
-            extra[f"q4k_gate_up_swiglu_m{m}"] = {"TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 2),
-                                                 "frac_bf16_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4)}
-    log("cpu baseline")
+            r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4)
+            extra[f"q4k_gate_up_swiglu_m{m}"] = {**gemm_fig(r), "weights_GB/s": round(2 * 17408 * 2880 / (r["ms"] * 1e-3) / 1e9, 1),
+                                                 "samples_us": r["samples_us"]}
+    log("cpu baseline (all host threads, then one)")
     cpu = cpu_baseline(Q4_K, head["wq"], 17408, 5120, head["x"], args.cpu_seconds)
+    one = cpu_baseline(Q4_K, head["wq"], 17408, 5120, head["x"], min(5.0, args.cpu_seconds), threads=1)
+    cpu["one_thread"] = {k: one[k] for k in ("value", "unit", "cores", "ms_per_call", "sample")}
 
     line = {
         "metric": "Q4_K GEMV GB/s at M=1 (17408x5120, BASELINE config 2)",
-        "value": round(head["gbs"], 1),
+        "value": round(achieved, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": head["steps"],
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["ms"], 6),
+        "ms_per_step": round(head["exact_ms"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic: N(0,0.02) weights quantized to Q4_K by this repo's quantizer, N(0,1) x",
         "config": {"workload": "Q4_K dequant-GEMV 17408x5120 M=1 (config 2), SLAB layout, "
-                               f"{math.ceil(MALL_BYTES / (17408 * 2880)) + 1}+ rotating weight copies"},
+                               f"{math.ceil(MALL_BYTES / (17408 * 2880)) + 1} rotating weight copies"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["traffic_bytes"] if traffic else None,
                      "algorithmic_bytes": head["bytes"], "kernel_us": round(kernel_us, 3),
+                     "kernel_us_window": round(head["ms"] * 1e3, 3),
                      "kernel_us_eager_median": round(head["event_median_us"], 3),
+                     "floor_us": round(floor["us"], 3), "floor_GB/s": round(floor["gbs"], 1),
+                     "frac_of_floor": round(floor["us"] / kernel_us, 4),
+                     "floor_note": "one read-only stream over the same 50 MB (halo_mi_stream_read, best of "
+                                   f"a sweep: {floor['workgroups_per_cu']} workgroups per CU, "
+                                   f"{floor['loads_in_flight']} 16 B loads in flight per thread)",
                      "traffic_source": traffic["source"] if traffic else None},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -39,6 +39,7 @@ from ._lib import (  # noqa: F401
     row_bytes,
     slab_bytes,
     stream_check,
+    stream_read,
     stream_release,
     swiglu,
     unpack_slab,

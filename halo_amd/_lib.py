@@ -193,6 +193,7 @@ SIGNATURES = {
     "halo_mi_dequant_rows": (_INT, [_U32, _U32, _VP, _U64, _U32, _U32, _U32, _U32, _VP, _U64, _VP]),
     "halo_mi_get_rows": (_INT, [ctypes.POINTER(_GetRowsParams), _VP]),
     "halo_mi_rms_norm": (_INT, [_VP, _U64, _VP, _VP, _U64, _U32, _U32, ctypes.c_float, _VP]),
+    "halo_mi_stream_read": (_INT, [_VP, _U64, _U32, _U32, _VP, _VP]),
     "halo_mi_stream_check": (_INT, [_VP]),
     "halo_mi_stream_release": (_INT, [_VP]),
     "halo_mi_test_splitk_timeout": (_INT, [_U32, _INT]),
@@ -399,6 +400,11 @@ def rms_norm(x, w, out, rows: int, cols: int, *, eps: float = 1e-6, x_stride: in
     """RMS_NORM (halo_mi_rms_norm), bitwise cpu::rms_norm."""
     _check(lib().halo_mi_rms_norm(_ptr(x), int(x_stride), _ptr(w), _ptr(out), int(out_stride), int(rows), int(cols),
                                   float(eps), _stream(stream)))
+
+
+def stream_read(p, nbytes: int, workgroups: int, unroll: int, sink, stream=None) -> None:
+    """One read-only stream over nbytes at p (halo_mi_stream_read): the read floor's kernel."""
+    _check(lib().halo_mi_stream_read(_ptr(p), int(nbytes), int(workgroups), int(unroll), _ptr(sink), _stream(stream)))
 
 
 def stream_check(stream=None) -> None:

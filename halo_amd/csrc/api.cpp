@@ -581,6 +581,19 @@ int halo_mi_unpack_slab(uint32_t type, const void* src, uint32_t rows, uint32_t 
                               static_cast<hipStream_t>(stream));
 }
 
+int halo_mi_stream_read(const void* p, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t* sink, void* stream) {
+    clear_error();
+    const char* op = "stream_read";
+    if (bytes == 0) return HALO_MI_OK;
+    if (!p || !sink) return set_error(HALO_MI_E_KERNEL, "%s: empty operand", op);
+    if (bytes % 16 || reinterpret_cast<uintptr_t>(p) % 16 || reinterpret_cast<uintptr_t>(sink) % 4)
+        return set_error(HALO_MI_E_KERNEL, "%s: p and bytes must be 16-byte aligned, sink 4-byte aligned", op);
+    if (workgroups == 0 || workgroups > (1u << 20)) return set_error(HALO_MI_E_KERNEL, "%s: workgroups out of range", op);
+    if (unroll != 2 && unroll != 4 && unroll != 8 && unroll != 16)
+        return set_error(HALO_MI_E_KERNEL, "%s: unroll must be 2, 4, 8 or 16", op);
+    return launch_stream_read(p, bytes, workgroups, unroll, sink, static_cast<hipStream_t>(stream));
+}
+
 int halo_mi_stream_check(void* stream) {
     clear_error();
     auto st = static_cast<hipStream_t>(stream);

@@ -221,7 +221,41 @@ __global__ void k_fill_u32(uint32_t* p, uint64_t n, uint32_t v) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
 }
+
+// The read floor: a plain stream over n16 16-byte words, U nontemporal loads in flight per
+// thread, grid-stride. The words are folded into one value per thread that is stored only if it
+// equals a constant no input here produces, so the loads stay and nothing is written.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int U>
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4_t* __restrict__ p, uint64_t n16, uint32_t* sink) {
+    uint32_t acc = 0;
+    const uint64_t stride = (uint64_t)gridDim.x * 256 * U;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 * U + threadIdx.x; i < n16; i += stride) {
+        u32x4_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t k = i + (uint64_t)u * 256;
+            v[u] = __builtin_nontemporal_load(p + (k < n16 ? k : n16 - 1));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9E3779B9u) sink[blockIdx.x * 256 + threadIdx.x] = acc;
+}
 }  // namespace
+
+int launch_stream_read(const void* p, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t* sink, hipStream_t st) {
+    const uint64_t n16 = bytes / 16;
+    const dim3 grid(workgroups), block(256);
+    switch (unroll) {
+        case 2: hipLaunchKernelGGL(k_stream_read<2>, grid, block, 0, st, static_cast<const u32x4_t*>(p), n16, sink); break;
+        case 4: hipLaunchKernelGGL(k_stream_read<4>, grid, block, 0, st, static_cast<const u32x4_t*>(p), n16, sink); break;
+        case 8: hipLaunchKernelGGL(k_stream_read<8>, grid, block, 0, st, static_cast<const u32x4_t*>(p), n16, sink); break;
+        default: hipLaunchKernelGGL(k_stream_read<16>, grid, block, 0, st, static_cast<const u32x4_t*>(p), n16, sink); break;
+    }
+    return hip_status(hipGetLastError(), "stream_read launch");
+}
 
 int launch_repack_slab(uint32_t type, const uint8_t* src, uint64_t src_stride, uint32_t rows, uint32_t cols,
                        uint8_t* dst, hipStream_t st) {

@@ -154,6 +154,8 @@ int launch_dequant_slab(uint32_t type, const uint8_t* w, uint32_t cols, uint32_t
                         uint32_t* status = nullptr);
 constexpr uint32_t kStatusBadIndex = 8u;  // the reference's status bit for a GET_ROWS id outside the table
 int launch_fill_u32(uint32_t* p, uint64_t n, uint32_t v, hipStream_t st);
+// The read floor's stream (halo_mi_stream_read): unroll 2, 4, 8 or 16 loads of 16 B per thread.
+int launch_stream_read(const void* p, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t* sink, hipStream_t st);
 // k_gemv.hip
 int launch_gemv_gguf_ref(uint32_t type, const uint8_t* w, uint64_t w_stride, const float* x, uint64_t x_stride, float* y,
                          uint64_t y_stride, uint32_t rows, uint32_t cols, uint32_t n_vec, hipStream_t st);

@@ -365,6 +365,15 @@ int halo_mi_stream_release(void* stream);
  */
 int halo_mi_test_splitk_timeout(uint32_t spin_limit, int force);
 
+/*
+ * Measurement helper, no reference counterpart: one launch that only reads `bytes` of device
+ * memory at p (16 B per load, `unroll` loads of 2/4/8/16 in flight per thread, `workgroups` of
+ * 256 threads, grid-stride) and writes nothing (sink, workgroups * 256 uint32, is written only
+ * for an input no benchmark uses). Its duration is the single-launch read floor of that many
+ * bytes, the bound a GEMV streaming the same bytes cannot beat.
+ */
+int halo_mi_stream_read(const void* p, uint64_t bytes, uint32_t workgroups, uint32_t unroll, uint32_t* sink, void* stream);
+
 /* ---- geometry ------------------------------------------------------------------------------ */
 /* Bytes of one GGUF row of `cols` elements (src/tensor/quant.cpp:411-418); 0 on error. */
 uint64_t halo_mi_row_bytes(uint32_t type, uint32_t cols);

@@ -241,3 +241,21 @@ def test_stream_release_frees_and_reallocates(hl, oracle, dev):
     assert isclose_bits(outs[0], outs[1])
     ref = oracle.matmul(t, dense, rows, cols, x)
     assert np.all(np.abs(outs[0].astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dense, rows, cols, x))
+
+
+def test_stream_read_reads_and_writes_nothing(hl, dev):
+    """The read-floor helper: runs for every unroll, leaves its sink untouched, refuses misaligned
+    operands."""
+    import torch
+
+    buf = torch.arange(1 << 20, dtype=torch.int32, device=dev)
+    sink = torch.zeros(64 * 256, dtype=torch.int32, device=dev)
+    for unroll in (2, 4, 8, 16):
+        hl.stream_read(buf, buf.numel() * 4, 64, unroll, sink)
+    assert int(host(sink).astype(np.int64).sum()) == 0
+    with pytest.raises(hl.HaloError) as e:
+        hl.stream_read(buf.data_ptr() + 4, 1024, 64, 4, sink)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:
+        hl.stream_read(buf, 1024, 64, 3, sink)
+    assert e.value.code == hl.ErrorCode.Kernel
