@@ -131,7 +131,8 @@ def time_per_launch(torch, launch, n_copies, iters):
     return ts[len(ts) // 2], sum(ts) / len(ts)
 
 
-def gemv_case(hl, torch, t, rows, cols, m, seed, steps=0, warmup=0, outliers=0.0, norm=False, exact_steps=False):
+def gemv_case(hl, torch, t, rows, cols, m, seed, steps=0, warmup=0, outliers=0.0, norm=False, exact_steps=False,
+              variant=0):
     wq = make_weights(hl, t, rows, cols, seed, outliers)
     copies = device_copies(hl, torch, t, wq, rows, cols)
     x = torch.from_numpy(hl.fill_normal(seed + 1000, m * cols).reshape(m, cols)).to("cuda")
@@ -139,7 +140,7 @@ def gemv_case(hl, torch, t, rows, cols, m, seed, steps=0, warmup=0, outliers=0.0
     nw = torch.from_numpy(hl.fill_normal(seed + 2000, cols, 1.0, 0.1)).to("cuda") if norm else None
 
     def launch(i):
-        hl.gemv(t, copies[i], x, y, rows, cols, m, norm_w=nw)
+        hl.gemv(t, copies[i], x, y, rows, cols, m, norm_w=nw, variant=variant)
 
     ms, samples, n = time_window(torch, launch, len(copies))
     r = {"ms": ms, "samples_us": [round(v * 1e3, 3) for v in samples], "steps": n}
@@ -173,7 +174,7 @@ def lm_head_case(hl, torch, t, rows, cols, m, seed, outliers=0.0):
     return {"bytes": algo, "ms": ms, "steps": n, "gbs": algo / (ms * 1e-3) / 1e9}
 
 
-def gemm_case(hl, torch, t, rows, cols, m, seed):
+def gemm_case(hl, torch, t, rows, cols, m, seed, variant=0):
     wg = make_weights(hl, t, rows, cols, seed)
     wu = make_weights(hl, t, rows, cols, seed + 40)
     cg = device_copies(hl, torch, t, wg, rows, cols, MALL_BYTES // 2)
@@ -183,7 +184,7 @@ def gemm_case(hl, torch, t, rows, cols, m, seed):
     out = torch.empty((m, rows), dtype=torch.float32, device="cuda")
 
     def launch(i):
-        hl.gate_up_swiglu(t, cg[i], cu[i], x, out, rows, cols, m)
+        hl.gate_up_swiglu(t, cg[i], cu[i], x, out, rows, cols, m, variant=variant)
 
     ms, samples, nsteps = time_window(torch, launch, n)
     flops = 4.0 * m * rows * cols
@@ -425,6 +426,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--only", choices=sorted(WORKLOADS),
                     help="run one workload alone and print its figures (for profiling); no headline line")
+    ap.add_argument("--variant", type=int, default=0, help="kernel variant id for --only gemv / gemm workloads "
+                    "(halo_mi_gemv_params::variant; 0 = the default choice)")
+    ap.add_argument("--rows", type=int, default=0, help="--only gemv / gemm workloads: rows instead of the workload's")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the benchmark, copy a buffer of this many MiB 4 times (a plain copy kernel of "
                          "known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -468,16 +472,17 @@ def main() -> int:
                               "TFLOP/s": round(r["tflops"], 2)}), flush=True)
             return 0
         t = int(getattr(hl.DType, t))
+        rows = args.rows or rows
         if kind == "head":
             r = lm_head_case(hl, torch, t, rows, cols, m, seed, outliers=0.01)
             print(json.dumps({"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}), flush=True)
             return 0
         if kind in ("gemv", "gemv_norm"):
             r = gemv_case(hl, torch, t, rows, cols, m, seed, norm=kind == "gemv_norm",
-                          outliers=0.01 if rows == 151936 else 0.0)
+                          outliers=0.01 if rows == 151936 else 0.0, variant=args.variant)
             out = {"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}
         else:
-            r = gemm_case(hl, torch, t, rows, cols, m, seed)
+            r = gemm_case(hl, torch, t, rows, cols, m, seed, variant=args.variant)
             out = {"workload": args.only, "TFLOP/s": round(r["tflops"], 2), "us": round(r["ms"] * 1e3, 3)}
         print(json.dumps(out), flush=True)
         return 0

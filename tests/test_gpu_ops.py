@@ -151,7 +151,8 @@ def test_gemv_slab_valu_rejects_other_formats(hl, dev):
                 variant=hl.Variant.SLAB_GEMV_VALU)
     assert e.value.code == hl.ErrorCode.Unsupported
     with pytest.raises(hl.HaloError) as e:  # past the last id
-        hl.gemv(t, slab, to_dev(np.ones((1, cols), np.float32), dev), y, rows, cols, 1, variant=8)
+        hl.gemv(t, slab, to_dev(np.ones((1, cols), np.float32), dev), y, rows, cols, 1,
+                variant=max(int(v) for v in hl.Variant) + 1)
     assert e.value.code == hl.ErrorCode.Config
 
 
