@@ -212,6 +212,7 @@ WORKLOADS = {
     "upload_q4k_17408x5120": ("upload", "Q4_K", 17408, 5120, 0, 2),
     "model_upload_64_layers": ("model_upload", None, 0, 0, 64, 9),
     "q6k_lm_head_151936x5120_m1": ("head", "Q6_K", 151936, 5120, 1, 3),
+    "q6k_lm_head_248320x5120_m1": ("head", "Q6_K", 248320, 5120, 1, 8),
     "hybrid_layer_m1": ("layer", None, 0, 0, 1, 5),
     "hybrid_layer_m4": ("layer", None, 0, 0, 4, 5),
     "hybrid_layer_m512": ("layer", None, 0, 0, 512, 5),
@@ -527,6 +528,10 @@ def main() -> int:
         log("LM head: Q6_K 151936x5120 M=1 with the fused argmax (no logits kept)")
         r = lm_head_case(hl, torch, Q6_K, 151936, 5120, 1, 3, outliers=0.01)
         extra["q6k_lm_head_151936x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
+                                               "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("LM head at the model's own vocabulary: Q6_K 248320x5120 M=1 (1.04 GB), fused argmax")
+        r = lm_head_case(hl, torch, Q6_K, 248320, 5120, 1, 8, outliers=0.01)
+        extra["q6k_lm_head_248320x5120_m1"] = {"GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 2),
                                                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("part (c): GGUF -> SLAB repack and host upload, Q4_K 17408x5120")
         r = upload_case(hl, torch, Q4_K, 17408, 5120, 2)

@@ -21,11 +21,15 @@ class DType(enum.IntEnum):
     """ggml type ids (include/halo/tensor/dtype.h:18-49 of the reference)."""
 
     F32 = 0
+    F16 = 1
     Q4_0 = 2
     Q8_0 = 8
+    Q3_K = 11
     Q4_K = 12
     Q5_K = 13
     Q6_K = 14
+    IQ4_NL = 20
+    IQ3_S = 21
     IQ4_XS = 23
 
 
@@ -62,8 +66,9 @@ class HaloError(RuntimeError):
         super().__init__(f"{self.code.name.upper()}_ERROR: {message}")
 
 
-_BLOCK = {DType.F32: (1, 4), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q4_K: (256, 144),
-          DType.Q5_K: (256, 176), DType.Q6_K: (256, 210), DType.IQ4_XS: (256, 136)}
+_BLOCK = {DType.F32: (1, 4), DType.F16: (1, 2), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q3_K: (256, 110),
+          DType.Q4_K: (256, 144), DType.Q5_K: (256, 176), DType.Q6_K: (256, 210), DType.IQ4_NL: (32, 18),
+          DType.IQ3_S: (256, 110), DType.IQ4_XS: (256, 136)}
 
 
 def block_elems(t: int) -> int:

@@ -1,8 +1,8 @@
 // Device-side unpacking of GGUF blocks and SLAB slot records. Every weight value these
-// helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:79-90,
-// :143-151, :236-269, :271-299, :302-327, :330-347): all products in those expressions are
-// exact in fp32, and the one rounding step (Q4_K's and Q5_K's `- dmin * m`) is evaluated in the
-// same order.
+// helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:68-70,
+// :79-90, :143-151, :154-165, :196-233, :236-269, :271-299, :302-327, :330-347, :350-384): all
+// products in those expressions are exact in fp32, and the one rounding step (Q4_K's and
+// Q5_K's `- dmin * m`) is evaluated in the same order.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -88,6 +88,19 @@ __device__ __forceinline__ uint32_t iq4_lookup4(uint32_t q) {
     return __builtin_amdgcn_perm(hi, lo, ((q >> 1) & 0x04040404u) | 0x03020100u);
 }
 
+// ---- IQ3_S ----------------------------------------------------------------------------------
+// The GGUF IQ3_S codebook (ggml's iq3s_grid): entry g holds four magnitudes, byte j for
+// element j of a 4-element group.
+__device__ const uint32_t kIq3sGrid[512] = {
+#include "iq3s_grid.inc"
+};
+
+// Q3_K's 16 six-bit scales from the 12 packed bytes sb: scale i = nibble i / 8 of byte i % 8,
+// with bits 2 (i / 4) .. + 1 of byte 8 + i % 4 on top (quant.cpp:203-212's shuffle, per index).
+__device__ __forceinline__ int q3k_scale(const uint8_t* sb, uint32_t i) {
+    return (int)(((sb[i % 8] >> (4 * (i / 8))) & 15u) | (((sb[8 + i % 4] >> (2 * (i / 4))) & 3u) << 4));
+}
+
 // ---- per-element decode of a GGUF row (the reference variant; byte loads) -------------------
 // Same expressions as quant.cpp; contraction is off in every caller.
 __device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, uint32_t i) {
@@ -168,6 +181,37 @@ __device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, ui
             const int q = (int)(lo4 | (hi2 << 4)) - 32;
             const float sc = (float)(int8_t)blk[192 + 8 * n + l / 16 + 2 * k];
             return d * sc * (float)q;
+        }
+        case kF16:
+            return h2f(ld_u16(row + 2 * (uint64_t)i));
+        case kIQ4_NL: {
+            const uint8_t* blk = row + (i / 32) * 18;
+            const uint32_t e = i % 32;
+            const float d = h2f(ld_u16(blk));
+            const uint8_t qb = blk[2 + (e & 15)];
+            return d * (float)iq4_value(e < 16 ? (qb & 15u) : (qb >> 4));
+        }
+        case kQ3_K: {
+            // element e = 128 n + 32 j + l: code bits 2j..2j+1 of qs[32n + l] minus 4 unless bit
+            // 4n + j of hmask[l] is set; scale 8n + 2j + l / 16
+            const uint8_t* blk = row + (i / 256) * 110;
+            const uint32_t e = i % 256, n = e / 128, j = (e % 128) / 32, l = e % 32;
+            const float d_all = h2f(ld_u16(blk + 108));
+            const int q = (int)((blk[32 + 32 * n + l] >> (2 * j)) & 3u) - (((blk[l] >> (4 * n + j)) & 1u) ? 0 : 4);
+            const float dl = d_all * (float)(q3k_scale(blk + 96, 8 * n + 2 * j + l / 16) - 32);
+            return dl * (float)q;
+        }
+        case kIQ3_S: {
+            // sub-block b = e / 32: db = d (1 + 2 s); group k = (e % 32) / 4 takes codebook entry
+            // qs[8b + k] | (bit k of qh[b]) << 8; sign bit e % 8 of signs[4b + (e % 32) / 8]
+            const uint8_t* blk = row + (i / 256) * 110;
+            const uint32_t e = i % 256, b = e / 32, k = (e % 32) / 4;
+            const float d = h2f(ld_u16(blk));
+            const float db = d * (float)(1 + 2 * ((blk[106 + b / 2] >> (4 * (b % 2))) & 15u));
+            const uint32_t idx = blk[2 + 8 * b + k] | (((blk[66 + b] >> k) & 1u) << 8);
+            const float g = (float)((kIq3sGrid[idx] >> (8 * (e % 4))) & 0xFFu);
+            const float sgn = ((blk[74 + 4 * b + (e % 32) / 8] >> (e % 8)) & 1u) ? -1.0f : 1.0f;
+            return db * g * sgn;
         }
         default:
             return 0.0f;

@@ -1,12 +1,16 @@
 // Block geometry and the SLAB weight layout, shared by the host repack and the device kernels.
 //
-// GGUF block formats (ggml ids; geometry as src/tensor/dtype.cpp:22-34 of the reference):
+// GGUF block formats (ggml ids; geometry as src/tensor/dtype.cpp:20-44 of the reference):
+//   F16      1 weight  / 2 B
 //   Q4_0    32 weights / 18 B   { f16 d; u8 qs[16] }
+//   IQ4_NL  32 weights / 18 B   { f16 d; u8 qs[16] }            (codes index the IQ4_NL table)
 //   Q8_0    32 weights / 34 B   { f16 d; i8 qs[32] }
 //   Q4_K   256 weights / 144 B  { f16 d; f16 dmin; u8 scales[12]; u8 qs[128] }
 //   Q5_K   256 weights / 176 B  { f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128] }
 //   Q6_K   256 weights / 210 B  { u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d }
 //   IQ4_XS 256 weights / 136 B  { f16 d; u16 scales_h; u8 scales_l[4]; u8 qs[128] }
+//   Q3_K   256 weights / 110 B  { u8 hmask[32]; u8 qs[64]; u8 scales[12]; f16 d }
+//   IQ3_S  256 weights / 110 B  { f16 d; u8 qs[64]; u8 qh[8]; u8 signs[32]; u8 scales[4] }
 //
 // SLAB layout. Rows are grouped by 64 (one wave64, one row per lane). A row of K weights is
 // cut into S = K / 32 "slots" of 32 consecutive weights. Inside a slab every plane is stored
@@ -44,25 +48,30 @@
 
 namespace halo_mi {
 
-inline constexpr uint32_t kF32 = 0, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ4_XS = 23;
+inline constexpr uint32_t kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14,
+                          kIQ4_NL = 20, kIQ3_S = 21, kIQ4_XS = 23;
 inline constexpr uint32_t kSlabRows = 64;
 inline constexpr uint32_t kSlot = 32;  // weights per slot
 
+// Every type of the reference's HIP GEMV test matrix (tests/unit/hip/test_hip_gemv.cpp:217-218):
+// the GGUF layout takes all of them; is_quant() names those that also have a SLAB layout.
 HALO_HD constexpr uint32_t block_elems(uint32_t t) {
-    return t == kF32                                                           ? 1u
-           : (t == kQ4_0 || t == kQ8_0)                                        ? 32u
-           : (t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS) ? 256u
-                                                                               : 0u;
+    return (t == kF32 || t == kF16)                                                               ? 1u
+           : (t == kQ4_0 || t == kQ8_0 || t == kIQ4_NL)                                           ? 32u
+           : (t == kQ3_K || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS || t == kIQ3_S) ? 256u
+                                                                                                  : 0u;
 }
 HALO_HD constexpr uint32_t block_bytes(uint32_t t) {
-    return t == kF32      ? 4u
-           : t == kQ4_0   ? 18u
-           : t == kQ8_0   ? 34u
-           : t == kQ4_K   ? 144u
-           : t == kQ5_K   ? 176u
-           : t == kQ6_K   ? 210u
-           : t == kIQ4_XS ? 136u
-                          : 0u;
+    return t == kF32                      ? 4u
+           : t == kF16                    ? 2u
+           : (t == kQ4_0 || t == kIQ4_NL) ? 18u
+           : t == kQ8_0                   ? 34u
+           : (t == kQ3_K || t == kIQ3_S)  ? 110u
+           : t == kQ4_K                   ? 144u
+           : t == kQ5_K                   ? 176u
+           : t == kQ6_K                   ? 210u
+           : t == kIQ4_XS                 ? 136u
+                                          : 0u;
 }
 HALO_HD constexpr bool is_quant(uint32_t t) {
     return t == kQ4_0 || t == kQ8_0 || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS;

@@ -16,7 +16,10 @@
 #include <string.h>
 #include <unistd.h>
 
-enum { T_F32 = 0, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
+enum {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+    T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ4_XS = 23
+};
 
 /* ---- fp16 ------------------------------------------------------------------------------ */
 
@@ -51,9 +54,9 @@ static float f16_at(const uint8_t* p) { return oracle_fp16_to_fp32((uint16_t)(p[
 
 uint32_t oracle_block_elems(uint32_t type) {
     switch (type) {
-        case T_F32: return 1;
-        case T_Q4_0: case T_Q8_0: return 32;
-        case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: return 256;
+        case T_F32: case T_F16: return 1;
+        case T_Q4_0: case T_Q8_0: case T_IQ4_NL: return 32;
+        case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: case T_IQ3_S: return 256;
         default: return 0;
     }
 }
@@ -61,7 +64,9 @@ uint32_t oracle_block_elems(uint32_t type) {
 uint32_t oracle_block_bytes(uint32_t type) {
     switch (type) {
         case T_F32: return 4;
-        case T_Q4_0: return 18;
+        case T_F16: return 2;
+        case T_Q4_0: case T_IQ4_NL: return 18;
+        case T_Q3_K: case T_IQ3_S: return 110;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
         case T_Q5_K: return 176;
@@ -209,6 +214,70 @@ static void deq_q6_k(const uint8_t* blk, float* y, float* a, float* off) {
     }
 }
 
+/* quant.cpp:154-165. As Q4_0's nibble order (element j < 16: low nibble of qs[j]; j + 16:
+ * the high one), value d * fl(table[nibble]). */
+static void deq_iq4_nl(const uint8_t* blk, float* y, float* a, float* off) {
+    const float d = f16_at(blk);
+    for (int e = 0; e < 32; ++e) {
+        const uint8_t byte = blk[2 + (e & 15)];
+        const float v = d * (float)kIq4nl[e < 16 ? (byte & 0x0F) : (byte >> 4)];
+        if (y) y[e] = v;
+        if (a) { a[e] = v; off[e] = 128.0f * d; }
+    }
+}
+
+/* quant.cpp:196-233. Sixteen 6-bit scales packed in bytes 96..107: scale i takes nibble i / 8
+ * of byte i % 8 as its low 4 bits and bits 2 (i / 4) .. 2 (i / 4) + 1 of byte 8 + i % 4 as its
+ * top 2 (the reference's aux/kmask shuffle, written per index). Element e: half n = e / 128,
+ * shift pair j = (e % 128) / 32, l = e % 32; q = ((qs[32 n + l] >> 2 j) & 3) - 4 unless bit
+ * 4 n + j of hmask[l] is set; scale index 8 n + 2 j + l / 16; value (d * fl(sc - 32)) * fl(q). */
+static int q3k_scale(const uint8_t* sb, int i) {
+    return ((sb[i % 8] >> (4 * (i / 8))) & 0x0F) | (((sb[8 + i % 4] >> (2 * (i / 4))) & 3) << 4);
+}
+
+static void deq_q3_k(const uint8_t* blk, float* y, float* a, float* off) {
+    const float d_all = f16_at(blk + 108);
+    const uint8_t* hm = blk;
+    const uint8_t* qs = blk + 32;
+    const uint8_t* sb = blk + 96;
+    for (int e = 0; e < 256; ++e) {
+        const int n = e / 128, j = (e % 128) / 32, l = e % 32;
+        const int q = ((qs[32 * n + l] >> (2 * j)) & 3) - (((hm[l] >> (4 * n + j)) & 1) ? 0 : 4);
+        const float dl = d_all * (float)(q3k_scale(sb, 8 * n + 2 * j + l / 16) - 32);
+        const float v = dl * (float)q;
+        if (y) y[e] = v;
+        if (a) { a[e] = v; off[e] = 4.0f * dl; }
+    }
+}
+
+/* The IQ3_S codebook of the GGUF format (ggml's iq3s_grid; the reference's copy is
+ * src/tensor/ggml_tables.h:27-92), pinned against the reference's values by the tests. */
+static const uint32_t kIq3sGrid[512] = {
+#include "../halo_amd/csrc/iq3s_grid.inc"
+};
+
+/* quant.cpp:350-384. Sub-block b = e / 32 of 32 elements: multiplier db = d * fl(1 + 2 s) with s
+ * nibble b % 2 of scales[b / 2]; group k = (e % 32) / 4 of 4 elements takes codebook entry
+ * qs[8 b + k] | (bit k of qh[b]) << 8, element e its byte e % 4; the sign is bit e % 8 of
+ * signs[4 b + (e % 32) / 8] (set: -1). value (db * fl(byte)) * sign. */
+static void deq_iq3_s(const uint8_t* blk, float* y, float* a, float* off) {
+    const float d = f16_at(blk);
+    const uint8_t* qs = blk + 2;
+    const uint8_t* qh = blk + 66;
+    const uint8_t* signs = blk + 74;
+    const uint8_t* scales = blk + 106;
+    for (int e = 0; e < 256; ++e) {
+        const int b = e / 32, k = (e % 32) / 4;
+        const float db = d * (float)(1 + 2 * ((scales[b / 2] >> (4 * (b % 2))) & 0x0F));
+        const unsigned idx = qs[8 * b + k] | (((qh[b] >> k) & 1u) << 8);
+        const float g = (float)((kIq3sGrid[idx] >> (8 * (e % 4))) & 0xFFu);
+        const float sgn = ((signs[4 * b + (e % 32) / 8] >> (e % 8)) & 1) ? -1.0f : 1.0f;
+        const float v = db * g * sgn;
+        if (y) y[e] = v;
+        if (a) { a[e] = v; off[e] = 16.0f * db; }
+    }
+}
+
 static int dequant_blocks(uint32_t type, const uint8_t* src, float* dst, uint64_t nb) {
     const uint32_t bb = oracle_block_bytes(type), be = oracle_block_elems(type);
     for (uint64_t i = 0; i < nb; ++i) {
@@ -216,7 +285,11 @@ static int dequant_blocks(uint32_t type, const uint8_t* src, float* dst, uint64_
         float* y = dst + i * be;
         switch (type) {
             case T_F32: memcpy(y, blk, 4); break;
+            case T_F16: y[0] = f16_at(blk); break;
             case T_Q4_0: deq_q4_0(blk, y); break;
+            case T_IQ4_NL: deq_iq4_nl(blk, y, NULL, NULL); break;
+            case T_Q3_K: deq_q3_k(blk, y, NULL, NULL); break;
+            case T_IQ3_S: deq_iq3_s(blk, y, NULL, NULL); break;
             case T_Q8_0: deq_q8_0(blk, y); break;
             case T_Q4_K: deq_q4_k(blk, y, NULL, NULL); break;
             case T_Q5_K: deq_q5_k(blk, y, NULL, NULL); break;
@@ -274,6 +347,18 @@ int oracle_dequant_terms(uint32_t type, const uint8_t* src, float* a, float* b, 
                 break;
             case T_Q6_K:
                 deq_q6_k(blk, NULL, ab, ob);
+                for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
+                break;
+            case T_IQ4_NL:
+                deq_iq4_nl(blk, NULL, ab, ob);
+                for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
+                break;
+            case T_Q3_K:
+                deq_q3_k(blk, NULL, ab, ob);
+                for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
+                break;
+            case T_IQ3_S:
+                deq_iq3_s(blk, NULL, ab, ob);
                 for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
                 break;
             default: return ORACLE_EUNSUPPORTED;

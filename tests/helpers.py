@@ -6,10 +6,15 @@ import math
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, F32 = 2, 8, 12, 13, 14, 23, 0
+F16, Q3_K, IQ4_NL, IQ3_S = 1, 11, 20, 21
 QUANT_TYPES = (Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, IQ4_XS)
-NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K", IQ4_XS: "IQ4_XS"}
-BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210),
-         IQ4_XS: (256, 136)}
+SLAB_TYPES = QUANT_TYPES  # the types with a SLAB layout
+# the reference's HIP GEMV test matrix, in its order (tests/unit/hip/test_hip_gemv.cpp:217-218)
+ALL_TYPES = (Q4_K, Q5_K, Q6_K, Q8_0, F16, F32, IQ4_XS, IQ4_NL, Q3_K, IQ3_S, Q4_0)
+NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
+         IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144),
+         Q5_K: (256, 176), Q6_K: (256, 210), IQ4_NL: (32, 18), IQ3_S: (256, 110), IQ4_XS: (256, 136)}
 U = 2.0 ** -24  # fp32 unit roundoff
 
 
@@ -41,10 +46,17 @@ def make_weights(t: int, rows: int, cols: int, seed: int, stride_pad: int = 0, o
             vals[3 % cols] = np.float32(1e-40)  # one fp32 subnormal
             buf[row:row + 4 * cols] = vals.view(np.uint8)
             continue
+        if t == F16:
+            vals = rng.uniform(-1, 1, cols).astype(np.float16)
+            vals[3 % cols] = np.float16(3e-7)  # one fp16 subnormal
+            buf[row:row + 2 * cols] = vals.view(np.uint8)
+            continue
         for b in range(cols // be):
             sc = 2e-6 if b == 0 else rng.uniform(-0.05, 0.05)
-            if t in (Q4_0, Q8_0):
+            if t in (Q4_0, Q8_0, IQ4_NL, IQ3_S):
                 _put16(buf, row + bb * b, sc)
+            elif t == Q3_K:
+                _put16(buf, row + bb * b + 108, sc)
             elif t in (Q4_K, Q5_K):
                 _put16(buf, row + bb * b, 4e-6 if b == 0 else sc)
                 _put16(buf, row + bb * b + 2, abs(rng.uniform(-0.05, 0.05)))

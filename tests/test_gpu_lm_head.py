@@ -225,3 +225,41 @@ def test_baseline_q6_k_lm_head(hl, oracle, dev):
     if gap > 2 * tol.max():
         assert res[0, 0] == cpu[0, 0]
     assert abs(float(y[0, res[0, 0]]) - float(cpu_logits[0, cpu[0, 0]])) <= 2 * tol.max()
+
+
+@pytest.mark.parametrize("n_vec", [1, 4])
+def test_real_vocab_q6_k_lm_head(hl, oracle, dev, n_vec):
+    """The model's own vocabulary: the 248320 x 5120 Q6_K head (1.04 GB; process.md:662 of the
+    reference) at M = 1 and 4. Every logit against the CPU within the gemv bound; the fused
+    argmax without logits equals the one with them, and is the first maximum of the GPU's own
+    logits; the index agrees with the CPU's wherever the CPU's top-2 gap is decisive."""
+    import torch
+
+    t, rows, cols = Q6_K, 248320, 5120
+    say("real-vocabulary lm_head", rows, cols, n_vec)
+    key = ("real_vocab",)
+    if key not in _REAL:
+        wq = synth_matrix(hl, t, rows, cols, 8, outlier_cols=0.01)
+        _REAL.clear()
+        _REAL[key] = (wq, slab_of(hl, dev, t, wq, rows, cols))
+    wq, slab = _REAL[key]
+    x = hl.fill_normal(1800 + n_vec, n_vec * cols).reshape(n_vec, cols)
+    res_fused, _, _, _ = run_head(hl, dev, t, slab, x, rows, cols, logits=False)
+    res, y, _, _ = run_head(hl, dev, t, slab, x, rows, cols)
+    assert np.array_equal(res_fused, res), "the argmax changed with the logits kept"
+    ref = oracle.matmul(t, wq, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, wq, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    real-vocabulary head M={n_vec}: worst |d|/bound = {float(np.max(err / tol)):.4f}")
+    assert np.all(err <= tol)
+    for v in range(n_vec):
+        assert res[v].tolist() == [*first_max(y[v]), 0], f"vector {v}: not the first maximum of its own logits"
+        top2 = np.sort(ref[v])[-2:]
+        if top2[1] - top2[0] > 2 * tol[v].max():
+            assert res[v, 0] == int(np.argmax(ref[v])), f"vector {v}: decisive gap but a different index"
+    if n_vec == 4:
+        _REAL.clear()
+        torch.cuda.empty_cache()
+
+
+_REAL = {}

@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import (BLOCK, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
+from helpers import (ALL_TYPES, BLOCK, F16, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
                      gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 
 pytestmark = pytest.mark.gpu
@@ -134,12 +134,40 @@ def run_gemv(hl, dev, t, w, layout, x, rows, cols, variant, x_pad=0, y_pad=0, w_
     return y[:, :rows]
 
 
-@pytest.mark.parametrize("t", QUANT_TYPES + (F32,))
+def matrix_case(t, case):
+    """test_hip_gemv.cpp:219-227's two shapes for type t: plain types (F32, F16) take 100
+    columns in the first (a dot tail of 100 % 8) and a 4-byte row stride pad and offset in the
+    second; block types 512 columns, then a 3-byte pad and 1-byte offset."""
+    rows, cols, n_vec, pad, off, xp, yp = case
+    if t in (F32, F16):
+        cols = 100 if rows == 37 else cols
+        pad, off = (4, 4) if pad else (0, 0)
+    return rows, cols, n_vec, pad, off, xp, yp
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("case", CASES)
+def test_dequant_gguf_type_matrix_bitwise(hl, oracle, dev, t, case):
+    """GGUF-layout dequantization of every type of the reference's HIP test matrix is bitwise
+    tensor::dequantize_row, at an unaligned row stride and start."""
+    import torch
+
+    rows, cols, _, pad, off, _, _ = matrix_case(t, case)
+    say("dequant gguf", NAMES[t], rows, cols, pad, off)
+    buf, stride = make_weights(t, rows, cols, seed=300 + rows + t, stride_pad=pad, offset=off)
+    ref = oracle.dequantize_rows(t, buf[off:], rows, cols, stride)
+    wd = to_dev(buf, dev)
+    out = torch.full((rows, cols), SENTINEL, dtype=torch.float32, device=dev)
+    hl.dequant_rows(t, hl.Layout.GGUF, wd.data_ptr() + off, rows, cols, out, w_stride=stride)
+    assert isclose_bits(host(out), ref), "GGUF dequant differs from tensor::dequantize_row"
+
+
+@pytest.mark.parametrize("t", ALL_TYPES)
 @pytest.mark.parametrize("case", CASES)
 def test_gemv_gguf_ref_bitwise(hl, oracle, dev, t, case):
-    rows, cols, n_vec, pad, off, xp, yp = case
-    if t == F32:
-        cols, pad, off = 100, 4, 4  # dot tail (100 % 8) and 4-byte aligned rows
+    """The reference-order variant over GGUF rows is bitwise cpu::matmul for every type of the
+    matrix; on the GGUF layout the default variant is that kernel."""
+    rows, cols, n_vec, pad, off, xp, yp = matrix_case(t, case)
     say("gemv_gguf_ref", NAMES[t], rows, cols, n_vec)
     buf, stride = make_weights(t, rows, cols, seed=100 + t + rows, stride_pad=pad, offset=off)
     x = np.random.default_rng(1000 + t).uniform(-1, 1, (n_vec, cols)).astype(np.float32)
@@ -147,6 +175,26 @@ def test_gemv_gguf_ref_bitwise(hl, oracle, dev, t, case):
     wd = to_dev(buf, dev)
     y = run_gemv(hl, dev, t, wd.data_ptr() + off, hl.Layout.GGUF, x, rows, cols, hl.Variant.GGUF_REF, xp, yp, stride)
     assert isclose_bits(y, ref), "reference-order gemv is not bitwise cpu::matmul"
+    y0 = run_gemv(hl, dev, t, wd.data_ptr() + off, hl.Layout.GGUF, x, rows, cols, hl.Variant.DEFAULT, xp, yp, stride)
+    assert isclose_bits(y0, ref), "the GGUF layout's default variant is not the reference-order kernel"
+
+
+def test_f16_dequant_every_pattern(hl, oracle, dev):
+    """All 65536 fp16 patterns as one F16 row: bitwise the reference's widening for every
+    pattern that is not a NaN; a NaN stays a NaN of the same sign (the payload of a signalling
+    NaN may be quieted differently by the device conversion)."""
+    import torch
+
+    pats = np.arange(65536, dtype=np.uint16)
+    ref = oracle.dequantize_row(F16, pats.view(np.uint8), 65536)
+    out = torch.empty((1, 65536), dtype=torch.float32, device=dev)
+    hl.dequant_rows(F16, hl.Layout.GGUF, to_dev(pats.view(np.uint8), dev), 1, 65536, out)
+    y = host(out)[0]
+    nan = np.isnan(ref)
+    assert np.array_equal(y[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert np.all(np.isnan(y[nan])) and np.array_equal(np.signbit(y[nan]), np.signbit(ref[nan]))
+    print(f"    NaN patterns with the reference's exact bits: {int(np.sum(y[nan].view(np.uint32) == ref[nan].view(np.uint32)))}"
+          f" of {int(nan.sum())}")
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)

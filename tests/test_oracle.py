@@ -407,6 +407,226 @@ def isbits(a, b) -> bool:
                           np.ascontiguousarray(b, np.float32).view(np.uint32))
 
 
+# ---- the canonical pack's remaining types: F16, IQ4_NL, Q3_K, IQ3_S ---------------------------
+# (quant.cpp:68-70, :154-165, :196-233, :350-384; the reference's HIP test matrix,
+# tests/unit/hip/test_hip_gemv.cpp:217-218)
+
+F16, Q3_K, IQ4_NL, IQ3_S = 1, 11, 20, 21
+_TABLES = json.loads((Path(__file__).resolve().parent / "golden" / "iq3s_tables.json").read_text())
+IQ3S_GRID = _TABLES["iq3s_grid"]
+KMASK = _TABLES["kmask_iq2xs"]
+_INC = Path(__file__).resolve().parents[1] / "halo_amd" / "csrc" / "iq3s_grid.inc"
+
+
+def test_iq3s_codebook_include_is_the_reference_table():
+    """The one codebook source of the device decoder and the oracle equals the reference's
+    iq3s_grid entry for entry (fixture read from src/tensor/ggml_tables.h as data), and the sign
+    masks are the single bits 1 << j."""
+    import re
+
+    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-fA-F]{8})u", _INC.read_text())]
+    assert vals == IQ3S_GRID
+    assert KMASK == [1 << j for j in range(8)]
+
+
+def test_new_type_geometry(oracle):
+    """dtype.cpp:20, :29, :39-40 and test_dequant.cpp:41's literal."""
+    assert oracle.row_bytes(IQ4_NL, 17408) == 544 * 18
+    assert oracle.row_bytes(F16, 100) == 200  # one element per block: any length
+    assert oracle.row_bytes(Q3_K, 5120) == 20 * 110
+    assert oracle.row_bytes(IQ3_S, 5120) == 20 * 110
+    for t, n in ((Q3_K, 100), (IQ3_S, 128), (IQ4_NL, 16)):
+        with pytest.raises(oracle.OracleError) as e:
+            oracle.row_bytes(t, n)
+        assert e.value.code == oracle.EMODEL
+
+
+def test_f16_rows_widen_every_pattern(oracle):
+    """An F16 row is its elements widened one by one (quant.cpp:68-70): every one of the 65536
+    patterns equals the pinned fp16 widening bitwise (NaN included)."""
+    pats = np.arange(65536, dtype=np.uint16)
+    y = oracle.dequantize_row(F16, pats.view(np.uint8), 65536)
+    lib = oracle.lib()
+    want = np.array([lib.oracle_fp16_to_fp32(int(h)) for h in pats], np.float32)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def iq4nl_block(d_bits: int, qs: bytes) -> np.ndarray:
+    return np.frombuffer(struct.pack("<H", d_bits) + qs, np.uint8)
+
+
+def test_iq4_nl_table_nibble_order_and_subnormal_scale(oracle):
+    """Element j < 16 is table[low nibble of qs[j]], j + 16 table[high nibble], times d; d = 2
+    and d = 2^-24 (the smallest fp16 subnormal, 0x0001) give exact multiples of the table."""
+    qs = bytes(((15 - j) << 4) | j for j in range(16))
+    for d_bits, d in ((0x4000, 2.0), (0x0001, 2.0 ** -24)):
+        y = oracle.dequantize_row(IQ4_NL, iq4nl_block(d_bits, qs), 32)
+        for j in range(16):
+            assert y[j] == np.float32(d * IQ4NL[j])
+            assert y[j + 16] == np.float32(d * IQ4NL[15 - j])
+
+
+def q3k_block(hmask: bytes, qs: bytes, scales: bytes, d: float) -> np.ndarray:
+    assert len(hmask) == 32 and len(qs) == 64 and len(scales) == 12
+    return np.frombuffer(hmask + qs + scales + f16_bytes(d), np.uint8)
+
+
+def test_q3_k_literal_six_bit_scales(oracle):
+    """Bytes 0..7 of the scales = 0x21 (low nibble 1, high 2), bytes 8..11 = 0xE4 (2-bit fields
+    0, 1, 2, 3): the 16 scales are 1, 1, 1, 1, 17, 17, 17, 17, 34, 34, 34, 34, 50, 50, 50, 50.
+    With every 2-bit code 1 and every high bit set (q = 1), element e's value is d (sc - 32) for
+    the scale of its 16-element run e // 16."""
+    sc = [1] * 4 + [17] * 4 + [34] * 4 + [50] * 4
+    y = oracle.dequantize_row(Q3_K, q3k_block(b"\xff" * 32, b"\x55" * 64, b"\x21" * 8 + b"\xe4" * 4, 0.5), 256)
+    # runs of 16 in element order take scales 0, 1, ..., 15 (is++ in quant.cpp:219-224)
+    for e in range(256):
+        assert y[e] == np.float32(0.5 * (sc[e // 16] - 32)), e
+
+
+def test_q3_k_codes_and_high_bit(oracle):
+    """Scale bytes 0..7 = 0x11 and 8..11 = 0xAA (every 2-bit field 2): all 16 scales are
+    1 | 32 = 33, so dl = d. qs bytes 0xE4 hold the codes 0, 1, 2, 3 at shifts 0, 2, 4, 6, so
+    element 128 n + 32 j + l has code j; with its hmask bit clear the value drops by 4. Only
+    hmask[5]'s bit 6 is set: half 1, shift pair 2, lane 5 (element 128 + 64 + 5)."""
+    hm = bytearray(32)
+    hm[5] = 1 << 6
+    y = oracle.dequantize_row(Q3_K, q3k_block(bytes(hm), b"\xe4" * 64, bytes([0x11] * 8 + [0xAA] * 4), 1.0), 256)
+    for e in range(256):
+        j = (e % 128) // 32
+        code = j - (0 if e == 128 + 64 + 5 else 4)
+        assert y[e] == np.float32(code), e
+
+
+def _q3k_walk(blk: bytes) -> np.ndarray:
+    """quant.cpp:196-233's loops walked literally: the 32-bit aux shuffle with kmask1/kmask2,
+    then 2 halves x 4 shifts x 2 runs of 16, moving q by 32 per half and the hmask bit per
+    shift."""
+    d = float(np.frombuffer(blk[108:110], np.float16)[0])
+    aux = list(struct.unpack("<3I", blk[96:108])) + [0]
+    km1, km2 = 0x03030303, 0x0F0F0F0F
+    tmp = aux[2]
+    aux[2] = ((aux[0] >> 4) & km2) | (((tmp >> 4) & km1) << 4)
+    aux[3] = ((aux[1] >> 4) & km2) | (((tmp >> 6) & km1) << 4)
+    aux[0] = (aux[0] & km2) | (((tmp >> 0) & km1) << 4)
+    aux[1] = (aux[1] & km2) | (((tmp >> 2) & km1) << 4)
+    scales = np.frombuffer(struct.pack("<4I", *aux), np.int8)
+    out, q, m, is_ = [], 32, 1, 0
+    for _ in range(2):
+        shift = 0
+        for _ in range(4):
+            for half in (0, 16):
+                dl = np.float32(d) * np.float32(int(scales[is_]) - 32)
+                is_ += 1
+                for l in range(16):
+                    v = ((blk[q + l + half] >> shift) & 3) - (0 if blk[l + half] & m else 4)
+                    out.append(np.float32(dl * np.float32(v)))
+            shift += 2
+            m <<= 1
+        q += 32
+    return np.array(out, np.float32)
+
+
+def _iq3s_walk(blk: bytes) -> np.ndarray:
+    """quant.cpp:350-384's loops walked literally: pairs of sub-blocks, each half moving qs by
+    8 and signs by 4, qh by 2 per pair, the 9th index bit taken from h << (8 - 2 l) and
+    h << (7 - 2 l)."""
+    d = np.float32(np.frombuffer(blk[0:2], np.float16)[0])
+    qs, qh, signs, scales = 2, 66, 74, 106
+    out = []
+    for ib32 in range(0, 8, 2):
+        db1 = d * np.float32(1 + 2 * (blk[scales + ib32 // 2] & 0xF))
+        db2 = d * np.float32(1 + 2 * (blk[scales + ib32 // 2] >> 4))
+        for half in range(2):
+            db = db1 if half == 0 else db2
+            h = blk[qh + half]
+            for l in range(4):
+                g1 = blk[qs + 2 * l] | ((h << (8 - 2 * l)) & 256)
+                g2 = blk[qs + 2 * l + 1] | ((h << (7 - 2 * l)) & 256)
+                vals = [0.0] * 8
+                for j in range(4):
+                    s1 = np.float32(-1) if blk[signs + l] & KMASK[j] else np.float32(1)
+                    s2 = np.float32(-1) if blk[signs + l] & KMASK[j + 4] else np.float32(1)
+                    vals[j] = db * np.float32((IQ3S_GRID[g1] >> (8 * j)) & 0xFF) * s1
+                    vals[j + 4] = db * np.float32((IQ3S_GRID[g2] >> (8 * j)) & 0xFF) * s2
+                out.extend(vals)
+            qs += 8
+            signs += 4
+        qh += 2
+    return np.array(out, np.float32)
+
+
+def _blocks_with_scale(rng, n, bb, d_at):
+    w = rng.integers(0, 256, size=n * bb, dtype=np.uint8)
+    for b in range(n):
+        w[bb * b + d_at: bb * b + d_at + 2] = np.frombuffer(f16_bytes(rng.uniform(-0.05, 0.05)), np.uint8)
+    w[d_at: d_at + 2] = (0x07, 0x00)  # an fp16-subnormal d in the first block
+    return w
+
+
+@pytest.mark.parametrize("t,walk,d_at", [(Q3_K, _q3k_walk, 108), (IQ3_S, _iq3s_walk, 0)])
+def test_q3_k_iq3_s_equal_the_literal_loop_walk(oracle, t, walk, d_at):
+    """On random blocks the oracle's per-element index form equals a literal walk of the
+    reference's loops bitwise (signed zeros included)."""
+    rng = np.random.default_rng(21 + t)
+    w = _blocks_with_scale(rng, 24, 110, d_at)
+    y = oracle.dequantize_row(t, w, 24 * 256)
+    want = np.concatenate([walk(bytes(w[110 * b: 110 * (b + 1)])) for b in range(24)])
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def iq3s_block(d: float, qs: bytes, qh: bytes, signs: bytes, scales: bytes) -> np.ndarray:
+    assert len(qs) == 64 and len(qh) == 8 and len(signs) == 32 and len(scales) == 4
+    return np.frombuffer(f16_bytes(d) + qs + qh + signs + scales, np.uint8)
+
+
+def test_iq3_s_known_answers(oracle):
+    """All-zero fields, d = 0.25: codebook entry 0 (0x01010101), scale 1, no signs -> 0.25
+    everywhere. Then sub-block 3, group 5 takes entry 0x1FF (qs[29] = 0xFF, bit 5 of qh[3]),
+    element 3 * 32 + 5 * 4 + 1 is negated (bit 5 of signs[14]), and sub-block 3's scale
+    nibble (the high one of scales[1]) is 2 (multiplier 5)."""
+    z = iq3s_block(0.25, bytes(64), bytes(8), bytes(32), bytes(4))
+    assert np.all(oracle.dequantize_row(IQ3_S, z, 256) == np.float32(0.25))
+    qs, qh, signs, scales = bytearray(64), bytearray(8), bytearray(32), bytearray(4)
+    qs[3 * 8 + 5] = 0xFF
+    qh[3] = 1 << 5
+    signs[3 * 4 + 2] = 1 << 5  # elements 3*32 + 16 .. +23: the 6th one, i.e. 3*32 + 21
+    scales[1] = 0x20
+    y = oracle.dequantize_row(IQ3_S, iq3s_block(0.25, bytes(qs), bytes(qh), bytes(signs), bytes(scales)), 256)
+    g = IQ3S_GRID[0x1FF]
+    want = np.full(256, 0.25, np.float32)
+    want[96:128] = 0.25 * 5  # sub-block 3's multiplier
+    for k in range(4):
+        want[96 + 20 + k] = 0.25 * 5 * ((g >> (8 * k)) & 0xFF)
+    want[96 + 21] = -want[96 + 21]
+    assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("t,bb,be,d_at", [(IQ4_NL, 18, 32, 0), (Q3_K, 110, 256, 108), (IQ3_S, 110, 256, 0)])
+def test_new_type_dequant_terms(oracle, t, bb, be, d_at):
+    """a is the dequantized weight bitwise, b = 0, and off is the multiplier times the code
+    bias the kernels add (IQ4_NL 128 d; Q3_K 4 d (sc - 32) per 16-element run; IQ3_S 16 db per
+    32-element sub-block), recomputed here from the block bytes."""
+    rng = np.random.default_rng(40 + t)
+    n = 6
+    w = _blocks_with_scale(rng, n, bb, d_at)
+    a, b_, off = oracle.dequant_terms(t, w, 1, n * be)
+    y = oracle.dequantize_row(t, w, n * be)
+    assert np.array_equal(a[0].view(np.uint32), y.view(np.uint32)) and np.all(b_ == 0)
+    for b in range(n):
+        blk = bytes(w[bb * b: bb * (b + 1)])
+        d = _f16(blk, d_at)
+        if t == IQ4_NL:
+            want = np.full(32, np.float32(128) * d, np.float32)
+        elif t == Q3_K:
+            s = [((blk[96 + i % 8] >> (4 * (i // 8))) & 15) | (((blk[104 + i % 4] >> (2 * (i // 4))) & 3) << 4)
+                 for i in range(16)]
+            want = np.repeat([np.float32(4) * np.float32(d * np.float32(v - 32)) for v in s], 16).astype(np.float32)
+        else:
+            s = [(blk[106 + i // 2] >> (4 * (i % 2))) & 15 for i in range(8)]
+            want = np.repeat([np.float32(16) * np.float32(d * np.float32(1 + 2 * v)) for v in s], 32).astype(np.float32)
+        assert np.array_equal(off[0, be * b: be * (b + 1)], want), b
+
+
 # ---- rms_norm (backends/cpu/ops_basic.cpp:18-33) ------------------------------------------
 
 
