@@ -80,6 +80,12 @@ struct GemmPcArgs {
     uint32_t kchunks;
     float* partials;
     uint32_t split_unit0 = 0;  // W tile of the first split tile (units when both kinds share a launch)
+    // the small-M kernel at up to 8 rows reads x itself (fp32, normalized as k_x_to_frag does
+    // when nw is set) instead of the staged fragments
+    const float* x = nullptr;
+    uint64_t x_stride = 0;
+    const float* inv = nullptr;
+    const float* nw = nullptr;
 };
 
 // Producer barrier: its LDS writes are complete, then s_barrier. Global loads stay in flight.
@@ -573,13 +579,19 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
 
 // Sum of the K-chunk partials of a split launch (in chunk order) and the epilogue.
 // grid = (tiles * BM * 128 / 256), block 256; one output element (pair) per thread.
+// With one M tile the grid covers only its n_vec rows (reduce_rows).
+__host__ __device__ inline uint32_t reduce_rows(uint32_t bm, uint32_t m_tiles, uint32_t n_vec) {
+    return m_tiles == 1 && n_vec < bm ? n_vec : bm;
+}
+
 template <bool PAIR, int BM>
 __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
     const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     constexpr uint32_t NC = PAIR ? 64 : kPcW;  // output columns per tile
     const uint64_t tiles = (uint64_t)a.split_units * a.m_tiles;
-    if (idx >= tiles * BM * NC) return;
-    const uint32_t tile = (uint32_t)(idx / (BM * NC)), e = (uint32_t)(idx % (BM * NC));
+    const uint32_t R = reduce_rows(BM, a.m_tiles, a.n_vec);
+    if (idx >= tiles * R * NC) return;
+    const uint32_t tile = (uint32_t)(idx / (R * NC)), e = (uint32_t)(idx % (R * NC));
     const uint32_t ml = e / NC, nl = e % NC;
     const uint32_t u = a.split_unit0 + tile / a.m_tiles, mt = tile % a.m_tiles;
     const uint32_t m = mt * BM + ml;
@@ -840,25 +852,109 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Small-M GEMM: k_gemm_sm<T, PAIR> (at most 32 x rows)
+// Small-M GEMM: k_gemm_sm<T, PAIR, XR> (at most 32 x rows; XR = 8, 16 or 32 rows kept)
 //
 // A workgroup owns W unit u (PAIR: the gate and up rows of slab u; else slabs 2u and 2u + 1)
-// over K chunk `chunk` (whole super-blocks) and all 32 x rows of the staged buffer. Wave w takes
-// matrix w / 2 and row block w % 2 (32 W rows). Lane l dequantizes row l % 32, half l / 32 of
-// each slot record, which is exactly its B operand of v_mfma_f32_32x32x16_bf16 for the slot's
-// two K halves: no LDS, no barrier, every wave streams on its own with kSmDepth slots of
-// weight records and kSmXDepth slots of x fragments in flight (the four waves read the same x
-// fragments: L1 hits). Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128]
-// (columns 64 * matrix + 32 * block), and k_gemm_pc_reduce adds the chunks in order and applies
-// the epilogue. Per slot and lane: one exact dequantization and two MFMAs, so the kernel is
-// bound by the dequantization's VALU work instead of a per-stage barrier chain.
+// over K chunk `chunk` (whole super-blocks) and all x rows. Wave w takes matrix w / 2 and row
+// block w % 2 (32 W rows). Lane l dequantizes row l % 32, half l / 32 of each slot record,
+// which is exactly its B operand of v_mfma_f32_32x32x16_bf16 for the slot's two K halves: no
+// W through LDS, no barrier in the loop. What the vector-memory path carries per slot is only
+// the weights themselves:
+//   - x: the chunk's x fragments (rows < XR of the staged buffer) are copied into LDS once, at
+//     the start; each slot's A operands are then two ds_read_b128 (rows past XR read a zero
+//     entry). Loading them from global memory per wave and slot took 2 KB of L1 traffic per
+//     64 x 32 weights and kept the texture path busy three quarters of the kernel;
+//   - the block headers (Q4_K / Q5_K scales and mins, IQ4_XS scales, Q6_K's scales and d) are
+//     loaded once per super-block, two ahead, not once per slot;
+//   - the per-slot codes stream kSmDepth slots ahead.
+// Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128] (columns 64 *
+// matrix + 32 * block), and k_gemm_pc_reduce adds the chunks in order and applies the epilogue.
 // ------------------------------------------------------------------------------------------
-constexpr int kSmDepth = 16;  // slots of weight records in flight per wave (two half-rounds of 8)
-constexpr int kSmXDepth = 2;  // slots of x fragments in flight per wave
+constexpr int kSmDepth = 16;  // slots of weight codes in flight per wave (two super-blocks)
 constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
+constexpr uint32_t kSmLdsMax = 48 * 1024;  // x bytes of one workgroup's K chunk in LDS
+constexpr uint32_t kSmLdsMax8 = 24 * 1024;  // the same at 8 rows, read from fp32 x by the kernel
+__host__ __device__ constexpr uint32_t sm_lds_max(uint32_t xr) { return xr == 8 ? kSmLdsMax8 : kSmLdsMax; }
 
-template <uint32_t T, bool PAIR>
+// The per-super-block fields of a weight record (none for the 32-weight block formats).
+template <uint32_t T>
+struct SmH {};
+template <>
+struct SmH<kQ4_K> {
+    uint4 hdr;
+};
+template <>
+struct SmH<kQ5_K> {
+    uint4 hdr;
+};
+template <>
+struct SmH<kIQ4_XS> {
+    uint2 hdr;
+};
+template <>
+struct SmH<kQ6_K> {
+    uint4 sc;  // the 16 int8 scales of the row's super-block
+    uint32_t d;
+};
+
+// The per-slot fields of pc_load_w (codes; Q4_0 / Q8_0's d, Q5_K / Q6_K's high bits).
+template <uint32_t T>
+__device__ __forceinline__ void sm_load_q(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
+                                          uint32_t s, bool live) {
+    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
+    if constexpr (T == kQ4_K || T == kIQ4_XS) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+    } else if constexpr (T == kQ4_0) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+    } else if constexpr (T == kQ5_K) {
+        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 256));
+    } else if constexpr (T == kQ8_0) {
+        R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
+        R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
+        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+    } else {
+        R.ql = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 512));
+    }
+}
+
+// The per-super-block fields of super-block sb.
+template <uint32_t T>
+__device__ __forceinline__ void sm_load_h(SmH<T>& H, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
+                                          uint32_t sb, bool live) {
+    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
+    if constexpr (T == kQ4_K) {
+        H.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
+    } else if constexpr (T == kQ5_K) {
+        H.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+    } else if constexpr (T == kIQ4_XS) {
+        H.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
+    } else if constexpr (T == kQ6_K) {
+        H.sc = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+        H.d = bld16(slab, o.d, so(g.d_off + sb * 128));
+    }
+}
+
+// Completes R with sub-block j's fields of the super-block header H.
+template <uint32_t T>
+__device__ __forceinline__ void sm_merge(PcW<T>& R, const SmH<T>& H, int j) {
+    if constexpr (T == kQ4_K || T == kQ5_K || T == kIQ4_XS) {
+        R.hdr = H.hdr;
+    } else if constexpr (T == kQ6_K) {
+        const uint32_t w = (j >> 1) == 0 ? H.sc.x : (j >> 1) == 1 ? H.sc.y : (j >> 1) == 2 ? H.sc.z : H.sc.w;
+        R.sc = (w >> (16 * (j & 1))) & 0xFFFFu;
+        R.d = H.d;
+    }
+}
+
+// x bytes in LDS per slot of K: two K halves x two lane halves x XR rows x 16 B.
+__host__ __device__ constexpr uint32_t sm_x_bytes_per_slot(uint32_t xr) { return 64u * xr; }
+
+template <uint32_t T, bool PAIR, uint32_t XR>
 __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
+    extern __shared__ uint4 xl[];  // [slot][K half][lane half][XR rows], then one zero entry
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = a.cols / kSlot;
@@ -868,6 +964,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
     const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
     const uint32_t g0 = chunk * base + min(chunk, extra);
     const uint32_t s_begin = 8 * g0, s_end = 8 * (g0 + base + (chunk < extra ? 1u : 0u));
+    const uint32_t ns = s_end - s_begin;
     const uint32_t mat = wave >> 1, rb = wave & 1u;
     const uint32_t r = lane & 31u, h = lane >> 5;
     const uint8_t* slab_ptr;
@@ -880,53 +977,123 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(slab_ptr, (uint32_t)g.slab_bytes);
     const PcOff off = pc_offsets<T>(32 * rb + r, h);
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
-    const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf, (uint32_t)((uint64_t)kSmRows * a.cols * 2));
-    const uint32_t xlane = lane * 16;
-    // weight records kSmDepth slots ahead (HBM), x fragments kSmXDepth slots ahead (L2)
+
+    // x of the chunk into LDS: the loads first, then the weight stream's first loads, then the
+    // LDS stores (which wait only for the x loads: loads return in order). At 8 rows the kernel
+    // reads fp32 x itself and rounds it to bf16 (RNE) as k_x_to_frag does, so no staging launch
+    // runs; above, the staged fragments are copied.
+    constexpr bool kFuseX = XR == 8;
+    constexpr uint32_t kXPer = sm_lds_max(XR) / 16 / 256;  // 16-byte entries per thread: the largest chunk's
+    const uint32_t n16 = ns * 4 * XR;
     PcW<T> R[kSmDepth];
-    uint4 X[kSmXDepth][2];
-    auto load_w = [&](int q, uint32_t s) { pc_load_w<T>(R[q], wres, g, off, s, s < s_end); };
-    auto load_x = [&](int q, uint32_t s) {
+    SmH<T> H[2];
+    auto load_q = [&](int q, uint32_t s) { sm_load_q<T>(R[q], wres, g, off, s, s < s_end); };
+    auto load_h = [&](int i, uint32_t sb) { sm_load_h<T>(H[i], wres, g, off, sb, 8 * sb < s_end); };
+    if constexpr (kFuseX) {
+        float4 xa[kXPer], xb[kXPer];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) X[q][k] = bld128(xres, xlane, s < s_end ? (s * 2 + k) * 1024 : kPcOob);
-    };
+        for (int i = 0; i < (int)kXPer; ++i) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            const uint32_t row = e % 8, k8 = (e / 8) & 1u, hk = e / 16;  // hk = 2 (slot - s_begin) + K half
+            const uint32_t k = 32 * (s_begin + hk / 2) + 16 * (hk & 1u) + 8 * k8;
+            xa[i] = xb[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (e < n16 && row < a.n_vec) {
+                const float* xp = a.x + (uint64_t)row * a.x_stride + k;
+                xa[i] = *reinterpret_cast<const float4*>(xp);
+                xb[i] = *reinterpret_cast<const float4*>(xp + 4);
+            }
+        }
+        load_h(0, s_begin / 8);
+        load_h(1, s_begin / 8 + 1);
 #pragma unroll
-    for (int q = 0; q < kSmXDepth; ++q) load_x(q, s_begin + q);
+        for (int q = 0; q < kSmDepth; ++q) load_q(q, s_begin + q);
 #pragma unroll
-    for (int q = 0; q < kSmDepth; ++q) load_w(q, s_begin + q);
+        for (int i = 0; i < (int)kXPer; ++i) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            if (e >= n16) break;
+            float v[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+            const uint32_t row = e % 8;
+            if (a.nw && row < a.n_vec) {
+#pragma clang fp contract(off)
+                const uint32_t k8 = (e / 8) & 1u, hk = e / 16;
+                const uint32_t k = 32 * (s_begin + hk / 2) + 16 * (hk & 1u) + 8 * k8;
+                const float sc = a.inv[row];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float t = v[j] * sc;
+                    v[j] = t * a.nw[k + j];
+                }
+            }
+            const bf16x8 b{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3],
+                           (__bf16)v[4], (__bf16)v[5], (__bf16)v[6], (__bf16)v[7]};
+            xl[e] = __builtin_bit_cast(uint4, b);
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf, (uint32_t)((uint64_t)kSmRows * a.cols * 2));
+        uint4 xv[kXPer];
+#pragma unroll
+        for (int i = 0; i < (int)kXPer; ++i) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            const uint32_t row = e % XR, k8 = (e / XR) & 1u, hk = e / (2 * XR);  // hk = 2 (slot - s_begin) + K half
+            // a per-lane condition goes in the lane offset: the scalar offset must stay uniform
+            xv[i] = bld128(xres, e < n16 ? (s_begin * 2 + hk) * 1024 + (k8 * 32 + row) * 16 : kPcOob, 0);
+        }
+        load_h(0, s_begin / 8);
+        load_h(1, s_begin / 8 + 1);
+#pragma unroll
+        for (int q = 0; q < kSmDepth; ++q) load_q(q, s_begin + q);
+#pragma unroll
+        for (int i = 0; i < (int)kXPer; ++i) {
+            const uint32_t e = threadIdx.x + 256u * i;
+            if (e < n16) xl[e] = xv[i];
+        }
+    }
+    if (threadIdx.x == 0) xl[n16] = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    // this lane's A entries: row r, lane half h; rows past XR read the zero entry
+    const uint32_t xrow = (r < XR) ? h * XR + r : ~0u;
     floatx16 acc = floatx16{};
-    // slot s: ring slots s % kSmDepth and s % kSmXDepth, static in the unrolled half-rounds;
-    // chunks are whole super-blocks, so the loop may end after either half
     auto step = [&](int q, uint32_t s) {
+        PcW<T> W = R[q];
+        sm_merge<T>(W, H[q >> 3], q & 7);
         bf16x8 lo, hi;
-        pc_dequant<T>(R[q], h, q % 8, inv_unit, lo, hi);  // s_begin: a multiple of 8
-        const int qx = q % kSmXDepth;
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[qx][0]), lo, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, X[qx][1]), hi, acc, 0, 0, 0);
-        load_x(qx, s + kSmXDepth);
-        load_w(q, s + kSmDepth);
+        pc_dequant<T>(W, h, q & 7, inv_unit, lo, hi);  // s_begin: a multiple of 8
+        const uint32_t ls = s - s_begin;
+        const uint4 x0 = xl[xrow != ~0u ? (2 * ls) * 2 * XR + xrow : n16];
+        const uint4 x1 = xl[xrow != ~0u ? (2 * ls + 1) * 2 * XR + xrow : n16];
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x0), lo, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x1), hi, acc, 0, 0, 0);
+        load_q(q, s + kSmDepth);
     };
+    // two super-blocks per iteration: H[0] serves the first, H[1] the second; each is reloaded
+    // with the super-block two ahead once its own is done
     for (uint32_t i0 = s_begin; i0 < s_end; i0 += kSmDepth) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) step(q, i0 + q);
+        load_h(0, i0 / 8 + 2);
         if (i0 + 8 >= s_end) break;
 #pragma unroll
         for (int q = 8; q < kSmDepth; ++q) step(q, i0 + q);
+        load_h(1, i0 / 8 + 3);
     }
     float* P = a.partials + ((uint64_t)u * a.kchunks + chunk) * kSmRows * kPcW + 64 * mat + 32 * rb + r;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) P[mfma32_row(e, lane) * kPcW] = acc[e];
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t m = mfma32_row(e, lane);
+        if (m < a.n_vec) P[m * kPcW] = acc[e];  // the reduce reads only the rows of x
+    }
 }
 
-template <bool PAIR>
-void launch_gemm_sm_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStream_t st) {
+template <bool PAIR, uint32_t XR>
+void launch_gemm_sm_xr(uint32_t type, const GemmPcArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     switch (type) {
-        case kQ4_0: hipLaunchKernelGGL((k_gemm_sm<kQ4_0, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kQ8_0: hipLaunchKernelGGL((k_gemm_sm<kQ8_0, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kQ4_K: hipLaunchKernelGGL((k_gemm_sm<kQ4_K, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kQ5_K: hipLaunchKernelGGL((k_gemm_sm<kQ5_K, PAIR>), grid, dim3(256), 0, st, a); break;
-        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sm<kIQ4_XS, PAIR>), grid, dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm_sm<kQ6_K, PAIR>), grid, dim3(256), 0, st, a); break;
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_sm<kQ4_0, PAIR, XR>), grid, dim3(256), lds, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_sm<kQ8_0, PAIR, XR>), grid, dim3(256), lds, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_sm<kQ4_K, PAIR, XR>), grid, dim3(256), lds, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_sm<kQ5_K, PAIR, XR>), grid, dim3(256), lds, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sm<kIQ4_XS, PAIR, XR>), grid, dim3(256), lds, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_sm<kQ6_K, PAIR, XR>), grid, dim3(256), lds, st, a); break;
     }
 }
 
@@ -957,7 +1124,7 @@ void launch_gemm_pc_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStrea
 // k_gemm_pc_reduce over the split tiles of p (BM-row tiles)
 template <bool PAIR, int BM>
 void launch_reduce(const GemmPcArgs& p, hipStream_t st) {
-    const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * BM * (PAIR ? 64 : kPcW);
+    const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * reduce_rows(BM, p.m_tiles, p.n_vec) * (PAIR ? 64 : kPcW);
     hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, BM>), dim3((uint32_t)((outs + 255) / 256)), dim3(256), 0, st, p);
 }
 
@@ -1041,22 +1208,55 @@ int launch_gemm_lm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
     return HALO_MI_OK;
 }
 
+// The k_gemm_sm launch plan: the x rows kept (XR) and the K chunks per unit. About four
+// workgroups per CU (three are resident at the kernel's registers), at least enough chunks that
+// one chunk's x fits kSmLdsMax, and the partials within the workspace. False if none fits.
+struct SmPlan {
+    uint32_t xr, kc;
+    size_t lds;
+};
+bool sm_plan(uint32_t units, uint32_t S, uint32_t n_vec, SmPlan& pl) {
+    if (n_vec > kSmRows || S % 8 != 0 || S == 0) return false;
+    const uint32_t ng = S / 8, cus = cu_count();
+    pl.xr = n_vec <= 8 ? 8u : n_vec <= 16 ? 16u : 32u;
+    const uint32_t max_groups = sm_lds_max(pl.xr) / (8 * sm_x_bytes_per_slot(pl.xr));
+    const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
+    pl.kc = std::clamp<uint32_t>((4 * cus + units - 1) / units, kc_min, ng);
+    while (pl.kc > kc_min && (uint64_t)units * pl.kc * kSmRows * kPcW > kPartialFloats) --pl.kc;
+    if ((uint64_t)units * pl.kc * kSmRows * kPcW > kPartialFloats) return false;
+    const uint32_t groups = (ng + pl.kc - 1) / pl.kc;  // the largest chunk
+    pl.lds = (size_t)groups * 8 * sm_x_bytes_per_slot(pl.xr) + 16;
+    return true;
+}
+
 // The k_gemm_sm path (at most 32 x rows, K in whole super-blocks): x staged as one 32-row
-// block, every unit split over K into about four workgroups per CU (three are resident at the
-// kernel's registers, so the last round is short), then the chunk-order reduce.
+// block, every unit split over K (sm_plan), then the chunk-order reduce.
 template <bool PAIR>
 int launch_gemm_sm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t units, hipStream_t st) {
-    const uint32_t S = a.cols / kSlot, cus = cu_count();
+    const uint32_t S = a.cols / kSlot;
     if ((uint64_t)kSmRows * a.cols > kXbElems || (uint64_t)kSmRows * a.cols * 2 > 0xFFFFFFFFull)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: cols %u too large for the x staging buffer", a.cols);
-    uint32_t kc = std::clamp<uint32_t>((4 * cus + units - 1) / units, 1u, S / 8);
-    while (kc > 1 && (uint64_t)units * kc * kSmRows * kPcW > kPartialFloats) --kc;
-    if ((uint64_t)units * kc * kSmRows * kPcW > kPartialFloats)
+    SmPlan pl;
+    if (!sm_plan(units, S, a.n_vec, pl))
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: %u rows exceed the small-M partials workspace", a.rows);
-    if (int rc = stage_x(a, 0, a.n_vec, kSmRows, ws, st)) return rc;
-    GemmPcArgs p{a.w0, a.w1, ws->xb, a.y, a.y_stride, a.rows, a.cols, a.n_vec, 0u, 1u, 0u, units, kc, ws->partials};
+    GemmPcArgs p{a.w0, a.w1, ws->xb, a.y, a.y_stride, a.rows, a.cols, a.n_vec, 0u, 1u, 0u, units, pl.kc, ws->partials};
     p.split_unit0 = 0;
-    launch_gemm_sm_type<PAIR>(type, p, dim3(units * kc), st);
+    if (pl.xr == 8) {  // the kernel reads x itself; with the norm, 1 / rms per row first
+        p.x = a.x;
+        p.x_stride = a.x_stride;
+        p.nw = a.norm_w;
+        p.inv = ws->inv;
+        if (a.norm_w)
+            if (int rc = launch_rms_inv(a.x, a.x_stride, a.n_vec, a.cols, a.norm_eps, ws->inv, st)) return rc;
+    } else if (int rc = stage_x(a, 0, a.n_vec, kSmRows, ws, st)) {
+        return rc;
+    }
+    const dim3 grid(units * pl.kc);
+    switch (pl.xr) {
+        case 8: launch_gemm_sm_xr<PAIR, 8>(type, p, grid, pl.lds, st); break;
+        case 16: launch_gemm_sm_xr<PAIR, 16>(type, p, grid, pl.lds, st); break;
+        default: launch_gemm_sm_xr<PAIR, 32>(type, p, grid, pl.lds, st); break;
+    }
     launch_reduce<PAIR, kSmRows>(p, st);
     return hip_status(hipGetLastError(), "gemm_sm launch");
 }
@@ -1086,8 +1286,8 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
                                     (uint64_t)units * ((a.n_vec + kLmBM - 1) / kLmBM) >= cus))
         return launch_gemm_lm<PAIR>(type, a, ws, units, st);
     // the small-M kernel: about 1.5x k_gemm_pc's rate at M = 8 (no per-stage barrier chain)
-    const uint64_t sm_floats = (uint64_t)units * kSmRows * kPcW;  // partials at one K chunk
-    const bool sm_fits = a.n_vec <= kSmRows && S % 8 == 0 && sm_floats <= kPartialFloats;
+    SmPlan sm_pl;
+    const bool sm_fits = sm_plan(units, S, a.n_vec, sm_pl);
     if (a.tiles == kGemmTilesSm && !sm_fits)
         return set_error(HALO_MI_E_UNSUPPORTED, "gemm: the small-M kernel takes at most %u x rows, cols a multiple of "
                                                 "256 and at most %llu rows", kSmRows,
