@@ -430,6 +430,7 @@ def main() -> int:
     ap.add_argument("--variant", type=int, default=0, help="kernel variant id for --only gemv / gemm workloads "
                     "(halo_mi_gemv_params::variant; 0 = the default choice)")
     ap.add_argument("--rows", type=int, default=0, help="--only gemv / gemm workloads: rows instead of the workload's")
+    ap.add_argument("--m", type=int, default=0, help="--only gemv / gemm workloads: vectors instead of the workload's")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the benchmark, copy a buffer of this many MiB 4 times (a plain copy kernel of "
                          "known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -474,6 +475,7 @@ def main() -> int:
             return 0
         t = int(getattr(hl.DType, t))
         rows = args.rows or rows
+        m = args.m or m
         if kind == "head":
             r = lm_head_case(hl, torch, t, rows, cols, m, seed, outliers=0.01)
             print(json.dumps({"workload": args.only, "GB/s": round(r["gbs"], 1), "us": round(r["ms"] * 1e3, 3)}), flush=True)

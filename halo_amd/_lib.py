@@ -47,6 +47,7 @@ class Variant(enum.IntEnum):
     SLAB_GEMM_BF16_M512 = 5
     SLAB_GEMV_VALU = 6
     SLAB_GEMM_BF16_SMALL_M = 7
+    SLAB_GEMM_EXACT_SMALL_M = 8
 
 
 class ErrorCode(enum.IntEnum):

@@ -21,7 +21,7 @@ ROOT = PKG.parent
 LIB = PKG / "libhalo_mi355x.so"
 CSRC = PKG / "csrc"
 # the kernel files first: they take longest and are compiled in parallel with the rest
-SOURCES = [CSRC / "k_gemv.hip", CSRC / "k_gemv_group.hip", CSRC / "k_gemm.hip", CSRC / "k_dequant.hip", CSRC / "k_argmax.hip", CSRC / "k_norm.hip",
+SOURCES = [CSRC / "k_gemv.hip", CSRC / "k_gemv_group.hip", CSRC / "k_gemm.hip", CSRC / "k_gemm_sx.hip", CSRC / "k_dequant.hip", CSRC / "k_argmax.hip", CSRC / "k_norm.hip",
            CSRC / "api.cpp", CSRC / "upload.cpp", CSRC / "host_utils.cpp", CSRC / "backend.cpp"]
 OBJ_DIR = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -147,11 +147,37 @@ int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t*
 }
 
 // The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
+// The kernel the auto variant runs for n_vec vectors (measured on MI355X at the BASELINE shapes):
+//   - the slab GEMV (exact products) up to 2 vectors (Q6_K: up to 4), where it streams the
+//     weights fastest;
+//   - the exact-product small-M GEMM from 3 (gate/up pair: 3 and 4), which streams them once for
+//     up to 8 vectors with the same arithmetic (plain matrices at 5..8 vectors: twice as fast as
+//     two GEMV passes);
+//   - above, the bf16 GEMM families (the pair from 5 vectors).
+// The exact GEMM needs cols a multiple of 256 (and its workspace to hold the shape); otherwise
+// the GEMV. The choice depends on the shape only, so a call with the fused norm takes the same
+// kernel as rms_norm followed by the plain call.
+uint32_t auto_gemv_variant(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n_vec, bool pair) {
+    const uint32_t gemv_max = pair ? 2u : (type == kQ6_K ? 4u : 2u);
+    const uint32_t exact_max = pair ? kGateUpGemvMax : kGemmSxMaxRows;
+    if (n_vec <= gemv_max) return HALO_MI_GEMV_SLAB;
+    if (n_vec <= exact_max) {
+        const uint32_t slabs = (rows + kSlabRows - 1) / kSlabRows;
+        uint32_t kc = 0;
+        size_t lds = 0;
+        if (gemm_sx_plan(pair ? slabs : (slabs + 1) / 2, cols, n_vec, &kc, &lds))
+            return HALO_MI_GEMM_SLAB_EXACT_SMALL_M;
+        return n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+    }
+    return HALO_MI_GEMM_SLAB_BF16;
+}
+
 uint32_t gemm_tiles(uint32_t variant) {
     switch (variant) {
         case HALO_MI_GEMM_SLAB_BF16: return kGemmTilesPc;
         case HALO_MI_GEMM_SLAB_BF16_M512: return kGemmTilesLm;
         case HALO_MI_GEMM_SLAB_BF16_SMALL_M: return kGemmTilesSm;
+        case HALO_MI_GEMM_SLAB_EXACT_SMALL_M: return kGemmTilesSx;
         default: return kGemmTilesAuto;
     }
 }
@@ -218,7 +244,7 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     if (reinterpret_cast<uintptr_t>(p->w) % 16) return set_error(HALO_MI_E_KERNEL, "%s: SLAB weights must be 16-byte aligned", op);
     if (ranges_overlap(p->y, yext, p->w, halo_mi_slab_bytes(p->type, p->rows, p->cols)))
         return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
-    if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = p->n_vec <= 8 ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+    if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = auto_gemv_variant(p->type, p->rows, p->cols, p->n_vec, false);
     if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
         a.norm_w = p->norm_w;
@@ -226,10 +252,10 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
         a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<false>(p->type, a, st);
     }
-    if (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
-        return set_error(HALO_MI_E_KERNEL, "%s: the MFMA GEMM needs 16-byte aligned x rows", op);
+    if (variant != HALO_MI_GEMM_SLAB_EXACT_SMALL_M && (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
+        return set_error(HALO_MI_E_KERNEL, "%s: the bf16 MFMA GEMM needs 16-byte aligned x rows", op);
     GemmArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
-    a.tiles = gemm_tiles(p->variant);
+    a.tiles = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M ? kGemmTilesSx : gemm_tiles(p->variant);
     a.norm_w = p->norm_w;
     a.norm_eps = p->norm_eps;
     return launch_gemm_pc<false>(p->type, a, st);
@@ -391,7 +417,7 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
         return set_error(HALO_MI_E_KERNEL, "%s: out overlaps a weight operand", op);
     if ((code = check_norm(op, p->norm_w, p->cols, p->out, oext))) return code;
     if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
-        variant = p->n_vec <= kGateUpGemvMax ? HALO_MI_GEMV_SLAB : HALO_MI_GEMM_SLAB_BF16;
+        variant = auto_gemv_variant(p->type, p->rows, p->cols, p->n_vec, true);
     auto st = static_cast<hipStream_t>(stream);
     if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
@@ -401,11 +427,11 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
         a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<true>(p->type, a, st);
     }
-    if (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
-        return set_error(HALO_MI_E_KERNEL, "%s: the MFMA GEMM needs 16-byte aligned x rows", op);
+    if (variant != HALO_MI_GEMM_SLAB_EXACT_SMALL_M && (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
+        return set_error(HALO_MI_E_KERNEL, "%s: the bf16 MFMA GEMM needs 16-byte aligned x rows", op);
     GemmArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                p->rows, p->cols, p->n_vec};
-    a.tiles = gemm_tiles(p->variant);
+    a.tiles = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M ? kGemmTilesSx : gemm_tiles(p->variant);
     a.norm_w = p->norm_w;
     a.norm_eps = p->norm_eps;
     return launch_gemm_pc<true>(p->type, a, st);

@@ -232,7 +232,7 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 17> kVariants{{
+constexpr std::array<VariantInfo, 19> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
     {kRmsNorm, "rms_norm_cpu_order", OpId::RmsNorm, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
@@ -242,6 +242,7 @@ constexpr std::array<VariantInfo, 17> kVariants{{
     {kGemmSlabBf16M512, "gemm_slab_bf16_mfma_m512", OpId::Gemv, {}},
     {kGemvSlabValu, "gemv_slab_valu_w64", OpId::Gemv, {}},
     {kGemmSlabBf16SmallM, "gemm_slab_bf16_mfma_small_m", OpId::Gemv, {}},
+    {kGemmSlabExactSmallM, "gemm_slab_exact_small_m", OpId::Gemv, {}},
     {kSwiglu, "swiglu_b256", OpId::Swiglu, {}},
     {kLmHeadFused, "lm_head_argmax_parts", OpId::LmHead, {}},
     {kArgmax, "argmax_parts_b256", OpId::Argmax, {}},
@@ -250,6 +251,7 @@ constexpr std::array<VariantInfo, 17> kVariants{{
     {kGateUpGemm, "gate_up_gemm_bf16_mfma", OpId::GateUpSwiglu, {}},
     {kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512", OpId::GateUpSwiglu, {}},
     {kGateUpGemmSmallM, "gate_up_gemm_bf16_mfma_small_m", OpId::GateUpSwiglu, {}},
+    {kGateUpExactSmallM, "gate_up_gemm_exact_small_m", OpId::GateUpSwiglu, {}},
 }};
 
 bool has_variant(OpId op, std::uint32_t id) {
@@ -258,7 +260,9 @@ bool has_variant(OpId op, std::uint32_t id) {
 }
 
 // MATMUL registry id -> the C ABI's variant id (the two lists are in the same order)
-std::uint32_t abi_gemv_variant(std::uint32_t id) { return id == 0 ? HALO_MI_GEMV_DEFAULT : id - kGemvGgufRef + 1; }
+std::uint32_t abi_gemv_variant(std::uint32_t id) {
+    return id == 0 ? HALO_MI_GEMV_DEFAULT : id == kGemmSlabExactSmallM ? HALO_MI_GEMM_SLAB_EXACT_SMALL_M : id - kGemvGgufRef + 1;
+}
 
 void check_no_status(const StatusRef& st, const char* op) {
     CHECK(st.empty(), ErrorCode::Unsupported, "%s: per-sequence status words are not implemented (WS-BI-1)", op);
@@ -537,6 +541,7 @@ public:
                                       : id == kGateUpGemm       ? HALO_MI_GEMM_SLAB_BF16
                                       : id == kGateUpGemmM512   ? HALO_MI_GEMM_SLAB_BF16_M512
                                       : id == kGateUpGemmSmallM ? HALO_MI_GEMM_SLAB_BF16_SMALL_M
+                                      : id == kGateUpExactSmallM ? HALO_MI_GEMM_SLAB_EXACT_SMALL_M
                                       : a.allow_gemm            ? HALO_MI_GEMV_SLAB_AUTO
                                                                 : HALO_MI_GEMV_SLAB;
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,

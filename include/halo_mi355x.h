@@ -82,10 +82,12 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *   3 HALO_MI_GEMM_SLAB_BF16 SLAB layout, bf16 MFMA GEMM (dequantized W and x rounded to
  *                            bf16, fp32 accumulate) on M tiles of 64 / 128 / 256 rows by n_vec;
  *                            any n_vec.
- *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 8; else the small-M bf16 GEMM
- *                            (same numerics as 3, no LDS stage) for n_vec <= 32 when cols is a
- *                            multiple of 256; else 5 when n_vec > 256 and its tiles fill the
- *                            GPU, else 3.
+ *   4 HALO_MI_GEMV_SLAB_AUTO SLAB layout: 2 for n_vec <= 2 (Q6_K: <= 4); 8 for the rest up to
+ *                            n_vec <= 8 (2 when cols is not a multiple of 256); so up to 8
+ *                            vectors the result is within 2's bound.
+ *                            Above 8, the small-M bf16 GEMM (same numerics as 3) for n_vec <= 32
+ *                            when cols is a multiple of 256; else 5 when n_vec > 256 and its
+ *                            tiles fill the GPU, else 3.
  *   5 HALO_MI_GEMM_SLAB_BF16_M512  the bf16 MFMA GEMM on 512-row M tiles (every wave both
  *                            dequantizes and multiplies; same numerics as 3); any n_vec.
  *   6 HALO_MI_GEMV_SLAB_VALU the SLAB GEMV with its multiply-adds on the VALU instead of the
@@ -94,6 +96,10 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *   7 HALO_MI_GEMM_SLAB_BF16_SMALL_M  the bf16 MFMA GEMM's small-M kernel (no LDS stage; waves
  *                            dequantize their own MFMA operands): n_vec <= 32, cols a multiple
  *                            of 256; same numerics as 3.
+ *   8 HALO_MI_GEMM_SLAB_EXACT_SMALL_M  the exact-product small-M GEMM: the slab GEMV's
+ *                            arithmetic (integer codes times x split exactly into three bf16
+ *                            pieces, fp32 sums, scales applied per slot) on 32x32 MFMA tiles;
+ *                            n_vec <= 8, cols a multiple of 256; within the bound of 2.
  */
 enum {
     HALO_MI_GEMV_DEFAULT = 0,
@@ -104,7 +110,8 @@ enum {
     HALO_MI_GEMM_SLAB_BF16_M512 = 5,
     HALO_MI_GEMV_SLAB_VALU = 6,
     HALO_MI_GEMM_SLAB_BF16_SMALL_M = 7,
-    HALO_MI_GEMV_VARIANT_LAST = 7
+    HALO_MI_GEMM_SLAB_EXACT_SMALL_M = 8,
+    HALO_MI_GEMV_VARIANT_LAST = 8
 };
 
 /*
@@ -205,10 +212,14 @@ int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream);
  * The reference composes it as gemv(gate), gemv(up), swiglu (src/models/qwen35.cpp:789-805;
  * backends/cpu/ops_basic.cpp:165-167); here both matmuls and the epilogue are one launch.
  * Wg and Wu share type, layout and shape (rows x cols). SLAB layout only; variant 0/4 = auto
- * (gemv kernel for n_vec <= 4, else the GEMM, its M tiles chosen as for halo_mi_gemv), 2 = gemv
- * kernel (any n_vec, 4 vectors per pass over the weights), 3 / 5 = bf16 MFMA GEMM on 64..256 /
- * 512-row M tiles. out may not overlap x, Wg or Wu. norm_w / norm_eps (optional): the fused
- * input norm as for halo_mi_gemv (the FFN's post-attention norm folded into the pair).
+ * (the gemv pair for n_vec <= 2, the exact small-M GEMM (8) for 3 and 4 when cols is a multiple
+ * of 256, else the gemv pair up to 4; above 4 the bf16 GEMM, its M
+ * tiles chosen as for halo_mi_gemv), 2 = gemv kernel (any n_vec, 4 vectors per pass over the
+ * weights), 3 / 5 / 7 = bf16 MFMA GEMM on 64..256 / 512-row / small-M tiles, 8 = the exact
+ * small-M GEMM (n_vec <= 8). The GEMMs' SiLU is the fast form (relative error at most
+ * (1.5 |v| + 8) 2^-24), the gemv pair's the IEEE one. out may not overlap x, Wg or Wu.
+ * norm_w / norm_eps (optional): the fused input norm as for halo_mi_gemv (the FFN's
+ * post-attention norm folded into the pair).
  */
 typedef struct halo_mi_gate_up_params {
     uint32_t type;

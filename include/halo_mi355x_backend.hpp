@@ -502,5 +502,7 @@ inline constexpr std::uint32_t kGateUpGemv = 43;        // GATE_UP_SWIGLU on the
 inline constexpr std::uint32_t kGateUpGemm = 44;        // ... on the 64..256-row-tile GEMM
 inline constexpr std::uint32_t kGateUpGemmM512 = 45;    // ... on the 512-row-tile GEMM
 inline constexpr std::uint32_t kGateUpGemmSmallM = 46;  // ... on the small-M GEMM
+inline constexpr std::uint32_t kGemmSlabExactSmallM = 47;  // HALO_MI_GEMM_SLAB_EXACT_SMALL_M
+inline constexpr std::uint32_t kGateUpExactSmallM = 48;    // GATE_UP_SWIGLU on the exact small-M GEMM
 
 }  // namespace halo_mi::backend

@@ -222,7 +222,8 @@ void run_type(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
     // fused gate/up (GEMV pair and bf16 GEMM variants) against the oracle's composition
     const std::vector<double> tu = slab_bound(type, wu, rows, cols, x, n_vec);
     const std::vector<double> gg = gemm_bound(type, wg, rows, cols, x, n_vec), gu = gemm_bound(type, wu, rows, cols, x, n_vec);
-    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512, hb::kGateUpGemmSmallM}) {
+    for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512, hb::kGateUpGemmSmallM,
+                             hb::kGateUpExactSmallM}) {
         hb::GateUpArgs g;
         g.wtype = static_cast<hb::DType>(type);
         g.w_gate = hb::TensorRef::of(*w_slab);
@@ -439,14 +440,15 @@ int main(int argc, char** argv) {
             {hb::OpId::RmsNorm, {{38, "rms_norm_cpu_order"}}},
             {hb::OpId::Gemv,
              {{30, "gemv_gguf_ref_b256"}, {31, "gemv_slab_w64"}, {32, "gemm_slab_bf16_mfma"}, {33, "gemv_slab_auto"},
-              {34, "gemm_slab_bf16_mfma_m512"}, {35, "gemv_slab_valu_w64"}, {36, "gemm_slab_bf16_mfma_small_m"}}},
+              {34, "gemm_slab_bf16_mfma_m512"}, {35, "gemv_slab_valu_w64"}, {36, "gemm_slab_bf16_mfma_small_m"},
+              {47, "gemm_slab_exact_small_m"}}},
             {hb::OpId::Swiglu, {{39, "swiglu_b256"}}},
             {hb::OpId::LmHead, {{40, "lm_head_argmax_parts"}}},
             {hb::OpId::Argmax, {{41, "argmax_parts_b256"}}},
             {hb::OpId::Copy, {{42, "copy_async"}}},
             {hb::OpId::GateUpSwiglu,
              {{43, "gate_up_gemv_w64"}, {44, "gate_up_gemm_bf16_mfma"}, {45, "gate_up_gemm_bf16_mfma_m512"},
-              {46, "gate_up_gemm_bf16_mfma_small_m"}}},
+              {46, "gate_up_gemm_bf16_mfma_small_m"}, {48, "gate_up_gemm_exact_small_m"}}},
         };
         for (const auto& [op, want] : pinned) {
             const auto got = be->variants(op);

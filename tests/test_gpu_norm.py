@@ -286,7 +286,14 @@ def test_lm_head_norm(hl, oracle, dev, t, variant):
         return
     tol = gemm_tol(oracle, t, dense, rows, cols, xn) if variant == 3 else slab_gemv_tol(oracle, t, dense, rows, cols, xn)
     assert np.all(np.abs(yl.astype(np.float64) - cpu_logits) <= tol)
-    assert isclose_bits(yl, unfused_gemv(hl, dev, t, wt, xn, rows, cols, variant)), "logits: the fused norm is not bitwise"
+    # the same head on RMS_NORM's output, without the norm: bitwise the same logits and result
+    res2 = torch.full((n_vec, 3), 0xABCD, dtype=torch.int32, device=dev)
+    y2 = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    xg = torch.empty((n_vec, cols), dtype=torch.float32, device=dev)
+    hl.rms_norm(to_dev(x, dev), to_dev(w, dev), xg, n_vec, cols, eps=EPS)
+    hl.lm_head(t, wt, xg, res2, rows, cols, n_vec, logits=y2, layout=lay, variant=variant)
+    assert isclose_bits(yl, host(y2)), "logits: the fused norm is not bitwise rms_norm then the head"
+    assert np.array_equal(r, host(res2).view(np.uint32))
     for v in range(n_vec):
         i = int(np.argmax(yl[v]))
         assert r[v].tolist() == [i, int(yl[v, i:i + 1].view(np.uint32)[0]), 0]

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from helpers import (NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, gemm_emulated, gemm_tol, isclose_bits,
-                     make_weights, max_ratio, slab_gemv_tol)
+                     make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -181,6 +181,70 @@ def test_gemm_small_m_variant(hl, oracle, dev, t, n_vec):
         hl.gemv(t, slab, x33, torch.zeros((33, rows), dtype=torch.float32, device=dev), rows, cols, 33,
                 variant=hl.Variant.SLAB_GEMM_BF16_SMALL_M)
     assert e.value.code == hl.ErrorCode.Unsupported
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("rows,cols", [(130, 1024), (576, 5120)])
+@pytest.mark.parametrize("n_vec", [1, 2, 3, 4, 5, 8])
+def test_gemm_exact_small_m_variant(hl, oracle, dev, t, rows, cols, n_vec):
+    """HALO_MI_GEMM_SLAB_EXACT_SMALL_M: the slab GEMV's arithmetic on 32x32 MFMA tiles, so within
+    the slab GEMV's bound (not the bf16 GEMM's); a second call is bitwise the first; x rows
+    4-byte aligned only, x and y strided with sentinels in the padding; more than 8 vectors is
+    Unsupported."""
+    import torch
+
+    say("gemm exact small-M", NAMES[t], rows, cols, n_vec)
+    buf, stride = make_weights(t, rows, cols, seed=1800 + t + rows)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.random.default_rng(1801 + n_vec).standard_normal((n_vec, cols)).astype(np.float32)
+    xs, ys = cols + 1, rows + 3  # x rows 4-byte aligned only
+    xh = np.full((n_vec, xs), 777.0, np.float32)
+    xh[:, :cols] = x
+    y = torch.full((n_vec, ys), SENTINEL, dtype=torch.float32, device=dev)
+    xd = to_dev(xh, dev)
+    hl.gemv(t, slab, xd, y, rows, cols, n_vec, x_stride=xs, y_stride=ys, variant=hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+    yh = host(y)
+    assert np.all(yh[:, rows:] == SENTINEL), "y padding overwritten"
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
+    err = np.abs(yh[:, :rows].astype(np.float64) - ref)
+    print(f"    exact small-M {NAMES[t]} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    hl.gemv(t, slab, xd, y, rows, cols, n_vec, x_stride=xs, y_stride=ys, variant=hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+    assert isclose_bits(host(y), yh), "a second call gave different bits"
+    if n_vec == 8 and rows == 130:
+        x9 = to_dev(np.ones((9, cols), np.float32), dev)
+        with pytest.raises(hl.HaloError) as e:
+            hl.gemv(t, slab, x9, torch.zeros((9, rows), dtype=torch.float32, device=dev), rows, cols, 9,
+                    variant=hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+        assert e.value.code == hl.ErrorCode.Unsupported
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q6_K, Q5_K))
+@pytest.mark.parametrize("n_vec", [2, 4, 8])
+def test_gate_up_exact_small_m_variant(hl, oracle, dev, t, n_vec):
+    """The fused gate/up pair on the exact small-M GEMM: gate and up each within the slab GEMV's
+    bound, through the chunk reduce's SwiGLU (the fast SiLU's error added)."""
+    import torch
+
+    rows, cols = 576, 5120
+    say("gate_up exact small-M", NAMES[t], n_vec)
+    bg, _ = make_weights(t, rows, cols, seed=1900 + t)
+    bu, _ = make_weights(t, rows, cols, seed=1950 + t)
+    dg, du = dense_of(bg, t, rows, cols, row_bytes(t, cols), 0), dense_of(bu, t, rows, cols, row_bytes(t, cols), 0)
+    sg, su = slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols)
+    x = np.random.default_rng(1901 + n_vec).standard_normal((n_vec, cols)).astype(np.float32)
+    out = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
+    hl.gate_up_swiglu(t, sg, su, to_dev(x, dev), out, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+    g = oracle.matmul(t, dg, rows, cols, x)
+    u = oracle.matmul(t, du, rows, cols, x)
+    ref = oracle.swiglu(g, u)
+    tol = swiglu_tol(g, u, slab_gemv_tol(oracle, t, dg, rows, cols, x), slab_gemv_tol(oracle, t, du, rows, cols, x), ref,
+                     fast=True)
+    err = np.abs(host(out).astype(np.float64) - ref)
+    print(f"    gate_up exact small-M {NAMES[t]} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
 
 
 # ---- split-K failure path and the stream's workspace ------------------------------------------

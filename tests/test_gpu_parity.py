@@ -520,10 +520,11 @@ def test_baseline_q6_k_head(hl, oracle, dev, n_vec):
     assert np.all(err <= tol)
 
 
-GATE_UP_GEMV_MAX = 4  # kGateUpGemvMax: the gate/up auto choice runs the GEMV pair up to 4 vectors
+GATE_UP_GEMV_MAX = 2  # the gate/up auto choice: the GEMV pair up to 2 vectors, the exact small-M GEMM at 3..4
+GATE_UP_EXACT_MAX = 4  # (kGateUpGemvMax), then the bf16 GEMM
 
 
-@pytest.mark.parametrize("n_vec", [2, 4, 8, 64, 512])
+@pytest.mark.parametrize("n_vec", [2, 3, 4, 8, 64, 512])
 def test_baseline_gate_up(hl, oracle, dev, n_vec):
     """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices (and config 5's FFN pair
     at M = 4); the oracle checks every output."""
@@ -549,14 +550,15 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
         u = oracle.matmul(t, wu_c, n, cols, x)
         ref = oracle.swiglu(g, u)  # oracle.gate_up_swiglu's composition (pinned in test_oracle)
         y = yall[:, c0:c1]
-        gemv = n_vec <= GATE_UP_GEMV_MAX  # the auto choice: the GEMV pair up to 4 vectors, then the GEMM
-        if gemv:
+        exact = n_vec <= GATE_UP_EXACT_MAX  # the GEMV pair or the exact small-M GEMM: the GEMV's bound
+        if exact:
             tg = slab_gemv_tol(oracle, t, wg_c, n, cols, x)
             tu = slab_gemv_tol(oracle, t, wu_c, n, cols, x)
         else:
             tg = gemm_tol(oracle, t, wg_c, n, cols, x)
             tu = gemm_tol(oracle, t, wu_c, n, cols, x)
-        tol = swiglu_tol(g, u, tg, tu, ref, fast=not gemv)
+        # the GEMV pair's SiLU is the IEEE form, the GEMMs' the fast one
+        tol = swiglu_tol(g, u, tg, tu, ref, fast=n_vec > GATE_UP_GEMV_MAX)
         err = np.abs(y.astype(np.float64) - ref)
         print(f"    gate_up M={n_vec} columns [{c0}, {c1}): worst |d|/bound = {max_ratio(err, tol):.4f}, "
               f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
