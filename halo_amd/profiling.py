@@ -11,6 +11,10 @@
         device-to-device copy of N bytes in the same run (the copy reads N and writes N bytes), so the
         result is in bytes whatever the counters' unit and sampling.
 
+    python -m halo_amd.profiling counters <counter_collection.csv> [--match NAME]
+        per kernel, the median over its dispatches of every counter of a `rocprofv3 --pmc ...
+        --output-format csv` run, with the dispatch count and the kernel's VGPR / LDS figures.
+
 The traffic summary is a small JSON file that bench.py reports as `roofline.traffic`.
 """
 from __future__ import annotations
@@ -107,6 +111,25 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dic
     }
 
 
+def counters(path: str, match: str | None = None) -> list[dict]:
+    per: dict[str, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    meta: dict[str, dict] = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if match and match not in name:
+                continue
+            per[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            meta[name] = {"grid": r.get("Grid_Size"), "workgroup": r.get("Workgroup_Size"),
+                          "vgpr": r.get("VGPR_Count"), "agpr": r.get("Accum_VGPR_Count"), "lds": r.get("LDS_Block_Size")}
+    out = []
+    for name, cs in per.items():
+        n = max(len(v) for v in cs.values())
+        out.append({"kernel": _short(name), "dispatches": n, **meta[name],
+                    "counters": {c: statistics.median(v) for c, v in sorted(cs.items())}})
+    return sorted(out, key=lambda d: -d["dispatches"])
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m halo_amd.profiling")
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -119,7 +142,17 @@ def main(argv=None) -> int:
     t.add_argument("--kernel", required=True)
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--out")
+    c = sub.add_parser("counters")
+    c.add_argument("csv")
+    c.add_argument("--match")
     a = ap.parse_args(argv)
+    if a.cmd == "counters":
+        for k in counters(a.csv, a.match):
+            print(f"{k['kernel']}: {k['dispatches']} dispatches, grid {k['grid']}, workgroup {k['workgroup']}, "
+                  f"vgpr {k['vgpr']}, agpr {k['agpr']}, lds {k['lds']}")
+            for cn, v in k["counters"].items():
+                print(f"    {cn:34s} {v:18,.0f}")
+        return 0
     if a.cmd == "stats":
         for r in kernel_stats(a.csv, a.match):
             print(f"{r['calls']:8d}  avg {r['avg_us']:10.3f} us  min {r['min_us']:10.3f}  max {r['max_us']:10.3f}  "
