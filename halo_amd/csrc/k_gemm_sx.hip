@@ -9,11 +9,15 @@
 //   - the per-slot scales, mins and code offsets are applied per lane after each slot's two
 //     MFMAs, as the reference's expressions factor them, and each group's sum is brought back
 //     with ldexp.
-// Rows and the arithmetic are those of the slab GEMV (same bound), but a workgroup streams 128
-// W rows x one K chunk with 32 rows per wave and every wave dequantizes nothing: per slot a lane
-// unpacks 16 codes with about 10 masks and folds its vectors' sums, instead of converting and
-// rounding 16 weights. x enters LDS once per workgroup; the chunks' partials go to the
-// workspace and k_gemm_pc_reduce adds them in chunk order (the small-M GEMM's layout).
+// Rows and the arithmetic are those of the slab GEMV (same bound), but a workgroup streams two
+// units (256 W rows) x one K chunk, one 64-row slab per wave, and no wave dequantizes: per slot
+// and row block a lane unpacks 16 codes with about 10 masks and folds its vectors' sums,
+// instead of converting and rounding 16 weights. Each lane loads its row's whole 16-byte slot
+// record (one 1 KB load instruction per wave and slot: half the load instructions of 8-byte
+// loads, which is what lets the stream run at the plain-read rate) and v_permlane32_swap hands
+// each lane half the bytes of the MFMA B layout. x enters LDS once per workgroup; the chunks'
+// partials go to the workspace and k_gemm_pc_reduce adds them in chunk order (the small-M
+// GEMM's layout).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -30,9 +34,10 @@ using namespace dev;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kSxOob = 0x80000000u;  // buffer offset past every resource: the load returns 0
-constexpr int kSxDepth = 16;              // slots of weight codes in flight per wave
+constexpr int kSxDepth = 8;               // slots of weight records in flight per wave (8 KB)
 constexpr uint32_t kSxLdsMax = 52 * 1024;  // x pieces, sums and exponents of one K chunk
 constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per wave of the fill
+constexpr uint32_t kSxWgsPerCu = 1;        // workgroups per CU the K split aims for
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sx_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
@@ -97,56 +102,112 @@ struct SxArgs {
     uint32_t rows, cols, n_vec, kchunks;
 };
 
-// One lane's record of one slot (half h of the row's 16-byte code record and what goes with it)
-// and of one super-block (the header fields), per format; offsets as the SLAB layout.
+// One lane's records of one slot: lane l loads row l's whole 16-byte code record (a wave reads
+// the slab's 1 KB slot record in one 16-byte load per lane) and the side words that go with it;
+// and of one super-block, the header fields of row l. Offsets as the SLAB layout.
 template <uint32_t T>
 struct SxQ {
-    uint2 q;
-    uint32_t aux;  // Q5_K / Q6_K: the top-bit word; Q4_0 / Q8_0: the f16 d
-    uint2 q2;      // Q8_0: the second 16-byte half
+    uint4 q;    // the code record (Q8_0: its first 16 bytes)
+    uint4 q2;   // Q8_0: the second 16 bytes
+    uint2 aux;  // Q5_K: .x the top-bit word; Q6_K: the two halves' top-bit words; Q4_0 / Q8_0: .x the f16 d
 };
 template <uint32_t T>
 struct SxH {
     uint4 hdr;  // Q4_K / Q5_K: bytes 0..15; IQ4_XS: bytes 0..7; Q6_K: the 16 scales
     uint32_t d;  // Q6_K: the f16 d
 };
+// What lane (r, h) = (l % 32, l / 32) needs of one 32-row block b of the slab: half h of row
+// 32 b + r's record (the B operand layout of v_mfma_f32_32x32x16_bf16) and that row's side words.
+struct SxV {
+    uint32_t q0, q1;  // the 8 code bytes (Q8_0: of the first 16 bytes)
+    uint32_t r0, r1;  // Q8_0: of the second 16 bytes
+    uint32_t aux;
+};
 
-template <uint32_t T>
-__device__ __forceinline__ void sx_load_q(SxQ<T>& R, __amdgpu_buffer_rsrc_t w, const SlabGeom& g, uint32_t row, uint32_t h,
-                                          uint32_t s, bool live) {
-    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kSxOob; };
-    if constexpr (T == kQ8_0) {
-        R.q = sx_ld64(w, row * 16 + 8 * h, so(g.q_off + s * 2048));
-        R.q2 = sx_ld64(w, row * 16 + 8 * h, so(g.q_off + s * 2048 + 1024));
-    } else {
-        R.q = sx_ld64(w, row * 16 + 8 * h, so(g.q_off + s * 1024));
-    }
-    if constexpr (T == kQ5_K) R.aux = sx_ld32(w, row * 4, so(g.aux_off + s * 256));
-    if constexpr (T == kQ6_K) R.aux = sx_ld32(w, row * 8 + 4 * h, so(g.aux_off + s * 512));
-    if constexpr (T == kQ4_0 || T == kQ8_0) R.aux = sx_ld16(w, row * 2, so(g.aux_off + s * 128));
+// v_permlane32_swap: {a, b} -> {a with its upper 32 lanes replaced by b's lower 32, b with its
+// lower 32 lanes replaced by a's upper 32}. With a = bytes 0..7 and b = bytes 8..15 of each
+// lane's own row, the first result is half h of row r (block 0) and the second half h of row
+// r + 32 (block 1); with a = b = a per-row word, the row r and row r + 32 words.
+__device__ __forceinline__ uint2 sx_swap(uint32_t a, uint32_t b) {
+    const auto v = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    return uint2{v[0], v[1]};
 }
 
 template <uint32_t T>
-__device__ __forceinline__ void sx_load_h(SxH<T>& H, __amdgpu_buffer_rsrc_t w, const SlabGeom& g, uint32_t row, uint32_t sb,
+__device__ __forceinline__ void sx_views(const SxQ<T>& R, SxV (&V)[2]) {
+    uint2 t = sx_swap(R.q.x, R.q.z);
+    V[0].q0 = t.x, V[1].q0 = t.y;
+    t = sx_swap(R.q.y, R.q.w);
+    V[0].q1 = t.x, V[1].q1 = t.y;
+    if constexpr (T == kQ8_0) {
+        t = sx_swap(R.q2.x, R.q2.z);
+        V[0].r0 = t.x, V[1].r0 = t.y;
+        t = sx_swap(R.q2.y, R.q2.w);
+        V[0].r1 = t.x, V[1].r1 = t.y;
+    }
+    if constexpr (T == kQ6_K) {
+        t = sx_swap(R.aux.x, R.aux.y);  // half h's word of rows r and r + 32
+        V[0].aux = t.x, V[1].aux = t.y;
+    } else if constexpr (T == kQ5_K || T == kQ4_0 || T == kQ8_0) {
+        t = sx_swap(R.aux.x, R.aux.x);
+        V[0].aux = t.x, V[1].aux = t.y;
+    }
+}
+template <uint32_t T>
+__device__ __forceinline__ void sx_hviews(const SxH<T>& H, SxH<T> (&V)[2]) {
+    uint2 t = sx_swap(H.hdr.x, H.hdr.x);
+    V[0].hdr.x = t.x, V[1].hdr.x = t.y;
+    t = sx_swap(H.hdr.y, H.hdr.y);
+    V[0].hdr.y = t.x, V[1].hdr.y = t.y;
+    if constexpr (T != kIQ4_XS) {
+        t = sx_swap(H.hdr.z, H.hdr.z);
+        V[0].hdr.z = t.x, V[1].hdr.z = t.y;
+        t = sx_swap(H.hdr.w, H.hdr.w);
+        V[0].hdr.w = t.x, V[1].hdr.w = t.y;
+    }
+    if constexpr (T == kQ6_K) {
+        t = sx_swap(H.d, H.d);
+        V[0].d = t.x, V[1].d = t.y;
+    }
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void sx_load_q(SxQ<T>& R, __amdgpu_buffer_rsrc_t w, const SlabGeom& g, uint32_t lane, uint32_t s,
                                           bool live) {
     auto so = [&](uint64_t x) { return live ? (uint32_t)x : kSxOob; };
-    if constexpr (T == kQ4_K) H.hdr = sx_ld128(w, row * 16, so(g.aux_off + sb * 1024));
-    if constexpr (T == kQ5_K) H.hdr = sx_ld128(w, row * 16, so(g.sc_off + sb * 1024));
+    if constexpr (T == kQ8_0) {
+        R.q = sx_ld128(w, lane * 16, so(g.q_off + s * 2048));
+        R.q2 = sx_ld128(w, lane * 16, so(g.q_off + s * 2048 + 1024));
+    } else {
+        R.q = sx_ld128(w, lane * 16, so(g.q_off + s * 1024));
+    }
+    if constexpr (T == kQ5_K) R.aux.x = sx_ld32(w, lane * 4, so(g.aux_off + s * 256));
+    if constexpr (T == kQ6_K) R.aux = sx_ld64(w, lane * 8, so(g.aux_off + s * 512));
+    if constexpr (T == kQ4_0 || T == kQ8_0) R.aux.x = sx_ld16(w, lane * 2, so(g.aux_off + s * 128));
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void sx_load_h(SxH<T>& H, __amdgpu_buffer_rsrc_t w, const SlabGeom& g, uint32_t lane, uint32_t sb,
+                                          bool live) {
+    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kSxOob; };
+    if constexpr (T == kQ4_K) H.hdr = sx_ld128(w, lane * 16, so(g.aux_off + sb * 1024));
+    if constexpr (T == kQ5_K) H.hdr = sx_ld128(w, lane * 16, so(g.sc_off + sb * 1024));
     if constexpr (T == kIQ4_XS) {
-        const uint2 v = sx_ld64(w, row * 8, so(g.aux_off + sb * 512));
+        const uint2 v = sx_ld64(w, lane * 8, so(g.aux_off + sb * 512));
         H.hdr = uint4{v.x, v.y, 0u, 0u};
     }
     if constexpr (T == kQ6_K) {
-        H.hdr = sx_ld128(w, row * 16, so(g.sc_off + sb * 1024));
-        H.d = sx_ld16(w, row * 2, so(g.d_off + sb * 128));
+        H.hdr = sx_ld128(w, lane * 16, so(g.sc_off + sb * 1024));
+        H.d = sx_ld16(w, lane * 2, so(g.d_off + sb * 128));
     }
 }
 
-// The two B operands of one slot: K half 0 (record elements 8h + (0, 2, 1, 3, 4, 6, 5, 7)) and
-// K half 1 (16 + the same). Q4_K / Q4_0 deliver K half 1 as 16 q (the A side divides x by 16).
+// The two B operands of one slot for one row block: K half 0 (record elements 8h + (0, 2, 1, 3,
+// 4, 6, 5, 7)) and K half 1 (16 + the same). Q4_K / Q4_0 deliver K half 1 as 16 q (the A side
+// divides x by 16).
 template <uint32_t T>
-__device__ __forceinline__ void sx_codes(const SxQ<T>& R, uint32_t h, u32x4_t& b0, u32x4_t& b1) {
-    const uint32_t Q0 = R.q.x, Q1 = R.q.y;
+__device__ __forceinline__ void sx_codes(const SxV& R, uint32_t h, u32x4_t& b0, u32x4_t& b1) {
+    const uint32_t Q0 = R.q0, Q1 = R.q1;
     if constexpr (T == kQ4_K || T == kQ4_0) {
         const uint32_t S0 = Q0 >> 8, S1 = Q1 >> 8;
         b0 = u32x4_t{Q0 & 0x000F000Fu, S0 & 0x000F000Fu, Q1 & 0x000F000Fu, S1 & 0x000F000Fu};
@@ -159,8 +220,8 @@ __device__ __forceinline__ void sx_codes(const SxQ<T>& R, uint32_t h, u32x4_t& b
             const uint32_t Q[2] = {Q0, Q1};
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
-                lo[w] = and_or_opaque(Q[w], 0x0F0F0F0Fu, (hq << (4 - w)) & 0x10101010u);
-                hi[w] = and_or_opaque(Q[w] >> 4, 0x0F0F0F0Fu, (hq >> w) & 0x10101010u);
+                lo[w] = (Q[w] & 0x0F0F0F0Fu) | ((hq << (4 - w)) & 0x10101010u);
+                hi[w] = ((Q[w] >> 4) & 0x0F0F0F0Fu) | ((hq >> w) & 0x10101010u);
             }
         } else if constexpr (T == kIQ4_XS) {
             lo[0] = iq4_lookup4(Q0);
@@ -169,15 +230,15 @@ __device__ __forceinline__ void sx_codes(const SxQ<T>& R, uint32_t h, u32x4_t& b
             hi[1] = iq4_lookup4(Q1 >> 4);
         } else if constexpr (T == kQ6_K) {
             const uint32_t hq = R.aux;
-            lo[0] = and_or_opaque(Q0, 0x0F0F0F0Fu, hq & 0x30303030u);
-            lo[1] = and_or_opaque(Q1, 0x0F0F0F0Fu, (hq << 4) & 0x30303030u);
-            hi[0] = and_or_opaque(Q0 >> 4, 0x0F0F0F0Fu, (hq >> 2) & 0x30303030u);
-            hi[1] = and_or_opaque(Q1 >> 4, 0x0F0F0F0Fu, (hq << 2) & 0x30303030u);
+            lo[0] = (Q0 & 0x0F0F0F0Fu) | (hq & 0x30303030u);
+            lo[1] = (Q1 & 0x0F0F0F0Fu) | ((hq << 4) & 0x30303030u);
+            hi[0] = ((Q0 >> 4) & 0x0F0F0F0Fu) | ((hq >> 2) & 0x30303030u);
+            hi[1] = ((Q1 >> 4) & 0x0F0F0F0Fu) | ((hq << 2) & 0x30303030u);
         } else {  // Q8_0: q + 128 as unsigned bytes
             lo[0] = Q0 ^ 0x80808080u;
             lo[1] = Q1 ^ 0x80808080u;
-            hi[0] = R.q2.x ^ 0x80808080u;
-            hi[1] = R.q2.y ^ 0x80808080u;
+            hi[0] = R.r0 ^ 0x80808080u;
+            hi[1] = R.r1 ^ 0x80808080u;
         }
         b0 = u32x4_t{sx_b02(lo[0]), sx_b13(lo[0]), sx_b02(lo[1]), sx_b13(lo[1])};
         b1 = u32x4_t{sx_b02(hi[0]), sx_b13(hi[0]), sx_b02(hi[1]), sx_b13(hi[1])};
@@ -205,23 +266,27 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     const uint32_t S = a.cols / kSlot;
     const SlabGeom g = slab_geom(T, a.cols);
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
-    const uint32_t u = blockIdx.x / a.kchunks, chunk = blockIdx.x % a.kchunks;
+    const uint32_t units = PAIR ? slabs : (slabs + 1) / 2;
+    const uint32_t chunk = blockIdx.x % a.kchunks;
     const uint32_t ng = S / 8, base = ng / a.kchunks, extra = ng % a.kchunks;
     const uint32_t g0 = chunk * base + min(chunk, extra);
     const uint32_t ngc = base + (chunk < extra ? 1u : 0u);  // super-blocks of this chunk
     const uint32_t s_begin = 8 * g0, s_end = 8 * (g0 + ngc);
     const uint32_t ns = s_end - s_begin;
-    const uint32_t mat = wave >> 1, rb = wave & 1u;
+    // wave w: unit 2 (blockIdx / kchunks) + w / 2, matrix w % 2 (PAIR: gate / up; else the
+    // unit's two slabs), all 64 rows of that slab
+    const uint32_t unit = 2 * (blockIdx.x / a.kchunks) + (wave >> 1), mat = wave & 1u;
+    const bool live_unit = unit < units;  // an odd unit count leaves the last workgroup's second unit empty
+    const uint32_t lu = min(unit, units - 1);
     const uint32_t r = lane & 31u, h = lane >> 5;
     const uint8_t* slab_ptr;
     if constexpr (PAIR) {
-        slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)u * g.slab_bytes;
+        slab_ptr = (mat ? a.w1 : a.w0) + (uint64_t)lu * g.slab_bytes;
     } else {
         // a missing second slab reads the last one again: its outputs are never stored
-        slab_ptr = a.w0 + (uint64_t)min(2 * u + mat, slabs - 1) * g.slab_bytes;
+        slab_ptr = a.w0 + (uint64_t)min(2 * lu + mat, slabs - 1) * g.slab_bytes;
     }
     const __amdgpu_buffer_rsrc_t wres = sx_rsrc(slab_ptr, (uint32_t)g.slab_bytes);
-    const uint32_t wrow = 32 * rb + r;
     // LDS: pieces [slot][K half][lane half][RS rows] x 16 B, then x sums [slot][K half][8 vectors],
     // then the groups' exponents [group][8 vectors]
     uint8_t* lds = reinterpret_cast<uint8_t*>(sxl);
@@ -245,8 +310,8 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     }
     SxQ<T> R[kSxDepth];
     SxH<T> H[2];
-    auto load_q = [&](int q, uint32_t s) { sx_load_q<T>(R[q], wres, g, wrow, h, s, s < s_end); };
-    auto load_h = [&](int i, uint32_t sb) { sx_load_h<T>(H[i], wres, g, wrow, sb, 8 * sb < s_end); };
+    auto load_q = [&](int q, uint32_t s) { sx_load_q<T>(R[q], wres, g, lane, s, s < s_end); };
+    auto load_h = [&](int i, uint32_t sb) { sx_load_h<T>(H[i], wres, g, lane, sb, 8 * sb < s_end); };
     load_h(0, s_begin / 8);
     load_h(1, s_begin / 8 + 1);
 #pragma unroll
@@ -284,111 +349,131 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     }
     __syncthreads();
 
-    // ---- the slots: two MFMAs into a fresh tile, then the fold into each vector's sums
+    // ---- the slots: per row block, two MFMAs into a fresh tile, then the fold into each
+    // vector's sums
     const uint32_t hd = h;  // the accumulator layout's lane half: vectors hd, hd + 2, ...
     const uint32_t arow = min(r, RS - 1);  // this lane's A row (rows past RS hold no piece)
     const uint8_t* abase = lds + (h * RS + arow) * 16;
     const uint32_t nv_lane = (a.n_vec + 1 - hd) / 2;  // vectors of this lane half
-    float acc[NP];
+    float acc[2][NP];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) acc[p] = 0.0f;
-    float sa[NP], sb[NP];
-    auto group_begin = [&]() {
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int p = 0; p < NP; ++p) sa[p] = sb[p] = 0.0f;
+        for (int p = 0; p < NP; ++p) acc[b][p] = 0.0f;
+    float sa[2][NP], sb[2][NP];
+    SxH<T> HV[2];  // the current super-block's header words of rows r and r + 32
+    auto group_begin = [&](int hi) {
+        sx_hviews<T>(H[hi], HV);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) sa[b][p] = sb[b][p] = 0.0f;
     };
     auto slot = [&](int q, uint32_t s) {
+        const int qr = q & (kSxDepth - 1);
         const uint32_t ls = s - s_begin, j = (uint32_t)(q & 7);
-        u32x4_t b0, b1;
-        sx_codes<T>(R[q], h, b0, b1);
+        SxV V[2];
+        sx_views<T>(R[qr], V);
         const uint4 a0 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 0) * 2 * RS * 16);
         const uint4 a1 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 1) * 2 * RS * 16);
         const float* xs = xsum + ls * 16 + hd;  // [K half][vector], vector 2 p + hd
-        floatx16 D0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, b0),
-                                                              floatx16{}, 0, 0, 0);
-        if constexpr (T == kQ6_K) {
-            // the two halves have their own scales
-            const floatx16 D1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1),
-                                                                        __builtin_bit_cast(bf16x8, b1), floatx16{}, 0, 0, 0);
-            const SxH<T>& Hs = H[q >> 3];
-            const uint32_t w = (j >> 1) == 0 ? Hs.hdr.x : (j >> 1) == 1 ? Hs.hdr.y : (j >> 1) == 2 ? Hs.hdr.z : Hs.hdr.w;
-            const float sA = sbyte(w, 2 * (j & 1)), sB = sbyte(w, 2 * (j & 1) + 1);
+        load_q(qr, s + kSxDepth);
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                const float dlo = (D0[3 * p] + D0[3 * p + 1]) + D0[3 * p + 2];
-                const float dhi = (D1[3 * p] + D1[3 * p + 1]) + D1[3 * p + 2];
-                sa[p] = fmaf(sA, fmaf(-32.0f, xs[2 * p], dlo), sa[p]);
-                sa[p] = fmaf(sB, fmaf(-32.0f, xs[8 + 2 * p], dhi), sa[p]);
-            }
-        } else {
-            D0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, b1), D0, 0, 0, 0);
-            float dot[NP], xss[NP];
-#pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                dot[p] = (D0[3 * p] + D0[3 * p + 1]) + D0[3 * p + 2];
-                xss[p] = xs[2 * p] + xs[8 + 2 * p];
-            }
-            if constexpr (T == kQ4_K || T == kQ5_K) {
-                const SxH<T>& Hs = H[q >> 3];
-                uint32_t sc, m;
-                q4k_sc_m(Hs.hdr.y, Hs.hdr.z, Hs.hdr.w, j, sc, m);
-                const float fsc = (float)sc, fm = (float)m;
+        for (int b = 0; b < 2; ++b) {
+            u32x4_t b0, b1;
+            sx_codes<T>(V[b], h, b0, b1);
+            floatx16 D0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a0), __builtin_bit_cast(bf16x8, b0),
+                                                                  floatx16{}, 0, 0, 0);
+            if constexpr (T == kQ6_K) {
+                // the two halves have their own scales
+                const floatx16 D1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1),
+                                                                            __builtin_bit_cast(bf16x8, b1), floatx16{}, 0, 0, 0);
+                const SxH<T>& Hs = HV[b];
+                const uint32_t w = (j >> 1) == 0 ? Hs.hdr.x : (j >> 1) == 1 ? Hs.hdr.y : (j >> 1) == 2 ? Hs.hdr.z : Hs.hdr.w;
+                const float sA = sbyte(w, 2 * (j & 1)), sB = sbyte(w, 2 * (j & 1) + 1);
 #pragma unroll
                 for (int p = 0; p < NP; ++p) {
-                    sa[p] = fmaf(fsc, dot[p], sa[p]);
-                    sb[p] = fmaf(fm, xss[p], sb[p]);
+                    const float dlo = (D0[3 * p] + D0[3 * p + 1]) + D0[3 * p + 2];
+                    const float dhi = (D1[3 * p] + D1[3 * p + 1]) + D1[3 * p + 2];
+                    sa[b][p] = fmaf(sA, fmaf(-32.0f, xs[2 * p], dlo), sa[b][p]);
+                    sa[b][p] = fmaf(sB, fmaf(-32.0f, xs[8 + 2 * p], dhi), sa[b][p]);
                 }
-            } else if constexpr (T == kIQ4_XS) {
-                const SxH<T>& Hs = H[q >> 3];
-                const float fl = (float)iq4xs_ls(Hs.hdr.x >> 16, Hs.hdr.y, j);
+            } else {
+                D0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), __builtin_bit_cast(bf16x8, b1), D0, 0,
+                                                             0, 0);
+                float dot[NP], xss[NP];
 #pragma unroll
-                for (int p = 0; p < NP; ++p) sa[p] = fmaf(fl, fmaf(-128.0f, xss[p], dot[p]), sa[p]);
-            } else {  // Q4_0, Q8_0: the slot's own d
-                const float d = h2f(R[q].aux);
-                constexpr float off = T == kQ4_0 ? -8.0f : -128.0f;
+                for (int p = 0; p < NP; ++p) {
+                    dot[p] = (D0[3 * p] + D0[3 * p + 1]) + D0[3 * p + 2];
+                    xss[p] = xs[2 * p] + xs[8 + 2 * p];
+                }
+                if constexpr (T == kQ4_K || T == kQ5_K) {
+                    const SxH<T>& Hs = HV[b];
+                    uint32_t sc, m;
+                    q4k_sc_m(Hs.hdr.y, Hs.hdr.z, Hs.hdr.w, j, sc, m);
+                    const float fsc = (float)sc, fm = (float)m;
 #pragma unroll
-                for (int p = 0; p < NP; ++p) sa[p] = fmaf(d, fmaf(off, xss[p], dot[p]), sa[p]);
+                    for (int p = 0; p < NP; ++p) {
+                        sa[b][p] = fmaf(fsc, dot[p], sa[b][p]);
+                        sb[b][p] = fmaf(fm, xss[p], sb[b][p]);
+                    }
+                } else if constexpr (T == kIQ4_XS) {
+                    const SxH<T>& Hs = HV[b];
+                    const float fl = (float)iq4xs_ls(Hs.hdr.x >> 16, Hs.hdr.y, j);
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) sa[b][p] = fmaf(fl, fmaf(-128.0f, xss[p], dot[p]), sa[b][p]);
+                } else {  // Q4_0, Q8_0: the slot's own d
+                    const float d = h2f(V[b].aux);
+                    constexpr float off = T == kQ4_0 ? -8.0f : -128.0f;
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) sa[b][p] = fmaf(d, fmaf(off, xss[p], dot[p]), sa[b][p]);
+                }
             }
         }
-        load_q(q, s + kSxDepth);
     };
-    auto group_end = [&](int hi, uint32_t gg) {
+    auto group_end = [&](uint32_t gg) {
         const int* ex = expo + gg * 8 + hd;
-        float d = 1.0f, dmin = 0.0f;
-        if constexpr (T == kQ4_K || T == kQ5_K) {
-            d = h2f(H[hi].hdr.x & 0xFFFFu);
-            dmin = h2f(H[hi].hdr.x >> 16);
-        } else if constexpr (T == kIQ4_XS) {
-            d = h2f(H[hi].hdr.x & 0xFFFFu);
-        } else if constexpr (T == kQ6_K) {
-            d = h2f(H[hi].d);
-        }
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            float grp;
-            if constexpr (T == kQ4_K || T == kQ5_K) grp = fmaf(d, sa[p], -(dmin * sb[p]));
-            else if constexpr (T == kQ4_0 || T == kQ8_0) grp = sa[p];
-            else grp = d * sa[p];
-            acc[p] += ldexpf(grp, ex[2 * p]);
+        for (int b = 0; b < 2; ++b) {
+            float d = 1.0f, dmin = 0.0f;
+            if constexpr (T == kQ4_K || T == kQ5_K) {
+                d = h2f(HV[b].hdr.x & 0xFFFFu);
+                dmin = h2f(HV[b].hdr.x >> 16);
+            } else if constexpr (T == kIQ4_XS) {
+                d = h2f(HV[b].hdr.x & 0xFFFFu);
+            } else if constexpr (T == kQ6_K) {
+                d = h2f(HV[b].d);
+            }
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                float grp;
+                if constexpr (T == kQ4_K || T == kQ5_K) grp = fmaf(d, sa[b][p], -(dmin * sb[b][p]));
+                else if constexpr (T == kQ4_0 || T == kQ8_0) grp = sa[b][p];
+                else grp = d * sa[b][p];
+                acc[b][p] += ldexpf(grp, ex[2 * p]);
+            }
         }
     };
-    for (uint32_t i0 = s_begin; i0 < s_end; i0 += kSxDepth) {
-        group_begin();
+    for (uint32_t i0 = s_begin; i0 < s_end; i0 += 16) {
+        group_begin(0);
 #pragma unroll
         for (int q = 0; q < 8; ++q) slot(q, i0 + q);
-        group_end(0, (i0 - s_begin) / 8);
+        group_end((i0 - s_begin) / 8);
         load_h(0, i0 / 8 + 2);
         if (i0 + 8 >= s_end) break;
-        group_begin();
+        group_begin(1);
 #pragma unroll
-        for (int q = 8; q < kSxDepth; ++q) slot(q, i0 + q);
-        group_end(1, (i0 - s_begin) / 8 + 1);
+        for (int q = 8; q < 16; ++q) slot(q, i0 + q);
+        group_end((i0 - s_begin) / 8 + 1);
         load_h(1, i0 / 8 + 3);
     }
-    float* P = a.partials + ((uint64_t)u * a.kchunks + chunk) * 32 * 128 + 64 * mat + 32 * rb + r;
+    if (!live_unit) return;
+    float* P = a.partials + ((uint64_t)unit * a.kchunks + chunk) * 32 * 128 + 64 * mat + r;
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-        if ((uint32_t)p < nv_lane) P[(2 * p + hd) * 128] = acc[p];
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            if ((uint32_t)p < nv_lane) P[(2 * p + hd) * 128 + 32 * b] = acc[b][p];
 }
 
 template <bool PAIR, int NP>
@@ -423,12 +508,12 @@ bool gemm_sx_plan(uint32_t units, uint32_t cols, uint32_t n_vec, uint32_t* kc, s
     // a chunk's (vector, group) pairs: at most kSxPairs per wave of the fill
     const uint32_t max_groups = std::min<uint32_t>(kSxLdsMax / per_group, 4 * kSxPairs / n_vec);
     const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
-    uint32_t k = std::clamp<uint32_t>((4 * sx_cu_count() + units - 1) / units, kc_min, ng);
+    const uint32_t wgs = (units + 1) / 2;  // a workgroup streams two units
+    uint32_t k = std::clamp<uint32_t>((kSxWgsPerCu * sx_cu_count() + wgs - 1) / wgs, kc_min, ng);
     while (k > kc_min && (uint64_t)units * k * 32 * 128 > kPartialFloats) --k;
     if ((uint64_t)units * k * 32 * 128 > kPartialFloats) return false;
-    const uint32_t groups = (ng + k - 1) / k;
     *kc = k;
-    *lds = (size_t)groups * per_group;
+    *lds = (size_t)((ng + k - 1) / k) * per_group;
     return true;
 }
 
@@ -446,7 +531,7 @@ int launch_gemm_sx(uint32_t type, bool pair, const GemmArgs& g, Workspace* ws, u
         xs = g.cols;
     }
     const SxArgs a{g.w0, g.w1, x, xs, ws->partials, g.rows, g.cols, g.n_vec, kc};
-    const dim3 grid(units * kc);
+    const dim3 grid(((units + 1) / 2) * kc);
     const int np = (int)(g.n_vec + 1) / 2;
     switch (np) {
         case 1: pair ? launch_sx_np<true, 1>(type, a, grid, lds, st) : launch_sx_np<false, 1>(type, a, grid, lds, st); break;
