@@ -361,7 +361,7 @@ int halo_mi_stream_check(void* stream);
 
 /*
  * Every (device, stream) pair that runs a gemv-family call gets a workspace of device memory
- * (split-K words, GEMM partials and staging, argmax parts: about 116 MiB), allocated on the
+ * (split-K words, GEMM partials and staging, argmax parts, normalized x: about 136 MiB), allocated on the
  * first call. halo_mi_stream_release() synchronizes `stream` and frees its workspace on the
  * current device; call it before destroying the stream. A later call on the stream allocates
  * a new one.
