@@ -43,8 +43,10 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     };
     uint32_t ks = 1;
     // Measured on MI355X: about 4 workgroups per slab up to 1088 per launch; small matrices
-    // gain more from a short split-K fix-up than from more workgroups (floor of 128).
-    const uint32_t target_wg = std::clamp(4 * units, 128u, 1088u);
+    // gain more from a short split-K fix-up than from more workgroups: 2 per slab up to 128
+    // slabs (5120 x 5120 Q4_K: 7.56 -> 6.74 us; 12288 x 5120 keeps 4: 9.67 against 10.17 us),
+    // and a floor of 128.
+    const uint32_t target_wg = std::clamp((units <= 128 ? 2 : 4) * units, 128u, 1088u);
     if (have_ws && units < target_wg) ks = std::min((target_wg + units - 1) / units, ngrp);
     while (ks > 1 && !fits(ks)) --ks;
     // The one-group form (below 1024 slabs): enough K chunks that a chunk's groups fit one

@@ -97,7 +97,7 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
     // K split: a chip's worth of workgroups (as a single matrix of all the slabs would take), and
     // at least enough chunks that a chunk's slot groups fit one workgroup of one-group waves
     const uint32_t nw1 = group_waves<kMaxGemvVec>(ta, tb);
-    const uint32_t target = std::clamp<uint32_t>(4 * (uint32_t)slabs, 128u, 1088u);
+    const uint32_t target = std::clamp<uint32_t>((slabs <= 128 ? 2 : 4) * (uint32_t)slabs, 128u, 1088u);
     uint32_t ks = std::min<uint32_t>((target + (uint32_t)slabs - 1) / (uint32_t)slabs, ngrp);
     ks = std::min(std::max(ks, (ngrp + nw1 - 1) / nw1), ngrp);
     if (ks > 1 && (ks > kMaxChunks || slabs * ks * kMaxGemvVec * 64 > kSlots))
