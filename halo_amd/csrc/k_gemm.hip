@@ -209,27 +209,40 @@ __device__ __forceinline__ PcOff pc_offsets(uint32_t r, uint32_t h) {
     else return {r * 16 + 8 * h, r * 8 + 4 * h, r * 16, r * 2};
 }
 
-// Stage s (slot s of K) of one producer thread's records; `slab` is the wave's slab resource.
-// Stage s of one producer thread's records; `slab` is the wave's slab resource. A stage that is
-// not live reads past the resource (no branch): zero records, i.e. zero weights.
+// The per-super-block fields of a weight record (none for the 32-weight block formats).
 template <uint32_t T>
-__device__ __forceinline__ void pc_load_w(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
+struct SmH {};
+template <>
+struct SmH<kQ4_K> {
+    uint4 hdr;
+};
+template <>
+struct SmH<kQ5_K> {
+    uint4 hdr;
+};
+template <>
+struct SmH<kIQ4_XS> {
+    uint2 hdr;
+};
+template <>
+struct SmH<kQ6_K> {
+    uint4 sc;  // the 16 int8 scales of the row's super-block
+    uint32_t d;
+};
+
+// The per-slot fields of a weight record (codes; Q4_0 / Q8_0's d, Q5_K / Q6_K's high bits).
+template <uint32_t T>
+__device__ __forceinline__ void sm_load_q(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
                                           uint32_t s, bool live) {
-    const uint32_t sb = s / 8;
     auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
-    if constexpr (T == kQ4_K) {
+    if constexpr (T == kQ4_K || T == kIQ4_XS) {
         R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
     } else if constexpr (T == kQ4_0) {
         R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
         R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
     } else if constexpr (T == kQ5_K) {
         R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
         R.qh = bld32(slab, o.aux, so(g.aux_off + s * 256));
-        R.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
-    } else if constexpr (T == kIQ4_XS) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
     } else if constexpr (T == kQ8_0) {
         R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
         R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
@@ -237,8 +250,35 @@ __device__ __forceinline__ void pc_load_w(PcW<T>& R, __amdgpu_buffer_rsrc_t slab
     } else {
         R.ql = bld64(slab, o.q, so(g.q_off + s * 1024));
         R.qh = bld32(slab, o.aux, so(g.aux_off + s * 512));
-        R.sc = bld16(slab, o.sc, so(g.sc_off + sb * 1024 + 2 * (s % 8)));
-        R.d = bld16(slab, o.d, so(g.d_off + sb * 128));
+    }
+}
+
+// The per-super-block fields of super-block sb.
+template <uint32_t T>
+__device__ __forceinline__ void sm_load_h(SmH<T>& H, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
+                                          uint32_t sb, bool live) {
+    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
+    if constexpr (T == kQ4_K) {
+        H.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
+    } else if constexpr (T == kQ5_K) {
+        H.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+    } else if constexpr (T == kIQ4_XS) {
+        H.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
+    } else if constexpr (T == kQ6_K) {
+        H.sc = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+        H.d = bld16(slab, o.d, so(g.d_off + sb * 128));
+    }
+}
+
+// Completes R with sub-block j's fields of the super-block header H.
+template <uint32_t T>
+__device__ __forceinline__ void sm_merge(PcW<T>& R, const SmH<T>& H, int j) {
+    if constexpr (T == kQ4_K || T == kQ5_K || T == kIQ4_XS) {
+        R.hdr = H.hdr;
+    } else if constexpr (T == kQ6_K) {
+        const uint32_t w = (j >> 1) == 0 ? H.sc.x : (j >> 1) == 1 ? H.sc.y : (j >> 1) == 2 ? H.sc.z : H.sc.w;
+        R.sc = (w >> (16 * (j & 1))) & 0xFFFFu;
+        R.d = H.d;
     }
 }
 
@@ -543,16 +583,22 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     const PcOff off = pc_offsets<T>(r, h);
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
     const uint32_t wdst = (mat * 64 + r) * kPcLd + 8 * h;
+    // per-slot codes in a ring of kPcDepth stages; the super-block fields (scales, mins, d) once
+    // per super-block: Hc serves the stages being written, Hn is the next super-block's
     PcW<T> R[kPcDepth];
-    auto load = [&](int slot, uint32_t s) { pc_load_w<T>(R[slot], slab, g, off, s, s < s_end); };
+    SmH<T> Hc, Hn;
+    auto load = [&](int slot, uint32_t s) { sm_load_q<T>(R[slot], slab, g, off, s, s < s_end); };
     // j: the stage's slot within its super-block (static in the unrolled loop)
     auto store = [&](int slot, uint32_t j, int buf) {
+        PcW<T> W = R[slot];
+        sm_merge<T>(W, Hc, j);
         bf16x8 lo, hi;
-        pc_dequant<T>(R[slot], h, j, inv_unit, lo, hi);
+        pc_dequant<T>(W, h, j, inv_unit, lo, hi);
         __bf16* st = lds + buf * STAGE;
         *reinterpret_cast<bf16x8*>(st + wdst) = lo;
         *reinterpret_cast<bf16x8*>(st + wdst + 16) = hi;
     };
+    sm_load_h<T>(Hc, slab, g, off, s_begin / 8, s_begin < s_end);
 #pragma unroll
     for (int p = 0; p < kPcDepth; ++p) load(p, s_begin + p);
     store(0, 0, 0);
@@ -562,13 +608,18 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     pc_sync();  // B_0
     // iteration i writes local stage i + 2 from ring slot (i + 2) % 4 into buffer (i + 2) % 4;
     // unrolled by 8 so slot, buffer and sub-block are static, and branch-free so the loads'
-    // waits are exact (stages past the end are junk that no consumer reads)
+    // waits are exact (stages past the end are junk that no consumer reads). Iteration q = 2
+    // loads the first stage of the next super-block and its header; q = 6 writes that stage.
+    static_assert(kPcUnroll == 8 && kPcDepth == 4, "one super-block per unrolled iteration");
     for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcUnroll) {
 #pragma unroll
         for (int q = 0; q < kPcUnroll; ++q) {
             const int k = (q + 2) % kPcDepth;
+            if (q == 6) Hc = Hn;
             store(k, (q + 2) % 8, (q + 2) % kPcBufs);
-            load(k, s_begin + i0 + q + 2 + kPcDepth);
+            const uint32_t sl = s_begin + i0 + q + 2 + kPcDepth;
+            load(k, sl);
+            if (q == 2) sm_load_h<T>(Hn, slab, g, off, sl / 8, sl < s_end);
             pc_sync();  // B_{i+1}
             // keep each stage's work between its barriers: hoisting a later stage's decode would
             // make it wait for that stage's loads
@@ -698,11 +749,19 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
     const PcOff off = pc_offsets<T>(srow, h);
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
     const uint32_t wdst = (32 * wave + r) * kPcLd + 8 * h;
+    // per-slot codes kLmWDepth stages ahead; the super-block fields once per super-block (Hc
+    // serves the stages being dequantized, Hn is the next super-block's)
     PcW<T> R[kLmWDepth];
-    auto load_w = [&](int slot, uint32_t s) { pc_load_w<T>(R[slot], wres, g, off, s, s < s_end); };
+    SmH<T> Hc, Hn;
+    auto load_w = [&](int slot, uint32_t s) { sm_load_q<T>(R[slot], wres, g, off, s, s < s_end); };
+    auto dequant = [&](int slot, uint32_t j, bf16x8& lo, bf16x8& hi) {
+        PcW<T> W = R[slot];
+        sm_merge<T>(W, Hc, j);
+        pc_dequant<T>(W, h, j, inv_unit, lo, hi);
+    };
     auto store_w = [&](int slot, uint32_t j, int buf) {
         bf16x8 lo, hi;
-        pc_dequant<T>(R[slot], h, j, inv_unit, lo, hi);
+        dequant(slot, j, lo, hi);
         __bf16* dst = lds + buf * STAGE + wdst;
         *reinterpret_cast<bf16x8*>(dst) = lo;
         *reinterpret_cast<bf16x8*>(dst + 16) = hi;
@@ -743,6 +802,8 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 
     // prologue: W records of stages 0..3; stages 0 and 1 dequantized into LDS buffers 0 and 1;
     // x of stages 0 and 1; stage 0's W fragments
+    static_assert(kPcUnroll == 8 && kLmWDepth == 4, "one super-block per unrolled iteration");
+    sm_load_h<T>(Hc, wres, g, off, s_begin / 8, s_begin < s_end);
 #pragma unroll
     for (int p = 0; p < kLmWDepth; ++p) load_w(p, s_begin + p);
     load_a(0, 0, s_begin);
@@ -768,7 +829,8 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
             mma(xb, 0, Bc[0]);
             read_b(bufn, Bn);
             bf16x8 lo, hi;
-            pc_dequant<T>(R[ws], h, (q + 2) % 8, inv_unit, lo, hi);
+            if (q == 6) Hc = Hn;  // stage i + 2 starts the next super-block
+            dequant(ws, (q + 2) % 8, lo, hi);
             load_a(xb, 0, s_begin + i0 + q + 2);
             if constexpr (MBW == 4) {  // with fewer MFMAs the VALU work dominates: no pattern
 #pragma unroll
@@ -791,7 +853,9 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
             // x before W: vmcnt counts in order, so the wait for these x fragments (two stages
             // on) then covers only W records issued a stage earlier, which have come from HBM
             load_a(xb, 1, s_begin + i0 + q + 2);
-            load_w(ws, s_begin + i0 + q + 2 + kLmWDepth);
+            const uint32_t sl = s_begin + i0 + q + 2 + kLmWDepth;
+            load_w(ws, sl);
+            if (q == 2) sm_load_h<T>(Hn, wres, g, off, sl / 8, sl < s_end);  // the next super-block
             if constexpr (MBW == 4) {
 #pragma unroll
                 for (int k = 0; k < 16; ++k) {
@@ -875,79 +939,6 @@ constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
 constexpr uint32_t kSmLdsMax = 48 * 1024;  // x bytes of one workgroup's K chunk in LDS
 constexpr uint32_t kSmLdsMax8 = 24 * 1024;  // the same at 8 rows, read from fp32 x by the kernel
 __host__ __device__ constexpr uint32_t sm_lds_max(uint32_t xr) { return xr == 8 ? kSmLdsMax8 : kSmLdsMax; }
-
-// The per-super-block fields of a weight record (none for the 32-weight block formats).
-template <uint32_t T>
-struct SmH {};
-template <>
-struct SmH<kQ4_K> {
-    uint4 hdr;
-};
-template <>
-struct SmH<kQ5_K> {
-    uint4 hdr;
-};
-template <>
-struct SmH<kIQ4_XS> {
-    uint2 hdr;
-};
-template <>
-struct SmH<kQ6_K> {
-    uint4 sc;  // the 16 int8 scales of the row's super-block
-    uint32_t d;
-};
-
-// The per-slot fields of pc_load_w (codes; Q4_0 / Q8_0's d, Q5_K / Q6_K's high bits).
-template <uint32_t T>
-__device__ __forceinline__ void sm_load_q(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
-                                          uint32_t s, bool live) {
-    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
-    if constexpr (T == kQ4_K || T == kIQ4_XS) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-    } else if constexpr (T == kQ4_0) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
-    } else if constexpr (T == kQ5_K) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 256));
-    } else if constexpr (T == kQ8_0) {
-        R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
-        R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
-        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
-    } else {
-        R.ql = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 512));
-    }
-}
-
-// The per-super-block fields of super-block sb.
-template <uint32_t T>
-__device__ __forceinline__ void sm_load_h(SmH<T>& H, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
-                                          uint32_t sb, bool live) {
-    auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
-    if constexpr (T == kQ4_K) {
-        H.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
-    } else if constexpr (T == kQ5_K) {
-        H.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
-    } else if constexpr (T == kIQ4_XS) {
-        H.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
-    } else if constexpr (T == kQ6_K) {
-        H.sc = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
-        H.d = bld16(slab, o.d, so(g.d_off + sb * 128));
-    }
-}
-
-// Completes R with sub-block j's fields of the super-block header H.
-template <uint32_t T>
-__device__ __forceinline__ void sm_merge(PcW<T>& R, const SmH<T>& H, int j) {
-    if constexpr (T == kQ4_K || T == kQ5_K || T == kIQ4_XS) {
-        R.hdr = H.hdr;
-    } else if constexpr (T == kQ6_K) {
-        const uint32_t w = (j >> 1) == 0 ? H.sc.x : (j >> 1) == 1 ? H.sc.y : (j >> 1) == 2 ? H.sc.z : H.sc.w;
-        R.sc = (w >> (16 * (j & 1))) & 0xFFFFu;
-        R.d = H.d;
-    }
-}
 
 // x bytes in LDS per slot of K: two K halves x two lane halves x XR rows x 16 B.
 __host__ __device__ constexpr uint32_t sm_x_bytes_per_slot(uint32_t xr) { return 64u * xr; }
