@@ -61,7 +61,8 @@ constexpr int kPcDepth = 4;   // stages of producer W loads in flight (a ring of
 constexpr int kPcADepth = 4;  // stages of consumer x-fragment loads in flight
 constexpr uint32_t kPcOob = 0x80000000u;  // buffer offset past every resource: the load returns 0
 constexpr int kPcBufs = 4;    // LDS stages (the producers write two stages ahead)
-constexpr int kPcUnroll = 8;  // producer loop unroll: ring slot, LDS buffer and Q4_K sub-block static
+constexpr int kPcUnroll = 8;  // k_gemm_lm's loop unroll: ring slot, LDS buffer and Q4_K sub-block static
+constexpr int kPcPUnroll = kPcDepth > 8 ? kPcDepth : 8;  // the same for k_gemm_pc's producers
 
 struct GemmPcArgs {
     const uint8_t* w0;     // gate (PAIR) or the matrix
@@ -417,7 +418,10 @@ __device__ __forceinline__ uint32_t mfma32_row(uint32_t r, uint32_t lane) { retu
 template <uint32_t T, bool PAIR, int MB>
 __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     constexpr int BM = 64 * MB;
-    constexpr int WM = MB == 1 ? 2 : 4, WN = 4 / WM;
+    // KH (64-row tiles): wave w multiplies x block w % 2 by all four W blocks over K half w / 2
+    // of every stage, so each x fragment is loaded by one wave; the pairs' sums meet at the end
+    constexpr bool KH = MB == 1;
+    constexpr int WM = MB == 1 ? 2 : 4, WN = KH ? 1 : 4 / WM;
     constexpr int MBW = BM / WM / 32, NBW = 4 / WN;
     constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage (W only)
     __shared__ __bf16 lds[kPcBufs * STAGE];
@@ -457,11 +461,11 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
         s_end = 8 * (g0 + base + (chunk < extra ? 1u : 0u));
     }
     const uint32_t n = s_end - s_begin;
-    const uint32_t n_pad = (n + kPcUnroll - 1) / kPcUnroll * kPcUnroll;
+    const uint32_t n_pad = (n + kPcPUnroll - 1) / kPcPUnroll * kPcPUnroll;
 
     if (wave < 4) {
         // ---------------- consumers ----------------
-        const uint32_t wm = wave % WM, wn = wave / WM;
+        const uint32_t wm = wave % WM, wn = KH ? 0u : wave / WM, kh = KH ? wave / WM : 0u;
         floatx16 acc[MBW][NBW];
 #pragma unroll
         for (int i = 0; i < MBW; ++i)
@@ -480,14 +484,16 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
         // is at ((blk * S + s) * 2 + k) KB, lane l at 16 l bytes
         const __amdgpu_buffer_rsrc_t xres = make_rsrc(a.xf + (uint64_t)m0 * a.cols, (uint32_t)(BM * a.cols * 2));
         const uint32_t xlane = lane * 16;
-        uint4 AR[kPcADepth][MBW][2];
+        constexpr int NK = KH ? 1 : 2;  // K halves per wave and stage
+        uint4 AR[kPcADepth][MBW][NK];
         // stages past s_end read zeros (out of range), so padded stages add exactly 0
         auto load_a = [&](int slot, uint32_t s) {
 #pragma unroll
             for (int i = 0; i < MBW; ++i)
 #pragma unroll
-                for (int k = 0; k < 2; ++k)
-                    AR[slot][i][k] = bld128(xres, xlane, s < s_end ? (((wm * MBW + i) * S + s) * 2 + k) * 1024 : kPcOob);
+                for (int k = 0; k < NK; ++k)
+                    AR[slot][i][k] = bld128(xres, xlane,
+                                            s < s_end ? (((wm * MBW + i) * S + s) * 2 + kh + k) * 1024 : kPcOob);
         };
         bf16x8 B0[NBW], B1[NBW];
         auto read_b = [&](uint32_t buf, int k, bf16x8 (&B)[NBW]) {
@@ -506,26 +512,61 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
 #pragma unroll
         for (int p = 0; p < kPcADepth; ++p) load_a(p, s_begin + p);
         pc_barrier();  // B_0: stages 0 and 1 are in LDS
-        read_b(0, 0, B0);
+        read_b(0, KH ? kh : 0u, B0);
         // stage i: x fragments from ring slot i % 4, W from LDS buffer i % 4; unrolled so both
         // are static, and branch-free so the loads' waits are exact (padded stages are zeros)
         static_assert(kPcADepth == kPcBufs, "one static index for the x ring and the LDS buffers");
-        for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcBufs) {
+        if constexpr (KH) {
+            for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcBufs) {
 #pragma unroll
-            for (int q = 0; q < kPcBufs; ++q) {
-                read_b(q, 1, B1);
-                mma(q, 0, B0);
-                read_b((q + 1) % kPcBufs, 0, B0);  // stage i + 1 (zeros or junk past the end, unused)
-                mma(q, 1, B1);
-                load_a(q, s_begin + i0 + q + kPcADepth);
-                // issue order: W reads for the second half first, so neither batch of MFMAs waits
-                // for LDS; then the next stage's first W reads behind the first batch
-                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: B1
-                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 0
-                __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: next B0
-                __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 1
-                __builtin_amdgcn_sched_group_barrier(0x020, 2 * MBW, 0);    // VMEM read: x ring
-                pc_barrier();  // B_{i+1}
+                for (int q = 0; q < kPcBufs; ++q) {
+                    read_b((q + 1) % kPcBufs, kh, B1);  // stage i + 1 (complete since B_i)
+                    mma(q, 0, B0);
+                    load_a(q, s_begin + i0 + q + kPcADepth);
+                    __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);  // DS read: next stage
+                    __builtin_amdgcn_sched_group_barrier(0x008, NBW, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read: x ring
+                    pc_barrier();  // B_{i+1}
+#pragma unroll
+                    for (int j = 0; j < NBW; ++j) B0[j] = B1[j];
+                }
+            }
+            // the K halves meet: after every LDS access of the loop has completed (a barrier
+            // the producers join too), the second wave of each pair leaves its sums in LDS
+            // and the first adds them
+            pc_sync();
+            float* red = reinterpret_cast<float*>(lds) + wm * (NBW * 16 * 64) + lane;
+            static_assert(2 * NBW * 16 * 64 * 4 <= sizeof(lds), "the pair sums fit the stage buffers");
+            if (kh == 1) {
+#pragma unroll
+                for (int j = 0; j < NBW; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[(j * 16 + r) * 64] = acc[0][j][r];
+            }
+            pc_sync();
+            if (kh == 1) return;
+#pragma unroll
+            for (int j = 0; j < NBW; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[0][j][r] += red[(j * 16 + r) * 64];
+        } else {
+            for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcBufs) {
+#pragma unroll
+                for (int q = 0; q < kPcBufs; ++q) {
+                    read_b(q, 1, B1);
+                    mma(q, 0, B0);
+                    read_b((q + 1) % kPcBufs, 0, B0);  // stage i + 1 (zeros or junk past the end)
+                    mma(q, 1, B1);
+                    load_a(q, s_begin + i0 + q + kPcADepth);
+                    // issue order: W reads for the second half first, so neither batch of MFMAs waits
+                    // for LDS; then the next stage's first W reads behind the first batch
+                    __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: B1
+                    __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 0
+                    __builtin_amdgcn_sched_group_barrier(0x100, NBW, 0);        // DS read: next B0
+                    __builtin_amdgcn_sched_group_barrier(0x008, MBW * NBW, 0);  // MFMA: k16 = 1
+                    __builtin_amdgcn_sched_group_barrier(0x020, 2 * MBW, 0);    // VMEM read: x ring
+                    pc_barrier();  // B_{i+1}
+                }
             }
         }
         if (split) {
@@ -584,47 +625,59 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     const float inv_unit = __uint_as_float(0x7F000000u - __float_as_uint(fp8_unit()));
     const uint32_t wdst = (mat * 64 + r) * kPcLd + 8 * h;
     // per-slot codes in a ring of kPcDepth stages; the super-block fields (scales, mins, d) once
-    // per super-block: Hc serves the stages being written, Hn is the next super-block's
+    // per super-block, loaded with the codes of its first slot: H[0] serves the stages being
+    // written, H[1 ..] the super-blocks whose first slot is already loaded
+    constexpr int NH = (kPcDepth + 7) / 8 + 1;
     PcW<T> R[kPcDepth];
-    SmH<T> Hc, Hn;
-    auto load = [&](int slot, uint32_t s) { sm_load_q<T>(R[slot], slab, g, off, s, s < s_end); };
+    SmH<T> H[NH];
+    // first: s starts a super-block (known statically: s_begin is a multiple of 8)
+    auto load = [&](int slot, uint32_t s, bool first, int hslot) {
+        if (first) sm_load_h<T>(H[hslot], slab, g, off, s / 8, s < s_end);
+        sm_load_q<T>(R[slot], slab, g, off, s, s < s_end);
+    };
     // j: the stage's slot within its super-block (static in the unrolled loop)
     auto store = [&](int slot, uint32_t j, int buf) {
         PcW<T> W = R[slot];
-        sm_merge<T>(W, Hc, j);
+        sm_merge<T>(W, H[0], j);
         bf16x8 lo, hi;
         pc_dequant<T>(W, h, j, inv_unit, lo, hi);
         __bf16* st = lds + buf * STAGE;
         *reinterpret_cast<bf16x8*>(st + wdst) = lo;
         *reinterpret_cast<bf16x8*>(st + wdst + 16) = hi;
     };
-    sm_load_h<T>(Hc, slab, g, off, s_begin / 8, s_begin < s_end);
 #pragma unroll
-    for (int p = 0; p < kPcDepth; ++p) load(p, s_begin + p);
+    for (int p = 0; p < kPcDepth; ++p) load(p, s_begin + p, p % 8 == 0, p / 8);
     store(0, 0, 0);
-    load(0, s_begin + kPcDepth);
+    load(0, s_begin + kPcDepth, kPcDepth % 8 == 0, kPcDepth / 8);
     store(1, 1, 1);
-    load(1, s_begin + kPcDepth + 1);
+    load(1, s_begin + kPcDepth + 1, (kPcDepth + 1) % 8 == 0, (kPcDepth + 1) / 8);
     pc_sync();  // B_0
-    // iteration i writes local stage i + 2 from ring slot (i + 2) % 4 into buffer (i + 2) % 4;
-    // unrolled by 8 so slot, buffer and sub-block are static, and branch-free so the loads'
-    // waits are exact (stages past the end are junk that no consumer reads). Iteration q = 2
-    // loads the first stage of the next super-block and its header; q = 6 writes that stage.
-    static_assert(kPcUnroll == 8 && kPcDepth == 4, "one super-block per unrolled iteration");
-    for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcUnroll) {
+    // iteration i writes local stage i + 2 from ring slot (i + 2) % kPcDepth into buffer
+    // (i + 2) % 4 and loads stage i + 2 + kPcDepth into that slot; unrolled so slot, buffer and
+    // sub-block are static, and branch-free so the loads' waits are exact (stages past the end
+    // are junk that no consumer reads). Writing the first stage of a super-block moves the
+    // header ring on by one.
+    static_assert(kPcPUnroll % 8 == 0 && kPcPUnroll % kPcDepth == 0 && kPcPUnroll % kPcBufs == 0,
+                  "static ring slots, LDS buffers and sub-blocks");
+    for (uint32_t i0 = 0; i0 < n_pad; i0 += kPcPUnroll) {
 #pragma unroll
-        for (int q = 0; q < kPcUnroll; ++q) {
+        for (int q = 0; q < kPcPUnroll; ++q) {
             const int k = (q + 2) % kPcDepth;
-            if (q == 6) Hc = Hn;
+            if ((q + 2) % 8 == 0) {
+#pragma unroll
+                for (int e = 0; e + 1 < NH; ++e) H[e] = H[e + 1];
+            }
             store(k, (q + 2) % 8, (q + 2) % kPcBufs);
-            const uint32_t sl = s_begin + i0 + q + 2 + kPcDepth;
-            load(k, sl);
-            if (q == 2) sm_load_h<T>(Hn, slab, g, off, sl / 8, sl < s_end);
+            load(k, s_begin + i0 + q + 2 + kPcDepth, (q + 2 + kPcDepth) % 8 == 0, NH - 1);
             pc_sync();  // B_{i+1}
             // keep each stage's work between its barriers: hoisting a later stage's decode would
             // make it wait for that stage's loads
             __builtin_amdgcn_sched_barrier(0);
         }
+    }
+    if constexpr (KH) {  // the consumers' two barriers around the meeting of the K halves
+        pc_sync();
+        pc_sync();
     }
 }
 
