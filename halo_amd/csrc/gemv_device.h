@@ -810,10 +810,12 @@ __host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw) {
 }
 
 // Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
-// the Q8_0, Q6_K and Q5_K loops (two register groups); the others run at most 8 waves.
+// the Q8_0, Q6_K and Q5_K loops (two register groups); so do the one-group loops of the other
+// formats at up to 4 vectors; the rest run at most 8 waves.
 template <uint32_t T, int NV, bool ONE>
 constexpr uint32_t mx_max_threads() {
-    return (NV == 1 && (ONE || (T != kQ8_0 && T != kQ6_K && T != kQ5_K))) ? 1024u : 512u;
+    constexpr bool heavy = T == kQ8_0 || T == kQ6_K || T == kQ5_K;
+    return ((ONE && !heavy) || (NV == 1 && (ONE || !heavy))) ? 1024u : 512u;
 }
 
 // grid, split and LDS as k_gemv_slab, plus one A table per wave after the partials. ONE: every
