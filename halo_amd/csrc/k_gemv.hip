@@ -64,14 +64,10 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     }
     const uint32_t gwg = (ngrp + ks - 1) / ks;  // groups of the largest chunk
     if (gwg <= nw1 && (ks == 1 || have_ws)) return {ks, gwg, true};
-    // Q6_K from 1024 slabs (the LM heads): at most 6 waves per workgroup, so that two workgroups
-    // share a CU at the two-group loop's 3 waves per SIMD (measured on MI355X: 151936 x 5120
-    // 118.6 -> 116.9 us, 248320 x 5120 191.4 -> 188.5 us, against 8 waves)
-    const uint32_t ncap = (T == kQ6_K && slabs >= 1024) ? 6u : 16u;
-    uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, ncap);
+    uint32_t nw = std::clamp((gwg + groups_per_wave - 1) / groups_per_wave, 1u, 16u);
     // a wave holds the x sums of at most 4 groups (one per lane)
     while (ks < ngrp && (gwg + nw - 1) / nw > 4) {
-        if (nw < ncap) ++nw;
+        if (nw < 16) ++nw;
         else ++ks;
         const uint32_t g2 = (ngrp + ks - 1) / ks;
         if ((g2 + nw - 1) / nw <= 4) break;
