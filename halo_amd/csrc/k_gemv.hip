@@ -53,8 +53,9 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     // workgroup (LDS: the waves' partials and A tables).
     // Up to 16 waves per workgroup (160 KB of LDS per workgroup) when the matrix has at most 128
     // units: fewer, larger workgroups (measured on MI355X: 6144 x 5120 Q4_K 7.81 -> 6.91 us at
-    // M = 1, 14.1 -> 11.3 us at M = 4). Larger matrices keep 8: their two-vector calls would
-    // lose occupancy (the 17408 x 5120 gate/up pair at M = 2: 28.7 -> 33.7 us with 10 waves).
+    // M = 1, 14.1 -> 11.3 us at M = 4). Larger matrices keep 8: with 10 waves the 17408 x 5120
+    // gate/up pair gained at M = 1 (22.9 -> 21.4 us) but lost at M = 2 (28.7 -> 33.7 us), and the
+    // split may not depend on the number of vectors.
     const size_t per_wave = NVW * 64 * sizeof(float) + mx_table_bytes<NVW>();
     uint32_t nw1 = std::min(mx_max_threads<T, NVW, true>() / 64, units <= 128 ? 16u : 8u);
     while (nw1 > 1 && nw1 * per_wave > 163840) --nw1;
