@@ -148,9 +148,10 @@ int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t*
 
 // The GEMM's M tile family for a requested variant id (the auto ids choose by shape).
 // The kernel the auto variant runs for n_vec vectors (measured on MI355X at the BASELINE shapes):
-//   - the slab GEMV (exact products) up to 2 vectors (Q6_K, and Q4_K matrices of at most 128
-//     slabs: up to 4), where it streams the weights fastest (6144 x 5120 Q4_K at 4 vectors: 11.2
-//     against 14.8 us; at 192 slabs the small-M GEMM is ahead again, 19.2 against 19.7 us);
+//   - the slab GEMV (exact products) up to 2 vectors (Q6_K, and Q4_K, Q5_K and IQ4_XS matrices
+//     of at most 128 slabs: up to 4), where it streams the weights fastest (6144 x 5120 at 4
+//     vectors: Q4_K 11.2 against 14.8 us, IQ4_XS 13.3 against 17.9, Q5_K 15.6 against 17.2; at
+//     192 slabs the small-M GEMM is ahead again for Q4_K, 19.2 against 19.7 us);
 //   - the exact-product small-M GEMM from 3 (gate/up pair: 3 and 4), which streams them once for
 //     up to 8 vectors with the same arithmetic (plain matrices at 5..8 vectors: twice as fast as
 //     two GEMV passes);
@@ -160,7 +161,8 @@ int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t*
 // kernel as rms_norm followed by the plain call.
 uint32_t auto_gemv_variant(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n_vec, bool pair) {
     const uint32_t slabs = (rows + kSlabRows - 1) / kSlabRows;
-    const uint32_t gemv_max = pair ? 2u : (type == kQ6_K || (type == kQ4_K && slabs <= 128) ? 4u : 2u);
+    const bool small = slabs <= 128 && (type == kQ4_K || type == kQ5_K || type == kIQ4_XS);
+    const uint32_t gemv_max = pair ? 2u : (type == kQ6_K || small ? 4u : 2u);
     const uint32_t exact_max = pair ? kGateUpGemvMax : kGemmSxMaxRows;
     if (n_vec <= gemv_max) return HALO_MI_GEMV_SLAB;
     if (n_vec <= exact_max) {

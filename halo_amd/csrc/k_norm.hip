@@ -22,46 +22,54 @@ constexpr uint32_t kPerThread = kNormChunk / kNormBlock;
 constexpr uint32_t kChainStride = kNormChunk / 8 + 4;  // LDS floats per chain row (padded)
 constexpr uint32_t kNormLds = 8 * kChainStride + 4;     // the chain rows, then the result
 
-// Adds one chunk's n squares (n a multiple of 8; v: this thread's elements tid + 256 i of the
-// chunk) to the 8 chain sums p of lanes 0..7 of wave 0.
-__device__ void chunk_chains(const float (&v)[kPerThread], uint32_t n, float* lds, float& p) {
-#pragma clang fp contract(off)
-    const uint32_t tid = threadIdx.x;
-#pragma unroll
-    for (uint32_t i = 0; i < kPerThread; ++i) {
-        const uint32_t e = tid + i * kNormBlock;
-        if (e < n) lds[(e % 8) * kChainStride + e / 8] = v[i] * v[i];
-    }
-    __syncthreads();
-    if (tid < 8) {
-        // batches of 8 16-byte reads issued before their 32 additions (the LDS latency is
-        // paid once per batch, not once per read)
-        const float* r = lds + tid * kChainStride;
-        const uint32_t m = n / 8;
-        uint32_t k = 0;
-        for (; k + 32 <= m; k += 32) {
-            float4 q[8];
-#pragma unroll
-            for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                p = p + q[b].x;
-                p = p + q[b].y;
-                p = p + q[b].z;
-                p = p + q[b].w;
-            }
-        }
-        for (; k < m; ++k) p = p + r[k];
-    }
-    __syncthreads();
-}
-
-// The 8 chain sums combined in the dot's order, plus the sequential tail of the last cols % 8
-// elements (read by thread 0), then 1 / sqrt(mean + eps), for the whole block.
-__device__ float rms_inv_finish(const float* __restrict__ x, uint32_t cols, float eps, float* lds, float p) {
+// 1 / sqrt(dot(x, x) / cols + eps) of one row, for the whole block. The block stages the squares
+// of a chunk of the row in LDS transposed, element e in chain row e % 8 at e / 8 (every load of
+// the chunk is issued before the first is used: one memory round trip per chunk); lanes 0..7 of
+// wave 0 run the dot's 8 interleaved sequential sums over their rows (16-byte LDS reads), then
+// combine them as ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)) and add the sequential tail of the last
+// cols % 8 elements. The squares are rounded as the CPU's products are, so every sum is the
+// CPU's bitwise.
+__device__ float row_rms_inv(const float* __restrict__ x, uint32_t cols, float eps, float* lds) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x;
     const uint32_t full = cols - cols % 8u;
+    float p = 0.0f;
+    for (uint32_t c0 = 0; c0 < full; c0 += kNormChunk) {
+        const uint32_t n = min(kNormChunk, full - c0);  // a multiple of 8
+        float v[kPerThread];
+#pragma unroll
+        for (uint32_t i = 0; i < kPerThread; ++i) {
+            const uint32_t e = tid + i * kNormBlock;
+            v[i] = x[c0 + min(e, n - 1)];  // clamped: the value past n is never stored
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kPerThread; ++i) {
+            const uint32_t e = tid + i * kNormBlock;
+            if (e < n) lds[(e % 8) * kChainStride + e / 8] = v[i] * v[i];
+        }
+        __syncthreads();
+        if (tid < 8) {
+            // batches of 8 16-byte reads issued before their 32 additions (the LDS latency is
+            // paid once per batch, not once per read)
+            const float* r = lds + tid * kChainStride;
+            const uint32_t m = n / 8;
+            uint32_t k = 0;
+            for (; k + 32 <= m; k += 32) {
+                float4 q[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    p = p + q[b].x;
+                    p = p + q[b].y;
+                    p = p + q[b].z;
+                    p = p + q[b].w;
+                }
+            }
+            for (; k < m; ++k) p = p + r[k];
+        }
+        __syncthreads();
+    }
     if (tid < 64) {
         const float q = p + __shfl_down(p, 4, 8);  // lanes 0..3: p_j + p_{j+4}
         const float r = q + __shfl_down(q, 1, 8);  // lane 0: left, lane 2: right
@@ -83,30 +91,6 @@ __device__ float rms_inv_finish(const float* __restrict__ x, uint32_t cols, floa
     return lds[8 * kChainStride];
 }
 
-// 1 / sqrt(dot(x, x) / cols + eps) of one row, for the whole block. The block stages the squares
-// of a chunk of the row in LDS transposed, element e in chain row e % 8 at e / 8 (every load of
-// the chunk is issued before the first is used: one memory round trip per chunk); lanes 0..7 of
-// wave 0 run the dot's 8 interleaved sequential sums over their rows (16-byte LDS reads), then
-// combine them as ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)) and add the sequential tail of the last
-// cols % 8 elements. The squares are rounded as the CPU's products are, so every sum is the
-// CPU's bitwise.
-__device__ float row_rms_inv(const float* __restrict__ x, uint32_t cols, float eps, float* lds) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t full = cols - cols % 8u;
-    float p = 0.0f;
-    for (uint32_t c0 = 0; c0 < full; c0 += kNormChunk) {
-        const uint32_t n = min(kNormChunk, full - c0);  // a multiple of 8
-        float v[kPerThread];
-#pragma unroll
-        for (uint32_t i = 0; i < kPerThread; ++i) {
-            const uint32_t e = tid + i * kNormBlock;
-            v[i] = x[c0 + min(e, n - 1)];  // clamped: the value past n is never stored
-        }
-        chunk_chains(v, n, lds, p);
-    }
-    return rms_inv_finish(x, cols, eps, lds, p);
-}
-
 // grid rows, block kNormBlock. out may be x (each element is read before it is written, by
 // the same thread, after the whole row has been summed).
 __global__ __launch_bounds__(kNormBlock) void k_rms_norm_rows(const float* x, uint64_t x_stride,
@@ -115,32 +99,8 @@ __global__ __launch_bounds__(kNormBlock) void k_rms_norm_rows(const float* x, ui
 #pragma clang fp contract(off)
     __shared__ float lds[kNormLds];
     const float* xr = x + (uint64_t)blockIdx.x * x_stride;
-    float* o = out + (uint64_t)blockIdx.x * out_stride;
-    if (cols <= kNormChunk) {
-        // one chunk: x and w are loaded together before the sum, and x stays in registers, so
-        // the row costs one memory round trip
-        float xv[kPerThread], wv[kPerThread];
-#pragma unroll
-        for (uint32_t i = 0; i < kPerThread; ++i) {
-            const uint32_t e = min(threadIdx.x + i * kNormBlock, cols - 1);
-            xv[i] = xr[e];
-            wv[i] = w[e];
-        }
-        float p = 0.0f;
-        const uint32_t full = cols - cols % 8u;
-        if (full > 0) chunk_chains(xv, full, lds, p);
-        const float inv = rms_inv_finish(xr, cols, eps, lds, p);
-#pragma unroll
-        for (uint32_t i = 0; i < kPerThread; ++i) {
-            const uint32_t e = threadIdx.x + i * kNormBlock;
-            if (e < cols) {
-                const float t = xv[i] * inv;
-                o[e] = t * wv[i];
-            }
-        }
-        return;
-    }
     const float inv = row_rms_inv(xr, cols, eps, lds);
+    float* o = out + (uint64_t)blockIdx.x * out_stride;
     // every load of a chunk before the first store: one memory round trip per chunk
     for (uint32_t c0 = 0; c0 < cols; c0 += kNormChunk) {
         const uint32_t n = min(kNormChunk, cols - c0);
