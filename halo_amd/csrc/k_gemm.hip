@@ -1367,7 +1367,13 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
         if (S % 8 == 0 && ((tiles > cus && tiles % cus != 0) || 2 * tiles < cus)) {
             main_units = tiles > cus ? (uint32_t)(tiles / cus * cus / m_tiles) : 0u;
             const uint64_t rest = (uint64_t)(units - main_units) * m_tiles;
-            kc = (uint32_t)std::min<uint64_t>({cus / std::max<uint64_t>(rest, 1), S / 8, 16});
+            // Tiles left over beside a whole round: 64-row tiles run two workgroups per CU, so
+            // their chunks run beside the whole tiles and 2 chunks suffice (the fewer partials,
+            // the shorter the reduce); larger tiles hold a CU alone, so their chunks run after
+            // the round and 8 keep that tail short (measured on MI355X, gate/up 17408 x 5120:
+            // M = 64 57.3 -> 49.0 us, M = 128 70.4 -> 68.4, M = 256 105.2 -> 102.5, against 16)
+            const uint32_t cap = main_units == 0 ? 16u : (MB == 1 ? 2u : 8u);
+            kc = (uint32_t)std::min<uint64_t>({cus / std::max<uint64_t>(rest, 1), S / 8, cap});
             while (kc > 1 && rest * kc * BM * kPcW > kPartialFloats) --kc;
             if (kc < 2) main_units = units;  // nothing to gain: one launch
         }
