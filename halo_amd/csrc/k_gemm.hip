@@ -983,11 +983,13 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 //     64 x 32 weights and kept the texture path busy three quarters of the kernel;
 //   - the block headers (Q4_K / Q5_K scales and mins, IQ4_XS scales, Q6_K's scales and d) are
 //     loaded once per super-block, two ahead, not once per slot;
-//   - the per-slot codes stream kSmDepth slots ahead.
+//   - the per-slot codes stream kSmAhead slots ahead (a ring of 8: the kernel then fits five
+//     workgroups per CU, so the M = 8 gate/up launch of 4 K chunks x 272 units runs in one round).
 // Each wave writes its 32 x 32 partial to partials[(u * kchunks + chunk)][32][128] (columns 64 *
 // matrix + 32 * block), and k_gemm_pc_reduce adds the chunks in order and applies the epilogue.
 // ------------------------------------------------------------------------------------------
-constexpr int kSmDepth = 16;  // slots of weight codes in flight per wave (two super-blocks)
+constexpr int kSmDepth = 16;  // slots per loop iteration (two super-blocks)
+constexpr int kSmAhead = 8;   // slots of weight codes in flight per wave (a ring; divides kSmDepth)
 constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
 constexpr uint32_t kSmLdsMax = 48 * 1024;  // x bytes of one workgroup's K chunk in LDS
 constexpr uint32_t kSmLdsMax8 = 24 * 1024;  // the same at 8 rows, read from fp32 x by the kernel
@@ -1029,7 +1031,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
     constexpr bool kFuseX = XR == 8;
     constexpr uint32_t kXPer = sm_lds_max(XR) / 16 / 256;  // 16-byte entries per thread: the largest chunk's
     const uint32_t n16 = ns * 4 * XR;
-    PcW<T> R[kSmDepth];
+    PcW<T> R[kSmAhead];
     SmH<T> H[2];
     auto load_q = [&](int q, uint32_t s) { sm_load_q<T>(R[q], wres, g, off, s, s < s_end); };
     auto load_h = [&](int i, uint32_t sb) { sm_load_h<T>(H[i], wres, g, off, sb, 8 * sb < s_end); };
@@ -1050,7 +1052,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
         load_h(0, s_begin / 8);
         load_h(1, s_begin / 8 + 1);
 #pragma unroll
-        for (int q = 0; q < kSmDepth; ++q) load_q(q, s_begin + q);
+        for (int q = 0; q < kSmAhead; ++q) load_q(q, s_begin + q);
 #pragma unroll
         for (int i = 0; i < (int)kXPer; ++i) {
             const uint32_t e = threadIdx.x + 256u * i;
@@ -1085,7 +1087,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
         load_h(0, s_begin / 8);
         load_h(1, s_begin / 8 + 1);
 #pragma unroll
-        for (int q = 0; q < kSmDepth; ++q) load_q(q, s_begin + q);
+        for (int q = 0; q < kSmAhead; ++q) load_q(q, s_begin + q);
 #pragma unroll
         for (int i = 0; i < (int)kXPer; ++i) {
             const uint32_t e = threadIdx.x + 256u * i;
@@ -1099,7 +1101,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
     const uint32_t xrow = (r < XR) ? h * XR + r : ~0u;
     floatx16 acc = floatx16{};
     auto step = [&](int q, uint32_t s) {
-        PcW<T> W = R[q];
+        PcW<T> W = R[q % kSmAhead];
         sm_merge<T>(W, H[q >> 3], q & 7);
         bf16x8 lo, hi;
         pc_dequant<T>(W, h, q & 7, inv_unit, lo, hi);  // s_begin: a multiple of 8
@@ -1108,7 +1110,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
         const uint4 x1 = xl[xrow != ~0u ? (2 * ls + 1) * 2 * XR + xrow : n16];
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x0), lo, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x1), hi, acc, 0, 0, 0);
-        load_q(q, s + kSmDepth);
+        load_q(q % kSmAhead, s + kSmAhead);
     };
     // two super-blocks per iteration: H[0] serves the first, H[1] the second; each is reloaded
     // with the super-block two ahead once its own is done
@@ -1253,7 +1255,7 @@ int launch_gemm_lm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
 }
 
 // The k_gemm_sm launch plan: the x rows kept (XR) and the K chunks per unit. About four
-// workgroups per CU (three are resident at the kernel's registers), at least enough chunks that
+// workgroups per CU (four or five are resident at the kernel's registers), at least enough chunks that
 // one chunk's x fits kSmLdsMax, and the partials within the workspace. False if none fits.
 struct SmPlan {
     uint32_t xr, kc;
