@@ -1,4 +1,4 @@
-// gfx950 exact-product small-M GEMM: k_gemm_sx<T, PAIR, NP> for 2..8 rows of x.
+// gfx950 exact-product small-M GEMM: k_gemm_sx<T, PAIR, NP, KH> for 2..8 rows of x.
 //
 // The slab GEMV's arithmetic (exact products, fp32 sums) on v_mfma_f32_32x32x16_bf16 tiles:
 //   - B: the weights' integer codes themselves as bf16 bit patterns (a code c < 256 in the low
@@ -10,7 +10,8 @@
 //     MFMAs, as the reference's expressions factor them, and each group's sum is brought back
 //     with ldexp.
 // Rows and the arithmetic are those of the slab GEMV (same bound), but a workgroup streams two
-// units (256 W rows) x one K chunk, one 64-row slab per wave, and no wave dequantizes: per slot
+// units (256 W rows) x one K chunk, one 64-row slab per wave (KH: two waves per slab, each
+// taking alternate super-blocks, their sums meeting in LDS), and no wave dequantizes: per slot
 // and row block a lane unpacks 16 codes with about 10 masks and folds its vectors' sums,
 // instead of converting and rounding 16 weights. Each lane loads its row's whole 16-byte slot
 // record (one 1 KB load instruction per wave and slot: half the load instructions of 8-byte
@@ -36,8 +37,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t kSxOob = 0x80000000u;  // buffer offset past every resource: the load returns 0
 constexpr int kSxDepth = 8;               // slots of weight records in flight per wave (8 KB)
 constexpr uint32_t kSxLdsMax = 52 * 1024;  // x pieces, sums and exponents of one K chunk
-constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per wave of the fill
+constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per four waves of the fill
 constexpr uint32_t kSxWgsPerCu = 1;        // workgroups per CU the K split aims for
+constexpr size_t kSxKhLds = 4 * 64 * 2 * 2 * sizeof(float);  // the two-wave form's meeting: 4 waves x 64 lanes x 2 x NP <= 2
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sx_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
@@ -256,8 +258,8 @@ __host__ __device__ constexpr uint32_t sx_rows(int np) { return np <= 2 ? 16u : 
 // LDS bytes per slot of the chunk: the pieces, then per K half and vector the x sum.
 __host__ __device__ constexpr uint32_t sx_slot_bytes(int np) { return 64u * sx_rows(np) + 2u * 8u * 4u; }
 
-template <uint32_t T, bool PAIR, int NP>
-__global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
+template <uint32_t T, bool PAIR, int NP, bool KH>
+__global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a) {
     extern __shared__ uint4 sxl[];
     constexpr uint32_t RS = sx_rows(NP);
     constexpr bool kHi16 = T == kQ4_K || T == kQ4_0;  // K half 1's codes arrive as 16 q
@@ -273,9 +275,14 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     const uint32_t ngc = base + (chunk < extra ? 1u : 0u);  // super-blocks of this chunk
     const uint32_t s_begin = 8 * g0, s_end = 8 * (g0 + ngc);
     const uint32_t ns = s_end - s_begin;
-    // wave w: unit 2 (blockIdx / kchunks) + w / 2, matrix w % 2 (PAIR: gate / up; else the
-    // unit's two slabs), all 64 rows of that slab
-    const uint32_t unit = 2 * (blockIdx.x / a.kchunks) + (wave >> 1), mat = wave & 1u;
+    // wave w: unit 2 (blockIdx / kchunks) + (w % 4) / 2, matrix w % 2 (PAIR: gate / up; else the
+    // unit's two slabs), all 64 rows of that slab. KH: eight waves, two per slab, wave w taking
+    // the chunk's super-blocks of parity kh = w / 4 (two waves per SIMD at one workgroup per CU,
+    // so each hides the other's MFMA, LDS and dequant latencies); the kh = 1 wave's sums meet the
+    // kh = 0 wave's in LDS at the end
+    constexpr uint32_t SB = KH ? 2 : 1;  // a wave's super-block stride
+    const uint32_t kh = KH ? wave >> 2 : 0u;
+    const uint32_t unit = 2 * (blockIdx.x / a.kchunks) + ((wave >> 1) & 1u), mat = wave & 1u;
     const bool live_unit = unit < units;  // an odd unit count leaves the last workgroup's second unit empty
     const uint32_t lu = min(unit, units - 1);
     const uint32_t r = lane & 31u, h = lane >> 5;
@@ -295,12 +302,13 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
 
     // ---- x of the chunk into LDS: one wave per (vector, group) pair. The x loads are issued
     // first, then the weight stream's first loads, then the split (which waits only for x).
-    constexpr int kPairs = (int)kSxPairs;
+    constexpr uint32_t kWaves = KH ? 8 : 4;
+    constexpr int kPairs = (int)((4 * kSxPairs + kWaves - 1) / kWaves);
     const uint32_t npairs = a.n_vec * ngc;
     float4 xv[kPairs];
 #pragma unroll
     for (int i = 0; i < kPairs; ++i) {
-        const uint32_t pi = wave + 4u * i;
+        const uint32_t pi = wave + kWaves * i;
         xv[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
         if (pi < npairs) {  // four dword loads: x rows need only 4-byte alignment
             const uint32_t v = pi % a.n_vec, gg = pi / a.n_vec;
@@ -312,13 +320,14 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     SxH<T> H[2];
     auto load_q = [&](int q, uint32_t s) { sx_load_q<T>(R[q], wres, g, lane, s, s < s_end); };
     auto load_h = [&](int i, uint32_t sb) { sx_load_h<T>(H[i], wres, g, lane, sb, 8 * sb < s_end); };
-    load_h(0, s_begin / 8);
-    load_h(1, s_begin / 8 + 1);
+    const uint32_t sb0 = s_begin / 8 + kh;  // this wave's first super-block
+    load_h(0, sb0);
+    load_h(1, sb0 + SB);
 #pragma unroll
-    for (int q = 0; q < kSxDepth; ++q) load_q(q, s_begin + q);
+    for (int q = 0; q < kSxDepth; ++q) load_q(q, 8 * sb0 + q);
 #pragma unroll
     for (int i = 0; i < kPairs; ++i) {
-        const uint32_t pi = wave + 4u * i;
+        const uint32_t pi = wave + kWaves * i;
         if (pi >= npairs) break;  // wave-uniform
         const uint32_t v = pi % a.n_vec, gg = pi / a.n_vec;
         const float xr[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
@@ -377,7 +386,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
         const uint4 a0 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 0) * 2 * RS * 16);
         const uint4 a1 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 1) * 2 * RS * 16);
         const float* xs = xsum + ls * 16 + hd;  // [K half][vector], vector 2 p + hd
-        load_q(qr, s + kSxDepth);
+        load_q(qr, s + 8 * SB);  // this wave's next super-block
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             u32x4_t b0, b1;
@@ -454,18 +463,39 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
             }
         }
     };
-    for (uint32_t i0 = s_begin; i0 < s_end; i0 += 16) {
+    // this wave's super-blocks sb0, sb0 + SB, ...: H[0] serves the first of each pair, H[1] the
+    // second, each reloaded with the wave's super-block two ahead once its own is done
+    for (uint32_t i0 = 8 * sb0; i0 < s_end; i0 += 16 * SB) {
         group_begin(0);
 #pragma unroll
         for (int q = 0; q < 8; ++q) slot(q, i0 + q);
         group_end((i0 - s_begin) / 8);
-        load_h(0, i0 / 8 + 2);
-        if (i0 + 8 >= s_end) break;
+        load_h(0, i0 / 8 + 2 * SB);
+        if (i0 + 8 * SB >= s_end) break;
         group_begin(1);
 #pragma unroll
-        for (int q = 8; q < 16; ++q) slot(q, i0 + q);
-        group_end((i0 - s_begin) / 8 + 1);
-        load_h(1, i0 / 8 + 3);
+        for (int q = 0; q < 8; ++q) slot(q, i0 + 8 * SB + q);
+        group_end((i0 - s_begin) / 8 + SB);
+        load_h(1, i0 / 8 + 3 * SB);
+    }
+    if constexpr (KH) {
+        // the kh = 1 wave's sums to LDS (the x pieces are dead once every wave has left the
+        // loop; kSxKhLds bytes), then the kh = 0 wave adds them: a fixed order, independent of
+        // the vector count
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(lds) + ((wave & 3u) * 64 + lane) * (2 * NP);
+        if (kh == 1) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int p = 0; p < NP; ++p) red[b * NP + p] = acc[b][p];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) acc[b][p] += red[b * NP + p];
     }
     if (!live_unit) return;
     float* P = a.partials + ((uint64_t)unit * a.kchunks + chunk) * 32 * 128 + 64 * mat + r;
@@ -476,15 +506,26 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
             if ((uint32_t)p < nv_lane) P[(2 * p + hd) * 128 + 32 * b] = acc[b][p];
 }
 
-template <bool PAIR, int NP>
+uint32_t sx_cu_count();
+
+template <bool PAIR, int NP, bool KH = false>
 void launch_sx_np(uint32_t type, const SxArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+    if constexpr (!KH && !PAIR && NP <= 2) {
+        // two waves per slab where every wave still gets two or more super-blocks and the grid
+        // stays within two of these workgroups per CU (GEMV M = 3-4: 22.5 -> 20.3 us; gate/up
+        // M = 4, 544 workgroups, and M = 8, 3 super-blocks per chunk, were slower)
+        const uint32_t ng = a.cols / kSlot / 8;
+        if ((ng + a.kchunks - 1) / a.kchunks >= 4 && grid.x <= 2 * sx_cu_count())
+            return launch_sx_np<PAIR, NP, true>(type, a, grid, std::max<size_t>(lds, kSxKhLds), st);
+    }
+    constexpr uint32_t NT = KH ? 512 : 256;
     switch (type) {
-        case kQ4_0: hipLaunchKernelGGL((k_gemm_sx<kQ4_0, PAIR, NP>), grid, dim3(256), lds, st, a); break;
-        case kQ8_0: hipLaunchKernelGGL((k_gemm_sx<kQ8_0, PAIR, NP>), grid, dim3(256), lds, st, a); break;
-        case kQ4_K: hipLaunchKernelGGL((k_gemm_sx<kQ4_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
-        case kQ5_K: hipLaunchKernelGGL((k_gemm_sx<kQ5_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
-        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sx<kIQ4_XS, PAIR, NP>), grid, dim3(256), lds, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm_sx<kQ6_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_sx<kQ4_0, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_sx<kQ8_0, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_sx<kQ4_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_sx<kQ5_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sx<kIQ4_XS, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_sx<kQ6_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
     }
 }
 
