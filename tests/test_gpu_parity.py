@@ -493,6 +493,35 @@ def test_baseline_shapes_gemv(hl, oracle, dev, t, rows, cols, seed, outliers, n_
     assert np.all(err <= tol)
 
 
+_TWO_WAVE = {}
+
+
+@pytest.mark.parametrize("n_vec", [1, 3])
+@pytest.mark.parametrize("t", QUANT_TYPES)
+def test_exact_small_m_two_wave_form(hl, oracle, dev, t, n_vec):
+    """The exact small-M kernel's two-wave form (two waves per slab on alternate super-blocks,
+    the odd wave's sums added to the even wave's through LDS). A plain 17408 x 5120 matrix at
+    1-4 vectors runs as 68 workgroups (two units each) x 4 K chunks of 5 super-blocks, which
+    takes it; every format, one and two vectors per lane half, within the slab GEMV's bound,
+    and a second call bitwise the first."""
+    rows, cols = 17408, 5120
+    say("exact small-M two-wave form", NAMES[t], rows, cols, n_vec)
+    if _TWO_WAVE.get("t") != t:  # one format's matrix serves both vector counts
+        _TWO_WAVE.clear()
+        wq = synth(hl, t, rows, cols, 40 + t)
+        _TWO_WAVE.update(t=t, w=(wq, slab_of(hl, dev, t, wq, rows, cols)))
+    wq, slab = _TWO_WAVE["w"]
+    x = hl.fill_normal(4000 + n_vec, n_vec * cols).reshape(n_vec, cols)
+    ref = oracle.matmul(t, wq, rows, cols, x)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+    tol = slab_gemv_tol(oracle, t, wq, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    two-wave {NAMES[t]} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    y2 = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMM_EXACT_SMALL_M)
+    assert isclose_bits(y2, y), "a second call gave different bits"
+
+
 _HEAD = {}
 
 
