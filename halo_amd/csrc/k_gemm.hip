@@ -978,8 +978,10 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 // W through LDS, no barrier in the loop. What the vector-memory path carries per slot is only
 // the weights themselves:
 //   - x: the chunk's x fragments (rows < XR of the staged buffer) are copied into LDS once, at
-//     the start; each slot's A operands are then two ds_read_b128 (rows past XR read a zero
-//     entry). Loading them from global memory per wave and slot took 2 KB of L1 traffic per
+//     the start; each slot's A operands are then two ds_read_b128 (lanes of rows past XR read
+//     row XR - 1's entry: an A row feeds only its own output row, and rows past the x rows are
+//     never stored, so no zero entry is kept and a 5-group chunk at XR = 16 takes exactly 40 KB,
+//     four workgroups per CU). Loading them from global memory per wave and slot took 2 KB of L1 traffic per
 //     64 x 32 weights and kept the texture path busy three quarters of the kernel;
 //   - the block headers (Q4_K / Q5_K scales and mins, IQ4_XS scales, Q6_K's scales and d) are
 //     loaded once per super-block, two ahead, not once per slot;
@@ -1000,7 +1002,7 @@ __host__ __device__ constexpr uint32_t sm_x_bytes_per_slot(uint32_t xr) { return
 
 template <uint32_t T, bool PAIR, uint32_t XR>
 __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
-    extern __shared__ uint4 xl[];  // [slot][K half][lane half][XR rows], then one zero entry
+    extern __shared__ uint4 xl[];  // [slot][K half][lane half][XR rows]
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t S = a.cols / kSlot;
@@ -1094,11 +1096,11 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
             if (e < n16) xl[e] = xv[i];
         }
     }
-    if (threadIdx.x == 0) xl[n16] = uint4{0u, 0u, 0u, 0u};
     __syncthreads();
 
-    // this lane's A entries: row r, lane half h; rows past XR read the zero entry
-    const uint32_t xrow = (r < XR) ? h * XR + r : ~0u;
+    // this lane's A entries: row r, lane half h; rows past XR read row XR - 1 (their output rows
+    // are never stored)
+    const uint32_t xrow = h * XR + min(r, XR - 1);
     floatx16 acc = floatx16{};
     auto step = [&](int q, uint32_t s) {
         PcW<T> W = R[q % kSmAhead];
@@ -1106,8 +1108,8 @@ __global__ __launch_bounds__(256, 3) void k_gemm_sm(GemmPcArgs a) {
         bf16x8 lo, hi;
         pc_dequant<T>(W, h, q & 7, inv_unit, lo, hi);  // s_begin: a multiple of 8
         const uint32_t ls = s - s_begin;
-        const uint4 x0 = xl[xrow != ~0u ? (2 * ls) * 2 * XR + xrow : n16];
-        const uint4 x1 = xl[xrow != ~0u ? (2 * ls + 1) * 2 * XR + xrow : n16];
+        const uint4 x0 = xl[(2 * ls) * 2 * XR + xrow];
+        const uint4 x1 = xl[(2 * ls + 1) * 2 * XR + xrow];
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x0), lo, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x1), hi, acc, 0, 0, 0);
         load_q(q % kSmAhead, s + kSmAhead);
@@ -1271,7 +1273,7 @@ bool sm_plan(uint32_t units, uint32_t S, uint32_t n_vec, SmPlan& pl) {
     while (pl.kc > kc_min && (uint64_t)units * pl.kc * kSmRows * kPcW > kPartialFloats) --pl.kc;
     if ((uint64_t)units * pl.kc * kSmRows * kPcW > kPartialFloats) return false;
     const uint32_t groups = (ng + pl.kc - 1) / pl.kc;  // the largest chunk
-    pl.lds = (size_t)groups * 8 * sm_x_bytes_per_slot(pl.xr) + 16;
+    pl.lds = (size_t)groups * 8 * sm_x_bytes_per_slot(pl.xr);
     return true;
 }
 
