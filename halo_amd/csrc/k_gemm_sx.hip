@@ -37,7 +37,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr uint32_t kSxOob = 0x80000000u;  // buffer offset past every resource: the load returns 0
 constexpr int kSxDepth = 8;               // slots of weight records in flight per wave (8 KB)
 constexpr uint32_t kSxLdsMax = 52 * 1024;  // x pieces, sums and exponents of one K chunk
-constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per four waves of the fill
+constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per wave of a four-wave fill
 constexpr uint32_t kSxWgsPerCu = 1;        // workgroups per CU the K split aims for
 constexpr size_t kSxKhLds = 4 * 64 * 2 * 2 * sizeof(float);  // the two-wave form's meeting: 4 waves x 64 lanes x 2 x NP <= 2
 
@@ -546,7 +546,8 @@ bool gemm_sx_plan(uint32_t units, uint32_t cols, uint32_t n_vec, uint32_t* kc, s
     if (n_vec < 1 || n_vec > kGemmSxMaxRows || cols % 256 != 0 || S == 0 || units == 0) return false;
     const int np = (int)(n_vec + 1) / 2;
     const uint32_t ng = S / 8, per_group = 8 * sx_slot_bytes(np) + 8 * 4;
-    // a chunk's (vector, group) pairs: at most kSxPairs per wave of the fill
+    // a chunk's (vector, group) pairs: at most 4 kSxPairs per workgroup (the fill's registers;
+    // the two-wave form spreads them over eight waves)
     const uint32_t max_groups = std::min<uint32_t>(kSxLdsMax / per_group, 4 * kSxPairs / n_vec);
     const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
     const uint32_t wgs = (units + 1) / 2;  // a workgroup streams two units
