@@ -969,7 +969,7 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Small-M GEMM: k_gemm_sm<T, PAIR, XR> (at most 32 x rows; XR = 8, 16 or 32 rows kept)
+// Small-M GEMM: k_gemm_sm<T, PAIR, XR> (at most 32 x rows; XR = 8, 12, 16 or 32 rows kept)
 //
 // A workgroup owns W unit u (PAIR: the gate and up rows of slab u; else slabs 2u and 2u + 1)
 // over K chunk `chunk` (whole super-blocks) and all x rows. Wave w takes matrix w / 2 and row
@@ -1266,7 +1266,8 @@ struct SmPlan {
 bool sm_plan(uint32_t units, uint32_t S, uint32_t n_vec, SmPlan& pl) {
     if (n_vec > kSmRows || S % 8 != 0 || S == 0) return false;
     const uint32_t ng = S / 8, cus = cu_count();
-    pl.xr = n_vec <= 8 ? 8u : n_vec <= 16 ? 16u : 32u;
+    // 12 rows: a 5-group chunk in 30 KB, so five workgroups per CU (16 rows: 40 KB, four)
+    pl.xr = n_vec <= 8 ? 8u : n_vec <= 12 ? 12u : n_vec <= 16 ? 16u : 32u;
     const uint32_t max_groups = sm_lds_max(pl.xr) / (8 * sm_x_bytes_per_slot(pl.xr));
     const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
     pl.kc = std::clamp<uint32_t>((4 * cus + units - 1) / units, kc_min, ng);
@@ -1302,6 +1303,7 @@ int launch_gemm_sm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
     const dim3 grid(units * pl.kc);
     switch (pl.xr) {
         case 8: launch_gemm_sm_xr<PAIR, 8>(type, p, grid, pl.lds, st); break;
+        case 12: launch_gemm_sm_xr<PAIR, 12>(type, p, grid, pl.lds, st); break;
         case 16: launch_gemm_sm_xr<PAIR, 16>(type, p, grid, pl.lds, st); break;
         default: launch_gemm_sm_xr<PAIR, 32>(type, p, grid, pl.lds, st); break;
     }
