@@ -969,7 +969,7 @@ __global__ __launch_bounds__(256) void k_gemm_lm(GemmPcArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Small-M GEMM: k_gemm_sm<T, PAIR, XR> (at most 32 x rows; XR = 8, 12, 16 or 32 rows kept)
+// Small-M GEMM: k_gemm_sm<T, PAIR, XR> (at most 32 x rows; XR = 8, 12, 16, 24 or 32 rows kept)
 //
 // A workgroup owns W unit u (PAIR: the gate and up rows of slab u; else slabs 2u and 2u + 1)
 // over K chunk `chunk` (whole super-blocks) and all x rows. Wave w takes matrix w / 2 and row
@@ -995,7 +995,8 @@ constexpr int kSmAhead = 8;   // slots of weight codes in flight per wave (a rin
 constexpr uint32_t kSmRows = 32;  // x rows of the small-M GEMM (one MFMA block)
 constexpr uint32_t kSmLdsMax = 48 * 1024;  // x bytes of one workgroup's K chunk in LDS
 constexpr uint32_t kSmLdsMax8 = 24 * 1024;  // the same at 8 rows, read from fp32 x by the kernel
-__host__ __device__ constexpr uint32_t sm_lds_max(uint32_t xr) { return xr == 8 ? kSmLdsMax8 : kSmLdsMax; }
+// 24 rows: 40 KB, so 3-group chunks of 36 KB and four workgroups per CU (32 rows: 48 KB, three)
+__host__ __device__ constexpr uint32_t sm_lds_max(uint32_t xr) { return xr == 8 ? kSmLdsMax8 : xr == 24 ? 40u * 1024 : kSmLdsMax; }
 
 // x bytes in LDS per slot of K: two K halves x two lane halves x XR rows x 16 B.
 __host__ __device__ constexpr uint32_t sm_x_bytes_per_slot(uint32_t xr) { return 64u * xr; }
@@ -1267,7 +1268,7 @@ bool sm_plan(uint32_t units, uint32_t S, uint32_t n_vec, SmPlan& pl) {
     if (n_vec > kSmRows || S % 8 != 0 || S == 0) return false;
     const uint32_t ng = S / 8, cus = cu_count();
     // 12 rows: a 5-group chunk in 30 KB, so five workgroups per CU (16 rows: 40 KB, four)
-    pl.xr = n_vec <= 8 ? 8u : n_vec <= 12 ? 12u : n_vec <= 16 ? 16u : 32u;
+    pl.xr = n_vec <= 8 ? 8u : n_vec <= 12 ? 12u : n_vec <= 16 ? 16u : n_vec <= 24 ? 24u : 32u;
     const uint32_t max_groups = sm_lds_max(pl.xr) / (8 * sm_x_bytes_per_slot(pl.xr));
     const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
     pl.kc = std::clamp<uint32_t>((4 * cus + units - 1) / units, kc_min, ng);
@@ -1305,6 +1306,7 @@ int launch_gemm_sm(uint32_t type, const GemmArgs& a, Workspace* ws, uint32_t uni
         case 8: launch_gemm_sm_xr<PAIR, 8>(type, p, grid, pl.lds, st); break;
         case 12: launch_gemm_sm_xr<PAIR, 12>(type, p, grid, pl.lds, st); break;
         case 16: launch_gemm_sm_xr<PAIR, 16>(type, p, grid, pl.lds, st); break;
+        case 24: launch_gemm_sm_xr<PAIR, 24>(type, p, grid, pl.lds, st); break;
         default: launch_gemm_sm_xr<PAIR, 32>(type, p, grid, pl.lds, st); break;
     }
     launch_reduce<PAIR, kSmRows>(p, st);

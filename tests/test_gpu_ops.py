@@ -157,7 +157,7 @@ def test_gemv_slab_valu_rejects_other_formats(hl, dev):
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
-@pytest.mark.parametrize("n_vec", [2, 9, 12, 16, 32])
+@pytest.mark.parametrize("n_vec", [2, 9, 12, 16, 24, 32])
 def test_gemm_small_m_variant(hl, oracle, dev, t, n_vec):
     """HALO_MI_GEMM_SLAB_BF16_SMALL_M: the small-M kernel by id, within the bf16 GEMM bounds; more
     than 32 vectors or cols not a multiple of 256 is Unsupported."""
