@@ -628,28 +628,35 @@ int halo_mi_stream_check(void* stream) {
     auto st = static_cast<hipStream_t>(stream);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "stream_check: hipGetDevice failed");
+    // both status words are read and cleared before anything is reported: the no-alloc scratch's
+    // (shared by the device) and this stream's workspace's
     uint32_t na_word = 0;
     if (int rc = noalloc_status_take(st, &na_word)) return rc;
-    if (na_word != 0)
-        return set_error(HALO_MI_E_DEVICE, "stream_check: a split-K reduction of halo_mi_gemv_noalloc gave up waiting for "
-                                           "partial sums (status 0x%x); outputs written since the last check hold NaN", na_word);
+    uint32_t word = 0;
     Workspace w;
+    bool have_ws = false;
     {
         std::lock_guard<std::mutex> lock(g_ws_mu);
         auto it = g_ws.find({dev, st});
-        if (it == g_ws.end()) return hip_status(hipStreamSynchronize(st), "stream_check");
-        w = it->second;
+        if (it != g_ws.end()) {
+            w = it->second;
+            have_ws = true;
+        }
     }
-    uint32_t word = 0;
-    if (int rc = hip_status(hipMemcpyAsync(&word, w.status, sizeof(word), hipMemcpyDeviceToHost, st), "stream_check"))
-        return rc;
+    if (have_ws) {
+        if (int rc = hip_status(hipMemcpyAsync(&word, w.status, sizeof(word), hipMemcpyDeviceToHost, st), "stream_check"))
+            return rc;
+        if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
+        if (word != 0) {
+            // the words and counters of a wait that gave up are in an unknown state: start again clean
+            if (int rc = clear_workspace(w, st)) return rc;
+        }
+    }
     if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
-    if (word == 0) return HALO_MI_OK;
-    // the words and counters of a wait that gave up are in an unknown state: start again clean
-    if (int rc = clear_workspace(w, st)) return rc;
-    if (int rc = hip_status(hipStreamSynchronize(st), "stream_check")) return rc;
-    return set_error(HALO_MI_E_DEVICE, "stream_check: a split-K reduction gave up waiting for partial sums "
-                                       "(status 0x%x); outputs written since the last check hold NaN", word);
+    if (word == 0 && na_word == 0) return HALO_MI_OK;
+    return set_error(HALO_MI_E_DEVICE, "stream_check: a split-K reduction gave up waiting for partial sums (stream "
+                                       "workspace status 0x%x, halo_mi_gemv_noalloc scratch status 0x%x); outputs written "
+                                       "since the last check hold NaN", word, na_word);
 }
 
 int halo_mi_stream_release(void* stream) {

@@ -313,7 +313,17 @@ public:
         if (tier == Tier::Vram) {
             CHECK(hipMalloc(&mem, n) == hipSuccess, ErrorCode::Memory, "mi355x backend: cannot allocate %llu bytes",
                   (unsigned long long)bytes);
-            (void)hipMemset(mem, 0, n);  // zero-filled like the CPU backend's allocate
+            // Zero-filled like the CPU backend's allocate, and complete before this returns: the
+            // fill runs on the null stream, which the backend's non-blocking streams do not wait
+            // for, so an unsynchronized fill could land after the buffer's first upload or kernel
+            // write on another stream and zero it.
+            const hipError_t fe = hipMemsetAsync(mem, 0, n, nullptr);
+            const hipError_t se = fe == hipSuccess ? hipStreamSynchronize(nullptr) : fe;
+            if (se != hipSuccess) {
+                (void)hipFree(mem);
+                fail(ErrorCode::Device, "mi355x backend: zero-filling %llu bytes failed: %s", (unsigned long long)bytes,
+                     hipGetErrorString(se));
+            }
             return std::make_unique<DeviceBuffer>(this, mem, bytes, tier, true, false, WeightLayout::Gguf, SlabMeta{});
         }
         CHECK(hipHostMalloc(&mem, n, hipHostMallocDefault) == hipSuccess, ErrorCode::Memory,

@@ -544,6 +544,10 @@ uint32_t sx_cu_count() {
 bool gemm_sx_plan(uint32_t units, uint32_t cols, uint32_t n_vec, uint32_t* kc, size_t* lds) {
     const uint32_t S = cols / kSlot;
     if (n_vec < 1 || n_vec > kGemmSxMaxRows || cols % 256 != 0 || S == 0 || units == 0) return false;
+    // with the fused norm the launch normalizes all n_vec rows into the workspace's norm buffer
+    // at once; the plan refuses shapes past it with or without the norm, so that the auto choice
+    // stays a function of the shape only
+    if ((uint64_t)n_vec * cols > kNormFloats) return false;
     const int np = (int)(n_vec + 1) / 2;
     const uint32_t ng = S / 8, per_group = 8 * sx_slot_bytes(np) + 8 * 4;
     // a chunk's (vector, group) pairs: at most 4 kSxPairs per workgroup (the fill's registers;

@@ -267,13 +267,16 @@ extern "C" int halo_mi_gemv_noalloc(const halo_mi_gemv_params* p, void* stream) 
     uint64_t xs = 0, ys = 0;
     if (int rc = check_gemv_slab_call(p, op, &xs, &ys)) return rc;
     if (p->n_vec == 0 || p->rows == 0) return HALO_MI_OK;
-    const uint32_t v = p->variant;
-    const bool gemv_leg = v == HALO_MI_GEMV_SLAB || v == HALO_MI_GEMV_SLAB_VALU ||
-                          ((v == HALO_MI_GEMV_DEFAULT || v == HALO_MI_GEMV_SLAB_AUTO) && p->n_vec <= 8);
-    if (!gemv_leg)
-        return set_error(HALO_MI_E_UNSUPPORTED, "gemv_noalloc: variant %u at n_vec %u runs the GEMM, whose staging does not "
-                                                "fit the scratch (the slab GEMV variants 0/4 up to 8 vectors, 2 and 6 only)",
-                         v, p->n_vec);
+    // Variants 0 and 4 resolve exactly as in halo_mi_gemv (auto_gemv_variant), so that whatever
+    // this entry point runs is bitwise what halo_mi_gemv runs for the same call; a shape whose
+    // auto choice is a GEMM is refused (its staging and partials do not fit the scratch).
+    const uint32_t v = p->variant == HALO_MI_GEMV_DEFAULT || p->variant == HALO_MI_GEMV_SLAB_AUTO
+                           ? auto_gemv_variant(p->type, p->rows, p->cols, p->n_vec, false)
+                           : p->variant;
+    if (v != HALO_MI_GEMV_SLAB && v != HALO_MI_GEMV_SLAB_VALU)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemv_noalloc: variant %u at %u x %u, n_vec %u runs GEMM kernel %u, whose "
+                                                "staging does not fit the scratch (only calls that run the slab GEMV)",
+                         p->variant, p->rows, p->cols, p->n_vec, v);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return set_error(HALO_MI_E_DEVICE, "gemv_noalloc: hipGetDevice failed");
     unsigned char* base = nullptr;

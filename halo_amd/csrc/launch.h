@@ -134,6 +134,9 @@ int check_xy(const char* op, const float* x, uint64_t x_stride, const float* y, 
 // here), read on st and cleared with the scratch's words and counters when set.
 int noalloc_status_take(hipStream_t st, uint32_t* word);
 
+// The kernel variant the auto ids (0 and 4 on a SLAB call; 0 of the gate/up pair) run for a shape.
+uint32_t auto_gemv_variant(uint32_t type, uint32_t rows, uint32_t cols, uint32_t n_vec, bool pair);
+
 // The checks halo_mi_gemv makes on a SLAB-layout call, bar the variant id: shapes, strides,
 // alignment, overlap and the fused norm's operand. xs / ys receive the resolved strides (floats).
 int check_gemv_slab_call(const halo_mi_gemv_params* p, const char* op, uint64_t* xs, uint64_t* ys);

@@ -158,7 +158,10 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
  * halo_mi_gemv without any allocation. No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). Same operands, checks and results as halo_mi_gemv (bitwise) for the
- * SLAB GEMV variants: 2 and 6 at any n_vec, 0 and 4 up to 8 vectors; other variants return
+ * calls that run the SLAB GEMV: variants 2 and 6 at any n_vec, and 0 and 4 where their auto
+ * choice is the SLAB GEMV (up to 2 vectors; up to 4 for Q6_K and for Q4_K, Q5_K and IQ4_XS
+ * matrices of at most 128 slabs; up to 8 where the exact small-M GEMM's plan does not fit).
+ * Where 0 or 4 would run a GEMM kernel, and for the GEMM variants, it returns
  * HALO_MI_E_UNSUPPORTED. The split-K words, slab counters and status word live in a fixed
  * device array of this library (about 8.3 MiB per GPU, held until the process ends), not in a
  * per-stream workspace: a shape whose split needs more than 65536 slabs of counters or 2^20

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from helpers import (ALL_TYPES, BLOCK, F16, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
-                     gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
+                     gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, silu64, slab_gemv_tol, swiglu_tol)
 
 pytestmark = pytest.mark.gpu
 
@@ -379,16 +379,25 @@ def test_gemm_m512_partial_round(hl, oracle, dev, t, pair, kind):
         pa = wa[r0 * rb:r1 * rb]
         ga = oracle.matmul(t, pa, n, cols, x)
         ta = gemm_tol(oracle, t, pa, n, cols, x)
+        ea, eta = gemm_emulated(oracle, t, pa, n, cols, x)
         if pair:
             pb = wb[r0 * rb:r1 * rb]
             ub = oracle.matmul(t, pb, n, cols, x)
             ref = oracle.gate_up_swiglu(t, pa, pb, n, cols, x)
             tol = swiglu_tol(ga, ub, ta, gemm_tol(oracle, t, pb, n, cols, x), ref, fast=True)
+            eb, etb = gemm_emulated(oracle, t, pb, n, cols, x)
+            refe = silu64(ea) * eb
+            tole = swiglu_tol(ea, eb, eta, etb, refe, fast=True)
         else:
             ref, tol = ga, ta
+            refe, tole = ea, eta
         err = np.abs(y[:, r0:r1].astype(np.float64) - ref)
         print(f"    rows [{r0}, {r1}): worst |d|/bound = {max_ratio(err, tol):.4f}")
         assert np.all(err <= tol)
+        # the split tiles' K chunks and their reduce, held to the bf16-exact products' bound
+        erre = np.abs(y[:, r0:r1].astype(np.float64) - refe)
+        print(f"    rows [{r0}, {r1}) vs bf16-exact products: worst |d|/bound = {max_ratio(erre, tole):.4f}")
+        assert np.all(erre <= tole)
 
 
 # ---- fused gate/up + SwiGLU ---------------------------------------------------------------
@@ -553,10 +562,11 @@ GATE_UP_GEMV_MAX = 2  # the gate/up auto choice: the GEMV pair up to 2 vectors, 
 GATE_UP_EXACT_MAX = 4  # (kGateUpGemvMax), then the bf16 GEMM
 
 
-@pytest.mark.parametrize("n_vec", [2, 3, 4, 8, 64, 512])
+@pytest.mark.parametrize("n_vec", [2, 3, 4, 8, 12, 20, 24, 64, 512])
 def test_baseline_gate_up(hl, oracle, dev, n_vec):
     """config 4: fused gate/up pair over two 17408 x 5120 Q4_K matrices (and config 5's FFN pair
-    at M = 4); the oracle checks every output."""
+    at M = 4); the oracle checks every output. 12, 20 and 24 vectors take the small-M GEMM's
+    12- and 24-row tiers, whose K chunks at this shape span several super-block groups."""
     import torch
 
     t, rows, cols = Q4_K, 17408, 5120
@@ -592,6 +602,17 @@ def test_baseline_gate_up(hl, oracle, dev, n_vec):
         print(f"    gate_up M={n_vec} columns [{c0}, {c1}): worst |d|/bound = {max_ratio(err, tol):.4f}, "
               f"max |d| = {float(err.max()):.3e}, max |ref| = {float(np.abs(ref).max()):.3e}")
         assert np.all(err <= tol)
+        if not exact:
+            # the bf16 GEMM against the fp64 products of its own bf16-rounded operands: only the
+            # fp32 accumulation's error is allowed ((K/32 + 42) u sum |x~||w~|), which a dropped
+            # or repeated sub-block, a wrong tile or a lost K chunk would exceed many times over
+            ge, gte = gemm_emulated(oracle, t, wg_c, n, cols, x)
+            ue, ute = gemm_emulated(oracle, t, wu_c, n, cols, x)
+            refe = silu64(ge) * ue
+            tole = swiglu_tol(ge, ue, gte, ute, refe, fast=True)
+            erre = np.abs(y.astype(np.float64) - refe)
+            print(f"    gate_up M={n_vec} vs bf16-exact products: worst |d|/bound = {max_ratio(erre, tole):.4f}")
+            assert np.all(erre <= tole)
     assert np.all(np.isfinite(host(out)))
 
 
@@ -617,3 +638,8 @@ def test_baseline_hybrid_layer_shapes(hl, oracle, dev, name, t, rows, cols, n_ve
     err = np.abs(yh.astype(np.float64) - ref)
     print(f"    {name} M={n_vec}: worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
+    if n_vec > 8:  # the bf16 GEMM: also against the fp64 products of its bf16-rounded operands
+        emu, etol = gemm_emulated(oracle, t, wq, rows, cols, x)
+        eerr = np.abs(yh.astype(np.float64) - emu)
+        print(f"    {name} M={n_vec} vs bf16-exact products: worst |d|/bound = {max_ratio(eerr, etol):.4f}")
+        assert np.all(eerr <= etol)

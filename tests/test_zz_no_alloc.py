@@ -25,9 +25,11 @@ def _case(hl, dev, t, rows, cols, seed):
 def test_noalloc_matches_gemv_bitwise_and_allocates_nothing(hl, dev):
     import torch
 
-    # first call: 17408 x 5120 Q4_K (272 slabs, 4 K chunks), 3 vectors with the fused norm; second
-    # call: a smaller matrix (5120 x 6144 Q6_K) and fewer vectors, on the same scratch
-    calls = [(Q4_K, 17408, 5120, 3, True, 2), (Q6_K, 5120, 6144, 1, False, 0)]
+    # first call: 17408 x 5120 Q4_K (272 slabs, 4 K chunks), 3 vectors with the fused norm; then
+    # smaller inputs on the same scratch: the auto ids 4 and 0 where their choice is the slab
+    # GEMV (Q6_K at 4 and 3 vectors; a Q4_K matrix of 96 slabs at 4), and a single vector
+    calls = [(Q4_K, 17408, 5120, 3, True, 2), (Q6_K, 5120, 6144, 4, False, 4), (Q4_K, 6144, 5120, 4, True, 0),
+             (Q6_K, 5120, 6144, 3, False, 0), (Q6_K, 5120, 6144, 1, False, 0)]
     mats = {(t, rows, cols): _case(hl, dev, t, rows, cols, 2100 + rows) for t, rows, cols, _, _, _ in calls}
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):  # the runtime's own lazy set-up of a new stream (first launch, first copy)
@@ -71,6 +73,18 @@ def test_noalloc_refuses_what_does_not_fit(hl, dev):
         with pytest.raises(hl.HaloError) as e:  # the GEMM's staging does not fit the scratch
             hl.gemv_noalloc(t, w, x, y, rows, cols, n_vec, variant=variant)
         assert e.value.code == hl.ErrorCode.Unsupported
+    # the auto ids where halo_mi_gemv's choice is the exact small-M GEMM (17408 x 5120 Q4_K at
+    # 3..8 vectors): refused, since that kernel's partials do not fit the scratch and the slab
+    # GEMV would not be bitwise what halo_mi_gemv returns
+    big = _case(hl, dev, t, 17408, 5120, 2301)
+    xs = to_dev(np.ones((8, 5120), np.float32), dev)
+    ys = torch.full((8, 17408), SENTINEL, dtype=torch.float32, device=dev)
+    for variant in (hl.Variant.DEFAULT, hl.Variant.SLAB_AUTO):
+        for n_vec in (3, 5, 8):
+            with pytest.raises(hl.HaloError) as e:
+                hl.gemv_noalloc(t, big, xs, ys, 17408, 5120, n_vec, variant=variant)
+            assert e.value.code == hl.ErrorCode.Unsupported
+    assert np.all(host(ys) == SENTINEL), "a refused call wrote its output"
     with pytest.raises(hl.HaloError) as e:  # y overlapping x: the same checks as halo_mi_gemv
         hl.gemv_noalloc(t, w, x, x, rows, cols, 1)
     assert e.value.code == hl.ErrorCode.Kernel
