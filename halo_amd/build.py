@@ -7,6 +7,11 @@ The library is compiled with hipcc for gfx950 only. Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 instructions
   -mcode-object-version=5            loadable by the HIP runtime torch bundles (ROCm 7.0) as well
                                      as /opt/rocm's (7.2)
+  -mllvm -amdgpu-atomic-optimizer-strategy=None
+                                     every atomic here is issued by one lane; the optimizer's
+                                     wave scan reads the returned value at once, which waits for
+                                     every load issued before it (the split-K ticket is taken after
+                                     the weight loads and needed only at the workgroup's end)
 """
 from __future__ import annotations
 
@@ -36,6 +41,7 @@ HIP_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
 ]
 

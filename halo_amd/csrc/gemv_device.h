@@ -11,6 +11,7 @@
 
 #include "device.h"
 #include "launch.h"
+#include "norm_device.h"
 
 namespace halo_mi {
 namespace {
@@ -803,6 +804,82 @@ __device__ __forceinline__ void mx_group(const SlotGroup<T>& G, const s16x4 (&A)
     }
 }
 
+// ---- the fused RMS norm (NORM: one vector, GemvArgs::norm_w) ---------------------------------
+// One dispatch, bitwise RMS_NORM then the unfused GEMV: every workgroup computes 1 / rms of the raw
+// x row itself in cpu::rms_norm's order (norm_device.h: the same chains, combine and finish as the
+// RMS_NORM kernel), then each wave normalizes its own slot group of x in registers, (x * inv) *
+// norm_w rounded as the CPU rounds it, before the three-piece split: the values RMS_NORM writes.
+// The row's x is loaded and its squares staged in LDS before the weight loads are issued (so its
+// registers are free again), and the chains run while the weights are on their way, in wave 0 at
+// raised wave priority: the chain is 640 dependent additions at 5120 columns, and at the default
+// priority it shares its SIMD's issue slots with the other workgroups' waves.
+constexpr uint32_t kNormPerThread = 16;  // x loads per thread: the host takes this form when the
+                                         // row's first cols - cols % 8 floats need no more
+constexpr uint32_t kNormMaxCols = 8192;  // the chain rows fit 33 KB of LDS
+
+__device__ __forceinline__ void lds_sync() { __asm__ __volatile__("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// The row's x into the chain rows as squares (sq: norm_lds_floats(full) floats of LDS): element
+// tid + i nt of the first `full` (> 0) floats, addresses clamped, every load issued before the
+// first square is written.
+__device__ __forceinline__ void norm_x_squares(const float* __restrict__ x, uint32_t cols, float* sq, uint32_t tid,
+                                               uint32_t nt) {
+#pragma clang fp contract(off)
+    const uint32_t full = cols - cols % 8u, stride = norm_chain_stride(full);
+    float v[kNormPerThread];
+#pragma unroll
+    for (uint32_t i = 0; i < kNormPerThread; ++i) v[i] = x[min(tid + i * nt, full - 1)];
+#pragma unroll
+    for (uint32_t i = 0; i < kNormPerThread; ++i) {
+        const uint32_t e = tid + i * nt;
+        if (e < full) sq[(e % 8) * stride + e / 8] = v[i] * v[i];
+    }
+}
+
+// After norm_x_squares: the chains in lanes 0..7 of wave 0 (wave priority raised for them), the
+// combine and the tail: 1 / sqrt(mean + eps) for the whole workgroup.
+__device__ __forceinline__ float norm_x_chains(const float* __restrict__ x, uint32_t cols, float eps, float* sq,
+                                               uint32_t wave, uint32_t lane) {
+    const uint32_t full = cols - cols % 8u, stride = norm_chain_stride(full);
+    lds_sync();
+    if (wave == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        float p = 0.0f;
+        if (lane < 8) p = norm_chain(sq + lane * stride, full / 8, p);
+        const float inv = norm_finish(p, x, full, cols, eps, lane);
+        if (lane == 0) sq[8 * stride] = inv;
+        __builtin_amdgcn_s_setprio(0);
+    }
+    lds_sync();
+    return sq[8 * stride];
+}
+
+// LDS bytes of the chain rows and the result word for a row of cols floats
+__host__ __device__ constexpr size_t norm_lds_bytes(uint32_t cols) { return (size_t)norm_lds_floats(cols - cols % 8u) * sizeof(float); }
+
+// norm_w at this lane's x elements of group grp (lane = 8 s + r: slot 8 grp + s, elements
+// 4 r .. 4 r + 3), the address clamped as mx_load_x's.
+__device__ __forceinline__ void mx_load_nw(float (&wr)[4], const float* __restrict__ nw, uint32_t grp, uint32_t S, uint32_t lane) {
+    const uint32_t slot = grp * 8 + (lane >> 3);
+    const uint64_t e = (uint64_t)min(slot, S - 1) * 32 + 4 * (lane & 7);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[i] = nw[e + i];
+}
+
+// xr (one vector, raw x of group grp) -> (x * inv) * norm_w, as cpu::rms_norm rounds it; zero
+// past the row's end, as mx_load_x leaves it.
+__device__ __forceinline__ void mx_norm_x(float (&xr)[1][4], const float (&wr)[4], float inv, uint32_t grp, uint32_t S,
+                                          uint32_t lane) {
+#pragma clang fp contract(off)
+    const bool in = grp * 8 + (lane >> 3) < S;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float t = xr[0][i] * inv;
+        const float n = t * wr[i];
+        xr[0][i] = in ? n : 0.0f;
+    }
+}
+
 // Dynamic LDS bytes of a k_gemv_mx workgroup of nw waves: the waves' partials and A tables.
 template <int NV>
 __host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw) {
@@ -822,8 +899,9 @@ constexpr uint32_t mx_max_threads() {
 // wave has at most one slot group (no second register buffer, so more waves fit per SIMD).
 // The body of workgroup `bid` of a k_gemv_mx launch over the matrix of `a` (also one segment of a
 // grouped launch, k_gemv_mx_group).
-template <uint32_t T, int NV, bool PAIR, bool ONE>
+template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
 __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid) {
+    static_assert(!NORM || NV == 1, "the in-kernel norm is the one-vector form");
     extern __shared__ float smem[];
     constexpr uint32_t MATS = PAIR ? 2 : 1;
     constexpr int M = mx_blocks<NV>();
@@ -831,6 +909,12 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
     const uint32_t nch = a.ks * MATS;
+    float* sq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + mx_lds_bytes<NV>(nw));
+    if constexpr (NORM) {
+        // the row's squares into LDS before the weight loads are issued (registers free again)
+        norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     const uint32_t slab = bid / nch, c = bid % nch;
     const uint32_t mat = c / a.ks, cc = c % a.ks;
     const uint32_t base = ngrp / a.ks, extra = ngrp % a.ks;
@@ -847,14 +931,19 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     for (int v = 0; v < NV; ++v) acc0[v] = 0.0f;
     float xr[NV][4];
     uint32_t ticket = 0;
+    float wr[4];  // NORM: norm_w at this lane's x elements
+    // NORM: the chains (wave 0) and 1 / rms for the workgroup
+    auto norm_inv = [&]() { return norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane); };
     if constexpr (ONE) {
         if (w0 < w1) {
             SlotGroup<T> G;
             // x first: the A table is built while the weights are on their way (loads are waited
             // for in issue order)
             mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
+            if constexpr (NORM) mx_load_nw(wr, a.norm_w, w0, S, lane);
             load_group<T>(G, slab0, geo, lane, w0, S);
             ticket = gemv_ticket(a, slab, nch);
+            if constexpr (NORM) mx_norm_x(xr, wr, norm_inv(), w0, S, lane);
             s16x4 A[4 * M];
             int es[NV];
             float xs[NV];
@@ -864,6 +953,7 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
             for (int v = 0; v < NV; ++v) acc0[v] = ldexpf(acc0[v], es[v]);
         } else {
             ticket = gemv_ticket(a, slab, nch);
+            if constexpr (NORM) (void)norm_inv();
         }
         gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
         return;
@@ -871,18 +961,23 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     SlotGroup<T> cur, nxt;
     if (w0 < w1) {  // x first: the A table is built while the weights are on their way
         mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
+        if constexpr (NORM) mx_load_nw(wr, a.norm_w, w0, S, lane);
         load_group<T>(cur, slab0, geo, lane, w0, S);
     }
     ticket = gemv_ticket(a, slab, nch);
+    float inv = 1.0f;
+    if constexpr (NORM) inv = norm_inv();
     // One group: build its A table from xr, prefetch x and the weights of the next group (past
     // the last group: the last one again, an L2 hit, so the loop stays branch-free), multiply.
     auto step = [&](const SlotGroup<T>& G, SlotGroup<T>& next, uint32_t grp) {
         s16x4 A[4 * M];
         int es[NV];
         float xs[NV];
+        if constexpr (NORM) mx_norm_x(xr, wr, inv, grp, S, lane);
         mx_build<T, NV>(xr, tab, lane, A, es, xs);
         const uint32_t gn = min(grp + 1, w1 - 1);
         mx_load_x<NV>(xr, a.x, a.x_stride, gn, S, lane);
+        if constexpr (NORM) mx_load_nw(wr, a.norm_w, gn, S, lane);
         load_group<T>(next, slab0, geo, lane, gn, S);
         float accg[NV];
 #pragma unroll
@@ -900,9 +995,9 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     gemv_finish<NV, PAIR>(a, acc0, red, wave, nw, lane, slab, c, nch, ticket);
 }
 
-template <uint32_t T, int NV, bool PAIR, bool ONE>
+template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
 __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
-    gemv_mx_body<T, NV, PAIR, ONE>(a, blockIdx.x);
+    gemv_mx_body<T, NV, PAIR, ONE, NORM>(a, blockIdx.x);
 }
 
 }  // namespace

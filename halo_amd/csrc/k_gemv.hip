@@ -109,9 +109,42 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
         }
     }
     const dim3 grid(slabs * a.ks * MATS), block(64 * sp.nw);
+    if (a.norm_w) {  // the in-kernel norm (one vector; norm_in_kernel chose it)
+        if constexpr (NV == 1) {
+            const size_t ln = lds + norm_lds_bytes(a.cols);
+            if (sp.one) hipLaunchKernelGGL((k_gemv_mx<T, 1, PAIR, true, true>), grid, block, ln, st, a);
+            else hipLaunchKernelGGL((k_gemv_mx<T, 1, PAIR, false, true>), grid, block, ln, st, a);
+            return hip_status(hipGetLastError(), "gemv_slab launch");
+        } else {
+            return set_error(HALO_MI_E_CONFIG, "gemv: the in-kernel norm takes one vector");
+        }
+    }
     if (sp.one) hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, true>), grid, block, lds, st, a);
     else hipLaunchKernelGGL((k_gemv_mx<T, NV, PAIR, false>), grid, block, lds, st, a);
     return hip_status(hipGetLastError(), "gemv_slab launch");
+}
+
+// Whether a one-vector call with the fused norm runs it inside the GEMV: the MFMA kernel, a row
+// of at most kNormMaxCols floats that the workgroup loads in one round (kNormPerThread per
+// thread), and LDS for the chain rows beside the kernel's own.
+template <uint32_t T>
+bool norm_in_kernel_t(uint32_t slabs, uint32_t cols, uint32_t mats, bool have_ws) {
+    const GemvSplit sp = pick_split<T>(slabs, cols / kSlot, mats, have_ws);
+    const uint32_t full = cols - cols % 8u;
+    return full > 0 && cols <= kNormMaxCols && cols % 32 == 0 && full <= kNormPerThread * 64 * sp.nw &&
+           mx_lds_bytes<1>(sp.nw) + norm_lds_bytes(cols) <= 163840;
+}
+
+bool norm_in_kernel(uint32_t type, uint32_t slabs, uint32_t cols, uint32_t mats, bool have_ws) {
+    switch (type) {
+        case kQ4_0: return norm_in_kernel_t<kQ4_0>(slabs, cols, mats, have_ws);
+        case kQ8_0: return norm_in_kernel_t<kQ8_0>(slabs, cols, mats, have_ws);
+        case kQ4_K: return norm_in_kernel_t<kQ4_K>(slabs, cols, mats, have_ws);
+        case kQ5_K: return norm_in_kernel_t<kQ5_K>(slabs, cols, mats, have_ws);
+        case kIQ4_XS: return norm_in_kernel_t<kIQ4_XS>(slabs, cols, mats, have_ws);
+        case kQ6_K: return norm_in_kernel_t<kQ6_K>(slabs, cols, mats, have_ws);
+        default: return false;
+    }
 }
 
 template <uint32_t T, bool PAIR>
@@ -138,6 +171,18 @@ int launch_gemv_slab_in(uint32_t type, GemvSlabArgs a, Workspace* ws, uint64_t s
         return set_error(HALO_MI_E_MEMORY, "gate_up: this stream is being captured and has no workspace yet "
                                            "(make one call on it before capturing)");
     if (PAIR && slabs > counters_cap) return set_error(HALO_MI_E_UNSUPPORTED, "gate_up: %u rows exceed the workspace", a.rows);
+    // One vector: the norm inside the GEMV, one dispatch (bitwise the RMS_NORM kernel's rows)
+    if (a.norm_w && a.n_vec == 1 && !a.valu &&
+        norm_in_kernel(type, slabs, a.cols, PAIR ? 2u : 1u, ws != nullptr && slabs <= kCounters)) {
+        switch (type) {
+            case kQ4_0: return launch_gemv_slab_nv<kQ4_0, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+            case kQ8_0: return launch_gemv_slab_nv<kQ8_0, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+            case kQ4_K: return launch_gemv_slab_nv<kQ4_K, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+            case kQ5_K: return launch_gemv_slab_nv<kQ5_K, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+            case kIQ4_XS: return launch_gemv_slab_nv<kIQ4_XS, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+            default: return launch_gemv_slab_nv<kQ6_K, PAIR>(a, slabs, ws, slots_cap, counters_cap, st);
+        }
+    }
     uint32_t per_norm = 0;  // vectors normalized at a time (a multiple of kMaxGemvVec)
     if (a.norm_w) {
         if (!ws || !ws->xn)

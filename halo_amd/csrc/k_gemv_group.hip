@@ -26,15 +26,16 @@ constexpr uint32_t group_max_threads() {
     return std::min(mx_max_threads<TA, NV, true>(), mx_max_threads<TB, NV, true>());
 }
 
-template <uint32_t TA, uint32_t TB, int NV>
+// NORM (one vector): the fused norm inside every workgroup (gemv_mx_body's prologue).
+template <uint32_t TA, uint32_t TB, int NV, bool NORM>
 __global__ __launch_bounds__((group_max_threads<TA, TB, NV>())) void k_gemv_mx_group(GemvGroupArgs g) {
     uint32_t s = 0;
     while (s + 1 < g.n && blockIdx.x >= g.wg_end[s]) ++s;
     const uint32_t bid = blockIdx.x - (s ? g.wg_end[s - 1] : 0u);
     if (g.type[s] == TA) {
-        gemv_mx_body<TA, NV, false, true>(g.seg[s], bid);
+        gemv_mx_body<TA, NV, false, true, NORM>(g.seg[s], bid);
     } else {
-        if constexpr (TB != TA) gemv_mx_body<TB, NV, false, true>(g.seg[s], bid);
+        if constexpr (TB != TA) gemv_mx_body<TB, NV, false, true, NORM>(g.seg[s], bid);
     }
 }
 
@@ -44,7 +45,13 @@ template <int NV, int IA, int IB>
 bool launch_pair(uint32_t ta, uint32_t tb, const GemvGroupArgs& g, dim3 grid, dim3 block, size_t lds, hipStream_t st) {
     constexpr uint32_t TA = kTypes[IA], TB = kTypes[IB];
     if (ta != TA || tb != TB) return false;
-    hipLaunchKernelGGL((k_gemv_mx_group<TA, TB, NV>), grid, block, lds, st, g);
+    if constexpr (NV == 1) {
+        if (g.seg[0].norm_w) {
+            hipLaunchKernelGGL((k_gemv_mx_group<TA, TB, 1, true>), grid, block, lds, st, g);
+            return true;
+        }
+    }
+    hipLaunchKernelGGL((k_gemv_mx_group<TA, TB, NV, false>), grid, block, lds, st, g);
     return true;
 }
 
@@ -86,9 +93,34 @@ uint32_t group_waves(uint32_t ta, uint32_t tb) {
     return nw;
 }
 
+// The group's K split and workgroup size (for the widest launch, so rows stay bitwise independent
+// of n_vec): ks K chunks, gwg one-group waves per workgroup; false when a chunk does not fit.
+bool group_split(uint64_t slabs, uint32_t ta, uint32_t tb, uint32_t cols, uint32_t* ks_out, uint32_t* gwg_out) {
+    const uint32_t S = cols / kSlot, ngrp = (S + 7) / 8;
+    const uint32_t nw1 = group_waves<kMaxGemvVec>(ta, tb);
+    const uint32_t target = std::clamp<uint32_t>((slabs <= 128 ? 2 : 4) * (uint32_t)slabs, 128u, 1088u);
+    uint32_t ks = std::min<uint32_t>((target + (uint32_t)slabs - 1) / (uint32_t)slabs, ngrp);
+    ks = std::min(std::max(ks, (ngrp + nw1 - 1) / nw1), ngrp);
+    *ks_out = ks;
+    *gwg_out = (ngrp + ks - 1) / ks;
+    return *gwg_out <= nw1;
+}
+
+// Whether a one-vector group with the fused norm runs it inside the kernel (as the single-matrix
+// GEMV's norm_in_kernel: one load round per workgroup, LDS for the chain rows).
+bool group_norm_in_kernel(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, uint32_t cols) {
+    uint64_t slabs = 0;
+    for (uint32_t i = 0; i < n; ++i) slabs += (segs[i].rows + kSlabRows - 1) / kSlabRows;
+    uint32_t ks = 0, gwg = 0;
+    if (slabs == 0 || !group_split(slabs, ta, tb, cols, &ks, &gwg)) return false;
+    const uint32_t full = cols - cols % 8u;
+    return full > 0 && cols <= kNormMaxCols && cols % 32 == 0 && full <= kNormPerThread * 64 * gwg &&
+           mx_lds_bytes<1>(gwg) + norm_lds_bytes(cols) <= 163840;
+}
+
 template <int NV>
 int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, const float* x, uint64_t x_stride,
-                    uint32_t cols, Workspace* ws, hipStream_t st) {
+                    uint32_t cols, Workspace* ws, hipStream_t st, const float* norm_w = nullptr, float eps = 0.0f) {
     const uint32_t S = cols / kSlot, ngrp = (S + 7) / 8;
     uint64_t slabs = 0;
     for (uint32_t i = 0; i < n; ++i) slabs += (segs[i].rows + kSlabRows - 1) / kSlabRows;
@@ -96,14 +128,12 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
     if (slabs > kCounters) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: %llu slabs exceed the workspace", (unsigned long long)slabs);
     // K split: a chip's worth of workgroups (as a single matrix of all the slabs would take), and
     // at least enough chunks that a chunk's slot groups fit one workgroup of one-group waves
-    const uint32_t nw1 = group_waves<kMaxGemvVec>(ta, tb);
-    const uint32_t target = std::clamp<uint32_t>((slabs <= 128 ? 2 : 4) * (uint32_t)slabs, 128u, 1088u);
-    uint32_t ks = std::min<uint32_t>((target + (uint32_t)slabs - 1) / (uint32_t)slabs, ngrp);
-    ks = std::min(std::max(ks, (ngrp + nw1 - 1) / nw1), ngrp);
+    uint32_t ks = 0, gwg = 0;
+    const bool fits = group_split(slabs, ta, tb, cols, &ks, &gwg);
     if (ks > 1 && (ks > kMaxChunks || slabs * ks * kMaxGemvVec * 64 > kSlots))
         return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: %llu slabs exceed the split-K workspace", (unsigned long long)slabs);
-    const uint32_t gwg = (ngrp + ks - 1) / ks;
-    if (gwg > nw1) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: cols %u too large for one workgroup per chunk", cols);
+    if (!fits) return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: cols %u too large for one workgroup per chunk", cols);
+    (void)ngrp;
     GemvGroupArgs g{};
     g.n = n;
     uint32_t slab0 = 0, wg = 0;
@@ -112,6 +142,8 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         GemvSlabArgs a{static_cast<const uint8_t*>(segs[i].w), nullptr, x, x_stride, segs[i].y, segs[i].y_stride,
                        segs[i].rows, cols, (uint32_t)NV};
         a.ks = ks;
+        a.norm_w = norm_w;
+        a.norm_eps = eps;
         a.slots = ws->slots;
         a.counters = ws->counters;
         a.slab0 = slab0;
@@ -124,7 +156,8 @@ int launch_group_nv(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, 
         g.wg_end[i] = wg;
     }
     for (uint32_t i = 0; i < n; ++i) g.seg[i].wg_total = wg;
-    if (!launch_types<NV>(ta, tb, g, dim3(wg), dim3(64 * gwg), mx_lds_bytes<NV>(gwg), st))
+    const size_t lds = mx_lds_bytes<NV>(gwg) + (norm_w ? norm_lds_bytes(cols) : 0);
+    if (!launch_types<NV>(ta, tb, g, dim3(wg), dim3(64 * gwg), lds, st))
         return set_error(HALO_MI_E_UNSUPPORTED, "gemv_group: no kernel for types %u and %u", ta, tb);
     return hip_status(hipGetLastError(), "gemv_group launch");
 }
@@ -147,6 +180,31 @@ int launch_gemv_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t
         bool seen = false;
         for (uint32_t k = 0; k < nt; ++k) seen |= types[k] == segs[i].type;
         if (!seen) types[nt++] = segs[i].type;
+    }
+    // one vector with the fused norm: inside the kernels when every launch's split allows it
+    if (norm_w && n_vec == 1) {
+        bool inside = true;
+        for (uint32_t k0 = 0; k0 < nt && inside; k0 += 2) {
+            uint32_t ta = types[k0], tb = k0 + 1 < nt ? types[k0 + 1] : types[k0];
+            if (type_index(ta) > type_index(tb)) std::swap(ta, tb);
+            GroupSeg part[HALO_MI_GEMV_GROUP_MAX];
+            uint32_t np = 0;
+            for (uint32_t i = 0; i < n; ++i)
+                if (segs[i].type == ta || segs[i].type == tb) part[np++] = segs[i];
+            inside = group_norm_in_kernel(part, np, ta, tb, cols);
+        }
+        if (inside) {
+            for (uint32_t k0 = 0; k0 < nt; k0 += 2) {
+                uint32_t ta = types[k0], tb = k0 + 1 < nt ? types[k0 + 1] : types[k0];
+                if (type_index(ta) > type_index(tb)) std::swap(ta, tb);
+                GroupSeg part[HALO_MI_GEMV_GROUP_MAX];
+                uint32_t np = 0;
+                for (uint32_t i = 0; i < n; ++i)
+                    if (segs[i].type == ta || segs[i].type == tb) part[np++] = segs[i];
+                if (int rc = launch_group_nv<1>(part, np, ta, tb, x, x_stride, cols, ws, st, norm_w, eps)) return rc;
+            }
+            return HALO_MI_OK;
+        }
     }
     uint32_t per = n_vec;  // vectors per normalized block
     if (norm_w) {

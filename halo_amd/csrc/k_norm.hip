@@ -12,6 +12,7 @@
 
 #include "device.h"
 #include "launch.h"
+#include "norm_device.h"
 
 namespace halo_mi {
 namespace {
@@ -19,16 +20,13 @@ namespace {
 constexpr uint32_t kNormBlock = 256;
 constexpr uint32_t kNormChunk = 8192;               // floats of a row staged in LDS at a time
 constexpr uint32_t kPerThread = kNormChunk / kNormBlock;
-constexpr uint32_t kChainStride = kNormChunk / 8 + 4;  // LDS floats per chain row (padded)
-constexpr uint32_t kNormLds = 8 * kChainStride + 4;     // the chain rows, then the result
+constexpr uint32_t kChainStride = dev::norm_chain_stride(kNormChunk);  // LDS floats per chain row (padded)
+constexpr uint32_t kNormLds = dev::norm_lds_floats(kNormChunk);        // the chain rows, then the result
 
-// 1 / sqrt(dot(x, x) / cols + eps) of one row, for the whole block. The block stages the squares
-// of a chunk of the row in LDS transposed, element e in chain row e % 8 at e / 8 (every load of
-// the chunk is issued before the first is used: one memory round trip per chunk); lanes 0..7 of
-// wave 0 run the dot's 8 interleaved sequential sums over their rows (16-byte LDS reads), then
-// combine them as ((p0+p4)+(p1+p5))+((p2+p6)+(p3+p7)) and add the sequential tail of the last
-// cols % 8 elements. The squares are rounded as the CPU's products are, so every sum is the
-// CPU's bitwise.
+// 1 / sqrt(dot(x, x) / cols + eps) of one row, for the whole block, in cpu::detail::dot's order
+// (norm_device.h): each chunk's squares are staged in LDS transposed (every load of the chunk is
+// issued before the first is used: one memory round trip per chunk), lanes 0..7 of wave 0 carry
+// the 8 chain sums across the chunks, then wave 0 combines them and thread 0 finishes.
 __device__ float row_rms_inv(const float* __restrict__ x, uint32_t cols, float eps, float* lds) {
 #pragma clang fp contract(off)
     const uint32_t tid = threadIdx.x;
@@ -48,44 +46,12 @@ __device__ float row_rms_inv(const float* __restrict__ x, uint32_t cols, float e
             if (e < n) lds[(e % 8) * kChainStride + e / 8] = v[i] * v[i];
         }
         __syncthreads();
-        if (tid < 8) {
-            // batches of 8 16-byte reads issued before their 32 additions (the LDS latency is
-            // paid once per batch, not once per read)
-            const float* r = lds + tid * kChainStride;
-            const uint32_t m = n / 8;
-            uint32_t k = 0;
-            for (; k + 32 <= m; k += 32) {
-                float4 q[8];
-#pragma unroll
-                for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    p = p + q[b].x;
-                    p = p + q[b].y;
-                    p = p + q[b].z;
-                    p = p + q[b].w;
-                }
-            }
-            for (; k < m; ++k) p = p + r[k];
-        }
+        if (tid < 8) p = dev::norm_chain(lds + tid * kChainStride, n / 8, p);
         __syncthreads();
     }
     if (tid < 64) {
-        const float q = p + __shfl_down(p, 4, 8);  // lanes 0..3: p_j + p_{j+4}
-        const float r = q + __shfl_down(q, 1, 8);  // lane 0: left, lane 2: right
-        float s = r + __shfl_down(r, 2, 8);        // lane 0: left + right
-        if (tid == 0) {
-            float tail = 0.0f;
-            for (uint32_t i = full; i < cols; ++i) {
-                const float q2 = x[i] * x[i];
-                tail = tail + q2;
-            }
-            s = s + tail;
-            // sqrtf and / are correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt, set
-            // by the build); __fsqrt_rn would be the native approximation in this toolchain
-            const float mean = s / (float)cols;
-            lds[8 * kChainStride] = 1.0f / sqrtf(mean + eps);
-        }
+        const float inv = dev::norm_finish(p, x, full, cols, eps, tid);
+        if (tid == 0) lds[8 * kChainStride] = inv;
     }
     __syncthreads();
     return lds[8 * kChainStride];

@@ -43,9 +43,10 @@ struct GemvSlabArgs {
     // at or past valid_rows (when not 0) are not ranked, but a NaN in them still counts
     ArgPart* parts = nullptr;
     uint32_t valid_rows = 0;
-    // Fused input norm: y = W (rms_norm(x) * norm_w) when norm_w is set. The launcher normalizes
-    // x into the workspace first (the RMS_NORM kernel, bitwise cpu::rms_norm); the kernels see
-    // only the normalized rows.
+    // Fused input norm: y = W (rms_norm(x) * norm_w) when norm_w is set. One vector: inside the
+    // MFMA kernel (every workgroup computes 1 / rms itself); otherwise the launcher normalizes x
+    // into the workspace first (the RMS_NORM kernel) and the kernels see only the normalized
+    // rows. Both are bitwise cpu::rms_norm then the unfused GEMV.
     const float* norm_w = nullptr;
     float norm_eps = 0.0f;
     // Workspace indexing in a grouped launch (k_gemv_mx_group): this matrix's first slab among

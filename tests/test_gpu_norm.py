@@ -155,8 +155,12 @@ def test_gemv_norm_reference_variant_bitwise(hl, oracle, dev, t):
     assert isclose_bits(y, ref), "reference-order gemv with the norm is not bitwise rms_norm + cpu::matmul"
 
 
+# One vector with cols <= 8192 takes the norm inside the GEMV kernel (one dispatch: the norm wave
+# of the first workgroup publishes 1 / rms); more vectors, and the 17408-column row, the RMS_NORM
+# kernel then the GEMV. (17408, 5120, 1) is the headline shape (1088 workgroups of 5 + 1 waves);
+# 65600 rows: more than 1024 slabs (two groups per wave).
 NORM_CASES = [(130, 1024, 1), (130, 1024, 4), (576, 5120, 1), (576, 5120, 3), (640, 17408, 1), (70, 512, 6),
-              (65600, 512, 1), (65600, 512, 4)]  # the last two: more than 1024 slabs
+              (65600, 512, 1), (65600, 512, 4), (17408, 5120, 1), (64, 256, 1)]  # (64, 256, 1): one workgroup
 
 
 def unfused_gemv(hl, dev, t, w, xn, rows, cols, variant):
@@ -173,7 +177,7 @@ def unfused_gemv(hl, dev, t, w, xn, rows, cols, variant):
 def test_gemv_norm_slab_bitwise(hl, oracle, dev, t, case):
     rows, cols, n_vec = case
     if rows > 10000 and t not in (Q4_K, Q6_K):
-        pytest.skip("the many-slab shapes run for Q4_K and Q6_K")
+        pytest.skip("the many-slab and headline shapes run for Q4_K and Q6_K")
     say("gemv norm slab", NAMES[t], rows, cols, n_vec)
     buf, stride = make_weights(t, rows, cols, seed=960 + t + rows)
     dense = dense_of(buf, t, rows, cols, stride, 0)
@@ -189,6 +193,31 @@ def test_gemv_norm_slab_bitwise(hl, oracle, dev, t, case):
     err = np.abs(y.astype(np.float64) - ref)
     print(f"    fused-norm gemv {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(err <= tol)
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+def test_gemv_norm_in_kernel_sum_order(hl, oracle, dev, t):
+    """The in-kernel norm's sum of squares follows cpu::detail::dot's order exactly: x[0] = 4096
+    and ones everywhere else put 2^24 and then ones into one chain, where the order decides the
+    sum (2^24 + 1 rounds back to 2^24 one addition at a time). The fused one-vector GEMV must equal
+    RMS_NORM (bitwise the oracle) then the GEMV, and the two orders give different inv here."""
+    rows, cols = 1024, 5120
+    say("gemv norm sum order", NAMES[t], rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=965 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    x = np.ones((1, cols), np.float32)
+    x[0, 0] = 4096.0
+    x[0, 1::2] *= -1.0
+    w = np.random.default_rng(966).uniform(0.25, 1.75, cols).astype(np.float32)
+    xn = oracle.rms_norm(x, w, EPS)
+    # a different order (the pairwise sum numpy uses in float32) gives a different inv
+    inv_other = np.float32(1.0) / np.sqrt(np.float32(np.sum(x * x, dtype=np.float32)) / np.float32(cols) + np.float32(EPS))
+    assert not isclose_bits((x * inv_other) * w, xn), "the test input does not separate the orders"
+    for variant in (hl.Variant.SLAB_GEMV, hl.Variant.DEFAULT):
+        y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, variant)
+        assert isclose_bits(y, unfused_gemv(hl, dev, t, slab, xn, rows, cols, variant)), \
+            f"variant {int(variant)}: the in-kernel norm is not bitwise rms_norm then the gemv"
 
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K, IQ4_XS))
@@ -260,12 +289,14 @@ def test_gate_up_norm(hl, oracle, dev, t, n_vec, variant):
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K))
 @pytest.mark.parametrize("variant", [0, 1, 3])
-def test_lm_head_norm(hl, oracle, dev, t, variant):
+@pytest.mark.parametrize("n_vec", [1, 3])
+def test_lm_head_norm(hl, oracle, dev, t, variant, n_vec):
     """The LM head with the output norm folded in: the argmax is the first maximum of the GPU's
-    own logits, the logits are within the variant's bound of the CPU's (rms_norm then matmul)."""
+    own logits, the logits are within the variant's bound of the CPU's (rms_norm then matmul).
+    One vector on the SLAB GEMV takes the norm inside the kernel."""
     import torch
 
-    rows, cols, n_vec = 1000, 512, 3
+    rows, cols = 1000, 512
     say("lm_head norm", NAMES[t], rows, cols, n_vec, variant)
     buf, stride = make_weights(t, rows, cols, seed=1000 + t)
     dense = dense_of(buf, t, rows, cols, stride, 0)
@@ -356,6 +387,31 @@ def test_gemv_group_within_bounds(hl, oracle, dev, g, n_vec, norm):
             assert np.all(err <= tol), f"{NAMES[t]}: worst |d|/bound = {max_ratio(err, tol):.3f}"
             if plain is not None:
                 assert isclose_bits(out[:, :rows], host(plain[k])), f"{NAMES[t]}: fused norm not bitwise"
+
+
+def test_gemv_group_norm_layer_shapes(hl, dev):
+    """The config-5 layer's q, k (Q4_K) and v (Q6_K) over the 5120-wide attention input, one
+    vector with the input norm: the norm inside the grouped kernel, bitwise RMS_NORM then the
+    same group."""
+    import torch
+
+    cols = 5120
+    say("gemv_group norm layer shapes", cols)
+    x, w = norm_inputs(cols, 1, 1250)
+    segs = []
+    for i, (t, rows) in enumerate([(Q4_K, 6144), (Q4_K, 1024), (Q6_K, 1024)]):
+        buf, stride = make_weights(t, rows, cols, seed=1260 + i)
+        segs.append((t, slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, 0), rows, cols), rows))
+    xg = torch.empty((1, cols), dtype=torch.float32, device=dev)
+    hl.rms_norm(to_dev(x, dev), to_dev(w, dev), xg, 1, cols, eps=EPS)
+    plain = [torch.zeros((1, rows), dtype=torch.float32, device=dev) for _, _, rows in segs]
+    hl.gemv_group([(t, wt, rows, p) for (t, wt, rows), p in zip(segs, plain)], xg, cols, 1)
+    for rep in range(2):
+        fused = [torch.full((1, rows), SENTINEL, dtype=torch.float32, device=dev) for _, _, rows in segs]
+        hl.gemv_group([(t, wt, rows, f) for (t, wt, rows), f in zip(segs, fused)], to_dev(x, dev), cols, 1,
+                      norm_w=to_dev(w, dev), norm_eps=EPS)
+        for k, (f, p) in enumerate(zip(fused, plain)):
+            assert isclose_bits(host(f), host(p)), f"segment {k}: the in-kernel norm is not bitwise rms_norm then the group"
 
 
 def test_gemv_group_rows_do_not_depend_on_the_batch(hl, dev):

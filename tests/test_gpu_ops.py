@@ -282,6 +282,44 @@ def test_split_k_timeout_is_reported_and_the_workspace_recovers(hl, oracle, dev)
     assert np.all(np.abs(host(y).astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dense, rows, cols, x))
 
 
+def test_fused_norm_split_k_timeout_is_reported_and_recovers(hl, oracle, dev):
+    """The one-vector fused norm inside the GEMV (every workgroup computes 1 / rms itself) under a
+    forced split-K timeout (the reductions wait for a tag no partial carries, 64 rounds): they
+    give up, leave NaN and mark the status word; the kernels exit normally, halo_mi_stream_check
+    reports a Device error once, and the next calls are bitwise the unfused RMS_NORM then GEMV."""
+    import torch
+
+    t, rows, cols = Q4_K, 1024, 5120  # 16 slabs x 8 K chunks: 128 workgroups
+    say("fused norm forced timeout", rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=1750)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    rng = np.random.default_rng(1751)
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    xd, wd = to_dev(x, dev), to_dev(w, dev)
+    y = torch.full((1, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.stream_check()
+    try:
+        hl.force_splitk_timeout(64, True)
+        hl.gemv(t, slab, xd, y, rows, cols, 1, variant=hl.Variant.SLAB_GEMV, norm_w=wd)
+    finally:
+        hl.force_splitk_timeout(0, False)
+    with pytest.raises(hl.HaloError) as e:
+        hl.stream_check()
+    assert e.value.code == hl.ErrorCode.Device
+    assert not np.all(np.isfinite(host(y))), "a wait that gave up must not leave only plausible values"
+    hl.stream_check()  # reported once
+    for _ in range(2):  # the launch state moved on: later calls are correct, twice in a row
+        hl.gemv(t, slab, xd, y, rows, cols, 1, variant=hl.Variant.SLAB_GEMV, norm_w=wd)
+        hl.stream_check()
+        xn = torch.empty((1, cols), dtype=torch.float32, device=dev)
+        hl.rms_norm(xd, wd, xn, 1, cols)
+        y2 = torch.full((1, rows), SENTINEL, dtype=torch.float32, device=dev)
+        hl.gemv(t, slab, xn, y2, rows, cols, 1, variant=hl.Variant.SLAB_GEMV)
+        assert isclose_bits(host(y), host(y2)), "after the timeout the fused norm is not bitwise rms_norm then the gemv"
+
+
 def test_stream_release_frees_and_reallocates(hl, oracle, dev):
     import torch
 
