@@ -219,6 +219,9 @@ WORKLOADS = {
     "hybrid_layer_m1_qk_fused": ("layer_qk", None, 0, 0, 1, 5),
     "hybrid_layer_m1_qkv_group": ("layer_qkv", None, 0, 0, 1, 5),
     "hybrid_layer_m1_qk_fused_qkv_group": ("layer_qk_qkv", None, 0, 0, 1, 5),
+    "hybrid_layer_m4_qkv_group": ("layer_qkv", None, 0, 0, 4, 5),
+    "hybrid_layer_m512_qkv_group": ("layer_qkv", None, 0, 0, 512, 5),
+    "q4k_gemv_17408x5120_m8": ("gemv", "Q4_K", 17408, 5120, 8, 2),
     "q6k_gemv_151936x5120_m1": ("gemv", "Q6_K", 151936, 5120, 1, 3),
     "q4k_gate_up_swiglu_m4": ("gemm", "Q4_K", 17408, 5120, 4, 4),
     "read_floor_50MB": ("read_floor", None, 17408 * 2880, 0, 0, 0),
@@ -330,7 +333,8 @@ def layer_case(hl, torch, m, seed=5, fuse_qk=False, group_qkv=False):
     enough copies of the layer's weights that the MALL cannot serve repeats. fuse_qk: q and k
     (both Q4_K, 5120 columns) as one row-fused 7168-row matrix, one GEMV instead of two (the
     reference's try_make_fused; v is Q6_K, so it stays apart). group_qkv: q (or q|k), k and v
-    in one halo_mi_gemv_group launch (two weight types)."""
+    in one grouped call (two weight types): halo_mi_gemv_group up to 8 vectors, the grouped bf16
+    GEMM halo_mi_gemm_group above."""
     layer = LAYER
     if fuse_qk:
         layer = [(n, tn, r, c) for n, tn, r, c in LAYER if n not in ("q", "k")]
@@ -362,7 +366,7 @@ def layer_case(hl, torch, m, seed=5, fuse_qk=False, group_qkv=False):
             else:
                 hl.gemv(t, dev[0], xs[cols], ys[name], rows, cols, m)
         if group:
-            hl.gemv_group(group, xs[5120], 5120, m)
+            (hl.gemm_group if m > 8 else hl.gemv_group)(group, xs[5120], 5120, m)
 
     ms, samples, nsteps = time_window(torch, launch, n_copies)
     algo = sum(wb + 4 * m * cols + 4 * m * rows for name, _, rows, cols, _, wb in mats)
@@ -556,15 +560,24 @@ def main() -> int:
             r = layer_case(hl, torch, m)
             extra[f"hybrid_layer_m{m}"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                            "TFLOP/s": round(r["tflops"], 2)}
-        for m in (1, 4):
-            log(f"config 5 with q|k row-fused (one GEMV for both) M={m}")
-            r = layer_case(hl, torch, m, fuse_qk=True)
-            extra[f"hybrid_layer_m{m}_qk_fused"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-                                                    "TFLOP/s": round(r["tflops"], 2)}
+        for m in (1, 4, 512):
+            if m != 512:
+                log(f"config 5 with q|k row-fused (one GEMV for both) M={m}")
+                r = layer_case(hl, torch, m, fuse_qk=True)
+                extra[f"hybrid_layer_m{m}_qk_fused"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                                        "TFLOP/s": round(r["tflops"], 2)}
             log(f"config 5 with q, k, v in one grouped launch M={m}")
             r = layer_case(hl, torch, m, group_qkv=True)
             extra[f"hybrid_layer_m{m}_qkv_group"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                                      "TFLOP/s": round(r["tflops"], 2)}
+        for m in (2, 4, 8):
+            # what the Backend adapter runs for decode and MTP verify (GemvArgs::allow_gemm off):
+            # the slab GEMV, every row bitwise its own n_vec == 1 row
+            log(f"decode / MTP verify through the adapter's choice (slab GEMV) M={m}")
+            extra[f"q4k_gemv_17408x5120_m{m}_allow_gemm_off"] = gemv_fig(gemv_case(hl, torch, Q4_K, 17408, 5120, m, 2, variant=2))
+            r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, variant=2)
+            extra[f"q4k_gate_up_swiglu_m{m}_allow_gemm_off"] = {**gemm_fig(r),
+                                                                "weights_GB/s": round(2 * 17408 * 2880 / (r["ms"] * 1e-3) / 1e9, 1)}
         for m in (2, 4, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
             r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4)

@@ -27,6 +27,7 @@ from ._lib import (  # noqa: F401
     force_splitk_timeout,
     gate_up_swiglu,
     gemv,
+    gemm_group,
     gemv_group,
     gemv_noalloc,
     get_rows,

@@ -192,6 +192,7 @@ SIGNATURES = {
     "halo_mi_gemv": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
     "halo_mi_gemv_noalloc": (_INT, [ctypes.POINTER(_GemvParams), _VP]),
     "halo_mi_gemv_group": (_INT, [ctypes.POINTER(_GemvGroupParams), _VP]),
+    "halo_mi_gemm_group": (_INT, [ctypes.POINTER(_GemvGroupParams), _VP]),
     "halo_mi_gate_up_swiglu": (_INT, [ctypes.POINTER(_GateUpParams), _VP]),
     "halo_mi_lm_head": (_INT, [ctypes.POINTER(_LmHeadParams), _VP]),
     "halo_mi_argmax": (_INT, [_VP, _U64, _U32, _U32, _VP, _VP]),
@@ -342,16 +343,29 @@ def gemv_noalloc(t: int, w, x, y, rows: int, cols: int, n_vec: int, *, x_stride:
     _check(lib().halo_mi_gemv_noalloc(ctypes.byref(p), _stream(stream)))
 
 
-def gemv_group(segs, x, cols: int, n_vec: int, *, x_stride: int = 0, norm_w=None, norm_eps: float = 1e-6,
-               stream=None) -> None:
-    """Grouped GEMV (halo_mi_gemv_group): segs is a list of (type, w, rows, y) or (type, w, rows, y,
-    y_stride), SLAB matrices that share x; one launch per pair of weight types."""
+def _group_params(segs, x, cols, n_vec, x_stride, norm_w, norm_eps):
     arr = (_GemvSegment * len(segs))()
     for i, seg in enumerate(segs):
         t, w, rows, y = seg[:4]
         arr[i] = _GemvSegment(int(t), _ptr(w), int(rows), _ptr(y), int(seg[4]) if len(seg) > 4 else 0)
-    p = _GemvGroupParams(arr, len(segs), _ptr(x), int(x_stride), int(cols), int(n_vec), _ptr(norm_w), float(norm_eps))
+    # the segment array is kept alive with the params (ctypes keeps the reference)
+    return _GemvGroupParams(arr, len(segs), _ptr(x), int(x_stride), int(cols), int(n_vec), _ptr(norm_w), float(norm_eps))
+
+
+def gemv_group(segs, x, cols: int, n_vec: int, *, x_stride: int = 0, norm_w=None, norm_eps: float = 1e-6,
+               stream=None) -> None:
+    """Grouped GEMV (halo_mi_gemv_group): segs is a list of (type, w, rows, y) or (type, w, rows, y,
+    y_stride), SLAB matrices that share x; one launch per pair of weight types."""
+    p = _group_params(segs, x, cols, n_vec, x_stride, norm_w, norm_eps)
     _check(lib().halo_mi_gemv_group(ctypes.byref(p), _stream(stream)))
+
+
+def gemm_group(segs, x, cols: int, n_vec: int, *, x_stride: int = 0, norm_w=None, norm_eps: float = 1e-6,
+               stream=None) -> None:
+    """Grouped bf16 GEMM (halo_mi_gemm_group): the segments of gemv_group on the bf16 MFMA GEMM,
+    x staged once, one launch per pair of weight types."""
+    p = _group_params(segs, x, cols, n_vec, x_stride, norm_w, norm_eps)
+    _check(lib().halo_mi_gemm_group(ctypes.byref(p), _stream(stream)))
 
 
 def gate_up_swiglu(t: int, w_gate, w_up, x, out, rows: int, cols: int, n_vec: int, *, layout: int = Layout.SLAB,

@@ -264,20 +264,25 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     return launch_gemm_pc<false>(p->type, a, st);
 }
 
-int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream) {
-    clear_error();
-    const char* op = "MATMUL_GROUP";
+}  // extern "C"
+
+namespace {
+
+// The checks both grouped entry points make (halo_mi_gemv_group's contract); segs and *xs
+// receive the resolved segments and x stride. *empty: nothing to compute.
+int check_group(const halo_mi_gemv_group_params* p, const char* op, GroupSeg (&segs)[HALO_MI_GEMV_GROUP_MAX], uint64_t* xs,
+                bool* empty) {
+    *empty = true;
     if (!p) return set_error(HALO_MI_E_KERNEL, "%s: null params", op);
     if (p->n_segs == 0 || p->n_vec == 0) return HALO_MI_OK;
     if (!p->segs) return set_error(HALO_MI_E_KERNEL, "%s: null segment list", op);
     if (p->n_segs > HALO_MI_GEMV_GROUP_MAX)
         return set_error(HALO_MI_E_UNSUPPORTED, "%s: %u segments (at most %u)", op, p->n_segs, HALO_MI_GEMV_GROUP_MAX);
     if (!p->x) return set_error(HALO_MI_E_KERNEL, "%s: operand x is empty", op);
-    const uint64_t xs = p->x_stride ? p->x_stride : p->cols;
-    if (p->n_vec > 1 && xs < p->cols) return set_error(HALO_MI_E_KERNEL, "%s: x row stride < cols", op);
+    *xs = p->x_stride ? p->x_stride : p->cols;
+    if (p->n_vec > 1 && *xs < p->cols) return set_error(HALO_MI_E_KERNEL, "%s: x row stride < cols", op);
     if (reinterpret_cast<uintptr_t>(p->x) % 4) return set_error(HALO_MI_E_KERNEL, "%s: x must be 4-byte aligned", op);
-    const uint64_t xext = extent(p->n_vec, xs * 4, (uint64_t)p->cols * 4);
-    GroupSeg segs[HALO_MI_GEMV_GROUP_MAX];
+    const uint64_t xext = extent(p->n_vec, *xs * 4, (uint64_t)p->cols * 4);
     uint64_t wext[HALO_MI_GEMV_GROUP_MAX], yext[HALO_MI_GEMV_GROUP_MAX];
     for (uint32_t i = 0; i < p->n_segs; ++i) {
         const halo_mi_gemv_segment& g = p->segs[i];
@@ -308,7 +313,36 @@ int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream) {
     }
     if (p->norm_w && reinterpret_cast<uintptr_t>(p->norm_w) % 4)
         return set_error(HALO_MI_E_KERNEL, "%s: norm_w must be 4-byte aligned", op);
+    *empty = false;
+    return HALO_MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream) {
+    clear_error();
+    GroupSeg segs[HALO_MI_GEMV_GROUP_MAX];
+    uint64_t xs = 0;
+    bool empty = true;
+    if (int rc = check_group(p, "MATMUL_GROUP", segs, &xs, &empty)) return rc;
+    if (empty) return HALO_MI_OK;
     return launch_gemv_group(segs, p->n_segs, p->x, xs, p->cols, p->n_vec, p->norm_w, p->norm_eps,
+                             static_cast<hipStream_t>(stream));
+}
+
+int halo_mi_gemm_group(const halo_mi_gemv_group_params* p, void* stream) {
+    clear_error();
+    const char* op = "GEMM_GROUP";
+    GroupSeg segs[HALO_MI_GEMV_GROUP_MAX];
+    uint64_t xs = 0;
+    bool empty = true;
+    if (int rc = check_group(p, op, segs, &xs, &empty)) return rc;
+    if (empty) return HALO_MI_OK;
+    if (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16)
+        return set_error(HALO_MI_E_KERNEL, "%s: the bf16 MFMA GEMM needs 16-byte aligned x rows", op);
+    return launch_gemm_group(segs, p->n_segs, p->x, xs, p->cols, p->n_vec, p->norm_w, p->norm_eps,
                              static_cast<hipStream_t>(stream));
 }
 

@@ -415,16 +415,19 @@ __device__ __forceinline__ uint32_t mfma32_row(uint32_t r, uint32_t lane) { retu
 // Consumer waves: WM along M x WN along N; a wave owns MBW 32-row x blocks and NBW 32-row W
 // blocks. With PAIR its first NBW / 2 W blocks are gate rows and the others the up rows of the
 // same range, so every lane holds matching gate and up sums.
+constexpr uint32_t kPcStage = kPcW * kPcLd;  // bf16 per LDS stage of k_gemm_pc (W only)
+
+// The body of workgroup `bid` of a k_gemm_pc launch over the matrix of `a` (also one segment of a
+// grouped launch, k_gemm_pc_group); lds: kPcBufs stages.
 template <uint32_t T, bool PAIR, int MB>
-__global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
+__device__ __forceinline__ void gemm_pc_body(const GemmPcArgs& a, uint32_t bid, __bf16* lds) {
     constexpr int BM = 64 * MB;
     // KH (64-row tiles): wave w multiplies x block w % 2 by all four W blocks over K half w / 2
     // of every stage, so each x fragment is loaded by one wave; the pairs' sums meet at the end
     constexpr bool KH = MB == 1;
     constexpr int WM = MB == 1 ? 2 : 4, WN = KH ? 1 : 4 / WM;
     constexpr int MBW = BM / WM / 32, NBW = 4 / WN;
-    constexpr uint32_t STAGE = kPcW * kPcLd;  // bf16 per LDS stage (W only)
-    __shared__ __bf16 lds[kPcBufs * STAGE];
+    constexpr uint32_t STAGE = kPcStage;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t S = a.cols / kSlot;
@@ -433,10 +436,10 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
 
     // workgroup -> (W tile u, M tile mt) for a whole tile, or (split tile st, K chunk)
     const uint32_t whole = a.units * a.m_tiles;
-    const bool split = blockIdx.x >= whole;
+    const bool split = bid >= whole;
     uint32_t u, mt, st = 0, chunk = 0;
     if (!split) {
-        const uint32_t wg = blockIdx.x;
+        const uint32_t wg = bid;
         if (a.xcd_map) {
             const uint32_t grp = 8 / a.m_tiles, xcd = wg % 8;
             mt = xcd / grp;
@@ -446,8 +449,8 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
             mt = wg % a.m_tiles;
         }
     } else {
-        st = (blockIdx.x - whole) / a.kchunks;
-        chunk = (blockIdx.x - whole) % a.kchunks;
+        st = (bid - whole) / a.kchunks;
+        chunk = (bid - whole) % a.kchunks;
         u = a.split_unit0 + st / a.m_tiles;
         mt = st % a.m_tiles;
     }
@@ -536,7 +539,7 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
             // and the first adds them
             pc_sync();
             float* red = reinterpret_cast<float*>(lds) + wm * (NBW * 16 * 64) + lane;
-            static_assert(2 * NBW * 16 * 64 * 4 <= sizeof(lds), "the pair sums fit the stage buffers");
+            static_assert(2 * NBW * 16 * 64 * 4 <= kPcBufs * kPcStage * sizeof(__bf16), "the pair sums fit the stage buffers");
             if (kh == 1) {
 #pragma unroll
                 for (int j = 0; j < NBW; ++j)
@@ -688,9 +691,14 @@ __host__ __device__ inline uint32_t reduce_rows(uint32_t bm, uint32_t m_tiles, u
     return m_tiles == 1 && n_vec < bm ? n_vec : bm;
 }
 
+template <uint32_t T, bool PAIR, int MB>
+__global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
+    __shared__ __bf16 lds[kPcBufs * kPcStage];
+    gemm_pc_body<T, PAIR, MB>(a, blockIdx.x, lds);
+}
+
 template <bool PAIR, int BM>
-__global__ void k_gemm_pc_reduce(GemmPcArgs a) {
-    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void pc_reduce_elem(const GemmPcArgs& a, uint64_t idx) {
     constexpr uint32_t NC = PAIR ? 64 : kPcW;  // output columns per tile
     const uint64_t tiles = (uint64_t)a.split_units * a.m_tiles;
     const uint32_t R = reduce_rows(BM, a.m_tiles, a.n_vec);
@@ -714,6 +722,44 @@ __global__ void k_gemm_pc_reduce(GemmPcArgs a) {
         const uint32_t col = 2 * u * kSlabRows + nl;
         if (col < a.rows) yrow[col] = s0;
     }
+}
+
+template <bool PAIR, int BM>
+__global__ void k_gemm_pc_reduce(GemmPcArgs a) {
+    pc_reduce_elem<PAIR, BM>(a, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// ---- grouped bf16 GEMM (halo_mi_gemm_group): SLAB matrices sharing x ----------------------
+// The x rows are staged once; the segments' tiles (all whole, or all split over the same K
+// chunks) form one launch per pair of weight types, each workgroup running the k_gemm_pc body of
+// its segment's type; split tiles are reduced by one launch over all segments.
+struct GemmGroupArgs {
+    GemmPcArgs seg[HALO_MI_GEMV_GROUP_MAX];
+    uint32_t type[HALO_MI_GEMV_GROUP_MAX];
+    uint32_t wg_end[HALO_MI_GEMV_GROUP_MAX];   // workgroups of segments [0, i]
+    uint64_t out_end[HALO_MI_GEMV_GROUP_MAX];  // reduce outputs of segments [0, i]
+    uint32_t n;
+};
+
+template <uint32_t TA, uint32_t TB, int MB>
+__global__ __launch_bounds__(512) void k_gemm_pc_group(GemmGroupArgs g) {
+    __shared__ __bf16 lds[kPcBufs * kPcStage];
+    uint32_t s = 0;
+    while (s + 1 < g.n && blockIdx.x >= g.wg_end[s]) ++s;
+    const uint32_t bid = blockIdx.x - (s ? g.wg_end[s - 1] : 0u);
+    if (g.type[s] == TA) {
+        gemm_pc_body<TA, false, MB>(g.seg[s], bid, lds);
+    } else {
+        if constexpr (TB != TA) gemm_pc_body<TB, false, MB>(g.seg[s], bid, lds);
+    }
+}
+
+template <int BM>
+__global__ void k_gemm_pc_reduce_group(GemmGroupArgs g) {
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t s = 0;
+    while (s + 1 < g.n && idx >= g.out_end[s]) ++s;
+    pc_reduce_elem<false, BM>(g.seg[s], idx - (s ? g.out_end[s - 1] : 0ull));
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1413,6 +1459,135 @@ int launch_gemm_chunk_reduce(bool pair, const GemmArgs& g, float* partials, uint
 
 template int launch_gemm_pc<false>(uint32_t, const GemmArgs&, hipStream_t);
 template int launch_gemm_pc<true>(uint32_t, const GemmArgs&, hipStream_t);
+
+namespace {
+
+constexpr uint32_t kGroupGemmTypes[6] = {kQ4_0, kQ8_0, kQ4_K, kQ5_K, kQ6_K, kIQ4_XS};
+
+int group_type_index(uint32_t t) {
+    for (int i = 0; i < 6; ++i)
+        if (kGroupGemmTypes[i] == t) return i;
+    return -1;
+}
+
+template <int MB, int IA, int IB>
+bool gemm_group_pair(uint32_t ta, uint32_t tb, const GemmGroupArgs& g, dim3 grid, hipStream_t st) {
+    constexpr uint32_t TA = kGroupGemmTypes[IA], TB = kGroupGemmTypes[IB];
+    if (ta != TA || tb != TB) return false;
+    hipLaunchKernelGGL((k_gemm_pc_group<TA, TB, MB>), grid, dim3(512), 0, st, g);
+    return true;
+}
+
+// (ta, tb) with ta's index <= tb's in kGroupGemmTypes
+template <int MB>
+bool gemm_group_types(uint32_t ta, uint32_t tb, const GemmGroupArgs& g, dim3 grid, hipStream_t st) {
+#define HALO_MI_GPAIR(A, B) gemm_group_pair<MB, A, B>(ta, tb, g, grid, st)
+    return HALO_MI_GPAIR(0, 0) || HALO_MI_GPAIR(0, 1) || HALO_MI_GPAIR(0, 2) || HALO_MI_GPAIR(0, 3) || HALO_MI_GPAIR(0, 4) ||
+           HALO_MI_GPAIR(0, 5) || HALO_MI_GPAIR(1, 1) || HALO_MI_GPAIR(1, 2) || HALO_MI_GPAIR(1, 3) || HALO_MI_GPAIR(1, 4) ||
+           HALO_MI_GPAIR(1, 5) || HALO_MI_GPAIR(2, 2) || HALO_MI_GPAIR(2, 3) || HALO_MI_GPAIR(2, 4) || HALO_MI_GPAIR(2, 5) ||
+           HALO_MI_GPAIR(3, 3) || HALO_MI_GPAIR(3, 4) || HALO_MI_GPAIR(3, 5) || HALO_MI_GPAIR(4, 4) || HALO_MI_GPAIR(4, 5) ||
+           HALO_MI_GPAIR(5, 5);
+#undef HALO_MI_GPAIR
+}
+
+// One launch over the segments of weight types ta and tb on the staged rows (mc of them, m_tiles
+// M tiles of 64 MB rows): whole tiles when they fill half the GPU or more (as k_gemm_pc's
+// choice), else every tile split over the same K chunks into the workspace's partials, then one
+// reduce over all of them. (Config 5's q|k|v at M = 512 is 128 whole tiles; two K chunks each
+// plus the reduce measured 533.0 against 531.3 us for the whole layer, same box.)
+template <int MB>
+int gemm_group_launch(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb, uint32_t cols, uint32_t mc, uint32_t m_tiles,
+                      uint64_t m_start, Workspace* ws, hipStream_t st) {
+    constexpr uint32_t BM = 64u * MB;
+    const uint32_t S = cols / kSlot, cus = cu_count();
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < n; ++i) tiles += (uint64_t)(((segs[i].rows + kSlabRows - 1) / kSlabRows + 1) / 2) * m_tiles;
+    if (tiles == 0) return HALO_MI_OK;
+    uint32_t kc = 1;
+    if (S % 8 == 0 && 2 * tiles < cus) {
+        kc = (uint32_t)std::min<uint64_t>({cus / tiles, S / 8, 16});
+        while (kc > 1 && tiles * kc * BM * kPcW > kPartialFloats) --kc;
+    }
+    GemmGroupArgs g{};
+    g.n = n;
+    uint32_t wg = 0;
+    uint64_t outs = 0, poff = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t units = ((segs[i].rows + kSlabRows - 1) / kSlabRows + 1) / 2;
+        GemmPcArgs p{static_cast<const uint8_t*>(segs[i].w), nullptr, ws->xb, segs[i].y + m_start * segs[i].y_stride,
+                     segs[i].y_stride, segs[i].rows, cols, mc, units, m_tiles, 0u, 0u, 1u, ws->partials + poff};
+        if (kc > 1) {  // every tile split over K
+            p.units = 0;
+            p.split_units = units;
+            p.split_unit0 = 0;
+            p.kchunks = kc;
+            poff += (uint64_t)units * m_tiles * kc * BM * kPcW;
+            outs += (uint64_t)units * m_tiles * reduce_rows(BM, m_tiles, mc) * kPcW;
+        } else if (wg % 8 == 0 && m_tiles <= 8 && 8 % m_tiles == 0 && ((uint64_t)units * m_tiles) % 8 == 0) {
+            p.xcd_map = 1;  // the segment starts on XCD 0 of the round robin
+        }
+        wg += units * m_tiles * kc;
+        g.seg[i] = p;
+        g.type[i] = segs[i].type;
+        g.wg_end[i] = wg;
+        g.out_end[i] = outs;
+    }
+    if (!gemm_group_types<MB>(ta, tb, g, dim3(wg), st))
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm_group: no kernel for types %u and %u", ta, tb);
+    if (kc > 1) hipLaunchKernelGGL((k_gemm_pc_reduce_group<BM>), dim3((uint32_t)((outs + 255) / 256)), dim3(256), 0, st, g);
+    return hip_status(hipGetLastError(), "gemm_group launch");
+}
+
+}  // namespace
+
+// The grouped bf16 GEMM (halo_mi_gemm_group): x staged once per block of rows (with the fused
+// norm as the single-matrix GEMM stages it), then one launch per pair of weight types, in the
+// order the types first appear. M tiles as k_gemm_pc: 64 rows up to 64 vectors, 128 up to 128,
+// 256 beyond.
+int launch_gemm_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t x_stride, uint32_t cols, uint32_t n_vec,
+                      const float* norm_w, float eps, hipStream_t st) {
+    Workspace* ws = nullptr;
+    if (int rc = workspace_for(st, &ws)) return rc;
+    if (!ws)
+        return set_error(HALO_MI_E_MEMORY, "gemm_group: this stream is being captured and has no workspace yet "
+                                           "(make one call on it before capturing)");
+    const int MB = n_vec <= 64 ? 1 : n_vec <= 128 ? 2 : 4;
+    const uint32_t BM = 64u * MB;
+    const uint64_t cap_rows = std::min(kXbElems / cols, kInvFloats) / BM * BM;
+    if (cap_rows == 0) return set_error(HALO_MI_E_UNSUPPORTED, "gemm_group: cols %u too large for the x staging buffer", cols);
+    if ((uint64_t)BM * cols * 2 > 0xFFFFFFFFull)
+        return set_error(HALO_MI_E_UNSUPPORTED, "gemm_group: cols %u too large for one M tile", cols);
+    uint32_t types[HALO_MI_GEMV_GROUP_MAX], nt = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        bool seen = false;
+        for (uint32_t k = 0; k < nt; ++k) seen |= types[k] == segs[i].type;
+        if (!seen) types[nt++] = segs[i].type;
+    }
+    GemmArgs a{nullptr, nullptr, x, x_stride, nullptr, 0, 0, cols, n_vec};
+    a.norm_w = norm_w;
+    a.norm_eps = eps;
+    for (uint64_t m_start = 0; m_start < n_vec; m_start += cap_rows) {
+        const uint32_t mc = (uint32_t)std::min<uint64_t>(cap_rows, n_vec - m_start);
+        const uint32_t m_tiles = (mc + BM - 1) / BM;
+        if (int rc = stage_x(a, m_start, mc, m_tiles * BM, ws, st)) return rc;
+        for (uint32_t k0 = 0; k0 < nt; k0 += 2) {
+            uint32_t ta = types[k0], tb = k0 + 1 < nt ? types[k0 + 1] : types[k0];
+            if (group_type_index(ta) > group_type_index(tb)) std::swap(ta, tb);
+            GroupSeg part[HALO_MI_GEMV_GROUP_MAX];
+            uint32_t np = 0;
+            for (uint32_t i = 0; i < n; ++i)
+                if (segs[i].type == ta || segs[i].type == tb) part[np++] = segs[i];
+            int rc;
+            switch (MB) {
+                case 1: rc = gemm_group_launch<1>(part, np, ta, tb, cols, mc, m_tiles, m_start, ws, st); break;
+                case 2: rc = gemm_group_launch<2>(part, np, ta, tb, cols, mc, m_tiles, m_start, ws, st); break;
+                default: rc = gemm_group_launch<4>(part, np, ta, tb, cols, mc, m_tiles, m_start, ws, st); break;
+            }
+            if (rc) return rc;
+        }
+    }
+    return HALO_MI_OK;
+}
 
 int launch_swiglu(const float* g, uint64_t gs, const float* u, uint64_t us, float* out, uint64_t os, uint32_t rows,
                   uint32_t cols, hipStream_t st) {

@@ -176,6 +176,9 @@ struct GroupSeg {
 };
 int launch_gemv_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t x_stride, uint32_t cols, uint32_t n_vec,
                       const float* norm_w, float eps, hipStream_t st);
+// k_gemm.hip: the same segments on the bf16 MFMA GEMM (x staged once, one launch per type pair)
+int launch_gemm_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t x_stride, uint32_t cols, uint32_t n_vec,
+                      const float* norm_w, float eps, hipStream_t st);
 // k_gemm.hip
 template <bool PAIR>
 int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st);

@@ -129,8 +129,11 @@ enum {
  *        - GGUF reference variant: x is normalized first exactly as cpu::rms_norm, so y is
  *          bitwise rms_norm then matmul;
  *        - bf16 GEMM variants: the same normalized x, rounded to bf16 while it is staged;
- *        - SLAB GEMV (2, 6 and the GEMV legs of the auto variants): x is normalized into the
- *          stream's workspace by the RMS_NORM kernel, then the GEMV runs on it.
+ *        - SLAB GEMV (2 and the GEMV legs of the auto variants), one vector: inside the MFMA
+ *          GEMV's launch, one dispatch: every workgroup computes 1 / rms in cpu::rms_norm's
+ *          order and normalizes its own x elements as cpu::rms_norm rounds them (cols <= 8192);
+ *        - otherwise (more vectors, wider rows, variant 6): x is normalized into the stream's
+ *          workspace by the RMS_NORM kernel, then the GEMV runs on it.
  *      So y is bitwise halo_mi_rms_norm then the same variant without the norm, at any n_vec
  *      (the reference's Limits::max_fused_norm_cols contract, backend.h:236-242).
  *      norm_w must not overlap y.
@@ -209,6 +212,19 @@ typedef struct halo_mi_gemv_group_params {
 } halo_mi_gemv_group_params;
 
 int halo_mi_gemv_group(const halo_mi_gemv_group_params* p, void* stream);
+
+/*
+ * Grouped bf16 GEMM: the same segments and operands as halo_mi_gemv_group, computed by the bf16
+ * MFMA GEMM (the prefill path, GemvArgs::allow_gemm: halo_mi_gemv's numerics for more than 8
+ * vectors), with x staged once for all segments and one launch per pair of weight types (M
+ * tiles of 64 / 128 / 256 rows by n_vec; when a launch's tiles fill less than half the GPU,
+ * every tile is split over the same K chunks and one reduce adds them in chunk order). The
+ * reference issues the projections one by one (Qwen35::Impl::gemv, src/models/qwen35.cpp:
+ * 486-498); a layer's q, k and v at M = 512 then pay three x stagings, three under-filled
+ * launches and three reduces. Numerics per output: halo_mi_gemv's bf16 GEMM bound; x rows
+ * 16-byte aligned (x_stride a multiple of 4 floats), as the single-matrix GEMM.
+ */
+int halo_mi_gemm_group(const halo_mi_gemv_group_params* p, void* stream);
 
 /*
  * Fused FFN gate/up: out[t][n] = silu((Wg x_t)[n]) * (Wu x_t)[n], silu(v) = v / (1 + exp(-v)).

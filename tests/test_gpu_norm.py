@@ -435,6 +435,84 @@ def test_gemv_group_rows_do_not_depend_on_the_batch(hl, dev):
         assert isclose_bits(batch[k], np.concatenate([s[k] for s in singles])), f"segment {k}: a row changed with n_vec"
 
 
+@pytest.mark.parametrize("g", range(len(GROUPS)))
+@pytest.mark.parametrize("n_vec,norm", [(9, False), (40, True), (130, False), (300, True), (600, False)])
+def test_gemm_group_within_bounds(hl, oracle, dev, g, n_vec, norm):
+    """The grouped bf16 GEMM (halo_mi_gemm_group): x staged once, one launch per pair of weight
+    types (64-, 128- and 256-row M tiles; small groups split over K and reduced together), every
+    output within the bf16 GEMM's bound against the CPU and the fp64 products of its own
+    bf16-rounded operands; a second call bitwise the first; padding untouched."""
+    import torch
+
+    cols = 1024
+    say("gemm_group", g, n_vec, norm)
+    x, w = norm_inputs(cols, n_vec, 1400 + g)
+    xn = oracle.rms_norm(x, w, EPS) if norm else x
+    segs, refs = [], []
+    for i, (t, rows) in enumerate(GROUPS[g]):
+        buf, stride = make_weights(t, rows, cols, seed=1410 + 10 * g + i)
+        dense = dense_of(buf, t, rows, cols, stride, 0)
+        y = torch.full((n_vec, rows + 3), SENTINEL, dtype=torch.float32, device=dev)
+        segs.append((t, slab_of(hl, dev, t, dense, rows, cols), rows, y, rows + 3))
+        emu, etol = gemm_emulated(oracle, t, dense, rows, cols, xn)
+        refs.append((oracle.matmul(t, dense, rows, cols, xn), gemm_tol(oracle, t, dense, rows, cols, xn), emu, etol))
+    xd = to_dev(x, dev)
+    first = None
+    for rep in range(2):
+        hl.gemm_group(segs, xd, cols, n_vec, norm_w=to_dev(w, dev) if norm else None, norm_eps=EPS)
+        outs = [host(y) for (_, _, _, y, _) in segs]
+        for (t, _, rows, _, _), out, (ref, tol, emu, etol) in zip(segs, outs, refs):
+            assert np.all(out[:, rows:] == SENTINEL), "y padding written"
+            o = out[:, :rows].astype(np.float64)
+            assert np.all(np.abs(o - ref) <= tol), f"{NAMES[t]}: vs cpu worst |d|/bound = {max_ratio(np.abs(o - ref), tol):.3f}"
+            assert np.all(np.abs(o - emu) <= etol), \
+                f"{NAMES[t]}: vs bf16-exact products worst |d|/bound = {max_ratio(np.abs(o - emu), etol):.3f}"
+        if first is None:
+            first = outs
+        else:
+            for a, b in zip(first, outs):
+                assert isclose_bits(a, b), "a second grouped GEMM call gave different bits"
+
+
+@pytest.mark.parametrize("n_vec", [64, 512])
+def test_gemm_group_layer_qkv(hl, oracle, dev, n_vec):
+    """Config 5's q (6144 rows), k (1024) and v (1024 rows, Q6_K) over the 5120-wide input at
+    M = 64 and 512 in one grouped GEMM call, every output within the bf16-exact-product bound."""
+    import torch
+
+    cols = 5120
+    say("gemm_group layer q|k|v", n_vec)
+    x = hl.fill_normal(1450 + n_vec, n_vec * cols).reshape(n_vec, cols)
+    segs, refs = [], []
+    for i, (t, rows) in enumerate([(Q4_K, 6144), (Q4_K, 1024), (Q6_K, 1024)]):
+        from helpers import synth_matrix
+        wq = synth_matrix(hl, t, rows, cols, 1460 + i)
+        y = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+        segs.append((t, slab_of(hl, dev, t, wq, rows, cols), rows, y))
+        refs.append(gemm_emulated(oracle, t, wq, rows, cols, x))
+    hl.gemm_group(segs, to_dev(x, dev), cols, n_vec)
+    for (t, _, rows, y), (emu, etol) in zip(segs, refs):
+        err = np.abs(host(y).astype(np.float64) - emu)
+        print(f"    {NAMES[t]} {rows} rows M={n_vec}: worst |d|/bound = {max_ratio(err, etol):.4f}")
+        assert np.all(err <= etol)
+
+
+def test_gemm_group_rejects(hl, dev):
+    import torch
+
+    cols = 256
+    buf, _ = make_weights(Q4_K, 64, cols, seed=4)
+    w = slab_of(hl, dev, Q4_K, buf[:64 * row_bytes(Q4_K, cols)], 64, cols)
+    x = torch.ones((16, cols + 1), dtype=torch.float32, device=dev)
+    y = torch.zeros((16, 128), dtype=torch.float32, device=dev)
+    with pytest.raises(hl.HaloError) as e:  # x rows not 16-byte aligned (stride of cols + 1 floats)
+        hl.gemm_group([(Q4_K, w, 64, y)], x, cols, 16, x_stride=cols + 1)
+    assert e.value.code == hl.ErrorCode.Kernel
+    with pytest.raises(hl.HaloError) as e:  # two outputs overlapping
+        hl.gemm_group([(Q4_K, w, 64, y), (Q4_K, w, 64, y.data_ptr() + 128)], x, cols, 16, x_stride=cols + 1)
+    assert e.value.code == hl.ErrorCode.Kernel
+
+
 def test_gemv_group_rejects(hl, dev):
     import torch
 
