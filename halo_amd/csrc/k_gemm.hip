@@ -697,30 +697,58 @@ __global__ __launch_bounds__(512) void k_gemm_pc(GemmPcArgs a) {
     gemm_pc_body<T, PAIR, MB>(a, blockIdx.x, lds);
 }
 
+// One thread: four consecutive output columns of one row (16-byte partial loads; the loads of
+// four chunks are issued before their additions, which stay in chunk order per output).
 template <bool PAIR, int BM>
 __device__ __forceinline__ void pc_reduce_elem(const GemmPcArgs& a, uint64_t idx) {
     constexpr uint32_t NC = PAIR ? 64 : kPcW;  // output columns per tile
+    constexpr uint32_t NQ = NC / 4;            // four-column groups per tile row
     const uint64_t tiles = (uint64_t)a.split_units * a.m_tiles;
     const uint32_t R = reduce_rows(BM, a.m_tiles, a.n_vec);
-    if (idx >= tiles * R * NC) return;
-    const uint32_t tile = (uint32_t)(idx / (R * NC)), e = (uint32_t)(idx % (R * NC));
-    const uint32_t ml = e / NC, nl = e % NC;
+    if (idx >= tiles * R * NQ) return;
+    const uint32_t tile = (uint32_t)(idx / (R * NQ)), e = (uint32_t)(idx % (R * NQ));
+    const uint32_t ml = e / NQ, nl = 4 * (e % NQ);
     const uint32_t u = a.split_unit0 + tile / a.m_tiles, mt = tile % a.m_tiles;
     const uint32_t m = mt * BM + ml;
     if (m >= a.n_vec) return;
-    const float* P = a.partials + (uint64_t)tile * a.kchunks * BM * kPcW + ml * kPcW;
-    float s0 = 0.0f, s1 = 0.0f;
-    for (uint32_t c = 0; c < a.kchunks; ++c) {
-        s0 += P[(uint64_t)c * BM * kPcW + nl];
-        if constexpr (PAIR) s1 += P[(uint64_t)c * BM * kPcW + 64 + nl];
+    const float* P = a.partials + (uint64_t)tile * a.kchunks * BM * kPcW + ml * kPcW + nl;
+    constexpr uint64_t CS = (uint64_t)BM * kPcW;  // floats per chunk
+    float4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto add = [](float4& s, const float4 v) {
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    };
+    uint32_t c = 0;
+    for (; c + 4 <= a.kchunks; c += 4) {
+        float4 q0[4], q1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q0[i] = *reinterpret_cast<const float4*>(P + (c + i) * CS);
+            if constexpr (PAIR) q1[i] = *reinterpret_cast<const float4*>(P + (c + i) * CS + 64);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            add(s0, q0[i]);
+            if constexpr (PAIR) add(s1, q1[i]);
+        }
+    }
+    for (; c < a.kchunks; ++c) {
+        add(s0, *reinterpret_cast<const float4*>(P + c * CS));
+        if constexpr (PAIR) add(s1, *reinterpret_cast<const float4*>(P + c * CS + 64));
     }
     float* yrow = a.y + (uint64_t)m * a.y_stride;
-    if constexpr (PAIR) {
-        const uint32_t col = u * kSlabRows + nl;
-        if (col < a.rows) yrow[col] = silu_fast(s0) * s1;
-    } else {
-        const uint32_t col = 2 * u * kSlabRows + nl;
-        if (col < a.rows) yrow[col] = s0;
+    const float g[4] = {s0.x, s0.y, s0.z, s0.w}, up[4] = {s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (PAIR) {
+            const uint32_t col = u * kSlabRows + nl + i;
+            if (col < a.rows) yrow[col] = silu_fast(g[i]) * up[i];
+        } else {
+            const uint32_t col = 2 * u * kSlabRows + nl + i;
+            if (col < a.rows) yrow[col] = g[i];
+        }
     }
 }
 
@@ -737,7 +765,7 @@ struct GemmGroupArgs {
     GemmPcArgs seg[HALO_MI_GEMV_GROUP_MAX];
     uint32_t type[HALO_MI_GEMV_GROUP_MAX];
     uint32_t wg_end[HALO_MI_GEMV_GROUP_MAX];   // workgroups of segments [0, i]
-    uint64_t out_end[HALO_MI_GEMV_GROUP_MAX];  // reduce outputs of segments [0, i]
+    uint64_t out_end[HALO_MI_GEMV_GROUP_MAX];  // reduce threads (four columns each) of segments [0, i]
     uint32_t n;
 };
 
@@ -1219,7 +1247,8 @@ void launch_gemm_pc_type(uint32_t type, const GemmPcArgs& a, dim3 grid, hipStrea
 // k_gemm_pc_reduce over the split tiles of p (BM-row tiles)
 template <bool PAIR, int BM>
 void launch_reduce(const GemmPcArgs& p, hipStream_t st) {
-    const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * reduce_rows(BM, p.m_tiles, p.n_vec) * (PAIR ? 64 : kPcW);
+    // threads: four output columns each
+    const uint64_t outs = (uint64_t)p.split_units * p.m_tiles * reduce_rows(BM, p.m_tiles, p.n_vec) * (PAIR ? 64 : kPcW) / 4;
     hipLaunchKernelGGL((k_gemm_pc_reduce<PAIR, BM>), dim3((uint32_t)((outs + 255) / 256)), dim3(256), 0, st, p);
 }
 
@@ -1522,7 +1551,7 @@ int gemm_group_launch(const GroupSeg* segs, uint32_t n, uint32_t ta, uint32_t tb
             p.split_unit0 = 0;
             p.kchunks = kc;
             poff += (uint64_t)units * m_tiles * kc * BM * kPcW;
-            outs += (uint64_t)units * m_tiles * reduce_rows(BM, m_tiles, mc) * kPcW;
+            outs += (uint64_t)units * m_tiles * reduce_rows(BM, m_tiles, mc) * kPcW / 4;  // four columns a thread
         } else if (wg % 8 == 0 && m_tiles <= 8 && 8 % m_tiles == 0 && ((uint64_t)units * m_tiles) % 8 == 0) {
             p.xcd_map = 1;  // the segment starts on XCD 0 of the round robin
         }
