@@ -23,7 +23,11 @@ class DType(enum.IntEnum):
     F32 = 0
     F16 = 1
     Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
+    Q2_K = 10
     Q3_K = 11
     Q4_K = 12
     Q5_K = 13
@@ -31,6 +35,7 @@ class DType(enum.IntEnum):
     IQ4_NL = 20
     IQ3_S = 21
     IQ4_XS = 23
+    BF16 = 30
 
 
 class Layout(enum.IntEnum):
@@ -67,9 +72,10 @@ class HaloError(RuntimeError):
         super().__init__(f"{self.code.name.upper()}_ERROR: {message}")
 
 
-_BLOCK = {DType.F32: (1, 4), DType.F16: (1, 2), DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q3_K: (256, 110),
-          DType.Q4_K: (256, 144), DType.Q5_K: (256, 176), DType.Q6_K: (256, 210), DType.IQ4_NL: (32, 18),
-          DType.IQ3_S: (256, 110), DType.IQ4_XS: (256, 136)}
+_BLOCK = {DType.F32: (1, 4), DType.F16: (1, 2), DType.BF16: (1, 2), DType.Q4_0: (32, 18), DType.Q4_1: (32, 20),
+          DType.Q5_0: (32, 22), DType.Q5_1: (32, 24), DType.Q8_0: (32, 34), DType.Q2_K: (256, 84),
+          DType.Q3_K: (256, 110), DType.Q4_K: (256, 144), DType.Q5_K: (256, 176), DType.Q6_K: (256, 210),
+          DType.IQ4_NL: (32, 18), DType.IQ3_S: (256, 110), DType.IQ4_XS: (256, 136)}
 
 
 def block_elems(t: int) -> int:

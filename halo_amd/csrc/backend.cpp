@@ -59,7 +59,12 @@ const char* type_name(DType t) {
     switch (t) {
         case DType::F32: return "F32";
         case DType::F16: return "F16";
+        case DType::BF16: return "BF16";
         case DType::Q4_0: return "Q4_0";
+        case DType::Q4_1: return "Q4_1";
+        case DType::Q5_0: return "Q5_0";
+        case DType::Q5_1: return "Q5_1";
+        case DType::Q2_K: return "Q2_K";
         case DType::Q8_0: return "Q8_0";
         case DType::Q3_K: return "Q3_K";
         case DType::Q4_K: return "Q4_K";
@@ -698,7 +703,18 @@ private:
         return *hs;
     }
 
+    // The weight types of the reference HIP backend's GEMV, GET_ROWS and dequant ops
+    // (backends/hip/src/ops.cpp:531-549): the library's GGUF-layout kernels also decode BF16,
+    // Q4_1, Q5_0, Q5_1 and Q2_K, but this backend refuses them as the reference's does.
     static std::uint64_t row_bytes(DType t, std::uint32_t cols, const char* op) {
+        switch (t) {
+            case DType::F32: case DType::F16: case DType::Q4_0: case DType::Q8_0: case DType::Q3_K: case DType::Q4_K:
+            case DType::Q5_K: case DType::Q6_K: case DType::IQ3_S: case DType::IQ4_NL: case DType::IQ4_XS: break;
+            default:
+                fail(ErrorCode::Unsupported,
+                     "%s: weight type id %u has no HIP GEMV kernel (F32, F16, Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ3_S, "
+                     "IQ4_NL, IQ4_XS)", op, static_cast<unsigned>(t));
+        }
         const std::uint64_t rb = halo_mi_row_bytes(static_cast<std::uint32_t>(t), cols);
         if (rb == 0) {
             const std::uint64_t one = halo_mi_row_bytes(static_cast<std::uint32_t>(t), 256);

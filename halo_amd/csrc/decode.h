@@ -1,8 +1,9 @@
 // Device-side unpacking of GGUF blocks and SLAB slot records. Every weight value these
-// helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:68-70,
-// :79-90, :143-151, :154-165, :196-233, :236-269, :271-299, :302-327, :330-347, :350-384): all
-// products in those expressions are exact in fp32, and the one rounding step (Q4_K's and
-// Q5_K's `- dmin * m`) is evaluated in the same order.
+// helpers produce is bit-identical to the reference dequantizer (src/tensor/quant.cpp:68-74,
+// :79-140, :143-151, :154-165, :168-193, :196-233, :236-269, :271-299, :302-327, :330-347,
+// :350-384): each expression is evaluated in the reference's order with contraction off, so
+// every rounding step (a product, then Q4_1's and Q5_1's `+ m`, Q2_K's `- ml`, Q4_K's and
+// Q5_K's `- dmin * m`) is the same one.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -184,6 +185,45 @@ __device__ __forceinline__ float gguf_elem(uint32_t type, const uint8_t* row, ui
         }
         case kF16:
             return h2f(ld_u16(row + 2 * (uint64_t)i));
+        case kBF16:
+            return __uint_as_float(ld_u16(row + 2 * (uint64_t)i) << 16);
+        case kQ4_1: {
+            // d, m; element e < 16 the low nibble of qs[e], e + 16 the high one: fl(q) * d + m
+            const uint8_t* blk = row + (i / 32) * 20;
+            const uint32_t e = i % 32;
+            const float d = h2f(ld_u16(blk)), m = h2f(ld_u16(blk + 2));
+            const uint8_t b = blk[4 + (e & 15)];
+            const float t = (float)(e < 16 ? (b & 15) : (b >> 4)) * d;
+            return t + m;
+        }
+        case kQ5_0:
+        case kQ5_1: {
+            // the nibble as Q4_0 / Q4_1, with bit e of the 32-bit qh as its fifth bit (quant.cpp's
+            // xh_0 = bit j << 4 for e = j < 16, xh_1 = bit j + 16 << 4 for e = j + 16)
+            const bool one = type == kQ5_1;
+            const uint8_t* blk = row + (i / 32) * (one ? 24 : 22);
+            const uint32_t e = i % 32;
+            const uint8_t* qhp = blk + (one ? 4 : 2);
+            const uint32_t qh = ld_u16(qhp) | (ld_u16(qhp + 2) << 16);
+            const uint8_t b = qhp[4 + (e & 15)];
+            const uint32_t code = (e < 16 ? (b & 15u) : (b >> 4)) | (((qh >> e) & 1u) << 4);
+            const float d = h2f(ld_u16(blk));
+            if (!one) return (float)((int)code - 16) * d;
+            const float t = (float)code * d;
+            return t + h2f(ld_u16(blk + 2));
+        }
+        case kQ2_K: {
+            // element e = 128 n + 32 j + 16 h + l: code bits 2j..2j+1 of qs[32 n + 16 h + l]; scale
+            // byte 8 n + 2 j + h gives dl = d * fl(low nibble), ml = dmin * fl(high nibble)
+            const uint8_t* blk = row + (i / 256) * 84;
+            const uint32_t e = i % 256, n = e / 128, j = (e % 128) / 32, hl = (e % 32) / 16, l = e % 16;
+            const float d = h2f(ld_u16(blk + 80)), dmin = h2f(ld_u16(blk + 82));
+            const uint32_t sc = blk[8 * n + 2 * j + hl];
+            const float dl = d * (float)(sc & 15u), ml = dmin * (float)(sc >> 4);
+            const uint32_t q = (blk[16 + 32 * n + 16 * hl + l] >> (2 * j)) & 3u;
+            const float t = dl * (float)q;
+            return t - ml;
+        }
         case kIQ4_NL: {
             const uint8_t* blk = row + (i / 32) * 18;
             const uint32_t e = i % 32;

@@ -48,30 +48,43 @@
 
 namespace halo_mi {
 
-inline constexpr uint32_t kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14,
-                          kIQ4_NL = 20, kIQ3_S = 21, kIQ4_XS = 23;
+inline constexpr uint32_t kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8, kQ2_K = 10,
+                          kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kIQ4_NL = 20, kIQ3_S = 21, kIQ4_XS = 23,
+                          kBF16 = 30;
 inline constexpr uint32_t kSlabRows = 64;
 inline constexpr uint32_t kSlot = 32;  // weights per slot
 
-// Every type of the reference's HIP GEMV test matrix (tests/unit/hip/test_hip_gemv.cpp:217-218):
-// the GGUF layout takes all of them; is_quant() names those that also have a SLAB layout.
+// Every type of the reference's HIP GEMV test matrix (tests/unit/hip/test_hip_gemv.cpp:217-218)
+// plus the rest of its CPU dequantizer's dispatch (BF16, Q4_1, Q5_0, Q5_1, Q2_K; quant.cpp:386-407;
+// geometry dtype.cpp:23-53): the GGUF layout takes all of them; is_quant() names those that also
+// have a SLAB layout, is_hip_gemv_type() the reference HIP backend's eleven.
 HALO_HD constexpr uint32_t block_elems(uint32_t t) {
-    return (t == kF32 || t == kF16)                                                               ? 1u
-           : (t == kQ4_0 || t == kQ8_0 || t == kIQ4_NL)                                           ? 32u
-           : (t == kQ3_K || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS || t == kIQ3_S) ? 256u
-                                                                                                  : 0u;
+    return (t == kF32 || t == kF16 || t == kBF16)                                               ? 1u
+           : (t == kQ4_0 || t == kQ4_1 || t == kQ5_0 || t == kQ5_1 || t == kQ8_0 || t == kIQ4_NL) ? 32u
+           : (t == kQ2_K || t == kQ3_K || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS || t == kIQ3_S)
+               ? 256u
+               : 0u;
 }
 HALO_HD constexpr uint32_t block_bytes(uint32_t t) {
     return t == kF32                      ? 4u
-           : t == kF16                    ? 2u
+           : (t == kF16 || t == kBF16)    ? 2u
            : (t == kQ4_0 || t == kIQ4_NL) ? 18u
+           : t == kQ4_1                   ? 20u
+           : t == kQ5_0                   ? 22u
+           : t == kQ5_1                   ? 24u
            : t == kQ8_0                   ? 34u
+           : t == kQ2_K                   ? 84u
            : (t == kQ3_K || t == kIQ3_S)  ? 110u
            : t == kQ4_K                   ? 144u
            : t == kQ5_K                   ? 176u
            : t == kQ6_K                   ? 210u
            : t == kIQ4_XS                 ? 136u
                                           : 0u;
+}
+// The types the reference's HIP GEMV and GET_ROWS take (backends/hip/src/ops.cpp:531-549).
+HALO_HD constexpr bool is_hip_gemv_type(uint32_t t) {
+    return t == kF32 || t == kF16 || t == kQ4_0 || t == kQ8_0 || t == kQ3_K || t == kQ4_K || t == kQ5_K || t == kQ6_K ||
+           t == kIQ3_S || t == kIQ4_NL || t == kIQ4_XS;
 }
 HALO_HD constexpr bool is_quant(uint32_t t) {
     return t == kQ4_0 || t == kQ8_0 || t == kQ4_K || t == kQ5_K || t == kQ6_K || t == kIQ4_XS;

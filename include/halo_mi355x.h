@@ -41,14 +41,31 @@ enum {
 const char* halo_mi_last_error(void);
 
 /* ---- weight types (ggml ids, include/halo/tensor/dtype.h:18-49) ------------------------- */
+/*
+ * Every type of the reference's CPU dequantizer (src/tensor/quant.cpp:386-407) is decoded on
+ * the GGUF layout by halo_mi_dequant_rows, halo_mi_get_rows and the reference-order GEMV
+ * (HALO_MI_GEMV_GGUF_REF), bitwise as dequantize_row and cpu::matmul. The SLAB layout, and with
+ * it every fast kernel, takes Q4_0, Q8_0, Q4_K, Q5_K, Q6_K and IQ4_XS. The reference's HIP
+ * backend has kernels for eleven of them (backends/hip/src/ops.cpp:531-549: not BF16, Q4_1,
+ * Q5_0, Q5_1, Q2_K); the C++ backend of this library refuses the same five.
+ */
 enum {
     HALO_MI_F32 = 0,
+    HALO_MI_F16 = 1,
     HALO_MI_Q4_0 = 2,
+    HALO_MI_Q4_1 = 3,
+    HALO_MI_Q5_0 = 6,
+    HALO_MI_Q5_1 = 7,
     HALO_MI_Q8_0 = 8,
+    HALO_MI_Q2_K = 10,
+    HALO_MI_Q3_K = 11,
     HALO_MI_Q4_K = 12,
     HALO_MI_Q5_K = 13,
     HALO_MI_Q6_K = 14,
-    HALO_MI_IQ4_XS = 23
+    HALO_MI_IQ4_NL = 20,
+    HALO_MI_IQ3_S = 21,
+    HALO_MI_IQ4_XS = 23,
+    HALO_MI_BF16 = 30
 };
 
 /* ---- weight layouts ---------------------------------------------------------------------- */

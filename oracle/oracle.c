@@ -17,8 +17,8 @@
 #include <unistd.h>
 
 enum {
-    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
-    T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ4_XS = 23
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q2_K = 10, T_Q3_K = 11,
+    T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_NL = 20, T_IQ3_S = 21, T_IQ4_XS = 23, T_BF16 = 30
 };
 
 /* ---- fp16 ------------------------------------------------------------------------------ */
@@ -54,9 +54,9 @@ static float f16_at(const uint8_t* p) { return oracle_fp16_to_fp32((uint16_t)(p[
 
 uint32_t oracle_block_elems(uint32_t type) {
     switch (type) {
-        case T_F32: case T_F16: return 1;
-        case T_Q4_0: case T_Q8_0: case T_IQ4_NL: return 32;
-        case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: case T_IQ3_S: return 256;
+        case T_F32: case T_F16: case T_BF16: return 1;
+        case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: case T_Q8_0: case T_IQ4_NL: return 32;
+        case T_Q2_K: case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: case T_IQ3_S: return 256;
         default: return 0;
     }
 }
@@ -64,8 +64,12 @@ uint32_t oracle_block_elems(uint32_t type) {
 uint32_t oracle_block_bytes(uint32_t type) {
     switch (type) {
         case T_F32: return 4;
-        case T_F16: return 2;
+        case T_F16: case T_BF16: return 2;
         case T_Q4_0: case T_IQ4_NL: return 18;
+        case T_Q4_1: return 20;
+        case T_Q5_0: return 22;
+        case T_Q5_1: return 24;
+        case T_Q2_K: return 84;
         case T_Q3_K: case T_IQ3_S: return 110;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
@@ -97,6 +101,69 @@ static void deq_q4_0(const uint8_t* blk, float* y) {
         const uint8_t byte = blk[2 + (e & 15)];
         const int q = (e < 16 ? (byte & 0x0F) : (byte >> 4)) - 8;
         y[e] = (float)q * d;
+    }
+}
+
+/* quant.cpp:72-74 and fp16.h:61-63: the 16 bits are the top half of the fp32 pattern. */
+static float bf16_at(const uint8_t* p) {
+    const uint32_t bits = (uint32_t)(p[0] | (p[1] << 8)) << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* quant.cpp:93-105. Header d, m (fp16); nibbles in Q4_0's order, unsigned; value fl(q) * d + m,
+ * the product rounded before the add. b (when asked) is -m, so that a - b is the value. */
+static void deq_q4_1(const uint8_t* blk, float* y, float* a, float* b) {
+    const float d = f16_at(blk), m = f16_at(blk + 2);
+    for (int e = 0; e < 32; ++e) {
+        const uint8_t byte = blk[4 + (e & 15)];
+        const float t = (float)(e < 16 ? (byte & 0x0F) : (byte >> 4)) * d;
+        if (y) y[e] = t + m;
+        if (a) { a[e] = t; b[e] = -m; }
+    }
+}
+
+/* The fifth bit of element e of a Q5_0 / Q5_1 block: bit e of the little-endian 32-bit qh.
+ * (The reference moves bit j to bit 4 for j < 16 and bit j + 16 for the high half,
+ * quant.cpp:114-115 and :132-133; both are bit e.) */
+static int q5_high(const uint8_t* qh, int e) { return (qh[e / 8] >> (e % 8)) & 1; }
+
+/* quant.cpp:108-122: d; qh at +2; qs at +6; value fl(code - 16) * d. */
+static void deq_q5_0(const uint8_t* blk, float* y) {
+    const float d = f16_at(blk);
+    for (int e = 0; e < 32; ++e) {
+        const uint8_t byte = blk[6 + (e & 15)];
+        const int code = (e < 16 ? (byte & 0x0F) : (byte >> 4)) | (q5_high(blk + 2, e) << 4);
+        y[e] = (float)(code - 16) * d;
+    }
+}
+
+/* quant.cpp:125-140: d, m; qh at +4; qs at +8; value fl(code) * d + m. b (when asked) is -m. */
+static void deq_q5_1(const uint8_t* blk, float* y, float* a, float* b) {
+    const float d = f16_at(blk), m = f16_at(blk + 2);
+    for (int e = 0; e < 32; ++e) {
+        const uint8_t byte = blk[8 + (e & 15)];
+        const int code = (e < 16 ? (byte & 0x0F) : (byte >> 4)) | (q5_high(blk + 4, e) << 4);
+        const float t = (float)code * d;
+        if (y) y[e] = t + m;
+        if (a) { a[e] = t; b[e] = -m; }
+    }
+}
+
+/* quant.cpp:168-193: scales[16], qs[64] at +16, d at +80, dmin at +82. Element
+ * e = 128 n + 32 j + 16 h + l (the reference's loops: half n, shift 2 j, run h, lane l) takes
+ * code bits 2 j, 2 j + 1 of qs[32 n + 16 h + l] and scale byte sc = scales[8 n + 2 j + h];
+ * dl = d * fl(sc & 15), ml = dmin * fl(sc >> 4); value dl * fl(code) - ml. b (when asked) = ml. */
+static void deq_q2_k(const uint8_t* blk, float* y, float* a, float* b) {
+    const float d = f16_at(blk + 80), dmin = f16_at(blk + 82);
+    for (int e = 0; e < 256; ++e) {
+        const int n = e / 128, j = (e % 128) / 32, h = (e % 32) / 16, l = e % 16;
+        const uint8_t sc = blk[8 * n + 2 * j + h];
+        const float dl = d * (float)(sc & 0x0F), ml = dmin * (float)(sc >> 4);
+        const float t = dl * (float)((blk[16 + 32 * n + 16 * h + l] >> (2 * j)) & 3);
+        if (y) y[e] = t - ml;
+        if (a) { a[e] = t; b[e] = ml; }
     }
 }
 
@@ -286,7 +353,12 @@ static int dequant_blocks(uint32_t type, const uint8_t* src, float* dst, uint64_
         switch (type) {
             case T_F32: memcpy(y, blk, 4); break;
             case T_F16: y[0] = f16_at(blk); break;
+            case T_BF16: y[0] = bf16_at(blk); break;
             case T_Q4_0: deq_q4_0(blk, y); break;
+            case T_Q4_1: deq_q4_1(blk, y, NULL, NULL); break;
+            case T_Q5_0: deq_q5_0(blk, y); break;
+            case T_Q5_1: deq_q5_1(blk, y, NULL, NULL); break;
+            case T_Q2_K: deq_q2_k(blk, y, NULL, NULL); break;
             case T_IQ4_NL: deq_iq4_nl(blk, y, NULL, NULL); break;
             case T_Q3_K: deq_q3_k(blk, y, NULL, NULL); break;
             case T_IQ3_S: deq_iq3_s(blk, y, NULL, NULL); break;
@@ -360,6 +432,24 @@ int oracle_dequant_terms(uint32_t type, const uint8_t* src, float* a, float* b, 
             case T_IQ3_S:
                 deq_iq3_s(blk, NULL, ab, ob);
                 for (uint32_t e = 0; e < be; ++e) bbv[e] = 0.0f;
+                break;
+            /* GGUF-layout-only types: the value split as a - b where the reference rounds an add
+             * (Q4_1, Q5_1: b = -m; Q2_K: b = ml); off = 0, no kernel takes a code bias out */
+            case T_Q4_1:
+                deq_q4_1(blk, NULL, ab, bbv);
+                for (uint32_t e = 0; e < be; ++e) ob[e] = 0.0f;
+                break;
+            case T_Q5_1:
+                deq_q5_1(blk, NULL, ab, bbv);
+                for (uint32_t e = 0; e < be; ++e) ob[e] = 0.0f;
+                break;
+            case T_Q2_K:
+                deq_q2_k(blk, NULL, ab, bbv);
+                for (uint32_t e = 0; e < be; ++e) ob[e] = 0.0f;
+                break;
+            case T_BF16: case T_Q5_0:
+                dequant_blocks(type, blk, ab, 1);
+                for (uint32_t e = 0; e < be; ++e) { bbv[e] = 0.0f; ob[e] = 0.0f; }
                 break;
             default: return ORACLE_EUNSUPPORTED;
         }

@@ -13,7 +13,8 @@
  * Type ids are ggml's (include/halo/tensor/dtype.h:18-49): F32 = 0, F16 = 1, Q4_0 = 2,
  * Q8_0 = 8, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ4_NL = 20, IQ3_S = 21, IQ4_XS = 23
  * (the weight types of the reference's HIP GEMV test matrix, tests/unit/hip/test_hip_gemv.cpp:
- * 217-218). F32 rows are read in place by the matmul.
+ * 217-218), and the rest of the reference dequantizer's dispatch (quant.cpp:386-407): Q4_1 = 3,
+ * Q5_0 = 6, Q5_1 = 7, Q2_K = 10, BF16 = 30. F32 rows are read in place by the matmul.
  *
  * Return codes: 0 = ok, ORACLE_EMODEL (1) = bad element count / byte size (the reference's
  * Error(Model), quant.cpp:411-428), ORACLE_EUNSUPPORTED (2) = type not on this path
@@ -57,6 +58,10 @@ int oracle_dequantize_row(uint32_t type, const uint8_t* src, float* dst, int64_t
  *   IQ4_NL a = d*table[q],    b = 0                          (quant.cpp:160-161)
  *   Q3_K  a = (d*(sc-32))*q,  b = 0                          (quant.cpp:220-226)
  *   IQ3_S a = (db*g)*sign,    b = 0                          (quant.cpp:368-369)
+ *   Q4_1  a = q*d,            b = -m                         (quant.cpp:101-102)
+ *   Q5_1  a = q*d,            b = -m                         (quant.cpp:136-137)
+ *   Q2_K  a = dl*q,           b = ml                         (quant.cpp:181, :186)
+ *   Q5_0  a = (q-16)*d,       b = 0; BF16 a = w, b = 0       (quant.cpp:118-119, :72-74)
  * and also returns the "factored" magnitude terms the GPU kernels sum: the offset they take
  * out of the quant, in off[] (Q4_0 8*d, Q6_K 32*d*sc, Q8_0 128*d, IQ4_XS 128*dl, IQ4_NL
  * 128*d, Q3_K 4*dl, IQ3_S 16*db), else 0. F32 and F16 have no terms (ORACLE_EUNSUPPORTED).

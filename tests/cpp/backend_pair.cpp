@@ -352,6 +352,22 @@ void run_type(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
     bad = a;
     bad.kernel.variant_id = hb::kGemvGgufRef;  // a GGUF-only kernel on a SLAB buffer
     check(code_of([&] { be.gemv(st, bad); }) == (int)hb::ErrorCode::Config, tn + ": layout/variant mismatch -> Config");
+    // the reference HIP backend's type set (test_hip_gemv.cpp:307-308): Q4_1 and the other
+    // GGUF-layout-only types are refused with its message
+    for (hb::DType wt : {hb::DType::Q4_1, hb::DType::Q5_0, hb::DType::Q5_1, hb::DType::Q2_K, hb::DType::BF16}) {
+        bad = a;
+        bad.wtype = wt;
+        std::string msg;
+        int code = -1;
+        try {
+            be.gemv(st, bad);
+        } catch (const hb::Error& e) {
+            code = static_cast<int>(e.code());
+            msg = e.what();
+        }
+        check(code == (int)hb::ErrorCode::Unsupported && msg.find("no HIP GEMV kernel") != std::string::npos,
+              tn + ": type " + std::to_string(static_cast<unsigned>(wt)) + " -> Unsupported, no HIP GEMV kernel");
+    }
 }
 
 // The reference interface outside the path: every op virtual exists, the ones this backend does

@@ -7,14 +7,21 @@ import numpy as np
 
 Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS, F32 = 2, 8, 12, 13, 14, 23, 0
 F16, Q3_K, IQ4_NL, IQ3_S = 1, 11, 20, 21
+Q4_1, Q5_0, Q5_1, Q2_K, BF16 = 3, 6, 7, 10, 30
 QUANT_TYPES = (Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, IQ4_XS)
 SLAB_TYPES = QUANT_TYPES  # the types with a SLAB layout
 # the reference's HIP GEMV test matrix, in its order (tests/unit/hip/test_hip_gemv.cpp:217-218)
 ALL_TYPES = (Q4_K, Q5_K, Q6_K, Q8_0, F16, F32, IQ4_XS, IQ4_NL, Q3_K, IQ3_S, Q4_0)
+# the rest of the reference dequantizer's dispatch (src/tensor/quant.cpp:386-407): GGUF layout only
+GGUF_EXTRA_TYPES = (BF16, Q4_1, Q5_0, Q5_1, Q2_K)
+GGUF_TYPES = ALL_TYPES + GGUF_EXTRA_TYPES
+PLAIN_TYPES = (F32, F16, BF16)  # one element per block
 NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
-         IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS"}
+         IQ4_NL: "IQ4_NL", IQ3_S: "IQ3_S", IQ4_XS: "IQ4_XS", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", Q2_K: "Q2_K",
+         BF16: "BF16"}
 BLOCK = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144),
-         Q5_K: (256, 176), Q6_K: (256, 210), IQ4_NL: (32, 18), IQ3_S: (256, 110), IQ4_XS: (256, 136)}
+         Q5_K: (256, 176), Q6_K: (256, 210), IQ4_NL: (32, 18), IQ3_S: (256, 110), IQ4_XS: (256, 136),
+         Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q2_K: (256, 84), BF16: (1, 2)}
 U = 2.0 ** -24  # fp32 unit roundoff
 
 
@@ -51,10 +58,21 @@ def make_weights(t: int, rows: int, cols: int, seed: int, stride_pad: int = 0, o
             vals[3 % cols] = np.float16(3e-7)  # one fp16 subnormal
             buf[row:row + 2 * cols] = vals.view(np.uint8)
             continue
+        if t == BF16:
+            vals = (rng.uniform(-1, 1, cols).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+            vals[3 % cols] = 0x0042  # one bf16 subnormal
+            buf[row:row + 2 * cols] = vals.view(np.uint8)
+            continue
         for b in range(cols // be):
             sc = 2e-6 if b == 0 else rng.uniform(-0.05, 0.05)
-            if t in (Q4_0, Q8_0, IQ4_NL, IQ3_S):
+            if t in (Q4_0, Q8_0, IQ4_NL, IQ3_S, Q5_0):
                 _put16(buf, row + bb * b, sc)
+            elif t in (Q4_1, Q5_1):
+                _put16(buf, row + bb * b, sc)
+                _put16(buf, row + bb * b + 2, rng.uniform(-0.05, 0.05))
+            elif t == Q2_K:
+                _put16(buf, row + bb * b + 80, sc)
+                _put16(buf, row + bb * b + 82, abs(rng.uniform(-0.05, 0.05)))
             elif t == Q3_K:
                 _put16(buf, row + bb * b + 108, sc)
             elif t in (Q4_K, Q5_K):

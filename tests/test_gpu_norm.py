@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from helpers import (ALL_TYPES, F16, F32, IQ4_XS, SLAB_TYPES, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, gemm_emulated, gemm_tol,
+from helpers import (ALL_TYPES, GGUF_TYPES, PLAIN_TYPES, F16, F32, IQ4_XS, SLAB_TYPES, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, gemm_emulated, gemm_tol,
                      isclose_bits, make_weights, max_ratio, row_bytes, slab_gemv_tol, swiglu_tol)
 from test_gpu_parity import SENTINEL, dense_of, host, say, slab_of, strided_xy, to_dev
 
@@ -70,7 +70,7 @@ def test_rms_norm_strided_and_rejects(hl, oracle, dev):
 # ---- GET_ROWS ---------------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("t", GGUF_TYPES)
 @pytest.mark.parametrize("layout", ["gguf", "slab"])
 def test_get_rows_bitwise_and_bad_ids(hl, oracle, dev, t, layout):
     import torch
@@ -79,7 +79,7 @@ def test_get_rows_bitwise_and_bad_ids(hl, oracle, dev, t, layout):
         pytest.skip(f"{NAMES[t]} has no SLAB layout")
     rows, cols = 70, 512
     say("get_rows", NAMES[t], layout, rows, cols)
-    pad, off = ((4, 4) if t in (F32, F16) else (3, 1)) if layout == "gguf" else (0, 0)
+    pad, off = ((4, 4) if t in PLAIN_TYPES else (3, 1)) if layout == "gguf" else (0, 0)
     buf, stride = make_weights(t, rows, cols, seed=900 + t, stride_pad=pad, offset=off)
     ref = oracle.dequantize_rows(t, buf[off:], rows, cols, stride)
     if layout == "gguf":

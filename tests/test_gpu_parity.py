@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import (ALL_TYPES, BLOCK, F16, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
+from helpers import (ALL_TYPES, BLOCK, BF16, GGUF_TYPES, PLAIN_TYPES, F16, F32, IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, QUANT_TYPES, U, depth_cpu, gemm_emulated, gemm_tol,
                      gemv_mag, isclose_bits, make_weights, max_ratio, row_bytes, silu64, slab_gemv_tol, swiglu_tol)
 
 pytestmark = pytest.mark.gpu
@@ -71,6 +71,18 @@ CASES = [
 
 
 # ---- dequantization is bit-exact --------------------------------------------------------
+
+
+def test_bf16_dequant_every_pattern(hl, oracle, dev):
+    """All 65536 bf16 patterns as one BF16 row, bitwise the reference's widening (the pattern is
+    the top half of the fp32 one, quant.cpp:72-74), NaN payloads included."""
+    import torch
+
+    pats = np.arange(65536, dtype=np.uint16)
+    ref = oracle.dequantize_row(BF16, pats.view(np.uint8), 65536)
+    out = torch.empty((1, 65536), dtype=torch.float32, device=dev)
+    hl.dequant_rows(BF16, hl.Layout.GGUF, to_dev(pats.view(np.uint8), dev), 1, 65536, out)
+    assert np.array_equal(host(out)[0].view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
@@ -135,20 +147,21 @@ def run_gemv(hl, dev, t, w, layout, x, rows, cols, variant, x_pad=0, y_pad=0, w_
 
 
 def matrix_case(t, case):
-    """test_hip_gemv.cpp:219-227's two shapes for type t: plain types (F32, F16) take 100
+    """test_hip_gemv.cpp:219-227's two shapes for type t: plain types (F32, F16, BF16) take 100
     columns in the first (a dot tail of 100 % 8) and a 4-byte row stride pad and offset in the
     second; block types 512 columns, then a 3-byte pad and 1-byte offset."""
     rows, cols, n_vec, pad, off, xp, yp = case
-    if t in (F32, F16):
+    if t in PLAIN_TYPES:
         cols = 100 if rows == 37 else cols
         pad, off = (4, 4) if pad else (0, 0)
     return rows, cols, n_vec, pad, off, xp, yp
 
 
-@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("t", GGUF_TYPES)
 @pytest.mark.parametrize("case", CASES)
 def test_dequant_gguf_type_matrix_bitwise(hl, oracle, dev, t, case):
-    """GGUF-layout dequantization of every type of the reference's HIP test matrix is bitwise
+    """GGUF-layout dequantization of every type of the reference's HIP test matrix, and of the
+    rest of its dequantizer's dispatch (BF16, Q4_1, Q5_0, Q5_1, Q2_K), is bitwise
     tensor::dequantize_row, at an unaligned row stride and start."""
     import torch
 
@@ -162,11 +175,11 @@ def test_dequant_gguf_type_matrix_bitwise(hl, oracle, dev, t, case):
     assert isclose_bits(host(out), ref), "GGUF dequant differs from tensor::dequantize_row"
 
 
-@pytest.mark.parametrize("t", ALL_TYPES)
+@pytest.mark.parametrize("t", GGUF_TYPES)
 @pytest.mark.parametrize("case", CASES)
 def test_gemv_gguf_ref_bitwise(hl, oracle, dev, t, case):
-    """The reference-order variant over GGUF rows is bitwise cpu::matmul for every type of the
-    matrix; on the GGUF layout the default variant is that kernel."""
+    """The reference-order variant over GGUF rows is bitwise cpu::matmul for every type the
+    reference dequantizes; on the GGUF layout the default variant is that kernel."""
     rows, cols, n_vec, pad, off, xp, yp = matrix_case(t, case)
     say("gemv_gguf_ref", NAMES[t], rows, cols, n_vec)
     buf, stride = make_weights(t, rows, cols, seed=100 + t + rows, stride_pad=pad, offset=off)
@@ -455,7 +468,7 @@ def test_gemv_rejects_bad_arguments(hl, dev):
         return None, ""
 
     assert code()[0] is None  # valid baseline
-    assert code(t=3)[0] == hl.ErrorCode.Unsupported  # Q4_1: not on this path
+    assert code(t=9)[0] == hl.ErrorCode.Unsupported  # Q8_1: no dequantizer in the reference either
     c, msg = code(cols=100)
     assert c == hl.ErrorCode.Kernel and "multiple of the block size 32" in msg
     c, msg = code(y=w.data_ptr() + 16)

@@ -627,6 +627,154 @@ def test_new_type_dequant_terms(oracle, t, bb, be, d_at):
         assert np.array_equal(off[0, be * b: be * (b + 1)], want), b
 
 
+# ---- the rest of the dequantizer's dispatch: BF16, Q4_1, Q5_0, Q5_1, Q2_K ---------------------
+# (quant.cpp:72-74, :93-140, :168-193; dispatch :386-407; geometry dtype.cpp:26-30, :33, :53)
+
+Q4_1, Q5_0, Q5_1, Q2_K, BF16 = 3, 6, 7, 10, 30
+
+
+def test_extra_type_geometry(oracle):
+    """dtype.cpp's table rows 3, 6, 7, 10 and 30 (block elements, block bytes)."""
+    for t, be, bb in ((Q4_1, 32, 20), (Q5_0, 32, 22), (Q5_1, 32, 24), (Q2_K, 256, 84), (BF16, 1, 2)):
+        assert oracle.row_bytes(t, 17408 if be > 1 else 7) == (17408 // be * bb if be > 1 else 14)
+    for t, n in ((Q4_1, 16), (Q5_0, 48), (Q5_1, 1), (Q2_K, 128)):
+        with pytest.raises(oracle.OracleError) as e:
+            oracle.row_bytes(t, n)
+        assert e.value.code == oracle.EMODEL
+    for t in (4, 5, 9, 15, 16, 24, 29):  # unassigned ids and types without a dequantizer
+        with pytest.raises(oracle.OracleError) as e:
+            oracle.row_bytes(t, 256)
+        assert e.value.code == oracle.EUNSUPPORTED
+
+
+def test_bf16_rows_are_the_top_half_of_fp32(oracle):
+    """Every one of the 65536 bf16 patterns widens to the fp32 pattern with the same top 16 bits
+    and zero below (fp16.h:61-63): a closed form, NaN payloads and signed zeros included."""
+    pats = np.arange(65536, dtype=np.uint16)
+    y = oracle.dequantize_row(BF16, pats.view(np.uint8), 65536)
+    assert np.array_equal(y.view(np.uint32), pats.astype(np.uint32) << 16)
+
+
+def _walk_q4_1_q5(blk: bytes, t: int) -> np.ndarray:
+    """quant.cpp:93-140's loops walked literally: j over 16 bytes writing y[j] and y[j + 16], the
+    fifth bits xh_0 = ((qh >> j) << 4) & 0x10 and xh_1 = (qh >> (j + 12)) & 0x10."""
+    d = np.float32(np.frombuffer(blk[0:2], np.float16)[0])
+    m = np.float32(np.frombuffer(blk[2:4], np.float16)[0]) if t in (Q4_1, Q5_1) else None
+    qh = struct.unpack("<I", blk[{Q5_0: 2, Q5_1: 4}[t]: {Q5_0: 2, Q5_1: 4}[t] + 4])[0] if t != Q4_1 else 0
+    qs = blk[{Q4_1: 4, Q5_0: 6, Q5_1: 8}[t]:]
+    y = [np.float32(0)] * 32
+    for j in range(16):
+        xh_0 = ((qh >> j) << 4) & 0x10
+        xh_1 = (qh >> (j + 12)) & 0x10
+        x0, x1 = (qs[j] & 0x0F) | xh_0, (qs[j] >> 4) | xh_1
+        if t == Q5_0:
+            y[j], y[j + 16] = np.float32(x0 - 16) * d, np.float32(x1 - 16) * d
+        else:
+            y[j], y[j + 16] = np.float32(x0) * d + m, np.float32(x1) * d + m
+    return np.array(y, np.float32)
+
+
+def _walk_q2_k(blk: bytes) -> np.ndarray:
+    """quant.cpp:168-193's loops walked literally: two halves moving q by 32, four shifts, two
+    runs of 16 per shift, each run taking the next scale byte (is++)."""
+    d = np.float32(np.frombuffer(blk[80:82], np.float16)[0])
+    dmin = np.float32(np.frombuffer(blk[82:84], np.float16)[0])
+    out, q, is_ = [], 16, 0
+    for _ in range(2):
+        shift = 0
+        for _ in range(4):
+            for half in (0, 16):
+                sc = blk[is_]
+                is_ += 1
+                dl, ml = d * np.float32(sc & 0xF), dmin * np.float32(sc >> 4)
+                for l in range(16):
+                    out.append(dl * np.float32((blk[q + half + l] >> shift) & 3) - ml)
+            shift += 2
+        q += 32
+    return np.array(out, np.float32)
+
+
+@pytest.mark.parametrize("t,bb,be", [(Q4_1, 20, 32), (Q5_0, 22, 32), (Q5_1, 24, 32), (Q2_K, 84, 256)])
+def test_extra_types_equal_the_literal_loop_walk(oracle, t, bb, be):
+    """On random blocks (finite scales, one fp16-subnormal d) the oracle's per-element index form
+    equals a literal walk of the reference's loops bitwise."""
+    rng = np.random.default_rng(60 + t)
+    n = 40
+    w = rng.integers(0, 256, size=n * bb, dtype=np.uint8)
+    hdr = (80, 82) if t == Q2_K else ((0, 2) if t in (Q4_1, Q5_1) else (0,))
+    for b in range(n):
+        for k, at in enumerate(hdr):
+            v = rng.uniform(-0.05, 0.05) if k == 0 else rng.uniform(-0.5, 0.5)
+            w[bb * b + at: bb * b + at + 2] = np.frombuffer(f16_bytes(v), np.uint8)
+    w[hdr[0]: hdr[0] + 2] = (0x03, 0x00)  # an fp16-subnormal d in the first block
+    y = oracle.dequantize_row(t, w, n * be)
+    walk = _walk_q2_k if t == Q2_K else (lambda blk: _walk_q4_1_q5(blk, t))
+    want = np.concatenate([walk(bytes(w[bb * b: bb * (b + 1)])) for b in range(n)])
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def test_q4_1_known_answers(oracle):
+    """qs[j] = (15 - j) << 4 | j: element j < 16 has code j, j + 16 code 15 - j. d = 1, m = 0
+    gives the codes; d = 0.5, m = -4 gives q / 2 - 4 exactly; m = 65504 with the smallest
+    subnormal d (2^-24) gives 65504 for every code (q d is below half an ulp of m)."""
+    qs = bytes(((15 - j) << 4) | j for j in range(16))
+    codes = np.array(list(range(16)) + [15 - j for j in range(16)], np.float32)
+
+    def blk(d_bits, m):
+        return np.frombuffer(struct.pack("<H", d_bits) + f16_bytes(m) + qs, np.uint8)
+
+    assert np.array_equal(oracle.dequantize_row(Q4_1, blk(0x3C00, 0.0), 32), codes)
+    assert np.array_equal(oracle.dequantize_row(Q4_1, blk(0x3800, -4.0), 32), codes / 2 - 4)
+    assert np.all(oracle.dequantize_row(Q4_1, blk(0x0001, 65504.0), 32) == np.float32(65504))
+
+
+@pytest.mark.parametrize("t", [Q5_0, Q5_1])
+def test_q5_fifth_bit_is_bit_e_of_qh(oracle, t):
+    """Every nibble 8 (qs bytes 0x88) and only bits 3 and 20 of qh set: elements 3 and 20 have
+    code 24, every other element code 8. With d = 0.5 (and m = 1 for Q5_1) the values are
+    Q5_0: (code - 16) / 2, Q5_1: code / 2 + 1. (Bit e for e >= 16 comes from xh_1's shift by
+    j + 12: reading bit e - 16 instead would move element 20's bit to element 4.)"""
+    qh = struct.pack("<I", (1 << 3) | (1 << 20))
+    hdr = f16_bytes(0.5) + (f16_bytes(1.0) if t == Q5_1 else b"")
+    y = oracle.dequantize_row(t, np.frombuffer(hdr + qh + b"\x88" * 16, np.uint8), 32)
+    code = np.full(32, 8.0, np.float32)
+    code[[3, 20]] = 24.0
+    want = (code - 16) / 2 if t == Q5_0 else code / 2 + 1
+    assert np.array_equal(y, want.astype(np.float32))
+
+
+def test_q2_k_known_answers(oracle):
+    """qs bytes 0xE4 hold codes 0, 1, 2, 3 at shifts 0, 2, 4, 6, so element 128 n + 32 j + l has
+    code j. Scale bytes 0x21 (scale 1, min 2) with d = 0.5, dmin = 0.25: value j / 2 - 0.5.
+    Then scale byte 11 alone = 0x53 (scale 3, min 5): the 16-element run 11 in element order
+    (elements 176 .. 191: half 1, shift pair 1, second run; code 1) becomes 3 / 2 - 5 / 4."""
+    def blk(scales):
+        return np.frombuffer(bytes(scales) + b"\xe4" * 64 + f16_bytes(0.5) + f16_bytes(0.25), np.uint8)
+
+    j = (np.arange(256) % 128) // 32
+    want = (j * 0.5 - 0.5).astype(np.float32)
+    assert np.array_equal(oracle.dequantize_row(Q2_K, blk([0x21] * 16), 256), want)
+    sc = [0x21] * 16
+    sc[11] = 0x53
+    want[176:192] = np.float32(1.5 - 1.25)
+    assert np.array_equal(oracle.dequantize_row(Q2_K, blk(sc), 256), want)
+
+
+@pytest.mark.parametrize("t,bb,be", [(Q4_1, 20, 32), (Q5_0, 22, 32), (Q5_1, 24, 32), (Q2_K, 84, 256), (BF16, 2, 1)])
+def test_extra_type_dequant_terms(oracle, t, bb, be):
+    """a - b is the dequantized weight bitwise (b = -m for Q4_1 / Q5_1, ml for Q2_K, else 0), and
+    no kernel takes a code bias out (off = 0)."""
+    rng = np.random.default_rng(80 + t)
+    n = 8 if be > 1 else 256
+    w = rng.integers(0, 256, size=n * bb, dtype=np.uint8)
+    w[1::2] &= 0xBF  # every fp16 / bf16 field finite
+    a, b_, off = oracle.dequant_terms(t, w, 1, n * be)
+    y = oracle.dequantize_row(t, w, n * be)
+    assert np.array_equal((a[0] - b_[0]).view(np.uint32), y.view(np.uint32)) and np.all(off == 0)
+    if t in (Q5_0, BF16):
+        assert np.all(b_ == 0)
+
+
 # ---- rms_norm (backends/cpu/ops_basic.cpp:18-33) ------------------------------------------
 
 
@@ -713,7 +861,7 @@ def test_vec_dot_row_matches_sequential_double(oracle):
     """tests/unit/tensor/test_dequant.cpp:90-112."""
     rng = np.random.default_rng(7)
     n = 1024
-    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+    for t in (F32, 1, 30, Q4_0, Q8_0, Q4_K, Q6_K, 20, 21):  # F16, BF16, IQ4_NL, IQ3_S by id
         row = rng.integers(0, 256, size=oracle.row_bytes(t, n), dtype=np.uint8)
         row[1::2] &= 0xBF  # cap exponents: every fp16 field stays finite
         x = ((rng.integers(0, 2001, n) - 1000) / 1000.0).astype(np.float32)
