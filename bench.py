@@ -570,14 +570,20 @@ def main() -> int:
             r = layer_case(hl, torch, m, group_qkv=True)
             extra[f"hybrid_layer_m{m}_qkv_group"] = {"us_per_layer": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                                      "TFLOP/s": round(r["tflops"], 2)}
-        for m in (2, 4, 8):
-            # what the Backend adapter runs for decode and MTP verify (GemvArgs::allow_gemm off):
-            # the slab GEMV, every row bitwise its own n_vec == 1 row
-            log(f"decode / MTP verify through the adapter's choice (slab GEMV) M={m}")
-            extra[f"q4k_gemv_17408x5120_m{m}_allow_gemm_off"] = gemv_fig(gemv_case(hl, torch, Q4_K, 17408, 5120, m, 2, variant=2))
-            r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, variant=2)
-            extra[f"q4k_gate_up_swiglu_m{m}_allow_gemm_off"] = {**gemm_fig(r),
-                                                                "weights_GB/s": round(2 * 17408 * 2880 / (r["ms"] * 1e-3) / 1e9, 1)}
+        for m in (1, 2, 4, 8):
+            # what the Backend adapter runs for decode and MTP verify (GemvArgs::allow_gemm off),
+            # every row bitwise its own n_vec == 1 row: the slab GEMV (MiOptions default,
+            # variant 2), or the exact GEMM with its K split fixed by the shape
+            # (BatchInvariantKernel::Exact, variant 9)
+            for fam, v in (("gemv", 2), ("exact", 9)):
+                log(f"decode / MTP verify, batch-invariant family {fam} (variant {v}) M={m}")
+                extra[f"q4k_gemv_17408x5120_m{m}_allow_gemm_off_{fam}"] = gemv_fig(
+                    gemv_case(hl, torch, Q4_K, 17408, 5120, m, 2, variant=v))
+                extra[f"q6k_gemv_5120x17408_m{m}_allow_gemm_off_{fam}"] = gemv_fig(
+                    gemv_case(hl, torch, Q6_K, 5120, 17408, m, 3, variant=v))
+                r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4, variant=v)
+                extra[f"q4k_gate_up_swiglu_m{m}_allow_gemm_off_{fam}"] = {
+                    **gemm_fig(r), "weights_GB/s": round(2 * 17408 * 2880 / (r["ms"] * 1e-3) / 1e9, 1)}
         for m in (2, 4, 8, 64, 512):
             log(f"config 4: Q4_K gate/up + SwiGLU M={m}")
             r = gemm_case(hl, torch, Q4_K, 17408, 5120, m, 4)

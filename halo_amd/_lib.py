@@ -53,6 +53,7 @@ class Variant(enum.IntEnum):
     SLAB_GEMV_VALU = 6
     SLAB_GEMM_BF16_SMALL_M = 7
     SLAB_GEMM_EXACT_SMALL_M = 8
+    SLAB_GEMM_EXACT_INVARIANT = 9
 
 
 class ErrorCode(enum.IntEnum):

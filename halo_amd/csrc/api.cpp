@@ -175,12 +175,24 @@ uint32_t auto_gemv_variant(uint32_t type, uint32_t rows, uint32_t cols, uint32_t
     return HALO_MI_GEMM_SLAB_BF16;
 }
 
+// Variant 9 where the exact GEMM's fixed split fits the shape, else the slab GEMV (variant 2):
+// a function of the shape only, so rows stay independent of n_vec either way.
+uint32_t exact_invariant_or_gemv(uint32_t rows, uint32_t cols, bool pair) {
+    const uint32_t slabs = (rows + kSlabRows - 1) / kSlabRows;
+    uint32_t kc = 0;
+    size_t lds = 0;
+    return gemm_sx_plan(pair ? slabs : (slabs + 1) / 2, cols, kGemmSxMaxRows, &kc, &lds)
+               ? HALO_MI_GEMM_SLAB_EXACT_INVARIANT
+               : HALO_MI_GEMV_SLAB;
+}
+
 uint32_t gemm_tiles(uint32_t variant) {
     switch (variant) {
         case HALO_MI_GEMM_SLAB_BF16: return kGemmTilesPc;
         case HALO_MI_GEMM_SLAB_BF16_M512: return kGemmTilesLm;
         case HALO_MI_GEMM_SLAB_BF16_SMALL_M: return kGemmTilesSm;
         case HALO_MI_GEMM_SLAB_EXACT_SMALL_M: return kGemmTilesSx;
+        case HALO_MI_GEMM_SLAB_EXACT_INVARIANT: return kGemmTilesSxFixed;
         default: return kGemmTilesAuto;
     }
 }
@@ -248,6 +260,7 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
     if (ranges_overlap(p->y, yext, p->w, halo_mi_slab_bytes(p->type, p->rows, p->cols)))
         return set_error(HALO_MI_E_KERNEL, "%s: y overlaps w", op);
     if (variant == HALO_MI_GEMV_SLAB_AUTO) variant = auto_gemv_variant(p->type, p->rows, p->cols, p->n_vec, false);
+    if (variant == HALO_MI_GEMM_SLAB_EXACT_INVARIANT) variant = exact_invariant_or_gemv(p->rows, p->cols, false);
     if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
         a.norm_w = p->norm_w;
@@ -255,10 +268,11 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream) {
         a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<false>(p->type, a, st);
     }
-    if (variant != HALO_MI_GEMM_SLAB_EXACT_SMALL_M && (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
+    const bool exact = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M || variant == HALO_MI_GEMM_SLAB_EXACT_INVARIANT;
+    if (!exact && (p->x_stride % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
         return set_error(HALO_MI_E_KERNEL, "%s: the bf16 MFMA GEMM needs 16-byte aligned x rows", op);
     GemmArgs a{static_cast<const uint8_t*>(p->w), nullptr, p->x, xs, p->y, ys, p->rows, p->cols, p->n_vec};
-    a.tiles = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M ? kGemmTilesSx : gemm_tiles(p->variant);
+    a.tiles = exact ? gemm_tiles(variant) : gemm_tiles(p->variant);
     a.norm_w = p->norm_w;
     a.norm_eps = p->norm_eps;
     return launch_gemm_pc<false>(p->type, a, st);
@@ -455,6 +469,7 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
     if ((code = check_norm(op, p->norm_w, p->cols, p->out, oext))) return code;
     if (variant == HALO_MI_GEMV_DEFAULT || variant == HALO_MI_GEMV_SLAB_AUTO)
         variant = auto_gemv_variant(p->type, p->rows, p->cols, p->n_vec, true);
+    if (variant == HALO_MI_GEMM_SLAB_EXACT_INVARIANT) variant = exact_invariant_or_gemv(p->rows, p->cols, true);
     auto st = static_cast<hipStream_t>(stream);
     if (variant == HALO_MI_GEMV_SLAB || variant == HALO_MI_GEMV_SLAB_VALU) {
         GemvSlabArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
@@ -464,11 +479,12 @@ int halo_mi_gate_up_swiglu(const halo_mi_gate_up_params* p, void* stream) {
         a.valu = variant == HALO_MI_GEMV_SLAB_VALU;
         return launch_gemv_slab<true>(p->type, a, st);
     }
-    if (variant != HALO_MI_GEMM_SLAB_EXACT_SMALL_M && (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
+    const bool exact = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M || variant == HALO_MI_GEMM_SLAB_EXACT_INVARIANT;
+    if (!exact && (xs % 4 || reinterpret_cast<uintptr_t>(p->x) % 16))
         return set_error(HALO_MI_E_KERNEL, "%s: the bf16 MFMA GEMM needs 16-byte aligned x rows", op);
     GemmArgs a{static_cast<const uint8_t*>(p->w_gate), static_cast<const uint8_t*>(p->w_up), p->x, xs, p->out, os,
                p->rows, p->cols, p->n_vec};
-    a.tiles = variant == HALO_MI_GEMM_SLAB_EXACT_SMALL_M ? kGemmTilesSx : gemm_tiles(p->variant);
+    a.tiles = exact ? gemm_tiles(variant) : gemm_tiles(p->variant);
     a.norm_w = p->norm_w;
     a.norm_eps = p->norm_eps;
     return launch_gemm_pc<true>(p->type, a, st);

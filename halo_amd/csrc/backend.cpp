@@ -237,7 +237,7 @@ private:
 
 // ---- variant registry (explicit, append-only ids; grouped by op) ----------------------------
 
-constexpr std::array<VariantInfo, 19> kVariants{{
+constexpr std::array<VariantInfo, 21> kVariants{{
     {kDequantRows, "dequant_rows_exact", OpId::GetRows, {}},
     {kRmsNorm, "rms_norm_cpu_order", OpId::RmsNorm, {}},
     {kGemvGgufRef, "gemv_gguf_ref_b256", OpId::Gemv, {}},
@@ -248,6 +248,7 @@ constexpr std::array<VariantInfo, 19> kVariants{{
     {kGemvSlabValu, "gemv_slab_valu_w64", OpId::Gemv, {}},
     {kGemmSlabBf16SmallM, "gemm_slab_bf16_mfma_small_m", OpId::Gemv, {}},
     {kGemmSlabExactSmallM, "gemm_slab_exact_small_m", OpId::Gemv, {}},
+    {kGemmSlabExactInvariant, "gemm_slab_exact_invariant", OpId::Gemv, {}},
     {kSwiglu, "swiglu_b256", OpId::Swiglu, {}},
     {kLmHeadFused, "lm_head_argmax_parts", OpId::LmHead, {}},
     {kArgmax, "argmax_parts_b256", OpId::Argmax, {}},
@@ -257,6 +258,7 @@ constexpr std::array<VariantInfo, 19> kVariants{{
     {kGateUpGemmM512, "gate_up_gemm_bf16_mfma_m512", OpId::GateUpSwiglu, {}},
     {kGateUpGemmSmallM, "gate_up_gemm_bf16_mfma_small_m", OpId::GateUpSwiglu, {}},
     {kGateUpExactSmallM, "gate_up_gemm_exact_small_m", OpId::GateUpSwiglu, {}},
+    {kGateUpExactInvariant, "gate_up_gemm_exact_invariant", OpId::GateUpSwiglu, {}},
 }};
 
 bool has_variant(OpId op, std::uint32_t id) {
@@ -264,9 +266,12 @@ bool has_variant(OpId op, std::uint32_t id) {
     return std::any_of(kVariants.begin(), kVariants.end(), [&](const VariantInfo& v) { return v.op == op && v.id == id; });
 }
 
-// MATMUL registry id -> the C ABI's variant id (the two lists are in the same order)
+// MATMUL registry id -> the C ABI's variant id (ids 30..36 are in the C ABI's order)
 std::uint32_t abi_gemv_variant(std::uint32_t id) {
-    return id == 0 ? HALO_MI_GEMV_DEFAULT : id == kGemmSlabExactSmallM ? HALO_MI_GEMM_SLAB_EXACT_SMALL_M : id - kGemvGgufRef + 1;
+    return id == 0                         ? HALO_MI_GEMV_DEFAULT
+           : id == kGemmSlabExactSmallM    ? HALO_MI_GEMM_SLAB_EXACT_SMALL_M
+           : id == kGemmSlabExactInvariant ? HALO_MI_GEMM_SLAB_EXACT_INVARIANT
+                                           : id - kGemvGgufRef + 1;
 }
 
 void check_no_status(const StatusRef& st, const char* op) {
@@ -277,7 +282,9 @@ void check_no_status(const StatusRef& st, const char* op) {
 
 class Mi355xBackend final : public MiBackend {
 public:
-    explicit Mi355xBackend(int device) : device_(device) {
+    Mi355xBackend(int device, MiOptions options)
+        : device_(device),
+          invariant_gemv_(options.batch_invariant == BatchInvariantKernel::Exact ? kGemmSlabExactInvariant : kGemvSlab) {
         int n = 0;
         CHECK(hipGetDeviceCount(&n) == hipSuccess && device >= 0 && device < n, ErrorCode::Device,
               "mi355x backend: no HIP device %d (%d visible)", device, n);
@@ -492,8 +499,9 @@ public:
         const bool slab = is_slab(a.w);
         std::uint32_t variant = a.kernel.variant_id;
         if (variant == 0) variant = slab ? kGemvSlabAuto : kGemvGgufRef;
-        // rows must not depend on the batch unless the caller accepts the GEMM's numerics
-        if (variant == kGemvSlabAuto && !a.allow_gemm) variant = kGemvSlab;
+        // rows must not depend on the batch unless the caller accepts the GEMM's numerics: the
+        // backend's batch-invariant family
+        if (variant == kGemvSlabAuto && !a.allow_gemm) variant = invariant_gemv_;
         CHECK(slab == (variant != kGemvGgufRef), ErrorCode::Config, "MATMUL: variant %u does not read the %s layout", variant,
               slab ? "SLAB" : "GGUF");
         const Operand w = slab ? r.slab(a.w, a.wtype, a.rows, a.cols, "w")
@@ -557,8 +565,9 @@ public:
                                       : id == kGateUpGemmM512   ? HALO_MI_GEMM_SLAB_BF16_M512
                                       : id == kGateUpGemmSmallM ? HALO_MI_GEMM_SLAB_BF16_SMALL_M
                                       : id == kGateUpExactSmallM ? HALO_MI_GEMM_SLAB_EXACT_SMALL_M
+                                      : id == kGateUpExactInvariant ? HALO_MI_GEMM_SLAB_EXACT_INVARIANT
                                       : a.allow_gemm            ? HALO_MI_GEMV_SLAB_AUTO
-                                                                : HALO_MI_GEMV_SLAB;
+                                                                : abi_gemv_variant(invariant_gemv_);
         halo_mi_gate_up_params p{static_cast<std::uint32_t>(a.wtype), HALO_MI_LAYOUT_SLAB, wg.base, wu.base,
                                  reinterpret_cast<const float*>(x.base), x.stride / kF32, reinterpret_cast<float*>(out.base),
                                  out.stride / kF32, a.rows, a.cols, a.n_vec, variant,
@@ -725,6 +734,7 @@ private:
     }
 
     int device_;
+    std::uint32_t invariant_gemv_;  // MATMUL registry id of the batch-invariant family (MiOptions)
     int cus_ = 0;
     std::string name_;
     bool lost_ = false, poisoned_ = false;
@@ -871,6 +881,8 @@ std::vector<ArgmaxResult> decode_argmax(std::span<const std::byte> words) {
     return out;
 }
 
-std::unique_ptr<MiBackend> make_mi355x_backend(int device) { return std::make_unique<Mi355xBackend>(device); }
+std::unique_ptr<MiBackend> make_mi355x_backend(int device, MiOptions options) {
+    return std::make_unique<Mi355xBackend>(device, options);
+}
 
 }  // namespace halo_mi::backend

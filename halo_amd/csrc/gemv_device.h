@@ -412,15 +412,6 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
         constexpr uint32_t kSpinLimit = 1u << 20;
         const uint32_t spin_limit = a.spin_limit ? a.spin_limit : kSpinLimit;
         const uint64_t want = tag ^ a.tag_flip;  // tag_flip: the host's forced-timeout test only
-        auto ready = [&](uint64_t w, const uint64_t* addr) {
-            for (uint32_t spin = 0; (w & ~0xFFFFFFFFull) != want && spin < spin_limit; ++spin) {
-                __builtin_amdgcn_s_sleep(2);
-                w = __hip_atomic_load(addr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            if ((w & ~0xFFFFFFFFull) == want) return __uint_as_float((uint32_t)w);
-            if (a.status) __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return __builtin_nanf("");
-        };
         for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
             uint64_t q[KB][NV];
 #pragma unroll
@@ -434,11 +425,40 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
             for (uint32_t kk = 0; kk < KB; ++kk) {
                 const uint32_t k = k0 + kk;
                 if (k >= nch) break;
+                float val[NV];
+                if (k == c) {
+#pragma unroll
+                    for (int v = 0; v < NV; ++v) val[v] = own[v];
+                } else {
+                    // while a word of this chunk is not ready, the chunk's words not ready are
+                    // loaded again together (one round trip per retry, not one per word)
+                    for (uint32_t spin = 0;; ++spin) {
+                        bool all = true;
+#pragma unroll
+                        for (int v = 0; v < NV; ++v) all = all && (q[kk][v] & ~0xFFFFFFFFull) == want;
+                        if (all || spin >= spin_limit) break;
+                        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                        for (int v = 0; v < NV; ++v)
+                            if ((q[kk][v] & ~0xFFFFFFFFull) != want)
+                                q[kk][v] = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+                    }
+#pragma unroll
+                    for (int v = 0; v < NV; ++v) {
+                        if ((q[kk][v] & ~0xFFFFFFFFull) == want) {
+                            val[v] = __uint_as_float((uint32_t)q[kk][v]);
+                        } else {  // gave up: the stream's status word, NaN in y
+                            if (a.status)
+                                __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            val[v] = __builtin_nanf("");
+                        }
+                    }
+                }
 #pragma unroll
                 for (int v = 0; v < NV; ++v) {
-                    const float val = k == c ? own[v] : ready(q[kk][v], P + ((uint64_t)k * NV + v) * 64 + lane);
-                    if (k < a.ks) acc0[v] += val;
-                    else acc1[v] += val;
+                    if (k < a.ks) acc0[v] += val[v];
+                    else acc1[v] += val[v];
                 }
             }
         }

@@ -1406,7 +1406,7 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
     const int MB = a.n_vec <= 64 ? 1 : a.n_vec <= 128 ? 2 : 4;
     const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
     const uint32_t units = PAIR ? slabs : (slabs + 1) / 2;
-    if (a.tiles == kGemmTilesSx) return launch_gemm_sx(type, PAIR, a, ws, units, st);
+    if (a.tiles == kGemmTilesSx || a.tiles == kGemmTilesSxFixed) return launch_gemm_sx(type, PAIR, a, ws, units, st);
     const uint32_t S = a.cols / kSlot, cus = cu_count();
     // k_gemm_lm (512-row M tiles) when its tiles alone fill the GPU; with fewer, the smaller
     // tiles of k_gemm_pc spread the work over more CUs
@@ -1476,14 +1476,6 @@ int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st) {
         if (int rc = hip_status(hipGetLastError(), "gemm_pc launch")) return rc;
     }
     return HALO_MI_OK;
-}
-
-int launch_gemm_chunk_reduce(bool pair, const GemmArgs& g, float* partials, uint32_t units, uint32_t kc, hipStream_t st) {
-    GemmPcArgs p{g.w0, g.w1, nullptr, g.y, g.y_stride, g.rows, g.cols, g.n_vec, 0u, 1u, 0u, units, kc, partials};
-    p.split_unit0 = 0;
-    if (pair) launch_reduce<true, kSmRows>(p, st);
-    else launch_reduce<false, kSmRows>(p, st);
-    return hip_status(hipGetLastError(), "gemm chunk reduce launch");
 }
 
 template int launch_gemm_pc<false>(uint32_t, const GemmArgs&, hipStream_t);

@@ -1,4 +1,4 @@
-// gfx950 exact-product small-M GEMM: k_gemm_sx<T, PAIR, NP, KH> for 2..8 rows of x.
+// gfx950 exact-product small-M GEMM: k_gemm_sx<T, PAIR, NP> for 1..8 rows of x.
 //
 // The slab GEMV's arithmetic (exact products, fp32 sums) on v_mfma_f32_32x32x16_bf16 tiles:
 //   - B: the weights' integer codes themselves as bf16 bit patterns (a code c < 256 in the low
@@ -10,15 +10,18 @@
 //     MFMAs, as the reference's expressions factor them, and each group's sum is brought back
 //     with ldexp.
 // Rows and the arithmetic are those of the slab GEMV (same bound), but a workgroup streams two
-// units (256 W rows) x one K chunk, one 64-row slab per wave (KH: two waves per slab, each
-// taking alternate super-blocks, their sums meeting in LDS), and no wave dequantizes: per slot
+// units (256 W rows) x one K chunk, one 64-row slab per wave, and no wave dequantizes: per slot
 // and row block a lane unpacks 16 codes with about 10 masks and folds its vectors' sums,
 // instead of converting and rounding 16 weights. Each lane loads its row's whole 16-byte slot
 // record (one 1 KB load instruction per wave and slot: half the load instructions of 8-byte
 // loads, which is what lets the stream run at the plain-read rate) and v_permlane32_swap hands
 // each lane half the bytes of the MFMA B layout. x enters LDS once per workgroup; the chunks'
-// partials go to the workspace and k_gemm_pc_reduce adds them in chunk order (the small-M
-// GEMM's layout).
+// partials go to the workspace and k_sx_reduce adds them in chunk order. The K split is the one
+// planned for 8 vectors whatever n_vec is, so a row's sums do not depend on the other vectors of
+// the batch: MFMA output element (i, j) takes only A row i and B column j, and nothing else in a
+// row's arithmetic looks at another vector. (A split planned per vector count, and a form with
+// two waves per slab taking alternate super-blocks, measured slower at every vector count on
+// the 17408 x 5120 and 5120 x 17408 shapes.)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,7 +42,6 @@ constexpr int kSxDepth = 8;               // slots of weight records in flight p
 constexpr uint32_t kSxLdsMax = 52 * 1024;  // x pieces, sums and exponents of one K chunk
 constexpr uint32_t kSxPairs = 10;          // (vector, group) pairs of x per wave of a four-wave fill
 constexpr uint32_t kSxWgsPerCu = 1;        // workgroups per CU the K split aims for
-constexpr size_t kSxKhLds = 4 * 64 * 2 * 2 * sizeof(float);  // the two-wave form's meeting: 4 waves x 64 lanes x 2 x NP <= 2
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sx_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
@@ -100,8 +102,10 @@ struct SxArgs {
     const uint8_t* w1;  // up (PAIR) or null
     const float* x;
     uint64_t x_stride;
-    float* partials;  // [unit][chunk][32 rows][128 columns], rows < n_vec written
+    float* partials;  // kchunks > 1: [unit][chunk][32 rows][128 columns], rows < n_vec written
     uint32_t rows, cols, n_vec, kchunks;
+    float* y;  // kchunks == 1: the result (SiLU(gate) * up for the pair), n_vec rows y_stride apart
+    uint64_t y_stride;
 };
 
 // One lane's records of one slot: lane l loads row l's whole 16-byte code record (a wave reads
@@ -258,8 +262,8 @@ __host__ __device__ constexpr uint32_t sx_rows(int np) { return np <= 2 ? 16u : 
 // LDS bytes per slot of the chunk: the pieces, then per K half and vector the x sum.
 __host__ __device__ constexpr uint32_t sx_slot_bytes(int np) { return 64u * sx_rows(np) + 2u * 8u * 4u; }
 
-template <uint32_t T, bool PAIR, int NP, bool KH>
-__global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a) {
+template <uint32_t T, bool PAIR, int NP>
+__global__ __launch_bounds__(256, 3) void k_gemm_sx(SxArgs a) {
     extern __shared__ uint4 sxl[];
     constexpr uint32_t RS = sx_rows(NP);
     constexpr bool kHi16 = T == kQ4_K || T == kQ4_0;  // K half 1's codes arrive as 16 q
@@ -275,13 +279,8 @@ __global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a
     const uint32_t ngc = base + (chunk < extra ? 1u : 0u);  // super-blocks of this chunk
     const uint32_t s_begin = 8 * g0, s_end = 8 * (g0 + ngc);
     const uint32_t ns = s_end - s_begin;
-    // wave w: unit 2 (blockIdx / kchunks) + (w % 4) / 2, matrix w % 2 (PAIR: gate / up; else the
-    // unit's two slabs), all 64 rows of that slab. KH: eight waves, two per slab, wave w taking
-    // the chunk's super-blocks of parity kh = w / 4 (two waves per SIMD at one workgroup per CU,
-    // so each hides the other's MFMA, LDS and dequant latencies); the kh = 1 wave's sums meet the
-    // kh = 0 wave's in LDS at the end
-    constexpr uint32_t SB = KH ? 2 : 1;  // a wave's super-block stride
-    const uint32_t kh = KH ? wave >> 2 : 0u;
+    // wave w: unit 2 (blockIdx / kchunks) + w / 2, matrix w % 2 (PAIR: gate / up; else the
+    // unit's two slabs), all 64 rows of that slab
     const uint32_t unit = 2 * (blockIdx.x / a.kchunks) + ((wave >> 1) & 1u), mat = wave & 1u;
     const bool live_unit = unit < units;  // an odd unit count leaves the last workgroup's second unit empty
     const uint32_t lu = min(unit, units - 1);
@@ -302,7 +301,7 @@ __global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a
 
     // ---- x of the chunk into LDS: one wave per (vector, group) pair. The x loads are issued
     // first, then the weight stream's first loads, then the split (which waits only for x).
-    constexpr uint32_t kWaves = KH ? 8 : 4;
+    constexpr uint32_t kWaves = 4;
     constexpr int kPairs = (int)((4 * kSxPairs + kWaves - 1) / kWaves);
     const uint32_t npairs = a.n_vec * ngc;
     float4 xv[kPairs];
@@ -320,9 +319,9 @@ __global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a
     SxH<T> H[2];
     auto load_q = [&](int q, uint32_t s) { sx_load_q<T>(R[q], wres, g, lane, s, s < s_end); };
     auto load_h = [&](int i, uint32_t sb) { sx_load_h<T>(H[i], wres, g, lane, sb, 8 * sb < s_end); };
-    const uint32_t sb0 = s_begin / 8 + kh;  // this wave's first super-block
+    const uint32_t sb0 = s_begin / 8;  // the chunk's first super-block
     load_h(0, sb0);
-    load_h(1, sb0 + SB);
+    load_h(1, sb0 + 1);
 #pragma unroll
     for (int q = 0; q < kSxDepth; ++q) load_q(q, 8 * sb0 + q);
 #pragma unroll
@@ -386,7 +385,7 @@ __global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a
         const uint4 a0 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 0) * 2 * RS * 16);
         const uint4 a1 = *reinterpret_cast<const uint4*>(abase + (ls * 2 + 1) * 2 * RS * 16);
         const float* xs = xsum + ls * 16 + hd;  // [K half][vector], vector 2 p + hd
-        load_q(qr, s + 8 * SB);  // this wave's next super-block
+        load_q(qr, s + 8);  // the next super-block
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             u32x4_t b0, b1;
@@ -463,69 +462,109 @@ __global__ __launch_bounds__(KH ? 512 : 256, KH ? 1 : 3) void k_gemm_sx(SxArgs a
             }
         }
     };
-    // this wave's super-blocks sb0, sb0 + SB, ...: H[0] serves the first of each pair, H[1] the
-    // second, each reloaded with the wave's super-block two ahead once its own is done
-    for (uint32_t i0 = 8 * sb0; i0 < s_end; i0 += 16 * SB) {
+    // the chunk's super-blocks: H[0] serves the first of each pair, H[1] the second, each
+    // reloaded with the super-block two ahead once its own is done
+    for (uint32_t i0 = 8 * sb0; i0 < s_end; i0 += 16) {
         group_begin(0);
 #pragma unroll
         for (int q = 0; q < 8; ++q) slot(q, i0 + q);
         group_end((i0 - s_begin) / 8);
-        load_h(0, i0 / 8 + 2 * SB);
-        if (i0 + 8 * SB >= s_end) break;
+        load_h(0, i0 / 8 + 2);
+        if (i0 + 8 >= s_end) break;
         group_begin(1);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) slot(q, i0 + 8 * SB + q);
-        group_end((i0 - s_begin) / 8 + SB);
-        load_h(1, i0 / 8 + 3 * SB);
+        for (int q = 0; q < 8; ++q) slot(q, i0 + 8 + q);
+        group_end((i0 - s_begin) / 8 + 1);
+        load_h(1, i0 / 8 + 3);
     }
-    if constexpr (KH) {
-        // the kh = 1 wave's sums to LDS (the x pieces are dead once every wave has left the
-        // loop; kSxKhLds bytes), then the kh = 0 wave adds them: a fixed order, independent of
-        // the vector count
-        __syncthreads();
-        float* red = reinterpret_cast<float*>(lds) + ((wave & 3u) * 64 + lane) * (2 * NP);
-        if (kh == 1) {
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int p = 0; p < NP; ++p) red[b * NP + p] = acc[b][p];
-        }
-        __syncthreads();
-        if (kh == 1) return;
+    if (!live_unit) return;
+    if (a.kchunks > 1) {
+        // the chunks' sums go to the workspace; k_sx_reduce adds them in chunk order
+        float* P = a.partials + ((uint64_t)unit * a.kchunks + chunk) * 32 * 128 + 64 * mat + r;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int p = 0; p < NP; ++p) acc[b][p] += red[b * NP + p];
+            for (int p = 0; p < NP; ++p)
+                if ((uint32_t)p < nv_lane) P[(2 * p + hd) * 128 + 32 * b] = acc[b][p];
+        return;
     }
-    if (!live_unit) return;
-    float* P = a.partials + ((uint64_t)unit * a.kchunks + chunk) * 32 * 128 + 64 * mat + r;
+    // one K chunk: y directly; row 32 b + r of the wave's slab, vectors 2 p + hd
+    if constexpr (PAIR) {
+        // gate (mat 0) and up (mat 1) of a unit are two waves: up goes through LDS (the x pieces
+        // are dead once every wave of the workgroup is past the loop)
+        __syncthreads();
+        float* ex = reinterpret_cast<float*>(lds) + ((wave >> 1) & 1u) * (2 * NP * 64) + lane;
+        if (mat == 1) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-            if ((uint32_t)p < nv_lane) P[(2 * p + hd) * 128 + 32 * b] = acc[b][p];
+                for (int p = 0; p < NP; ++p) ex[(b * NP + p) * 64] = acc[b][p];
+        }
+        __syncthreads();
+        if (mat == 1) return;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint32_t row = unit * kSlabRows + 32 * b + r;
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                if ((uint32_t)p < nv_lane && row < a.rows)
+                    a.y[(uint64_t)(2 * p + hd) * a.y_stride + row] = silu_f(acc[b][p]) * ex[(b * NP + p) * 64];
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint32_t row = 2 * unit * kSlabRows + 64 * mat + 32 * b + r;
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                if ((uint32_t)p < nv_lane && row < a.rows) a.y[(uint64_t)(2 * p + hd) * a.y_stride + row] = acc[b][p];
+        }
+    }
 }
 
-uint32_t sx_cu_count();
-
-template <bool PAIR, int NP, bool KH = false>
-void launch_sx_np(uint32_t type, const SxArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-    if constexpr (!KH && !PAIR && NP <= 2) {
-        // two waves per slab where every wave still gets two or more super-blocks and the grid
-        // stays within two of these workgroups per CU (GEMV M = 3-4: 22.5 -> 20.3 us; gate/up
-        // M = 4, 544 workgroups, and M = 8, 3 super-blocks per chunk, were slower)
-        const uint32_t ng = a.cols / kSlot / 8;
-        if ((ng + a.kchunks - 1) / a.kchunks >= 4 && grid.x <= 2 * sx_cu_count())
-            return launch_sx_np<PAIR, NP, true>(type, a, grid, std::max<size_t>(lds, kSxKhLds), st);
+// The chunks' sums in chunk order, 0 + c0 + c1 + ..., and the epilogue (SiLU(gate) * up for the
+// pair, the IEEE SiLU of the slab GEMV pair). One thread per (unit, vector, output column): the
+// loads of 8 chunks are in flight together, so a launch of up to 8 chunks is one memory round trip.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void k_sx_reduce(const float* __restrict__ partials, float* __restrict__ y,
+                                                   uint64_t y_stride, uint32_t rows, uint32_t units, uint32_t n_vec,
+                                                   uint32_t kc) {
+    constexpr uint32_t NC = PAIR ? 64 : 128;  // output columns of a unit
+    const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (uint64_t)units * n_vec * NC) return;
+    const uint32_t u = (uint32_t)(idx / (n_vec * NC)), e = (uint32_t)(idx % (n_vec * NC));
+    const uint32_t v = e / NC, n = e % NC;
+    const uint32_t row = PAIR ? u * kSlabRows + n : 2 * u * kSlabRows + n;
+    if (row >= rows) return;
+    const float* P = partials + (uint64_t)u * kc * 32 * 128 + v * 128 + n;
+    constexpr uint64_t CS = 32 * 128;  // floats per chunk
+    float s0 = 0.0f, s1 = 0.0f;
+    for (uint32_t c0 = 0; c0 < kc; c0 += 8) {
+        float q0[8], q1[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint64_t off = (uint64_t)min(c0 + i, kc - 1) * CS;
+            q0[i] = P[off];
+            if constexpr (PAIR) q1[i] = P[off + 64];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            if (c0 + i >= kc) break;
+            s0 += q0[i];
+            if constexpr (PAIR) s1 += q1[i];
+        }
     }
-    constexpr uint32_t NT = KH ? 512 : 256;
+    y[(uint64_t)v * y_stride + row] = PAIR ? silu_f(s0) * s1 : s0;
+}
+
+template <bool PAIR, int NP>
+void launch_sx_np(uint32_t type, const SxArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     switch (type) {
-        case kQ4_0: hipLaunchKernelGGL((k_gemm_sx<kQ4_0, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
-        case kQ8_0: hipLaunchKernelGGL((k_gemm_sx<kQ8_0, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
-        case kQ4_K: hipLaunchKernelGGL((k_gemm_sx<kQ4_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
-        case kQ5_K: hipLaunchKernelGGL((k_gemm_sx<kQ5_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
-        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sx<kIQ4_XS, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
-        default: hipLaunchKernelGGL((k_gemm_sx<kQ6_K, PAIR, NP, KH>), grid, dim3(NT), lds, st, a); break;
+        case kQ4_0: hipLaunchKernelGGL((k_gemm_sx<kQ4_0, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        case kQ8_0: hipLaunchKernelGGL((k_gemm_sx<kQ8_0, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        case kQ4_K: hipLaunchKernelGGL((k_gemm_sx<kQ4_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        case kQ5_K: hipLaunchKernelGGL((k_gemm_sx<kQ5_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        case kIQ4_XS: hipLaunchKernelGGL((k_gemm_sx<kIQ4_XS, PAIR, NP>), grid, dim3(256), lds, st, a); break;
+        default: hipLaunchKernelGGL((k_gemm_sx<kQ6_K, PAIR, NP>), grid, dim3(256), lds, st, a); break;
     }
 }
 
@@ -544,26 +583,40 @@ uint32_t sx_cu_count() {
 bool gemm_sx_plan(uint32_t units, uint32_t cols, uint32_t n_vec, uint32_t* kc, size_t* lds) {
     const uint32_t S = cols / kSlot;
     if (n_vec < 1 || n_vec > kGemmSxMaxRows || cols % 256 != 0 || S == 0 || units == 0) return false;
+    // the K split is planned for the most vectors a launch takes, so that every n_vec gets the
+    // same chunks (and the same sums)
+    const uint32_t pv = kGemmSxMaxRows;
     // with the fused norm the launch normalizes all n_vec rows into the workspace's norm buffer
     // at once; the plan refuses shapes past it with or without the norm, so that the auto choice
     // stays a function of the shape only
-    if ((uint64_t)n_vec * cols > kNormFloats) return false;
-    const int np = (int)(n_vec + 1) / 2;
-    const uint32_t ng = S / 8, per_group = 8 * sx_slot_bytes(np) + 8 * 4;
+    if ((uint64_t)pv * cols > kNormFloats) return false;
+    const uint32_t ng = S / 8;
+    const auto group_bytes = [](uint32_t nv) { return 8 * sx_slot_bytes((int)(nv + 1) / 2) + 8 * 4; };
     // a chunk's (vector, group) pairs: at most 4 kSxPairs per workgroup (the fill's registers;
     // the two-wave form spreads them over eight waves)
-    const uint32_t max_groups = std::min<uint32_t>(kSxLdsMax / per_group, 4 * kSxPairs / n_vec);
+    const uint32_t max_groups = std::min<uint32_t>(kSxLdsMax / group_bytes(pv), 4 * kSxPairs / pv);
     const uint32_t kc_min = (ng + max_groups - 1) / max_groups;
     const uint32_t wgs = (units + 1) / 2;  // a workgroup streams two units
     uint32_t k = std::clamp<uint32_t>((kSxWgsPerCu * sx_cu_count() + wgs - 1) / wgs, kc_min, ng);
     while (k > kc_min && (uint64_t)units * k * 32 * 128 > kPartialFloats) --k;
     if ((uint64_t)units * k * 32 * 128 > kPartialFloats) return false;
     *kc = k;
-    *lds = (size_t)((ng + k - 1) / k) * per_group;
+    *lds = (size_t)((ng + k - 1) / k) * group_bytes(n_vec);
     return true;
 }
 
 int launch_gemm_sx(uint32_t type, bool pair, const GemmArgs& g, Workspace* ws, uint32_t units, hipStream_t st) {
+    if (g.tiles == kGemmTilesSxFixed && g.n_vec > kGemmSxMaxRows) {
+        // passes of kGemmSxMaxRows vectors, each planned alike: rows stay independent of n_vec
+        for (uint32_t t0 = 0; t0 < g.n_vec; t0 += kGemmSxMaxRows) {
+            GemmArgs p = g;
+            p.x = g.x + (uint64_t)t0 * g.x_stride;
+            p.y = g.y + (uint64_t)t0 * g.y_stride;
+            p.n_vec = std::min(kGemmSxMaxRows, g.n_vec - t0);
+            if (int rc = launch_gemm_sx(type, pair, p, ws, units, st)) return rc;
+        }
+        return HALO_MI_OK;
+    }
     uint32_t kc = 0;
     size_t lds = 0;
     if (!gemm_sx_plan(units, g.cols, g.n_vec, &kc, &lds))
@@ -576,17 +629,32 @@ int launch_gemm_sx(uint32_t type, bool pair, const GemmArgs& g, Workspace* ws, u
         x = ws->xn;
         xs = g.cols;
     }
-    const SxArgs a{g.w0, g.w1, x, xs, ws->partials, g.rows, g.cols, g.n_vec, kc};
+    const SxArgs a{g.w0, g.w1, x, xs, ws->partials, g.rows, g.cols, g.n_vec, kc, g.y, g.y_stride};
     const dim3 grid(((units + 1) / 2) * kc);
     const int np = (int)(g.n_vec + 1) / 2;
     switch (np) {
-        case 1: pair ? launch_sx_np<true, 1>(type, a, grid, lds, st) : launch_sx_np<false, 1>(type, a, grid, lds, st); break;
-        case 2: pair ? launch_sx_np<true, 2>(type, a, grid, lds, st) : launch_sx_np<false, 2>(type, a, grid, lds, st); break;
-        case 3: pair ? launch_sx_np<true, 3>(type, a, grid, lds, st) : launch_sx_np<false, 3>(type, a, grid, lds, st); break;
-        default: pair ? launch_sx_np<true, 4>(type, a, grid, lds, st) : launch_sx_np<false, 4>(type, a, grid, lds, st); break;
+        case 1:
+            pair ? launch_sx_np<true, 1>(type, a, grid, lds, st) : launch_sx_np<false, 1>(type, a, grid, lds, st);
+            break;
+        case 2:
+            pair ? launch_sx_np<true, 2>(type, a, grid, lds, st) : launch_sx_np<false, 2>(type, a, grid, lds, st);
+            break;
+        case 3:
+            pair ? launch_sx_np<true, 3>(type, a, grid, lds, st) : launch_sx_np<false, 3>(type, a, grid, lds, st);
+            break;
+        default:
+            pair ? launch_sx_np<true, 4>(type, a, grid, lds, st) : launch_sx_np<false, 4>(type, a, grid, lds, st);
+            break;
     }
     if (int rc = hip_status(hipGetLastError(), "gemm_sx launch")) return rc;
-    return launch_gemm_chunk_reduce(pair, g, ws->partials, units, kc, st);
+    if (kc == 1) return HALO_MI_OK;
+    const uint64_t threads = (uint64_t)units * g.n_vec * (pair ? 64 : 128);
+    const dim3 rgrid((uint32_t)((threads + 255) / 256));
+    if (pair)
+        hipLaunchKernelGGL(k_sx_reduce<true>, rgrid, dim3(256), 0, st, ws->partials, g.y, g.y_stride, g.rows, units, g.n_vec, kc);
+    else
+        hipLaunchKernelGGL(k_sx_reduce<false>, rgrid, dim3(256), 0, st, ws->partials, g.y, g.y_stride, g.rows, units, g.n_vec, kc);
+    return hip_status(hipGetLastError(), "gemm_sx reduce launch");
 }
 
 }  // namespace halo_mi

@@ -77,7 +77,8 @@ constexpr uint32_t kTagMask = 0x7FFFFu;
 constexpr uint32_t kStatusSplitKTimeout = 0x100u;
 
 // M tile family of the bf16 GEMM: chosen by shape, k_gemm_pc (64..256 rows) or k_gemm_lm (512 rows)
-constexpr uint32_t kGemmTilesAuto = 0, kGemmTilesPc = 1, kGemmTilesLm = 2, kGemmTilesSm = 3, kGemmTilesSx = 4;
+constexpr uint32_t kGemmTilesAuto = 0, kGemmTilesPc = 1, kGemmTilesLm = 2, kGemmTilesSm = 3, kGemmTilesSx = 4,
+                   kGemmTilesSxFixed = 5;  // k_gemm_sx for any n_vec, in passes of kGemmSxMaxRows
 constexpr uint32_t kGemmSxMaxRows = 8;  // x rows of the exact small-M GEMM (k_gemm_sx)
 
 struct GemmArgs {
@@ -182,11 +183,9 @@ int launch_gemm_group(const GroupSeg* segs, uint32_t n, const float* x, uint64_t
 // k_gemm.hip
 template <bool PAIR>
 int launch_gemm_pc(uint32_t type, const GemmArgs& a, hipStream_t st);
-// k_gemm.hip: the chunk-order reduce of a small-M launch's partials ([unit][chunk][32][128],
-// rows < n_vec) and its epilogue (SwiGLU for the pair), into g.y
-int launch_gemm_chunk_reduce(bool pair, const GemmArgs& g, float* partials, uint32_t units, uint32_t kc, hipStream_t st);
 // k_gemm_sx.hip: the exact-product small-M GEMM (1..kGemmSxMaxRows rows of x, cols a multiple
-// of 256). gemm_sx_plan: whether a shape fits, its K chunks and LDS bytes.
+// of 256). gemm_sx_plan: whether a shape fits, its K chunks (those of kGemmSxMaxRows vectors
+// whatever n_vec is, so rows do not depend on n_vec) and LDS bytes.
 bool gemm_sx_plan(uint32_t units, uint32_t cols, uint32_t n_vec, uint32_t* kc, size_t* lds);
 int launch_gemm_sx(uint32_t type, bool pair, const GemmArgs& g, Workspace* ws, uint32_t units, hipStream_t st);
 // k_argmax.hip: stage 1 over a logits buffer (64-row parts, as the fused GEMV epilogue writes

@@ -116,7 +116,17 @@ enum { HALO_MI_LAYOUT_GGUF = 0, HALO_MI_LAYOUT_SLAB = 1 };
  *   8 HALO_MI_GEMM_SLAB_EXACT_SMALL_M  the exact-product small-M GEMM: the slab GEMV's
  *                            arithmetic (integer codes times x split exactly into three bf16
  *                            pieces, fp32 sums, scales applied per slot) on 32x32 MFMA tiles;
- *                            n_vec <= 8, cols a multiple of 256; within the bound of 2.
+ *                            n_vec <= 8, cols a multiple of 256; within the bound of 2. Its K
+ *                            split is the one planned for 8 vectors whatever n_vec is, so rows do
+ *                            not depend on n_vec.
+ *   9 HALO_MI_GEMM_SLAB_EXACT_INVARIANT  8's kernel for any n_vec, in passes of 8 vectors:
+ *                            every row of y is bitwise the row an n_vec = 1 call
+ *                            gives (the batch-invariance contract of GemvArgs::allow_gemm =
+ *                            false, backend.h:298-304). Where that split does not fit the shape
+ *                            (cols not a multiple of 256, or more partial sums than the stream's
+ *                            workspace holds) it runs 2, which is batch-invariant too: the
+ *                            choice follows the shape only. Within the bound of 2. Faster than
+ *                            2 from 3 vectors (one pass over the weights up to 8), slower at 1.
  */
 enum {
     HALO_MI_GEMV_DEFAULT = 0,
@@ -128,7 +138,8 @@ enum {
     HALO_MI_GEMV_SLAB_VALU = 6,
     HALO_MI_GEMM_SLAB_BF16_SMALL_M = 7,
     HALO_MI_GEMM_SLAB_EXACT_SMALL_M = 8,
-    HALO_MI_GEMV_VARIANT_LAST = 8
+    HALO_MI_GEMM_SLAB_EXACT_INVARIANT = 9,
+    HALO_MI_GEMV_VARIANT_LAST = 9
 };
 
 /*

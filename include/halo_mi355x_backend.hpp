@@ -479,8 +479,22 @@ public:
     virtual void gate_up_swiglu(Stream&, const GateUpArgs&) = 0;
 };
 
+/// The kernel family a MATMUL or GATE_UP_SWIGLU call with `allow_gemm == false` and kernel
+/// variant 0 runs on SLAB weights (GemvArgs::allow_gemm, backend.h:298-304: every row bitwise the
+/// row of an n_vec == 1 call). Both families keep that for any n_vec; the choice is per backend,
+/// so a decode at one vector and an MTP verify at K vectors always take the same one.
+enum class BatchInvariantKernel : std::uint8_t {
+    Gemv,   ///< the slab GEMV: fastest at 1-2 vectors, four vectors per pass over the weights
+    Exact,  ///< the exact small-M GEMM with its K split fixed by the shape (HALO_MI_GEMM_SLAB_EXACT_INVARIANT):
+            ///< fastest from 3 vectors, eight per pass; the slab GEMV where the split does not fit
+};
+
+struct MiOptions {
+    BatchInvariantKernel batch_invariant = BatchInvariantKernel::Gemv;
+};
+
 /// The MI355X backend on HIP device `device` (default 0). Error(Device) without a GPU.
-[[nodiscard]] std::unique_ptr<MiBackend> make_mi355x_backend(int device = 0);
+[[nodiscard]] std::unique_ptr<MiBackend> make_mi355x_backend(int device = 0, MiOptions options = {});
 
 /// Registered variant ids (explicit and append-only; never renumbered, a retired id is never
 /// reused). They start after the reference HIP backend's last id (29, copy_async;
@@ -504,5 +518,7 @@ inline constexpr std::uint32_t kGateUpGemmM512 = 45;    // ... on the 512-row-ti
 inline constexpr std::uint32_t kGateUpGemmSmallM = 46;  // ... on the small-M GEMM
 inline constexpr std::uint32_t kGemmSlabExactSmallM = 47;  // HALO_MI_GEMM_SLAB_EXACT_SMALL_M
 inline constexpr std::uint32_t kGateUpExactSmallM = 48;    // GATE_UP_SWIGLU on the exact small-M GEMM
+inline constexpr std::uint32_t kGemmSlabExactInvariant = 49;  // HALO_MI_GEMM_SLAB_EXACT_INVARIANT
+inline constexpr std::uint32_t kGateUpExactInvariant = 50;    // GATE_UP_SWIGLU on it
 
 }  // namespace halo_mi::backend

@@ -223,7 +223,7 @@ void run_type(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
     const std::vector<double> tu = slab_bound(type, wu, rows, cols, x, n_vec);
     const std::vector<double> gg = gemm_bound(type, wg, rows, cols, x, n_vec), gu = gemm_bound(type, wu, rows, cols, x, n_vec);
     for (uint32_t variant : {hb::kGateUpGemv, hb::kGateUpGemm, hb::kGateUpGemmM512, hb::kGateUpGemmSmallM,
-                             hb::kGateUpExactSmallM}) {
+                             hb::kGateUpExactSmallM, hb::kGateUpExactInvariant}) {
         hb::GateUpArgs g;
         g.wtype = static_cast<hb::DType>(type);
         g.w_gate = hb::TensorRef::of(*w_slab);
@@ -370,6 +370,77 @@ void run_type(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
     }
 }
 
+// MiOptions{BatchInvariantKernel::Exact}: allow_gemm == false runs the exact GEMM with its K split
+// fixed by the shape. Every row of n_vec = 3 and 9 is the n_vec = 1 row bitwise, rows are within the
+// slab bound, and the bits are those of the explicit registry id; the gate/up pair alike.
+void run_invariant(hb::MiBackend& be, hb::Stream& st, uint32_t type) {
+    const std::string tn = type_name(type) + std::string(" (Exact)");
+    const uint32_t rows = 130, cols = 1024, nv = 9;
+    const std::vector<uint8_t> wg = make_weights(type, rows, cols, 17 + type);
+    const std::vector<uint8_t> wu = make_weights(type, rows, cols, 47 + type);
+    std::vector<float> x((size_t)nv * cols);
+    halo_mi_fill_normal(1017 + type, x.data(), x.size(), 0.0f, 1.0f);
+    auto w_slab = be.import_weights(bytes_of(wg), static_cast<hb::DType>(type), rows, cols);
+    auto u_slab = be.import_weights(bytes_of(wu), static_cast<hb::DType>(type), rows, cols);
+    auto xb = be.allocate(x.size() * 4, hb::Tier::Vram);
+    auto yb = be.allocate((size_t)nv * rows * 4, hb::Tier::Vram);
+    be.upload(st, hb::TensorRef::of(*xb), bytes_of(x));
+    std::vector<float> ref((size_t)nv * rows);
+    oracle_matmul(type, wg.data(), 0, rows, cols, x.data(), 0, nv, ref.data(), 0, 1);
+    const std::vector<double> tol = slab_bound(type, wg, rows, cols, x, nv);
+    auto run = [&](auto&& call, uint32_t n) {
+        std::vector<float> y((size_t)n * rows);
+        call(n);
+        be.download(st, hb::TensorRef::of(*yb), std::as_writable_bytes(std::span<float>(y)));
+        st.submit();
+        st.wait();
+        return y;
+    };
+    auto gemv = [&](uint32_t variant) {
+        return [&, variant](uint32_t n) {
+            hb::GemvArgs a;
+            a.wtype = static_cast<hb::DType>(type);
+            a.w = hb::TensorRef::of(*w_slab);
+            a.x = hb::TensorRef::of(*xb);
+            a.y = hb::TensorRef::of(*yb);
+            a.rows = rows;
+            a.cols = cols;
+            a.n_vec = n;
+            a.kernel.variant_id = variant;
+            be.gemv(st, a);
+        };
+    };
+    auto gate_up = [&](uint32_t variant) {
+        return [&, variant](uint32_t n) {
+            hb::GateUpArgs g;
+            g.wtype = static_cast<hb::DType>(type);
+            g.w_gate = hb::TensorRef::of(*w_slab);
+            g.w_up = hb::TensorRef::of(*u_slab);
+            g.x = hb::TensorRef::of(*xb);
+            g.out = hb::TensorRef::of(*yb);
+            g.rows = rows;
+            g.cols = cols;
+            g.n_vec = n;
+            g.kernel.variant_id = variant;
+            be.gate_up_swiglu(st, g);
+        };
+    };
+    const std::vector<float> y9 = run(gemv(0), nv);
+    bool ok = true;
+    for (size_t i = 0; i < y9.size(); ++i) ok &= std::fabs((double)y9[i] - ref[i]) <= tol[i];
+    check(ok, tn + ": allow_gemm = false gemv within the slab bound");
+    for (uint32_t n : {1u, 3u}) {
+        const std::vector<float> yn = run(gemv(0), n);
+        check(std::memcmp(yn.data(), y9.data(), (size_t)n * rows * 4) == 0,
+              tn + ": n_vec = " + std::to_string(n) + " rows equal the n_vec = 9 rows");
+    }
+    check(run(gemv(hb::kGemmSlabExactInvariant), nv) == y9, tn + ": the default equals registry id 49");
+    const std::vector<float> g9 = run(gate_up(0), nv);
+    const std::vector<float> g1 = run(gate_up(0), 1);
+    check(std::memcmp(g1.data(), g9.data(), rows * 4) == 0, tn + ": gate_up n_vec = 1 row equals row 0 of n_vec = 9");
+    check(run(gate_up(hb::kGateUpExactInvariant), nv) == g9, tn + ": gate_up default equals registry id 50");
+}
+
 // The reference interface outside the path: every op virtual exists, the ones this backend does
 // not run throw Error(Unsupported); run_op dispatches by OpId and rejects mismatched args with
 // Error(Api); ARGMAX and COPY run; decode_argmax reads poisoned vectors as {-1, NaN}.
@@ -457,14 +528,15 @@ int main(int argc, char** argv) {
             {hb::OpId::Gemv,
              {{30, "gemv_gguf_ref_b256"}, {31, "gemv_slab_w64"}, {32, "gemm_slab_bf16_mfma"}, {33, "gemv_slab_auto"},
               {34, "gemm_slab_bf16_mfma_m512"}, {35, "gemv_slab_valu_w64"}, {36, "gemm_slab_bf16_mfma_small_m"},
-              {47, "gemm_slab_exact_small_m"}}},
+              {47, "gemm_slab_exact_small_m"}, {49, "gemm_slab_exact_invariant"}}},
             {hb::OpId::Swiglu, {{39, "swiglu_b256"}}},
             {hb::OpId::LmHead, {{40, "lm_head_argmax_parts"}}},
             {hb::OpId::Argmax, {{41, "argmax_parts_b256"}}},
             {hb::OpId::Copy, {{42, "copy_async"}}},
             {hb::OpId::GateUpSwiglu,
              {{43, "gate_up_gemv_w64"}, {44, "gate_up_gemm_bf16_mfma"}, {45, "gate_up_gemm_bf16_mfma_m512"},
-              {46, "gate_up_gemm_bf16_mfma_small_m"}, {48, "gate_up_gemm_exact_small_m"}}},
+              {46, "gate_up_gemm_bf16_mfma_small_m"}, {48, "gate_up_gemm_exact_small_m"},
+              {50, "gate_up_gemm_exact_invariant"}}},
         };
         for (const auto& [op, want] : pinned) {
             const auto got = be->variants(op);
@@ -482,6 +554,13 @@ int main(int argc, char** argv) {
             std::printf("[case] backend_pair %s\n", type_name(t));
             std::fflush(stdout);
             run_type(*be, *st, t);
+        }
+        auto be_exact = hb::make_mi355x_backend(0, hb::MiOptions{hb::BatchInvariantKernel::Exact});
+        auto st_exact = be_exact->create_stream();
+        for (uint32_t t : {HALO_MI_Q4_0, HALO_MI_Q8_0, HALO_MI_Q4_K, HALO_MI_Q6_K, HALO_MI_Q5_K, HALO_MI_IQ4_XS}) {
+            std::printf("[case] backend_pair Exact %s\n", type_name(t));
+            std::fflush(stdout);
+            run_invariant(*be_exact, *st_exact, t);
         }
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());

@@ -195,7 +195,7 @@ def test_lm_head_rejects_bad_arguments(hl, dev):
 
     assert code() == 0
     assert code(variant=3) == hl.ErrorCode.Kernel  # the GEMM ranks the logits: y needed
-    assert code(variant=9) == hl.ErrorCode.Config
+    assert code(variant=10) == hl.ErrorCode.Config  # past the last id
     assert code(ids_slots=ids, ids_scatter=ids, ids_scatter_len=1) == hl.ErrorCode.Kernel  # without ids
     assert code(ids=res) == hl.ErrorCode.Kernel  # ids overlaps result
     with pytest.raises(hl.HaloError):

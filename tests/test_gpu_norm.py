@@ -184,7 +184,10 @@ def test_gemv_norm_slab_bitwise(hl, oracle, dev, t, case):
     x, w = norm_inputs(cols, n_vec, 961 + cols + n_vec)
     xn = oracle.rms_norm(x, w, EPS)
     slab = slab_of(hl, dev, t, dense, rows, cols)
-    for variant in (hl.Variant.SLAB_GEMV, hl.Variant.SLAB_AUTO):
+    variants = [hl.Variant.SLAB_GEMV, hl.Variant.SLAB_AUTO]
+    if cols % 256 == 0:
+        variants.append(hl.Variant.SLAB_GEMM_EXACT_INVARIANT)
+    for variant in variants:
         y = run_norm_gemv(hl, dev, t, slab, x, w, rows, cols, variant, x_pad=1, y_pad=2)
         assert isclose_bits(y, unfused_gemv(hl, dev, t, slab, xn, rows, cols, variant)), \
             f"variant {int(variant)}: the fused norm is not bitwise rms_norm then the gemv"
@@ -222,15 +225,16 @@ def test_gemv_norm_in_kernel_sum_order(hl, oracle, dev, t):
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K, IQ4_XS))
 @pytest.mark.parametrize("rows,cols", [(130, 1024), (576, 5120)])
-def test_gemv_norm_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
-    say("gemv norm batch invariance", NAMES[t], rows, cols)
+@pytest.mark.parametrize("variant", ["SLAB_GEMV", "SLAB_GEMM_EXACT_INVARIANT"])
+def test_gemv_norm_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols, variant):
+    say("gemv norm batch invariance", variant, NAMES[t], rows, cols)
+    v = getattr(hl.Variant, variant)
     buf, stride = make_weights(t, rows, cols, seed=970 + t + rows)
     slab = slab_of(hl, dev, t, dense_of(buf, t, rows, cols, stride, 0), rows, cols)
     x, w = norm_inputs(cols, 9, 971)
-    singles = np.stack([run_norm_gemv(hl, dev, t, slab, x[i:i + 1], w, rows, cols, hl.Variant.SLAB_GEMV)[0]
-                        for i in range(9)])
+    singles = np.stack([run_norm_gemv(hl, dev, t, slab, x[i:i + 1], w, rows, cols, v)[0] for i in range(9)])
     for n_vec in (2, 3, 4, 5, 9):
-        y = run_norm_gemv(hl, dev, t, slab, x[:n_vec], w, rows, cols, hl.Variant.SLAB_GEMV)
+        y = run_norm_gemv(hl, dev, t, slab, x[:n_vec], w, rows, cols, v)
         assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
 
 
@@ -257,7 +261,7 @@ def test_gemm_norm_within_bounds(hl, oracle, dev, t, n_vec, variant):
 
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K, Q5_K, IQ4_XS, Q8_0, Q4_0))
-@pytest.mark.parametrize("n_vec,variant", [(1, 2), (4, 2), (17, 3), (600, 5)])
+@pytest.mark.parametrize("n_vec,variant", [(1, 2), (4, 2), (17, 3), (600, 5), (1, 9), (5, 9), (11, 9)])
 def test_gate_up_norm(hl, oracle, dev, t, n_vec, variant):
     import torch
 
@@ -270,11 +274,11 @@ def test_gate_up_norm(hl, oracle, dev, t, n_vec, variant):
     xn = oracle.rms_norm(x, w, EPS)
     ref = oracle.gate_up_swiglu(t, dg, du, rows, cols, xn)
     g, u = oracle.matmul(t, dg, rows, cols, xn), oracle.matmul(t, du, rows, cols, xn)
-    if variant == 2:
+    if variant in (2, 9):  # the exact arithmetic: the slab GEMV's bound (9: IEEE SiLU in the kernel)
         tg, tu = slab_gemv_tol(oracle, t, dg, rows, cols, xn), slab_gemv_tol(oracle, t, du, rows, cols, xn)
     else:
         tg, tu = gemm_tol(oracle, t, dg, rows, cols, xn), gemm_tol(oracle, t, du, rows, cols, xn)
-    tol = swiglu_tol(g, u, tg, tu, ref, fast=variant != 2)
+    tol = swiglu_tol(g, u, tg, tu, ref, fast=variant not in (2, 9))
     out = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
     sg, su = slab_of(hl, dev, t, dg, rows, cols), slab_of(hl, dev, t, du, rows, cols)
     hl.gate_up_swiglu(t, sg, su, to_dev(x, dev), out, rows, cols, n_vec, variant=variant, norm_w=to_dev(w, dev),

@@ -227,31 +227,48 @@ def test_gemv_slab_within_bound(hl, oracle, dev, t, case):
     assert np.all(err <= tol)
 
 
+INVARIANT_VARIANTS = ("SLAB_GEMV", "SLAB_GEMM_EXACT_INVARIANT")
+
+
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("rows,cols", [(130, 1024), (576, 5120)])
-def test_gemv_slab_rows_do_not_depend_on_the_batch(hl, dev, t, rows, cols):
+@pytest.mark.parametrize("variant", INVARIANT_VARIANTS)
+def test_gemv_slab_rows_do_not_depend_on_the_batch(hl, oracle, dev, t, rows, cols, variant):
     """GemvArgs::allow_gemm == false (include/halo/backend/backend.h:298-302): every row of a
-    batched call is bitwise the row of an n_vec == 1 call, whatever n_vec."""
-    say("gemv_slab batch invariance", NAMES[t], rows, cols)
+    batched call is bitwise the row of an n_vec == 1 call, whatever n_vec (the slab GEMV; the
+    exact GEMM with its K split fixed by the shape, in passes of 8 past 8 vectors). Every row is
+    within the slab GEMV's bound of cpu::matmul."""
+    v = getattr(hl.Variant, variant)
+    say("batch invariance", variant, NAMES[t], rows, cols)
     buf, stride = make_weights(t, rows, cols, seed=250 + t + rows)
     dense = dense_of(buf, t, rows, cols, stride, 0)
     slab = slab_of(hl, dev, t, dense, rows, cols)
-    x = np.random.default_rng(2500 + t).standard_normal((9, cols)).astype(np.float32)
-    singles = np.stack([run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[i:i + 1], rows, cols, hl.Variant.SLAB_GEMV, 0, 0)[0]
-                        for i in range(9)])
-    for n_vec in (2, 3, 4, 5, 9):
-        y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[:n_vec], rows, cols, hl.Variant.SLAB_GEMV, 0, 0)
+    n = 12
+    x = np.random.default_rng(2500 + t).standard_normal((n, cols)).astype(np.float32)
+    singles = np.stack([run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[i:i + 1], rows, cols, v, 0, 0)[0]
+                        for i in range(n)])
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
+    err = np.abs(singles.astype(np.float64) - ref)
+    print(f"    {variant} {NAMES[t]} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    for n_vec in (2, 3, 4, 5, 8, 9, 12):
+        y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[:n_vec], rows, cols, v, 1, 2)
         assert isclose_bits(y, singles[:n_vec]), f"n_vec={n_vec} changed a row"
 
 
 @pytest.mark.parametrize("t,rows,cols,pair", [(Q4_K, 17408, 5120, False), (Q4_K, 17408, 5120, True),
                                                (Q6_K, 5120, 17408, False), (Q6_K, 151936, 5120, False)])
-def test_gemv_rows_do_not_depend_on_the_batch_at_baseline_shapes(hl, dev, t, rows, cols, pair):
+@pytest.mark.parametrize("variant", INVARIANT_VARIANTS)
+def test_gemv_rows_do_not_depend_on_the_batch_at_baseline_shapes(hl, dev, t, rows, cols, pair, variant):
     """The same invariance at the BASELINE shapes, where the K split and the waves per chunk are
-    largest (the gate/up pair streams two matrices; 151936 rows takes the multi-group kernel)."""
+    largest (the gate/up pair streams two matrices; 151936 rows takes the multi-group kernel;
+    there the exact GEMM's fixed split does not fit the workspace and variant 9 runs the slab
+    GEMV, bitwise variant 2)."""
     import torch
 
-    say("gemv batch invariance", NAMES[t], rows, cols, "pair" if pair else "")
+    say("gemv batch invariance", variant, NAMES[t], rows, cols, "pair" if pair else "")
+    v = getattr(hl.Variant, variant)
     if rows == 151936:
         _, slab = head_weights(hl, dev)
     else:
@@ -264,14 +281,18 @@ def test_gemv_rows_do_not_depend_on_the_batch_at_baseline_shapes(hl, dev, t, row
         y = torch.full((n, rows), SENTINEL, dtype=torch.float32, device=dev)
         xv = xd[n0:n0 + n]
         if pair:
-            hl.gate_up_swiglu(t, slab, slab_u, xv, y, rows, cols, n, variant=hl.Variant.SLAB_GEMV)
+            hl.gate_up_swiglu(t, slab, slab_u, xv, y, rows, cols, n, variant=v)
         else:
-            hl.gemv(t, slab, xv, y, rows, cols, n, variant=hl.Variant.SLAB_GEMV)
+            hl.gemv(t, slab, xv, y, rows, cols, n, variant=v)
         return host(y)
 
     singles = np.concatenate([run(i, 1) for i in range(9)])
-    for n_vec in (2, 3, 4, 5, 9):
+    for n_vec in (2, 3, 4, 5, 8, 9):
         assert isclose_bits(run(0, n_vec), singles[:n_vec]), f"n_vec={n_vec} changed a row"
+    if rows == 151936 and v == hl.Variant.SLAB_GEMM_EXACT_INVARIANT:
+        y2 = torch.full((2, rows), SENTINEL, dtype=torch.float32, device=dev)
+        hl.gemv(t, slab, xd[:2], y2, rows, cols, 2, variant=hl.Variant.SLAB_GEMV)
+        assert isclose_bits(host(y2), singles[:2]), "variant 9 on a shape past its split is not variant 2"
 
 
 @pytest.mark.parametrize("t", (Q4_K, Q6_K))
@@ -473,7 +494,7 @@ def test_gemv_rejects_bad_arguments(hl, dev):
     assert c == hl.ErrorCode.Kernel and "multiple of the block size 32" in msg
     c, msg = code(y=w.data_ptr() + 16)
     assert c == hl.ErrorCode.Kernel and "y overlaps w" in msg
-    assert code(variant=9)[0] == hl.ErrorCode.Config
+    assert code(variant=10)[0] == hl.ErrorCode.Config  # past the last id
     assert code(variant=hl.Variant.SLAB_GEMV)[0] == hl.ErrorCode.Config  # GGUF bytes, SLAB kernel
     c, msg = code(t=F32, cols=64, w=w.data_ptr() + 2)
     assert c == hl.ErrorCode.Kernel and "4-byte aligned" in msg

@@ -69,7 +69,8 @@ def test_noalloc_refuses_what_does_not_fit(hl, dev):
     w = _case(hl, dev, t, rows, cols, 2300)
     x = to_dev(np.ones((16, cols), np.float32), dev)
     y = torch.zeros((16, rows), dtype=torch.float32, device=dev)
-    for variant, n_vec in ((hl.Variant.SLAB_GEMM_BF16, 1), (hl.Variant.DEFAULT, 16), (hl.Variant.SLAB_GEMM_BF16_M512, 2)):
+    for variant, n_vec in ((hl.Variant.SLAB_GEMM_BF16, 1), (hl.Variant.DEFAULT, 16), (hl.Variant.SLAB_GEMM_BF16_M512, 2),
+                           (hl.Variant.SLAB_GEMM_EXACT_INVARIANT, 1)):
         with pytest.raises(hl.HaloError) as e:  # the GEMM's staging does not fit the scratch
             hl.gemv_noalloc(t, w, x, y, rows, cols, n_vec, variant=variant)
         assert e.value.code == hl.ErrorCode.Unsupported
