@@ -469,8 +469,12 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
                     __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
-        if (lane == 0)
+        if (lane == 0) {
+            // the slab's published 1 / rms (in-kernel norm): every chunk has read it
+            if (a.norm_words)
+                __hip_atomic_store(a.norm_words + gs, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&a.counters[gs], (gen + 1) << kTicketBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     if constexpr (!PAIR) {
         // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
@@ -858,6 +862,8 @@ __device__ __forceinline__ void norm_x_squares(const float* __restrict__ x, uint
 
 // After norm_x_squares: the chains in lanes 0..7 of wave 0 (wave priority raised for them), the
 // combine and the tail: 1 / sqrt(mean + eps) for the whole workgroup.
+constexpr int kNormChainBatch = 4;  // 16-byte LDS reads per batch of the chains (16 VGPRs)
+constexpr uint32_t kNormPublishPerThread = 4;  // slabs per thread the leading workgroup publishes for
 __device__ __forceinline__ float norm_x_chains(const float* __restrict__ x, uint32_t cols, float eps, float* sq,
                                                uint32_t wave, uint32_t lane) {
     const uint32_t full = cols - cols % 8u, stride = norm_chain_stride(full);
@@ -865,13 +871,38 @@ __device__ __forceinline__ float norm_x_chains(const float* __restrict__ x, uint
     if (wave == 0) {
         __builtin_amdgcn_s_setprio(3);
         float p = 0.0f;
-        if (lane < 8) p = norm_chain(sq + lane * stride, full / 8, p);
+        if (lane < 8) p = norm_chain<kNormChainBatch>(sq + lane * stride, full / 8, p);
         const float inv = norm_finish(p, x, full, cols, eps, lane);
         if (lane == 0) sq[8 * stride] = inv;
         __builtin_amdgcn_s_setprio(0);
     }
     lds_sync();
     return sq[8 * stride];
+}
+
+// The published 1 / rms for this workgroup's slab (a.norm_words): thread 0, which holds the slab's
+// ticket (the generation), waits for the word with this launch's tag and hands it to the
+// workgroup through LDS. A wait that gives up sets the stream's status word and yields NaN.
+__device__ __forceinline__ float norm_x_wait(const GemvSlabArgs& a, uint32_t slab, uint32_t ticket, float* slot) {
+    if (threadIdx.x == 0) {
+        const uint32_t gen = ticket >> kTicketBits;
+        const uint64_t want = ((uint64_t)((gen & kTagMask) | (kTagMask + 1)) << 32) ^ a.tag_flip;
+        const uint64_t* word = a.norm_words + a.slab0 + slab;
+        const uint32_t spin_limit = a.spin_limit ? a.spin_limit : (1u << 20);
+        uint64_t v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t spin = 0; (v & ~0xFFFFFFFFull) != want && spin < spin_limit; ++spin) {
+            __builtin_amdgcn_s_sleep(2);
+            v = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        float inv = __uint_as_float((uint32_t)v);
+        if ((v & ~0xFFFFFFFFull) != want) {
+            if (a.status) __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            inv = __builtin_nanf("");
+        }
+        *slot = inv;
+    }
+    lds_sync();
+    return *slot;
 }
 
 // LDS bytes of the chain rows and the result word for a row of cols floats
@@ -930,9 +961,23 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
     const uint32_t nch = a.ks * MATS;
     float* sq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + mx_lds_bytes<NV>(nw));
+    // NORM with published words: only the first workgroup runs the chains
+    const bool leader = !NORM || a.norm_words == nullptr || bid == 0;
+    uint32_t gens[kNormPublishPerThread];  // the leader: the launch generations of the slabs it publishes for
     if constexpr (NORM) {
-        // the row's squares into LDS before the weight loads are issued (registers free again)
-        norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
+        if (leader) {
+            if (a.norm_words) {
+#pragma unroll
+                for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
+                    const uint32_t s = threadIdx.x + i * blockDim.x;
+                    gens[i] = s < a.norm_slabs ? __hip_atomic_load(&a.counters[a.slab0 + s], __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
+                                               : 0u;
+                }
+            }
+            // the row's squares into LDS before the weight loads are issued (registers free again)
+            norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
     const uint32_t slab = bid / nch, c = bid % nch;
@@ -952,8 +997,24 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     float xr[NV][4];
     uint32_t ticket = 0;
     float wr[4];  // NORM: norm_w at this lane's x elements
-    // NORM: the chains (wave 0) and 1 / rms for the workgroup
-    auto norm_inv = [&]() { return norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane); };
+    // NORM: 1 / rms for the workgroup: the chains (wave 0), and with published words the leader
+    // then stores it to every slab's word while the others wait for theirs
+    auto norm_inv = [&]() {
+        if (!leader) return norm_x_wait(a, bid / (a.ks * (PAIR ? 2u : 1u)), ticket, sq + 8 * norm_chain_stride(a.cols - a.cols % 8u));
+        const float inv = norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
+        if (a.norm_words) {
+#pragma unroll
+            for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
+                const uint32_t s = threadIdx.x + i * blockDim.x;
+                if (s < a.norm_slabs)
+                    __hip_atomic_store(a.norm_words + a.slab0 + s,
+                                       (uint64_t)__float_as_uint(inv) |
+                                           ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return inv;
+    };
     if constexpr (ONE) {
         if (w0 < w1) {
             SlotGroup<T> G;

@@ -111,6 +111,14 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
     const dim3 grid(slabs * a.ks * MATS), block(64 * sp.nw);
     if (a.norm_w) {  // the in-kernel norm (one vector; norm_in_kernel chose it)
         if constexpr (NV == 1) {
+            // with split K, the first workgroup alone runs the norm's chains and publishes 1 / rms
+            // in one word per slab, kept at the end of the split-K words (0 between launches)
+            const uint64_t words = (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64;
+            a.norm_words = nullptr;
+            if (a.ks * MATS > 1 && slabs <= kNormPublishPerThread * 64 * sp.nw && words + slabs <= slots_cap) {
+                a.norm_words = ws->slots + (slots_cap - slabs);
+                a.norm_slabs = slabs;
+            }
             const size_t ln = lds + norm_lds_bytes(a.cols);
             if (sp.one) hipLaunchKernelGGL((k_gemv_mx<T, 1, PAIR, true, true>), grid, block, ln, st, a);
             else hipLaunchKernelGGL((k_gemv_mx<T, 1, PAIR, false, true>), grid, block, ln, st, a);

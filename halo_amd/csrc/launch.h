@@ -49,6 +49,11 @@ struct GemvSlabArgs {
     // rows. Both are bitwise cpu::rms_norm then the unfused GEMV.
     const float* norm_w = nullptr;
     float norm_eps = 0.0f;
+    // In-kernel norm with split K: the first workgroup alone runs the norm's chains and publishes
+    // 1 / rms to every slab's word (fp32 bits and the slab's launch tag, as the split-K words);
+    // the other workgroups wait for their slab's word. Null: every workgroup runs the chains.
+    uint64_t* norm_words = nullptr;  // [slabs], 0 between launches (the slab's reducer clears it)
+    uint32_t norm_slabs = 0;         // slabs the first workgroup publishes for
     // Workspace indexing in a grouped launch (k_gemv_mx_group): this matrix's first slab among
     // the launch's slabs, and the launch's workgroups (0: a launch of its own).
     uint32_t slab0 = 0;

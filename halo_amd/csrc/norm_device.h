@@ -22,18 +22,20 @@ __host__ __device__ constexpr uint32_t norm_chain_stride(uint32_t n) { return n 
 // LDS floats of the 8 chain rows for n squares, then one word for the result
 __host__ __device__ constexpr uint32_t norm_lds_floats(uint32_t n) { return 8 * norm_chain_stride(n) + 4; }
 
-// Continues chain sum p over m squares of one chain row r (LDS), in order. Batches of eight
-// 16-byte reads are issued before their 32 additions, so the LDS latency is paid once per batch.
-// (Reading one batch ahead, in a second register set, measured slower in the GEMV's prologue.)
+// Continues chain sum p over m squares of one chain row r (LDS), in order. Batches of B 16-byte
+// reads are issued before their 4 B additions, so the LDS latency is paid once per batch; the
+// batch's 4 B registers count towards the caller's register budget. (Reading one batch ahead, in
+// a second register set, measured slower in the GEMV's prologue.)
+template <int B = 8>
 __device__ __forceinline__ float norm_chain(const float* r, uint32_t m, float p) {
 #pragma clang fp contract(off)
     uint32_t k = 0;
-    for (; k + 32 <= m; k += 32) {
-        float4 q[8];
+    for (; k + 4 * B <= m; k += 4 * B) {
+        float4 q[B];
 #pragma unroll
-        for (int b = 0; b < 8; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
+        for (int b = 0; b < B; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < B; ++b) {
             p = p + q[b].x;
             p = p + q[b].y;
             p = p + q[b].z;
