@@ -312,9 +312,6 @@ __device__ __forceinline__ void compute_group(const SlotGroup<T>& G, uint32_t gr
     }
 }
 
-// End of a slab-GEMV workgroup: the waves' partial sums meet in LDS in wave order, then (split
-// K) the workgroups of a slab meet in the workspace, and the result (SiLU(gate) * up for the
-// pair) is written. acc0 holds this wave's sums in fp32, rows = lanes.
 // Split-K: the workgroup's start ticket for its slab, taken when it starts and used only at its
 // end, so the device-scope round trip overlaps the weight stream. A slab's counter holds the
 // arrivals of the running launch in its low kTicketBits bits and the slab's launch generation
@@ -351,134 +348,127 @@ __device__ __forceinline__ float wave_sum(float s) {
     return (r0 + r1) + (r2 + r3);
 }
 
-template <int NV, bool PAIR>
-__device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
-                                            uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
+// Split-K meeting of one slab's pieces (the workgroups, or segments of workgroups, that summed
+// parts of its K range) in the workspace words, without cache maintenance and without a round
+// trip at the end of most pieces. The piece with the slab's last start ticket is the reducer:
+// every other piece of the slab started before it, so they are all running. The others store
+// their partials as 64-bit words (fp32 bits and this launch's tag: one atomic access carries the
+// value and its mark) and finish. The reducer loads those words, re-reads (bounded, with a pause)
+// any not yet ready, adds the pieces in piece order (deterministic), and clears the words and
+// the arrivals for the next launch.
+// c: this piece of nch, holding acc0; ticket: its start ticket (the calling wave's first lane).
+// Pieces [0, n0) are the gate rows of a pair (or all), [n0, nch) the up rows. gs: the slab's
+// index among the launch's slabs (a grouped launch covers several matrices); stride: the pieces
+// the workspace holds per slab. Returns false for a piece that stored its partial, true for the
+// reducer, which then holds the slab's sums in acc0 and acc1. SLAB_NORM: the in-kernel norm's
+// published words are per slab (the reducer clears the slab's), not per workgroup.
+template <int NV, bool SLAB_NORM = true>
+__device__ __forceinline__ bool splitk_meet(const GemvSlabArgs& a, float (&acc0)[NV], float (&acc1)[NV], uint32_t lane,
+                                            uint32_t gs, uint32_t c, uint32_t nch, uint32_t n0, uint32_t stride,
                                             uint32_t ticket) {
-    // waves -> wave 0, in wave order
-    if (nw > 1) {
+    uint64_t* P = a.slots + (uint64_t)gs * stride * NV * 64;
+    // A word is ready when its high half holds this launch's tag (the slab's generation, never
+    // 0): a word left over from an earlier launch (one that arrived after its reducer gave up
+    // waiting) is never taken for this launch's.
+    const uint32_t tk = __builtin_amdgcn_readfirstlane(ticket);
+    const uint32_t gen = tk >> kTicketBits;
+    const uint64_t tag = (uint64_t)((gen & kTagMask) | (kTagMask + 1)) << 32;
+    if ((tk & kArrivalMask) != nch - 1) {
 #pragma unroll
-        for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
-        __syncthreads();
-        if (wave != 0) return;
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            float s = red[v * 64 + lane];
-            for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
-            acc0[v] = s;
-        }
+        for (int v = 0; v < NV; ++v)
+            __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane, (uint64_t)__float_as_uint(acc0[v]) | tag,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
     }
-    const uint32_t row = slab * kSlabRows + lane;
-    float acc1[NV];  // the up sums (PAIR)
+    float own[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
-    if (nch > 1) {
-        // Split-K meeting point, without cache maintenance and without a round trip at the end
-        // of most workgroups. The workgroup with the slab's last start ticket is the reducer:
-        // every other chunk of the slab started before it, so they are all running. The others
-        // store their partials as 64-bit words (fp32 bits and this launch's tag: one atomic
-        // access carries the value and its mark) and finish. The reducer loads those words,
-        // re-reads (bounded, with a pause) any not yet ready, adds the chunks in chunk order
-        // (deterministic), and clears the words and the arrivals for the next launch.
-        // workspace words of this slab: its index among all slabs of the launch (a grouped launch
-        // covers several matrices)
-        const uint32_t gs = a.slab0 + slab;
-        uint64_t* P = a.slots + (uint64_t)gs * nch * NV * 64;
-        // A word is ready when its high half holds this launch's tag (the slab's generation,
-        // never 0): a word left over from an earlier launch (one that arrived after its reducer
-        // gave up waiting) is never taken for this launch's.
-        const uint32_t tk = __builtin_amdgcn_readfirstlane(ticket);
-        const uint32_t gen = tk >> kTicketBits;
-        const uint64_t tag = (uint64_t)((gen & kTagMask) | (kTagMask + 1)) << 32;
-        if ((tk & kArrivalMask) != nch - 1) {
+    for (int v = 0; v < NV; ++v) {
+        own[v] = acc0[v];
+        acc0[v] = 0.0f;
+    }
+    // The loads of 8 pieces are issued before any is used (one memory round trip per 8 pieces);
+    // past the last piece the address is clamped and the value dropped.
+    constexpr uint32_t KB = 8;
+    // The other pieces are running, so a word is a few microseconds away at most. A wait that
+    // gives up marks the stream's status word (the host reports it as a device error at its next
+    // check) and leaves NaN in the output.
+    constexpr uint32_t kSpinLimit = 1u << 20;
+    const uint32_t spin_limit = a.spin_limit ? a.spin_limit : kSpinLimit;
+    const uint64_t want = tag ^ a.tag_flip;  // tag_flip: the host's forced-timeout test only
+    for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
+        uint64_t q[KB][NV];
+#pragma unroll
+        for (uint32_t kk = 0; kk < KB; ++kk) {
+            const uint64_t* Q = P + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
 #pragma unroll
             for (int v = 0; v < NV; ++v)
-                __hip_atomic_store(P + ((uint64_t)c * NV + v) * 64 + lane, (uint64_t)__float_as_uint(acc0[v]) | tag,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return;
+                q[kk][v] = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        float own[NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            own[v] = acc0[v];
-            acc0[v] = 0.0f;
-        }
-        // The loads of 8 chunks are issued before any is used (one memory round trip per 8
-        // chunks); past the last chunk the address is clamped and the value dropped.
-        constexpr uint32_t KB = 8;
-        // The other chunks are running, so a word is a few microseconds away at most. A wait
-        // that gives up marks the stream's status word (the host reports it as a device error
-        // at its next check) and leaves NaN in the output.
-        constexpr uint32_t kSpinLimit = 1u << 20;
-        const uint32_t spin_limit = a.spin_limit ? a.spin_limit : kSpinLimit;
-        const uint64_t want = tag ^ a.tag_flip;  // tag_flip: the host's forced-timeout test only
-        for (uint32_t k0 = 0; k0 < nch; k0 += KB) {
-            uint64_t q[KB][NV];
+        for (uint32_t kk = 0; kk < KB; ++kk) {
+            const uint32_t k = k0 + kk;
+            if (k >= nch) break;
+            float val[NV];
+            if (k == c) {
 #pragma unroll
-            for (uint32_t kk = 0; kk < KB; ++kk) {
-                const uint64_t* Q = P + (uint64_t)min(k0 + kk, nch - 1) * NV * 64;
+                for (int v = 0; v < NV; ++v) val[v] = own[v];
+            } else {
+                // while a word of this piece is not ready, the piece's words not ready are loaded
+                // again together (one round trip per retry, not one per word)
+                for (uint32_t spin = 0;; ++spin) {
+                    bool all = true;
 #pragma unroll
-                for (int v = 0; v < NV; ++v)
-                    q[kk][v] = __hip_atomic_load(Q + v * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+                    for (int v = 0; v < NV; ++v) all = all && (q[kk][v] & ~0xFFFFFFFFull) == want;
+                    if (all || spin >= spin_limit) break;
+                    __builtin_amdgcn_s_sleep(2);
 #pragma unroll
-            for (uint32_t kk = 0; kk < KB; ++kk) {
-                const uint32_t k = k0 + kk;
-                if (k >= nch) break;
-                float val[NV];
-                if (k == c) {
-#pragma unroll
-                    for (int v = 0; v < NV; ++v) val[v] = own[v];
-                } else {
-                    // while a word of this chunk is not ready, the chunk's words not ready are
-                    // loaded again together (one round trip per retry, not one per word)
-                    for (uint32_t spin = 0;; ++spin) {
-                        bool all = true;
-#pragma unroll
-                        for (int v = 0; v < NV; ++v) all = all && (q[kk][v] & ~0xFFFFFFFFull) == want;
-                        if (all || spin >= spin_limit) break;
-                        __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-                        for (int v = 0; v < NV; ++v)
-                            if ((q[kk][v] & ~0xFFFFFFFFull) != want)
-                                q[kk][v] = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
-                                                             __HIP_MEMORY_SCOPE_AGENT);
-                    }
-#pragma unroll
-                    for (int v = 0; v < NV; ++v) {
-                        if ((q[kk][v] & ~0xFFFFFFFFull) == want) {
-                            val[v] = __uint_as_float((uint32_t)q[kk][v]);
-                        } else {  // gave up: the stream's status word, NaN in y
-                            if (a.status)
-                                __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            val[v] = __builtin_nanf("");
-                        }
-                    }
+                    for (int v = 0; v < NV; ++v)
+                        if ((q[kk][v] & ~0xFFFFFFFFull) != want)
+                            q[kk][v] = __hip_atomic_load(P + ((uint64_t)k * NV + v) * 64 + lane, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
                 }
 #pragma unroll
                 for (int v = 0; v < NV; ++v) {
-                    if (k < a.ks) acc0[v] += val[v];
-                    else acc1[v] += val[v];
+                    if ((q[kk][v] & ~0xFFFFFFFFull) == want) {
+                        val[v] = __uint_as_float((uint32_t)q[kk][v]);
+                    } else {  // gave up: the stream's status word, NaN in y
+                        if (a.status)
+                            __hip_atomic_fetch_or(a.status, kStatusSplitKTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        val[v] = __builtin_nanf("");
+                    }
                 }
             }
-        }
-        for (uint32_t k = 0; k < nch; ++k)
-            if (k != c) {
 #pragma unroll
-                for (int v = 0; v < NV; ++v)
-                    __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+            for (int v = 0; v < NV; ++v) {
+                if (k < n0) acc0[v] += val[v];
+                else acc1[v] += val[v];
             }
-        if (lane == 0) {
-            // the slab's published 1 / rms (in-kernel norm): every chunk has read it
-            if (a.norm_words)
-                __hip_atomic_store(a.norm_words + gs, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.counters[gs], (gen + 1) << kTicketBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    for (uint32_t k = 0; k < nch; ++k)
+        if (k != c) {
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+                __hip_atomic_store(P + ((uint64_t)k * NV + v) * 64 + lane, 0ull, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    if (lane == 0) {
+        // the slab's published 1 / rms (in-kernel norm): every piece has read it
+        if (SLAB_NORM && a.norm_words) __hip_atomic_store(a.norm_words + gs, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&a.counters[gs], (gen + 1) << kTicketBits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+}
+
+// End of a slab: the LM head's argmax parts and y (SiLU(gate) * up for the pair), one row per
+// lane of the calling wave (all 64 lanes).
+template <int NV, bool PAIR>
+__device__ __forceinline__ void gemv_store(const GemvSlabArgs& a, const float (&acc0)[NV], const float (&acc1)[NV],
+                                           uint32_t slab, uint32_t lane) {
+    const uint32_t row = slab * kSlabRows + lane;
     if constexpr (!PAIR) {
-        // LM head: the slab's argmax per vector, over exactly the values written to y (all 64
-        // lanes of wave 0 are here; rows past the matrix take no part)
+        // LM head: the slab's argmax per vector, over exactly the values written to y (rows past
+        // the matrix take no part)
         if (a.parts) {
             const uint32_t slabs = (a.rows + kSlabRows - 1) / kSlabRows;
             const bool live = row < a.rows;
@@ -500,6 +490,33 @@ __device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)
         if ((uint32_t)v >= a.n_vec) break;
         a.y[(uint64_t)v * a.y_stride + row] = PAIR ? silu_f(acc0[v]) * acc1[v] : acc0[v];
     }
+}
+
+// End of a chunked slab-GEMV workgroup: the waves' partial sums meet in LDS in wave order, then
+// (split K) the workgroups of the slab meet in the workspace, and the reducer writes the slab.
+// acc0 holds this wave's sums in fp32, rows = lanes.
+template <int NV, bool PAIR>
+__device__ __forceinline__ void gemv_finish(const GemvSlabArgs& a, float (&acc0)[NV], float* red, uint32_t wave,
+                                            uint32_t nw, uint32_t lane, uint32_t slab, uint32_t c, uint32_t nch,
+                                            uint32_t ticket) {
+    // waves -> wave 0, in wave order
+    if (nw > 1) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) red[(wave * NV + v) * 64 + lane] = acc0[v];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float s = red[v * 64 + lane];
+            for (uint32_t w = 1; w < nw; ++w) s += red[(w * NV + v) * 64 + lane];
+            acc0[v] = s;
+        }
+    }
+    float acc1[NV];  // the up sums (PAIR)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc1[v] = 0.0f;
+    if (nch > 1 && !splitk_meet<NV>(a, acc0, acc1, lane, a.slab0 + slab, c, nch, a.ks, nch, ticket)) return;
+    gemv_store<NV, PAIR>(a, acc0, acc1, slab, lane);
 }
 
 // grid.x = slabs * ks * MATS; block = 64 * nw (nw waves). Dynamic LDS: the waves' partials
@@ -937,6 +954,12 @@ __host__ __device__ constexpr size_t mx_lds_bytes(uint32_t nw) {
     return (size_t)nw * (NV * 64 * sizeof(float) + mx_table_bytes<NV>());
 }
 
+// Dynamic LDS bytes of a k_gemv_mx_even workgroup: nu unit entries and nw waves' A tables.
+template <int NV>
+__host__ __device__ constexpr size_t even_lds_bytes(uint32_t nu, uint32_t nw) {
+    return (size_t)nu * NV * 64 * sizeof(float) + (size_t)nw * mx_table_bytes<NV>();
+}
+
 // Workgroup size bound: single-vector kernels fit 128 VGPRs (16 waves per workgroup), except
 // the Q8_0, Q6_K and Q5_K loops (two register groups); so do the one-group loops of the other
 // formats at up to 4 vectors; the rest run at most 8 waves.
@@ -1079,6 +1102,192 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
 template <uint32_t T, int NV, bool PAIR, bool ONE, bool NORM = false>
 __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(GemvSlabArgs a) {
     gemv_mx_body<T, NV, PAIR, ONE, NORM>(a, blockIdx.x);
+}
+
+// ------------------------------------------------------------------------------------------
+// Even split: k_gemv_mx_even<T, NV, PAIR, NORM> (the one-group form of a large launch).
+//
+// A chunked split gives each workgroup one K chunk of one slab, so the workgroup count is slabs
+// x chunks, and the CUs do not get equal work: 272 slabs x 4 chunks = 1088 workgroups put 5
+// workgroups on 64 of the 256 CUs and 4 on the rest, and the last weights of the launch arrive
+// on the 64 (measured with per-wave timestamps). Here the launch's W workgroups (a multiple of
+// the CU count) take equal shares [b G / W, (b + 1) G / W) of the launch's G = slabs x matrices x
+// groups slot groups ("units"), in (slab, matrix, group) order.
+// Inside a workgroup, wave w takes the units w and w + nw of the share (one each when the share
+// has at most nw units), and each unit's sum goes to its own LDS entry.
+// The units of a (slab, matrix) in the share form a segment: one piece of its slab's split-K meeting, summed
+// from the entries in unit order by the wave holding its first unit (which took the slab's
+// ticket); the pieces of a slab are numbered by workgroup, the gate matrix's first. A slab that
+// lies wholly inside one workgroup meets in LDS alone. The sums depend on W only: nw is chosen
+// per vector count so that the launch's workgroups fit the CUs in one round.
+// In-kernel norm: the first workgroup runs the chains and publishes 1 / rms to one word per
+// workgroup, tagged with the generation of that workgroup's first slab (its wave 0 always holds
+// a ticket for that slab: the slab's reducer, or the workgroup itself for a slab wholly inside
+// it, moves the generation on); each workgroup clears its word when it has read it.
+// ------------------------------------------------------------------------------------------
+// Units per wave: at most two at two vectors (the kernel holds 4 waves per SIMD there, and a
+// second unit lets the workgroups of 2 per CU stay resident), else one (nw is the share's size;
+// a second unit's registers would spill at 3 and 4 vectors)
+template <int NV>
+constexpr uint32_t even_units_per_wave() { return NV == 2 ? 2u : 1u; }
+// The workgroup whose share holds unit u (of G over W workgroups)
+__device__ __forceinline__ uint32_t even_wg(uint32_t u, uint32_t W, uint32_t G) { return ((u + 1) * W - 1) / G; }
+
+template <uint32_t T, int NV, bool PAIR, bool NORM>
+__device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_t bid) {
+    static_assert(!NORM || NV == 1, "the in-kernel norm is the one-vector form");
+    extern __shared__ float smem[];
+    constexpr uint32_t MATS = PAIR ? 2 : 1;
+    constexpr int M = mx_blocks<NV>();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8, U = MATS * ngrp;
+    const uint32_t G = ((a.rows + kSlabRows - 1) / kSlabRows) * U, W = a.even;
+    const uint32_t L0 = bid * G / W, L1 = (bid + 1) * G / W;
+    const uint32_t nu = (G + W - 1) / W;  // LDS entries: the largest share
+    const SlabGeom geo = slab_geom(T, a.cols);
+    float* red = smem;  // [nu][NV][64]
+    uint8_t* tab = reinterpret_cast<uint8_t*>(smem + nu * NV * 64) + wave * mx_table_bytes<NV>();
+    float* sq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + even_lds_bytes<NV>(nu, nw));
+    const bool words = NORM && a.norm_words != nullptr;
+    const bool leader = !words || bid == 0;  // runs the norm's chains
+    uint32_t gens[kNormPublishPerThread];    // the leader: the generations of workgroups 1 + t + i nt
+    if constexpr (NORM) {
+        if (leader) {
+            if (words) {
+#pragma unroll
+                for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
+                    const uint32_t b = 1 + threadIdx.x + i * blockDim.x;
+                    gens[i] = b < W ? __hip_atomic_load(&a.counters[(b * G / W) / U], __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
+                                    : 0u;
+                }
+            }
+            // the row's squares into LDS before the weight loads are issued (registers free again)
+            norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // A unit u of the share: its segment (slab * MATS + matrix), the segment's first unit in the
+    // share, whether its slab lies inside the share, and whether u leads a segment that takes a
+    // ticket (every piece; with published words also the share's first unit, as above)
+    auto seg_of = [&](uint32_t u) { return u / ngrp; };
+    auto seg_first = [&](uint32_t u) { return max(L0, seg_of(u) * ngrp); };
+    auto whole_of = [&](uint32_t u) {
+        const uint32_t s_lo = seg_of(u) / MATS * U;
+        return s_lo >= L0 && s_lo + U <= L1;
+    };
+    auto ticketed = [&](uint32_t u) { return u == seg_first(u) && (!whole_of(u) || (words && u == L0)); };
+    constexpr uint32_t KU = even_units_per_wave<NV>();
+    uint32_t tickets[KU];
+    // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barriers of
+    // the chains or of the wait); the leader's threads publish the other workgroups' words
+    auto norm_inv = [&]() {
+        const uint32_t full = a.cols - a.cols % 8u;
+        if (!leader) {
+            const float inv = norm_x_wait(a, bid, tickets[0], sq + 8 * norm_chain_stride(full));
+            if (threadIdx.x == 0) __hip_atomic_store(a.norm_words + bid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return inv;
+        }
+        const float inv = norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
+        if (words) {
+#pragma unroll
+            for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
+                const uint32_t b = 1 + threadIdx.x + i * blockDim.x;
+                if (b < W)
+                    __hip_atomic_store(a.norm_words + b,
+                                       (uint64_t)__float_as_uint(inv) |
+                                           ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return inv;
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < KU; ++k) {
+        tickets[k] = 0;
+        const uint32_t u = L0 + wave + k * nw;
+        if (u >= L1) break;
+        const uint32_t seg = seg_of(u), slab = seg / MATS, mat = seg - slab * MATS, grp = u - seg * ngrp;
+        const uint8_t* wp = (mat ? a.w1 : a.w0) + (uint64_t)slab * geo.slab_bytes;
+        float xr[NV][4];
+        float wr[4];  // NORM: norm_w at this lane's x elements
+        SlotGroup<T> Gr;
+        // x first: the A table is built while the weights are on their way
+        mx_load_x<NV>(xr, a.x, a.x_stride, grp, S, lane);
+        if constexpr (NORM) mx_load_nw(wr, a.norm_w, grp, S, lane);
+        load_group<T>(Gr, wp, geo, lane, grp, S);
+        if (ticketed(u) && lane == 0)
+            tickets[k] = __hip_atomic_fetch_add(&a.counters[slab], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (NORM) mx_norm_x(xr, wr, norm_inv(), grp, S, lane);
+        s16x4 A[4 * M];
+        int es[NV];
+        float xs[NV];
+        float acc[NV];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+        mx_build<T, NV>(xr, tab, lane, A, es, xs);
+        mx_group<T, NV>(Gr, A, xs, min(8u, S - grp * 8), acc);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) red[((u - L0) * NV + v) * 64 + lane] = ldexpf(acc[v], es[v]);
+        // the next unit's loads after this one's arithmetic (its registers are free again)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (NORM) {
+        // a wave without a unit (the share is smaller than the workgroup) still takes part
+        if (wave >= L1 - L0) (void)norm_inv();
+    }
+    __syncthreads();
+    // the segments this wave leads: their units' entries in unit order, then the slab's meeting
+#pragma unroll
+    for (uint32_t k = 0; k < KU; ++k) {
+        const uint32_t u = L0 + wave + k * nw;
+        if (u >= L1) break;
+        if (u != seg_first(u)) continue;
+        const uint32_t seg = seg_of(u), slab = seg / MATS, mat = seg - slab * MATS;
+        const uint32_t s_lo = slab * U, s_hi = s_lo + U;
+        const bool whole = whole_of(u);
+        if (PAIR && whole && mat == 1) continue;  // a whole slab's gate lead takes its up half
+        const uint32_t seg_hi = min(L1, seg * ngrp + ngrp);
+        float acc0[NV], acc1[NV];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float s = red[((u - L0) * NV + v) * 64 + lane];
+            for (uint32_t e = u - L0 + 1; e < seg_hi - L0; ++e) s += red[(e * NV + v) * 64 + lane];
+            acc0[v] = s;
+            acc1[v] = 0.0f;
+        }
+        if (whole) {
+            if constexpr (PAIR) {
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    float s = red[((s_lo + ngrp - L0) * NV + v) * 64 + lane];
+                    for (uint32_t e = s_lo + ngrp - L0 + 1; e < s_hi - L0; ++e) s += red[(e * NV + v) * 64 + lane];
+                    acc1[v] = s;
+                }
+            }
+            if (ticketed(u) && lane == 0)  // no reducer: the generation moves on here
+                __hip_atomic_store(&a.counters[slab], ((tickets[k] >> kTicketBits) + 1) << kTicketBits, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            gemv_store<NV, PAIR>(a, acc0, acc1, slab, lane);
+            continue;
+        }
+        // this slab's pieces: the workgroups over its gate units, then those over its up units
+        const uint32_t wa0 = even_wg(s_lo, W, G), n0 = even_wg(s_lo + ngrp - 1, W, G) - wa0 + 1;
+        uint32_t nch = n0, c = bid - wa0;
+        if constexpr (PAIR) {
+            const uint32_t wa1 = even_wg(s_lo + ngrp, W, G);
+            nch += even_wg(s_hi - 1, W, G) - wa1 + 1;
+            if (mat) c = n0 + bid - wa1;
+        }
+        if (splitk_meet<NV, false>(a, acc0, acc1, lane, slab, c, nch, n0, a.even_stride, tickets[k]))
+            gemv_store<NV, PAIR>(a, acc0, acc1, slab, lane);
+    }
+}
+
+template <uint32_t T, int NV, bool PAIR, bool NORM = false>
+__global__ __launch_bounds__((mx_max_threads<T, NV, true>())) void k_gemv_mx_even(GemvSlabArgs a) {
+    gemv_mx_even_body<T, NV, PAIR, NORM>(a, blockIdx.x);
 }
 
 }  // namespace

@@ -78,6 +78,58 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     return {ks, nw, false};
 }
 
+// Even split (k_gemv_mx_even), for launches of at least kEvenMinGroups slot groups in the one-group
+// form: W = 2 workgroups per CU of an MI355X, each with an equal share of the groups, so every CU
+// streams the same bytes. Shape-only like the chunked split (rows are bitwise independent of
+// n_vec), and fixed for the full chip (the sums do not depend on how many CUs the device has).
+// Measured on MI355X at 17408 x 5120 Q4_K (1088 chunked workgroups): 12.86 -> 12.11 us at M = 1,
+// 15.2 / 21.8 / 23.4 -> 14.4 / 20.5 / 22.2 us at M = 2 / 3 / 4, 18.0 -> 17.3 us with the fused
+// norm. 3 and 4 workgroups per CU were slower at 2 to 4 vectors, and the formats whose 3- and
+// 4-vector kernels take at most 8 waves (Q5_K, Q6_K, Q8_0) and the gate/up pair, whose shares
+// would not fit one workgroup at 2 per CU, measured no better with 3 or 4 per CU than chunked.
+constexpr uint32_t kMi355xCus = 256;
+constexpr uint32_t kEvenWgPerCu = 2;
+constexpr uint32_t kEvenMinGroups = 4096;
+struct EvenSplit {
+    uint32_t W = 0, nu = 0, stride = 0;  // workgroups, units of the largest share, pieces per slab
+};
+
+template <uint32_t T>
+EvenSplit pick_even(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
+    const uint32_t ngrp = (S + 7) / 8, G = slabs * mats * ngrp;
+    if (!have_ws || slabs >= 1024 || G < kEvenMinGroups) return {};
+    // a share's units must fit one workgroup at every vector count
+    uint32_t max_nu = mx_max_threads<T, 1, true>() / 64;
+    max_nu = std::min(max_nu, even_units_per_wave<2>() * mx_max_threads<T, 2, true>() / 64);
+    max_nu = std::min(max_nu, even_units_per_wave<3>() * mx_max_threads<T, 3, true>() / 64);
+    max_nu = std::min(max_nu, even_units_per_wave<4>() * mx_max_threads<T, 4, true>() / 64);
+    const uint32_t W = kEvenWgPerCu * kMi355xCus, nu = (G + W - 1) / W;
+    if (nu > max_nu || even_lds_bytes<kMaxGemvVec>(nu, 1) > 65536) return {};
+    const uint32_t per = G / W;  // the fewest units of a share
+    const uint32_t stride = mats * ((ngrp + per - 1) / per + 1);
+    if (stride > kMaxChunks || (uint64_t)slabs * stride * kMaxGemvVec * 64 > kSlots) return {};
+    return {W, nu, stride};
+}
+
+// Waves per SIMD that a kernel's registers allow (512 VGPRs per lane on a CDNA SIMD, 8 waves at most).
+uint32_t kernel_waves_per_simd(const void* fn) {
+    hipFuncAttributes at{};
+    if (hipFuncGetAttributes(&at, fn) != hipSuccess || at.numRegs <= 0) return 1;
+    return (uint32_t)std::clamp(512 / ((at.numRegs + 7) / 8 * 8), 1, 8);
+}
+
+// Waves per workgroup of an even launch with NV vectors: one unit per wave when the CUs hold the
+// launch's workgroups that way (always at one vector), else as many as hold them in one round, at
+// most even_units_per_wave units per wave. The sums do not depend on it.
+template <uint32_t T, int NV, bool PAIR, bool NORM>
+uint32_t even_waves(const EvenSplit& ev) {
+    static const uint32_t wps = kernel_waves_per_simd(reinterpret_cast<const void*>(&k_gemv_mx_even<T, NV, PAIR, NORM>));
+    const uint32_t max_nw = mx_max_threads<T, NV, true>() / 64;
+    const uint32_t fit = 4 * wps / (ev.W / kMi355xCus);  // waves per workgroup with all resident
+    const uint32_t nw = std::max(std::min(ev.nu, fit), (ev.nu + even_units_per_wave<NV>() - 1) / even_units_per_wave<NV>());
+    return std::min(nw, max_nw);  // pick_even keeps every share within max_nw waves
+}
+
 // slots_cap / counters_cap: the split-K words and slab counters the workspace holds. The split is
 // always chosen for the allocated workspace's capacity (kSlots, kCounters), so a smaller workspace
 // (halo_mi_gemv_noalloc's scratch) gives the same bits or refuses the shape.
@@ -93,6 +145,37 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
     a.counters = ws ? ws->counters : nullptr;
     a.status = ws ? ws->status : nullptr;
     apply_test_hooks(a);
+    const EvenSplit ev = a.valu ? EvenSplit{} : pick_even<T>(slabs, S, MATS, have_ws);
+    if (ev.W) {
+        a.ks = 0;
+        a.even = ev.W;
+        a.even_stride = ev.stride;
+        const uint64_t words = (uint64_t)slabs * ev.stride * kMaxGemvVec * 64;
+        if (words > slots_cap || slabs > counters_cap)
+            return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows x %u cols exceed the split-K workspace (%llu words, %llu slabs)",
+                             a.rows, a.cols, (unsigned long long)slots_cap, (unsigned long long)counters_cap);
+        if (a.norm_w) {  // the in-kernel norm (one vector; norm_in_kernel chose it)
+            if constexpr (NV == 1) {
+                // the first workgroup runs the norm's chains and publishes 1 / rms in one word per
+                // workgroup, kept at the end of the split-K words (0 between launches); one unit
+                // per wave
+                const uint32_t nw = ev.nu;
+                a.norm_words = nullptr;
+                if (ev.W - 1 <= kNormPublishPerThread * 64 * nw && words + ev.W <= slots_cap)
+                    a.norm_words = ws->slots + (slots_cap - ev.W);
+                hipLaunchKernelGGL((k_gemv_mx_even<T, 1, PAIR, true>), dim3(ev.W), dim3(64 * nw),
+                                   even_lds_bytes<1>(ev.nu, nw) + norm_lds_bytes(a.cols), st, a);
+                return hip_status(hipGetLastError(), "gemv_slab launch");
+            } else {
+                return set_error(HALO_MI_E_CONFIG, "gemv: the in-kernel norm takes one vector");
+            }
+        }
+        const uint32_t nw = even_waves<T, NV, PAIR, false>(ev);
+        if (nw * even_units_per_wave<NV>() < ev.nu)
+            return set_error(HALO_MI_E_UNSUPPORTED, "gemv: even split of %u units over %u waves", ev.nu, nw);
+        hipLaunchKernelGGL((k_gemv_mx_even<T, NV, PAIR>), dim3(ev.W), dim3(64 * nw), even_lds_bytes<NV>(ev.nu, nw), st, a);
+        return hip_status(hipGetLastError(), "gemv_slab launch");
+    }
     // the chunks of a slab (or the pair's two matrices) meet in the workspace words
     if (a.ks * MATS > 1 &&
         (!have_ws || (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64 > slots_cap || slabs > counters_cap))
@@ -137,10 +220,12 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
 // thread), and LDS for the chain rows beside the kernel's own.
 template <uint32_t T>
 bool norm_in_kernel_t(uint32_t slabs, uint32_t cols, uint32_t mats, bool have_ws) {
-    const GemvSplit sp = pick_split<T>(slabs, cols / kSlot, mats, have_ws);
+    const EvenSplit ev = pick_even<T>(slabs, cols / kSlot, mats, have_ws);
+    const uint32_t nw = ev.W ? ev.nu : pick_split<T>(slabs, cols / kSlot, mats, have_ws).nw;
+    const size_t lds = ev.W ? even_lds_bytes<1>(ev.nu, nw) : mx_lds_bytes<1>(nw);
     const uint32_t full = cols - cols % 8u;
-    return full > 0 && cols <= kNormMaxCols && cols % 32 == 0 && full <= kNormPerThread * 64 * sp.nw &&
-           mx_lds_bytes<1>(sp.nw) + norm_lds_bytes(cols) <= 163840;
+    return full > 0 && cols <= kNormMaxCols && cols % 32 == 0 && full <= kNormPerThread * 64 * nw &&
+           lds + norm_lds_bytes(cols) <= 163840;
 }
 
 bool norm_in_kernel(uint32_t type, uint32_t slabs, uint32_t cols, uint32_t mats, bool have_ws) {

@@ -58,6 +58,12 @@ struct GemvSlabArgs {
     // the launch's slabs, and the launch's workgroups (0: a launch of its own).
     uint32_t slab0 = 0;
     uint32_t wg_total = 0;
+    // Even split (k_gemv_mx_even): the launch's `even` workgroups take equal shares of the
+    // (slab, matrix, slot group) units, and a slab's pieces meet in `even_stride` word sets
+    // (0: the chunked split, ks K chunks per slab). With the in-kernel norm, norm_words then
+    // holds one word per workgroup (the workgroup clears it when it has read it).
+    uint32_t even = 0;
+    uint32_t even_stride = 0;
     // The stream's status word: a split-K wait that gives up sets kStatusSplitKTimeout.
     uint32_t* status = nullptr;
     // Test hooks, set only by halo_mi_test_splitk_timeout: the reducer's wait bound (0 = the
