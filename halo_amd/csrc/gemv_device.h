@@ -1125,13 +1125,25 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
 // a ticket for that slab: the slab's reducer, or the workgroup itself for a slab wholly inside
 // it, moves the generation on); each workgroup clears its word when it has read it.
 // ------------------------------------------------------------------------------------------
+// The even split's workgroup count: 2 per CU of an MI355X
+constexpr uint32_t kEvenW = 512;
+// x / d for x, d < 2^22, given inv = 1.0f / d: the float quotient is within one of x / d (relative
+// error below 2^-22), then corrected (a few instructions where an integer divide takes about 30)
+__device__ __forceinline__ uint32_t udiv_inv(uint32_t x, uint32_t d, float inv) {
+    const uint32_t q = (uint32_t)((float)x * inv);
+    const int r = (int)(x - q * d);
+    return r < 0 ? q - 1 : (r >= (int)d ? q + 1 : q);
+}
+
 // Units per wave: at most two at two vectors (the kernel holds 4 waves per SIMD there, and a
 // second unit lets the workgroups of 2 per CU stay resident), else one (nw is the share's size;
 // a second unit's registers would spill at 3 and 4 vectors)
 template <int NV>
 constexpr uint32_t even_units_per_wave() { return NV == 2 ? 2u : 1u; }
-// The workgroup whose share holds unit u (of G over W workgroups)
-__device__ __forceinline__ uint32_t even_wg(uint32_t u, uint32_t W, uint32_t G) { return ((u + 1) * W - 1) / G; }
+// The workgroup whose share holds unit u (of G over kEvenW workgroups; inv_g = 1.0f / G)
+__device__ __forceinline__ uint32_t even_wg(uint32_t u, uint32_t G, float inv_g) {
+    return udiv_inv((u + 1) * kEvenW - 1, G, inv_g);
+}
 
 template <uint32_t T, int NV, bool PAIR, bool NORM>
 __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_t bid) {
@@ -1142,7 +1154,7 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8, U = MATS * ngrp;
-    const uint32_t G = ((a.rows + kSlabRows - 1) / kSlabRows) * U, W = a.even;
+    const uint32_t G = ((a.rows + kSlabRows - 1) / kSlabRows) * U, W = kEvenW;
     const uint32_t L0 = bid * G / W, L1 = (bid + 1) * G / W;
     const uint32_t nu = (G + W - 1) / W;  // LDS entries: the largest share
     const SlabGeom geo = slab_geom(T, a.cols);
@@ -1158,8 +1170,8 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
 #pragma unroll
                 for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
                     const uint32_t b = 1 + threadIdx.x + i * blockDim.x;
-                    gens[i] = b < W ? __hip_atomic_load(&a.counters[(b * G / W) / U], __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
+                    gens[i] = b < W ? __hip_atomic_load(&a.counters[udiv_inv(b * G / W, ngrp, a.even_inv_ngrp) / MATS],
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
                                     : 0u;
                 }
             }
@@ -1171,7 +1183,7 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     // A unit u of the share: its segment (slab * MATS + matrix), the segment's first unit in the
     // share, whether its slab lies inside the share, and whether u leads a segment that takes a
     // ticket (every piece; with published words also the share's first unit, as above)
-    auto seg_of = [&](uint32_t u) { return u / ngrp; };
+    auto seg_of = [&](uint32_t u) { return udiv_inv(u, ngrp, a.even_inv_ngrp); };
     auto seg_first = [&](uint32_t u) { return max(L0, seg_of(u) * ngrp); };
     auto whole_of = [&](uint32_t u) {
         const uint32_t s_lo = seg_of(u) / MATS * U;
@@ -1273,11 +1285,12 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
             continue;
         }
         // this slab's pieces: the workgroups over its gate units, then those over its up units
-        const uint32_t wa0 = even_wg(s_lo, W, G), n0 = even_wg(s_lo + ngrp - 1, W, G) - wa0 + 1;
+        const float ig = a.even_inv_units;
+        const uint32_t wa0 = even_wg(s_lo, G, ig), n0 = even_wg(s_lo + ngrp - 1, G, ig) - wa0 + 1;
         uint32_t nch = n0, c = bid - wa0;
         if constexpr (PAIR) {
-            const uint32_t wa1 = even_wg(s_lo + ngrp, W, G);
-            nch += even_wg(s_hi - 1, W, G) - wa1 + 1;
+            const uint32_t wa1 = even_wg(s_lo + ngrp, G, ig);
+            nch += even_wg(s_hi - 1, G, ig) - wa1 + 1;
             if (mat) c = n0 + bid - wa1;
         }
         if (splitk_meet<NV, false>(a, acc0, acc1, lane, slab, c, nch, n0, a.even_stride, tickets[k]))

@@ -87,8 +87,6 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
 // norm. 3 and 4 workgroups per CU were slower at 2 to 4 vectors, and the formats whose 3- and
 // 4-vector kernels take at most 8 waves (Q5_K, Q6_K, Q8_0) and the gate/up pair, whose shares
 // would not fit one workgroup at 2 per CU, measured no better with 3 or 4 per CU than chunked.
-constexpr uint32_t kMi355xCus = 256;
-constexpr uint32_t kEvenWgPerCu = 2;
 constexpr uint32_t kEvenMinGroups = 4096;
 struct EvenSplit {
     uint32_t W = 0, nu = 0, stride = 0;  // workgroups, units of the largest share, pieces per slab
@@ -103,7 +101,7 @@ EvenSplit pick_even(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     max_nu = std::min(max_nu, even_units_per_wave<2>() * mx_max_threads<T, 2, true>() / 64);
     max_nu = std::min(max_nu, even_units_per_wave<3>() * mx_max_threads<T, 3, true>() / 64);
     max_nu = std::min(max_nu, even_units_per_wave<4>() * mx_max_threads<T, 4, true>() / 64);
-    const uint32_t W = kEvenWgPerCu * kMi355xCus, nu = (G + W - 1) / W;
+    const uint32_t W = kEvenW, nu = (G + W - 1) / W;
     if (nu > max_nu || even_lds_bytes<kMaxGemvVec>(nu, 1) > 65536) return {};
     const uint32_t per = G / W;  // the fewest units of a share
     const uint32_t stride = mats * ((ngrp + per - 1) / per + 1);
@@ -125,7 +123,7 @@ template <uint32_t T, int NV, bool PAIR, bool NORM>
 uint32_t even_waves(const EvenSplit& ev) {
     static const uint32_t wps = kernel_waves_per_simd(reinterpret_cast<const void*>(&k_gemv_mx_even<T, NV, PAIR, NORM>));
     const uint32_t max_nw = mx_max_threads<T, NV, true>() / 64;
-    const uint32_t fit = 4 * wps / (ev.W / kMi355xCus);  // waves per workgroup with all resident
+    const uint32_t fit = 4 * wps / (ev.W / 256);  // waves per workgroup with all of them resident on 256 CUs
     const uint32_t nw = std::max(std::min(ev.nu, fit), (ev.nu + even_units_per_wave<NV>() - 1) / even_units_per_wave<NV>());
     return std::min(nw, max_nw);  // pick_even keeps every share within max_nw waves
 }
@@ -150,6 +148,8 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
         a.ks = 0;
         a.even = ev.W;
         a.even_stride = ev.stride;
+        a.even_inv_ngrp = 1.0f / (float)((S + 7) / 8);
+        a.even_inv_units = 1.0f / (float)(slabs * MATS * ((S + 7) / 8));
         const uint64_t words = (uint64_t)slabs * ev.stride * kMaxGemvVec * 64;
         if (words > slots_cap || slabs > counters_cap)
             return set_error(HALO_MI_E_UNSUPPORTED, "gemv: %u rows x %u cols exceed the split-K workspace (%llu words, %llu slabs)",

@@ -64,6 +64,7 @@ struct GemvSlabArgs {
     // holds one word per workgroup (the workgroup clears it when it has read it).
     uint32_t even = 0;
     uint32_t even_stride = 0;
+    float even_inv_ngrp = 0.0f, even_inv_units = 0.0f;  // 1 / slot groups per row, 1 / the launch's units
     // The stream's status word: a split-K wait that gives up sets kStatusSplitKTimeout.
     uint32_t* status = nullptr;
     // Test hooks, set only by halo_mi_test_splitk_timeout: the reducer's wait bound (0 = the
