@@ -196,7 +196,7 @@ int halo_mi_gemv(const halo_mi_gemv_params* p, void* stream);
  * HALO_MI_E_UNSUPPORTED. The split-K words, slab counters and status word live in a fixed
  * device array of this library (about 8.3 MiB per GPU, held until the process ends), not in a
  * per-stream workspace: a shape whose split needs more than 65536 slabs of counters or 2^20
- * words (e.g. the 17408 x 5120 headline needs 2^18.1) returns HALO_MI_E_UNSUPPORTED. Every call
+ * words (e.g. the 17408 x 5120 headline needs 2^17.7) returns HALO_MI_E_UNSUPPORTED. Every call
  * on one GPU shares that array, so calls that overlap in time on one GPU (other streams, other
  * threads) race and give wrong results: order them. halo_mi_stream_check also reports this
  * array's status word.

@@ -25,7 +25,8 @@ def _case(hl, dev, t, rows, cols, seed):
 def test_noalloc_matches_gemv_bitwise_and_allocates_nothing(hl, dev):
     import torch
 
-    # first call: 17408 x 5120 Q4_K (272 slabs, 4 K chunks), 3 vectors with the fused norm; then
+    # first call: 17408 x 5120 Q4_K (272 slabs over the even split's 512 workgroups), 3 vectors
+    # with the fused norm; then
     # smaller inputs on the same scratch: the auto ids 4 and 0 where their choice is the slab
     # GEMV (Q6_K at 4 and 3 vectors; a Q4_K matrix of 96 slabs at 4), and a single vector
     calls = [(Q4_K, 17408, 5120, 3, True, 2), (Q6_K, 5120, 6144, 4, False, 4), (Q4_K, 6144, 5120, 4, True, 0),
