@@ -1127,6 +1127,9 @@ __global__ __launch_bounds__((mx_max_threads<T, NV, ONE>())) void k_gemv_mx(Gemv
 // ------------------------------------------------------------------------------------------
 // The even split's workgroup count: 2 per CU of an MI355X
 constexpr uint32_t kEvenW = 512;
+// the even split's in-kernel norm: wave 0 of the first workgroup publishes for the other kEvenW - 1
+constexpr uint32_t kEvenPublishPerLane = 8;
+static_assert(kEvenW - 1 <= 64 * kEvenPublishPerLane, "one published word per workgroup");
 // x / d for x, d < 2^22, given inv = 1.0f / d: the float quotient is within one of x / d (relative
 // error below 2^-22), then corrected (a few instructions where an integer divide takes about 30)
 __device__ __forceinline__ uint32_t udiv_inv(uint32_t x, uint32_t d, float inv) {
@@ -1163,20 +1166,46 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     float* sq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + even_lds_bytes<NV>(nu, nw));
     const bool words = NORM && a.norm_words != nullptr;
     const bool leader = !words || bid == 0;  // runs the norm's chains
-    uint32_t gens[kNormPublishPerThread];    // the leader: the generations of workgroups 1 + t + i nt
+    const uint32_t slot = 8 * norm_chain_stride(a.cols - a.cols % 8u);  // sq[slot]: 1 / rms for the workgroup
     if constexpr (NORM) {
         if (leader) {
-            if (words) {
+            // The chains run before this workgroup issues any weight load: a barrier behind the
+            // weight loads would wait for every wave's issue, which the launch's saturated memory
+            // queue holds back for microseconds. Wave 0 reads the generations of the workgroups it
+            // publishes for (b = 1 + lane + 64 i; every load issued, the index clamped, so they
+            // are in flight together), the workgroup stages the row's squares, and wave 0 runs the
+            // chains and publishes while the other waves go on to their weight loads.
+            uint32_t gens[kEvenPublishPerLane];
+            if (words && wave == 0) {
 #pragma unroll
-                for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
-                    const uint32_t b = 1 + threadIdx.x + i * blockDim.x;
-                    gens[i] = b < W ? __hip_atomic_load(&a.counters[udiv_inv(b * G / W, ngrp, a.even_inv_ngrp) / MATS],
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
-                                    : 0u;
+                for (uint32_t i = 0; i < kEvenPublishPerLane; ++i) {
+                    const uint32_t b = min(1 + lane + 64 * i, W - 1);
+                    gens[i] = __hip_atomic_load(&a.counters[udiv_inv(b * G / W, ngrp, a.even_inv_ngrp) / MATS],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits;
                 }
             }
-            // the row's squares into LDS before the weight loads are issued (registers free again)
             norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
+            lds_sync();
+            if (wave == 0) {
+                const uint32_t full = a.cols - a.cols % 8u, stride = norm_chain_stride(full);
+                __builtin_amdgcn_s_setprio(3);
+                float p = 0.0f;
+                if (lane < 8) p = norm_chain<kNormChainBatch>(sq + lane * stride, full / 8, p);
+                const float inv = __shfl(norm_finish(p, a.x, full, a.cols, a.norm_eps, lane), 0);
+                if (lane == 0) sq[slot] = inv;
+                if (words) {
+#pragma unroll
+                    for (uint32_t i = 0; i < kEvenPublishPerLane; ++i) {
+                        const uint32_t b = 1 + lane + 64 * i;
+                        if (b < W)
+                            __hip_atomic_store(a.norm_words + b,
+                                               (uint64_t)__float_as_uint(inv) |
+                                                   ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                __builtin_amdgcn_s_setprio(0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1192,28 +1221,16 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     auto ticketed = [&](uint32_t u) { return u == seg_first(u) && (!whole_of(u) || (words && u == L0)); };
     constexpr uint32_t KU = even_units_per_wave<NV>();
     uint32_t tickets[KU];
-    // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barriers of
-    // the chains or of the wait); the leader's threads publish the other workgroups' words
+    // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barrier of the
+    // wait, or the leader's barrier after its wave 0 has run the chains)
     auto norm_inv = [&]() {
-        const uint32_t full = a.cols - a.cols % 8u;
         if (!leader) {
-            const float inv = norm_x_wait(a, bid, tickets[0], sq + 8 * norm_chain_stride(full));
+            const float inv = norm_x_wait(a, bid, tickets[0], sq + slot);
             if (threadIdx.x == 0) __hip_atomic_store(a.norm_words + bid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return inv;
         }
-        const float inv = norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
-        if (words) {
-#pragma unroll
-            for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
-                const uint32_t b = 1 + threadIdx.x + i * blockDim.x;
-                if (b < W)
-                    __hip_atomic_store(a.norm_words + b,
-                                       (uint64_t)__float_as_uint(inv) |
-                                           ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        return inv;
+        lds_sync();
+        return sq[slot];
     };
 #pragma unroll
     for (uint32_t k = 0; k < KU; ++k) {

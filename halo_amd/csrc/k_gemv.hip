@@ -161,7 +161,7 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
                 // per wave
                 const uint32_t nw = ev.nu;
                 a.norm_words = nullptr;
-                if (ev.W - 1 <= kNormPublishPerThread * 64 * nw && words + ev.W <= slots_cap)
+                if (words + ev.W <= slots_cap)
                     a.norm_words = ws->slots + (slots_cap - ev.W);
                 hipLaunchKernelGGL((k_gemv_mx_even<T, 1, PAIR, true>), dim3(ev.W), dim3(64 * nw),
                                    even_lds_bytes<1>(ev.nu, nw) + norm_lds_bytes(a.cols), st, a);
