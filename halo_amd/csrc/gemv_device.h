@@ -880,7 +880,7 @@ __device__ __forceinline__ void norm_x_squares(const float* __restrict__ x, uint
 // After norm_x_squares: the chains in lanes 0..7 of wave 0 (wave priority raised for them), the
 // combine and the tail: 1 / sqrt(mean + eps) for the whole workgroup.
 constexpr int kNormChainBatch = 4;  // 16-byte LDS reads per batch of the chains (16 VGPRs)
-constexpr uint32_t kNormPublishPerThread = 4;  // slabs per thread the leading workgroup publishes for
+constexpr uint32_t kNormPublishPerLane = 16;  // words per lane of the publishing wave (1024 at most)
 __device__ __forceinline__ float norm_x_chains(const float* __restrict__ x, uint32_t cols, float eps, float* sq,
                                                uint32_t wave, uint32_t lane) {
     const uint32_t full = cols - cols % 8u, stride = norm_chain_stride(full);
@@ -920,6 +920,61 @@ __device__ __forceinline__ float norm_x_wait(const GemvSlabArgs& a, uint32_t sla
     }
     lds_sync();
     return *slot;
+}
+
+// The in-kernel norm's publishing workgroup, before it issues any weight load: a barrier behind
+// the weight loads would wait for every wave's issue, which a launch's saturated memory queue holds
+// back for microseconds. x's loads, then wave 0's loads of the tags' generations (counter_of(i) for
+// word i < n_pub, i = lane + 64 j: all issued, the index clamped, so they are in flight
+// together), the squares into LDS and a barrier; then wave 0 runs the chains, leaves 1 / rms in
+// sq[8 stride] and publishes word_of(i) for every i while the other waves go on to their weight
+// loads. They read 1 / rms after one more barrier (norm_leader_inv). n_pub <= 64 P.
+template <uint32_t P, typename CounterOf, typename WordOf>
+__device__ __forceinline__ void norm_leader_publish(const GemvSlabArgs& a, float* sq, uint32_t wave, uint32_t lane,
+                                                    uint32_t n_pub, CounterOf counter_of, WordOf word_of) {
+    const uint32_t full = a.cols - a.cols % 8u, stride = norm_chain_stride(full);
+    float xv[kNormPerThread];
+#pragma unroll
+    for (uint32_t i = 0; i < kNormPerThread; ++i) xv[i] = a.x[min(threadIdx.x + i * blockDim.x, full - 1)];
+    uint32_t gens[P];
+    if (wave == 0) {
+#pragma unroll
+        for (uint32_t i = 0; i < P; ++i)
+            gens[i] = __hip_atomic_load(&a.counters[counter_of(min(lane + 64 * i, n_pub - 1))], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (uint32_t i = 0; i < kNormPerThread; ++i) {
+            const uint32_t e = threadIdx.x + i * blockDim.x;
+            if (e < full) sq[(e % 8) * stride + e / 8] = xv[i] * xv[i];
+        }
+    }
+    lds_sync();
+    if (wave == 0) {
+        __builtin_amdgcn_s_setprio(3);
+        float p = 0.0f;
+        if (lane < 8) p = norm_chain_ahead<kNormChainBatch>(sq + lane * stride, full / 8, p);
+        const float inv = __shfl(norm_finish(p, a.x, full, a.cols, a.norm_eps, lane), 0);
+        if (lane == 0) sq[8 * stride] = inv;
+#pragma unroll
+        for (uint32_t i = 0; i < P; ++i) {
+            const uint32_t w = lane + 64 * i;
+            if (w < n_pub)
+                __hip_atomic_store(word_of(w),
+                                   (uint64_t)__float_as_uint(inv) |
+                                       ((uint64_t)(((gens[i] >> kTicketBits) & kTagMask) | (kTagMask + 1)) << 32),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    }
+}
+
+// The publishing workgroup's waves: 1 / rms after norm_leader_publish (one barrier)
+__device__ __forceinline__ float norm_leader_inv(uint32_t cols, const float* sq) {
+    lds_sync();
+    return sq[8 * norm_chain_stride(cols - cols % 8u)];
 }
 
 // LDS bytes of the chain rows and the result word for a row of cols floats
@@ -984,23 +1039,15 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     const uint32_t S = a.cols / kSlot, ngrp = (S + 7) / 8;
     const uint32_t nch = a.ks * MATS;
     float* sq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(smem) + mx_lds_bytes<NV>(nw));
-    // NORM with published words: only the first workgroup runs the chains
+    // NORM with published words: only the first workgroup runs the chains, before its weight loads
     const bool leader = !NORM || a.norm_words == nullptr || bid == 0;
-    uint32_t gens[kNormPublishPerThread];  // the leader: the launch generations of the slabs it publishes for
     if constexpr (NORM) {
-        if (leader) {
-            if (a.norm_words) {
-#pragma unroll
-                for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
-                    const uint32_t s = threadIdx.x + i * blockDim.x;
-                    gens[i] = s < a.norm_slabs ? __hip_atomic_load(&a.counters[a.slab0 + s], __ATOMIC_RELAXED,
-                                                                   __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits
-                                               : 0u;
-                }
-            }
-            // the row's squares into LDS before the weight loads are issued (registers free again)
+        if (a.norm_words && bid == 0)
+            norm_leader_publish<kNormPublishPerLane>(
+                a, sq, wave, lane, a.norm_slabs, [&](uint32_t s) { return a.slab0 + s; },
+                [&](uint32_t s) { return a.norm_words + a.slab0 + s; });
+        else if (!a.norm_words)  // every workgroup runs the chains: the squares now, the chains after its loads
             norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
-        }
         __builtin_amdgcn_sched_barrier(0);
     }
     const uint32_t slab = bid / nch, c = bid % nch;
@@ -1020,23 +1067,12 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
     float xr[NV][4];
     uint32_t ticket = 0;
     float wr[4];  // NORM: norm_w at this lane's x elements
-    // NORM: 1 / rms for the workgroup: the chains (wave 0), and with published words the leader
-    // then stores it to every slab's word while the others wait for theirs
+    // NORM: 1 / rms for the workgroup: the published word, or what the publishing workgroup's wave
+    // 0 computed, or (no words) the chains here, after this workgroup's weight loads
     auto norm_inv = [&]() {
         if (!leader) return norm_x_wait(a, bid / (a.ks * (PAIR ? 2u : 1u)), ticket, sq + 8 * norm_chain_stride(a.cols - a.cols % 8u));
-        const float inv = norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
-        if (a.norm_words) {
-#pragma unroll
-            for (uint32_t i = 0; i < kNormPublishPerThread; ++i) {
-                const uint32_t s = threadIdx.x + i * blockDim.x;
-                if (s < a.norm_slabs)
-                    __hip_atomic_store(a.norm_words + a.slab0 + s,
-                                       (uint64_t)__float_as_uint(inv) |
-                                           ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-        return inv;
+        if (a.norm_words) return norm_leader_inv(a.cols, sq);
+        return norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
     };
     if constexpr (ONE) {
         if (w0 < w1) {
@@ -1168,45 +1204,15 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     const bool leader = !words || bid == 0;  // runs the norm's chains
     const uint32_t slot = 8 * norm_chain_stride(a.cols - a.cols % 8u);  // sq[slot]: 1 / rms for the workgroup
     if constexpr (NORM) {
-        if (leader) {
-            // The chains run before this workgroup issues any weight load: a barrier behind the
-            // weight loads would wait for every wave's issue, which the launch's saturated memory
-            // queue holds back for microseconds. Wave 0 reads the generations of the workgroups it
-            // publishes for (b = 1 + lane + 64 i; every load issued, the index clamped, so they
-            // are in flight together), the workgroup stages the row's squares, and wave 0 runs the
-            // chains and publishes while the other waves go on to their weight loads.
-            uint32_t gens[kEvenPublishPerLane];
-            if (words && wave == 0) {
-#pragma unroll
-                for (uint32_t i = 0; i < kEvenPublishPerLane; ++i) {
-                    const uint32_t b = min(1 + lane + 64 * i, W - 1);
-                    gens[i] = __hip_atomic_load(&a.counters[udiv_inv(b * G / W, ngrp, a.even_inv_ngrp) / MATS],
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kTicketBits;
-                }
-            }
+        // the first workgroup publishes for workgroups 1 .. W - 1, tagged with the generation of
+        // each one's first slab, before it issues any weight load
+        if (words && bid == 0)
+            norm_leader_publish<kEvenPublishPerLane>(
+                a, sq, wave, lane, W - 1,
+                [&](uint32_t i) { return udiv_inv((i + 1) * G / W, ngrp, a.even_inv_ngrp) / MATS; },
+                [&](uint32_t i) { return a.norm_words + i + 1; });
+        else if (!words)  // every workgroup runs the chains: the squares now, the chains after its loads
             norm_x_squares(a.x, a.cols, sq, threadIdx.x, blockDim.x);
-            lds_sync();
-            if (wave == 0) {
-                const uint32_t full = a.cols - a.cols % 8u, stride = norm_chain_stride(full);
-                __builtin_amdgcn_s_setprio(3);
-                float p = 0.0f;
-                if (lane < 8) p = norm_chain<kNormChainBatch>(sq + lane * stride, full / 8, p);
-                const float inv = __shfl(norm_finish(p, a.x, full, a.cols, a.norm_eps, lane), 0);
-                if (lane == 0) sq[slot] = inv;
-                if (words) {
-#pragma unroll
-                    for (uint32_t i = 0; i < kEvenPublishPerLane; ++i) {
-                        const uint32_t b = 1 + lane + 64 * i;
-                        if (b < W)
-                            __hip_atomic_store(a.norm_words + b,
-                                               (uint64_t)__float_as_uint(inv) |
-                                                   ((uint64_t)((gens[i] & kTagMask) | (kTagMask + 1)) << 32),
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-                __builtin_amdgcn_s_setprio(0);
-            }
-        }
         __builtin_amdgcn_sched_barrier(0);
     }
     // A unit u of the share: its segment (slab * MATS + matrix), the segment's first unit in the
@@ -1221,16 +1227,16 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
     auto ticketed = [&](uint32_t u) { return u == seg_first(u) && (!whole_of(u) || (words && u == L0)); };
     constexpr uint32_t KU = even_units_per_wave<NV>();
     uint32_t tickets[KU];
-    // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barrier of the
-    // wait, or the leader's barrier after its wave 0 has run the chains)
+    // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barriers of the
+    // wait, of the publishing workgroup, or of the chains when nothing is published)
     auto norm_inv = [&]() {
         if (!leader) {
             const float inv = norm_x_wait(a, bid, tickets[0], sq + slot);
             if (threadIdx.x == 0) __hip_atomic_store(a.norm_words + bid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return inv;
         }
-        lds_sync();
-        return sq[slot];
+        if (words) return norm_leader_inv(a.cols, sq);
+        return norm_x_chains(a.x, a.cols, a.norm_eps, sq, wave, lane);
     };
 #pragma unroll
     for (uint32_t k = 0; k < KU; ++k) {

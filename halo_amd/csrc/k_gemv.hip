@@ -198,7 +198,7 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
             // in one word per slab, kept at the end of the split-K words (0 between launches)
             const uint64_t words = (uint64_t)slabs * a.ks * MATS * kMaxGemvVec * 64;
             a.norm_words = nullptr;
-            if (a.ks * MATS > 1 && slabs <= kNormPublishPerThread * 64 * sp.nw && words + slabs <= slots_cap) {
+            if (a.ks * MATS > 1 && slabs <= 64 * kNormPublishPerLane && words + slabs <= slots_cap) {
                 a.norm_words = ws->slots + (slots_cap - slabs);
                 a.norm_slabs = slabs;
             }

@@ -46,6 +46,44 @@ __device__ __forceinline__ float norm_chain(const float* r, uint32_t m, float p)
     return p;
 }
 
+// norm_chain with the next batch's reads issued before the current batch's additions (two
+// register sets), so the LDS latency overlaps the additions: for a chain that runs alone on the
+// critical path (the even-split GEMV's first workgroup).
+template <int B = 4>
+__device__ __forceinline__ float norm_chain_ahead(const float* r, uint32_t m, float p) {
+#pragma clang fp contract(off)
+    uint32_t k = 0;
+    if (m >= 4 * B) {
+        float4 cur[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) cur[b] = *reinterpret_cast<const float4*>(r + 4 * b);
+        for (; k + 8 * B <= m; k += 4 * B) {
+            float4 nxt[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) nxt[b] = *reinterpret_cast<const float4*>(r + k + 4 * B + 4 * b);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                p = p + cur[b].x;
+                p = p + cur[b].y;
+                p = p + cur[b].z;
+                p = p + cur[b].w;
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) cur[b] = nxt[b];
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            p = p + cur[b].x;
+            p = p + cur[b].y;
+            p = p + cur[b].z;
+            p = p + cur[b].w;
+        }
+        k += 4 * B;
+    }
+    for (; k < m; ++k) p = p + r[k];
+    return p;
+}
+
 // Wave 0 (all 64 lanes, p: lane j < 8 holds chain sum p_j): the dot's combine, the sequential
 // tail of x[full .. cols) and 1 / sqrt(mean + eps), returned in lane 0 (other lanes: unspecified).
 // sqrtf and / are correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt, set by the build;
