@@ -93,3 +93,45 @@ def test_even_split_fused_norm_bitwise(hl, oracle, dev, t, rows, cols):
         fused = _run(hl, dev, t, wg, None, x, rows, cols, norm_w=w)
         assert isclose_bits(fused, _run(hl, dev, t, wg, None, xn, rows, cols)), \
             f"call {call}: the fused norm is not bitwise rms_norm then the gemv"
+
+
+@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 26200, 2560), (IQ4_XS, 26200, 2560), (Q4_0, 32768, 3104)])
+def test_even_split_partial_slab_and_group(hl, oracle, dev, t, rows, cols):
+    """A last slab of 24 rows (410 slabs x 10 groups) and, for Q4_0, a last slot group of one slot
+    (97 slots: 13 groups per row, 6656 units): within the bound, rows independent of n_vec, and
+    nothing written past the rows."""
+    say("even split partial", NAMES[t], rows, cols)
+    dg = synth_matrix(hl, t, rows, cols, 720 + rows + cols)
+    wg = slab_of(hl, dev, t, dg, rows, cols)
+    x = np.random.default_rng(7200 + cols).standard_normal((3, cols)).astype(np.float32)
+    singles = np.concatenate([_run(hl, dev, t, wg, None, x[i:i + 1], rows, cols) for i in range(3)])
+    ref = oracle.matmul(t, dg, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, dg, rows, cols, x)
+    err = np.abs(singles.astype(np.float64) - ref)
+    print(f"    even split {NAMES[t]} {rows}x{cols} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(err <= tol)
+    assert isclose_bits(_run(hl, dev, t, wg, None, x, rows, cols), singles), "n_vec=3 changed a row"
+
+
+@pytest.mark.parametrize("n_vec", [1, 3])
+def test_even_split_lm_head(hl, oracle, dev, n_vec):
+    """The LM head's argmax epilogue on the even split (500 slabs x 16 groups = 8000 units): the
+    result is the first maximum of its own logits, which are bitwise the plain GEMV's and within
+    its bound of the CPU."""
+    import torch
+
+    t, rows, cols = Q4_K, 32000, 4096
+    say("even split lm_head", rows, cols, n_vec)
+    dg = synth_matrix(hl, t, rows, cols, 730)
+    wg = slab_of(hl, dev, t, dg, rows, cols)
+    x = np.random.default_rng(7300 + n_vec).standard_normal((n_vec, cols)).astype(np.float32)
+    res = torch.full((n_vec, 3), 0xABCD, dtype=torch.int32, device=dev)
+    logits = torch.full((n_vec, rows), SENTINEL, dtype=torch.float32, device=dev)
+    hl.lm_head(t, wg, to_dev(x, dev), res, rows, cols, n_vec, logits=logits, variant=hl.Variant.SLAB_GEMV)
+    r, y = host(res).view(np.uint32), host(logits)
+    assert isclose_bits(y, _run(hl, dev, t, wg, None, x, rows, cols)), "the head's logits are not the GEMV's"
+    ref = oracle.matmul(t, dg, rows, cols, x)
+    assert np.all(np.abs(y.astype(np.float64) - ref) <= slab_gemv_tol(oracle, t, dg, rows, cols, x))
+    for v in range(n_vec):
+        i = int(np.argmax(y[v]))
+        assert r[v].tolist() == [i, int(y[v, i].view(np.uint32)), 0], f"vector {v}: not the first maximum"
