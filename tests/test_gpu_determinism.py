@@ -3,8 +3,8 @@
 The MFMA kernels read their accumulators back on the VALU; a missed wait between a dependent
 MFMA's write-back and such a read shows up as sums that change from run to run, not as a wrong
 result every time. So each instantiation (weight type x vectors per pass x gate/up pair x one or
-several slot groups per wave x fused norm, for the slab GEMV, its VALU form, the grouped GEMV, the
-exact small-M GEMM and the bf16 GEMM tile families) is run three times on the same inputs, with
+several slot groups per wave x fused norm, for the slab GEMV in its chunked and even splits, its
+VALU form, the grouped GEMV, the exact small-M GEMM and the bf16 GEMM tile families) is run three times on the same inputs, with
 other kernels in between, and every run must give the same bits.
 """
 from __future__ import annotations
@@ -81,6 +81,40 @@ def test_slab_gemv_every_instantiation_repeats(hl, dev, t, rows, cols):
             _three_runs(plain(norm=nw), other)
         if t in VALU_TYPES:
             _three_runs(plain(v=hl.Variant.SLAB_GEMV_VALU), other)
+
+
+@pytest.mark.parametrize("t", (Q4_K, Q4_0, IQ4_XS))
+@pytest.mark.parametrize("rows,cols,pair", [(32768, 2048, False), (8192, 5120, True)])
+def test_even_split_every_instantiation_repeats(hl, dev, t, rows, cols, pair):
+    """k_gemv_mx_even<T, NV, PAIR, NORM> (512 workgroups with equal shares of a large launch's slot
+    groups) for NV = 1..4, the gate/up pair, and the fused norm at one vector."""
+    import torch
+
+    say("determinism even split", NAMES[t], rows, cols, "pair" if pair else "")
+    wg = _matrix(hl, dev, t, rows, cols, 3900 + t)
+    wu = _matrix(hl, dev, t, rows, cols, 3950 + t) if pair else None
+    nw = to_dev(np.random.default_rng(3999).uniform(0.5, 1.5, cols).astype(np.float32), dev)
+    scratch = torch.empty((4, rows), dtype=torch.float32, device=dev)
+
+    def other():
+        hl.gemv(t, wg, to_dev(_x(4, cols, 3998), dev), scratch, rows, cols, 4, variant=hl.Variant.SLAB_GEMV)
+
+    for n_vec in (1, 2, 3, 4):
+        xd = to_dev(_x(n_vec, cols, 4000 + n_vec), dev)
+        y = torch.empty((n_vec, rows), dtype=torch.float32, device=dev)
+
+        def go(norm=None):
+            def run():
+                if pair:
+                    hl.gate_up_swiglu(t, wg, wu, xd, y, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMV, norm_w=norm)
+                else:
+                    hl.gemv(t, wg, xd, y, rows, cols, n_vec, variant=hl.Variant.SLAB_GEMV, norm_w=norm)
+                return host(y).copy()
+            return run
+
+        _three_runs(go(), other)
+        if n_vec == 1:
+            _three_runs(go(nw), other)
 
 
 @pytest.mark.parametrize("ta,tb", [(Q4_K, Q6_K), (Q8_0, IQ4_XS), (Q5_K, Q4_0)])
