@@ -1174,11 +1174,16 @@ __device__ __forceinline__ uint32_t udiv_inv(uint32_t x, uint32_t d, float inv) 
     return r < 0 ? q - 1 : (r >= (int)d ? q + 1 : q);
 }
 
-// Units per wave: at most two at two vectors (the kernel holds 4 waves per SIMD there, and a
-// second unit lets the workgroups of 2 per CU stay resident), else one (nw is the share's size;
-// a second unit's registers would spill at 3 and 4 vectors)
-template <int NV>
-constexpr uint32_t even_units_per_wave() { return NV == 2 ? 2u : 1u; }
+// Units per wave at most: two where the kernel's registers leave fewer resident waves than the
+// two workgroups of a CU need with one unit each (two vectors; every vector count of the formats
+// with the heavier loops, whose 2- to 4-vector kernels also take at most 8 waves), else one (nw is
+// then the share's size; a second unit's registers would spill in the 3- and 4-vector kernels of
+// the others)
+template <uint32_t T, int NV>
+constexpr uint32_t even_units_per_wave() {
+    constexpr bool heavy = T == kQ8_0 || T == kQ6_K || T == kQ5_K;
+    return (NV == 2 || heavy) ? 2u : 1u;
+}
 // The workgroup whose share holds unit u (of G over kEvenW workgroups; inv_g = 1.0f / G)
 __device__ __forceinline__ uint32_t even_wg(uint32_t u, uint32_t G, float inv_g) {
     return udiv_inv((u + 1) * kEvenW - 1, G, inv_g);
@@ -1225,7 +1230,7 @@ __device__ __forceinline__ void gemv_mx_even_body(const GemvSlabArgs& a, uint32_
         return s_lo >= L0 && s_lo + U <= L1;
     };
     auto ticketed = [&](uint32_t u) { return u == seg_first(u) && (!whole_of(u) || (words && u == L0)); };
-    constexpr uint32_t KU = even_units_per_wave<NV>();
+    constexpr uint32_t KU = even_units_per_wave<T, NV>();
     uint32_t tickets[KU];
     // NORM (one unit per wave): 1 / rms for the workgroup, once by every wave (the barriers of the
     // wait, of the publishing workgroup, or of the chains when nothing is published)

@@ -82,11 +82,11 @@ GemvSplit pick_split(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
 // form: W = 2 workgroups per CU of an MI355X, each with an equal share of the groups, so every CU
 // streams the same bytes. Shape-only like the chunked split (rows are bitwise independent of
 // n_vec), and fixed for the full chip (the sums do not depend on how many CUs the device has).
-// Measured on MI355X at 17408 x 5120 Q4_K (1088 chunked workgroups): 12.86 -> 12.11 us at M = 1,
-// 15.2 / 21.8 / 23.4 -> 14.4 / 20.5 / 22.2 us at M = 2 / 3 / 4, 18.0 -> 17.3 us with the fused
-// norm. 3 and 4 workgroups per CU were slower at 2 to 4 vectors, and the formats whose 3- and
-// 4-vector kernels take at most 8 waves (Q5_K, Q6_K, Q8_0) and the gate/up pair, whose shares
-// would not fit one workgroup at 2 per CU, measured no better with 3 or 4 per CU than chunked.
+// Measured on MI355X at 17408 x 5120 (1088 chunked workgroups), M = 1 / 2 / 4: Q4_K 12.86 / 15.2 /
+// 23.4 -> 12.1 / 14.4 / 22.2 us (18.0 -> 17.3 with the fused norm), Q5_K 15.6 / - / 26.4 -> 14.8 /
+// - / 20.3, Q8_0 25.5 / 31.8 / 37.1 -> 19.4 / 21.1 / 24.1. 3 and 4 workgroups per CU were slower at
+// 2 to 4 vectors; the gate/up pair's shares (22 units) do not fit one workgroup at 2 per CU, and
+// with 3 or 4 per CU it measured no better than chunked.
 constexpr uint32_t kEvenMinGroups = 4096;
 struct EvenSplit {
     uint32_t W = 0, nu = 0, stride = 0;  // workgroups, units of the largest share, pieces per slab
@@ -95,12 +95,15 @@ struct EvenSplit {
 template <uint32_t T>
 EvenSplit pick_even(uint32_t slabs, uint32_t S, uint32_t mats, bool have_ws) {
     const uint32_t ngrp = (S + 7) / 8, G = slabs * mats * ngrp;
-    if (!have_ws || slabs >= 1024 || G < kEvenMinGroups) return {};
+    // Q6_K keeps the chunked split: its 2-vector kernel holds 170 VGPRs (2 waves per SIMD), and
+    // with two units per wave the even split measured slower at every vector count (5120 x 17408:
+    // 19.2 -> 20.3 us at M = 1, 24.9 / 25.8 / 28.4 -> 27.8 / 29.2 / 31.1 at M = 2 / 3 / 4)
+    if (T == kQ6_K || !have_ws || slabs >= 1024 || G < kEvenMinGroups) return {};
     // a share's units must fit one workgroup at every vector count
-    uint32_t max_nu = mx_max_threads<T, 1, true>() / 64;
-    max_nu = std::min(max_nu, even_units_per_wave<2>() * mx_max_threads<T, 2, true>() / 64);
-    max_nu = std::min(max_nu, even_units_per_wave<3>() * mx_max_threads<T, 3, true>() / 64);
-    max_nu = std::min(max_nu, even_units_per_wave<4>() * mx_max_threads<T, 4, true>() / 64);
+    uint32_t max_nu = std::min(16u, even_units_per_wave<T, 1>() * mx_max_threads<T, 1, true>() / 64);
+    max_nu = std::min(max_nu, even_units_per_wave<T, 2>() * mx_max_threads<T, 2, true>() / 64);
+    max_nu = std::min(max_nu, even_units_per_wave<T, 3>() * mx_max_threads<T, 3, true>() / 64);
+    max_nu = std::min(max_nu, even_units_per_wave<T, 4>() * mx_max_threads<T, 4, true>() / 64);
     const uint32_t W = kEvenW, nu = (G + W - 1) / W;
     if (nu > max_nu || even_lds_bytes<kMaxGemvVec>(nu, 1) > 65536) return {};
     const uint32_t per = G / W;  // the fewest units of a share
@@ -124,7 +127,7 @@ uint32_t even_waves(const EvenSplit& ev) {
     static const uint32_t wps = kernel_waves_per_simd(reinterpret_cast<const void*>(&k_gemv_mx_even<T, NV, PAIR, NORM>));
     const uint32_t max_nw = mx_max_threads<T, NV, true>() / 64;
     const uint32_t fit = 4 * wps / (ev.W / 256);  // waves per workgroup with all of them resident on 256 CUs
-    const uint32_t nw = std::max(std::min(ev.nu, fit), (ev.nu + even_units_per_wave<NV>() - 1) / even_units_per_wave<NV>());
+    const uint32_t nw = std::max(std::min(ev.nu, fit), (ev.nu + even_units_per_wave<T, NV>() - 1) / even_units_per_wave<T, NV>());
     return std::min(nw, max_nw);  // pick_even keeps every share within max_nw waves
 }
 
@@ -171,7 +174,7 @@ int launch_gemv_slab_t(GemvSlabArgs a, uint32_t slabs, Workspace* ws, uint64_t s
             }
         }
         const uint32_t nw = even_waves<T, NV, PAIR, false>(ev);
-        if (nw * even_units_per_wave<NV>() < ev.nu)
+        if (nw * even_units_per_wave<T, NV>() < ev.nu)
             return set_error(HALO_MI_E_UNSUPPORTED, "gemv: even split of %u units over %u waves", ev.nu, nw);
         hipLaunchKernelGGL((k_gemv_mx_even<T, NV, PAIR>), dim3(ev.W), dim3(64 * nw), even_lds_bytes<NV>(ev.nu, nw), st, a);
         return hip_status(hipGetLastError(), "gemv_slab launch");

@@ -83,7 +83,7 @@ def test_slab_gemv_every_instantiation_repeats(hl, dev, t, rows, cols):
             _three_runs(plain(v=hl.Variant.SLAB_GEMV_VALU), other)
 
 
-@pytest.mark.parametrize("t", (Q4_K, Q4_0, IQ4_XS))
+@pytest.mark.parametrize("t", (Q4_K, Q4_0, IQ4_XS, Q5_K, Q8_0))
 @pytest.mark.parametrize("rows,cols,pair", [(32768, 2048, False), (8192, 5120, True)])
 def test_even_split_every_instantiation_repeats(hl, dev, t, rows, cols, pair):
     """k_gemv_mx_even<T, NV, PAIR, NORM> (512 workgroups with equal shares of a large launch's slot

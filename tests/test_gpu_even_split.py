@@ -15,14 +15,14 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from helpers import IQ4_XS, NAMES, Q4_0, Q4_K, isclose_bits, max_ratio, slab_gemv_tol, swiglu_tol, synth_matrix
+from helpers import IQ4_XS, NAMES, Q4_0, Q4_K, Q5_K, Q8_0, isclose_bits, max_ratio, slab_gemv_tol, swiglu_tol, synth_matrix
 from test_gpu_parity import SENTINEL, host, say, slab_of, to_dev
 
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
-# the formats whose shares fit one workgroup at every vector count (the others run chunked)
-EVEN_TYPES = (Q4_K, Q4_0, IQ4_XS)
+# the formats that take the even split (Q6_K runs chunked); Q5_K and Q8_0 with up to two units per wave
+EVEN_TYPES = (Q4_K, Q4_0, IQ4_XS, Q5_K, Q8_0)
 # (rows, cols, pair): 512 slabs x 8 groups = 4096 units, 8 per workgroup: every slab whole in one;
 # 410 x 10 = 4100 units, 8 or 9 per workgroup: slabs over two workgroups; the headline, 272 x 20,
 # 10 or 11 per workgroup: slabs over two or three; a pair of 128 slabs x 2 x 20; a pair of
@@ -95,11 +95,12 @@ def test_even_split_fused_norm_bitwise(hl, oracle, dev, t, rows, cols):
             f"call {call}: the fused norm is not bitwise rms_norm then the gemv"
 
 
-@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 26200, 2560), (IQ4_XS, 26200, 2560), (Q4_0, 32768, 3104)])
+@pytest.mark.parametrize("t,rows,cols", [(Q4_K, 26200, 2560), (IQ4_XS, 26200, 2560), (Q5_K, 26200, 2560),
+                                          (Q4_0, 32768, 3104), (Q8_0, 32768, 3104)])
 def test_even_split_partial_slab_and_group(hl, oracle, dev, t, rows, cols):
-    """A last slab of 24 rows (410 slabs x 10 groups) and, for Q4_0, a last slot group of one slot
-    (97 slots: 13 groups per row, 6656 units): within the bound, rows independent of n_vec, and
-    nothing written past the rows."""
+    """A last slab of 24 rows (410 slabs x 10 groups) and, for the 32-weight blocks, a last slot
+    group of one slot (97 slots: 13 groups per row, 6656 units): within the bound, rows
+    independent of n_vec, and nothing written past the rows."""
     say("even split partial", NAMES[t], rows, cols)
     dg = synth_matrix(hl, t, rows, cols, 720 + rows + cols)
     wg = slab_of(hl, dev, t, dg, rows, cols)
