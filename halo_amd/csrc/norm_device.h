@@ -46,39 +46,52 @@ __device__ __forceinline__ float norm_chain(const float* r, uint32_t m, float p)
     return p;
 }
 
-// norm_chain with the next batch's reads issued before the current batch's additions (two
-// register sets), so the LDS latency overlaps the additions: for a chain that runs alone on the
-// critical path (the even-split GEMV's first workgroup).
+// norm_chain with the reads of the next batch in flight while a batch is added (two register
+// sets used in turn, so no copies between them), so the LDS latency overlaps the additions: for a
+// chain that runs alone on the critical path (the GEMV's publishing workgroup). The additions are
+// norm_chain's, in the same order.
 template <int B = 4>
 __device__ __forceinline__ float norm_chain_ahead(const float* r, uint32_t m, float p) {
 #pragma clang fp contract(off)
-    uint32_t k = 0;
-    if (m >= 4 * B) {
-        float4 cur[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) cur[b] = *reinterpret_cast<const float4*>(r + 4 * b);
-        for (; k + 8 * B <= m; k += 4 * B) {
-            float4 nxt[B];
-#pragma unroll
-            for (int b = 0; b < B; ++b) nxt[b] = *reinterpret_cast<const float4*>(r + k + 4 * B + 4 * b);
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                p = p + cur[b].x;
-                p = p + cur[b].y;
-                p = p + cur[b].z;
-                p = p + cur[b].w;
-            }
-#pragma unroll
-            for (int b = 0; b < B; ++b) cur[b] = nxt[b];
-        }
+    constexpr uint32_t N = 4 * B;  // floats per batch
+    auto add = [&](const float4 (&q)[B]) __attribute__((always_inline)) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            p = p + cur[b].x;
-            p = p + cur[b].y;
-            p = p + cur[b].z;
-            p = p + cur[b].w;
+            p = p + q[b].x;
+            p = p + q[b].y;
+            p = p + q[b].z;
+            p = p + q[b].w;
         }
-        k += 4 * B;
+    };
+    auto load = [&](float4 (&q)[B], uint32_t k) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) q[b] = *reinterpret_cast<const float4*>(r + k + 4 * b);
+    };
+    uint32_t k = 0;
+    if (m >= 2 * N) {
+        // c0 holds r[k, k + N), c1 r[k + N, k + 2 N)
+        float4 c0[B], c1[B];
+        load(c0, 0);
+        load(c1, N);
+        for (; k + 4 * N <= m; k += 2 * N) {
+            // (the scheduling barriers keep each batch's reads where they are issued here)
+            add(c0);
+            __builtin_amdgcn_sched_barrier(0);
+            load(c0, k + 2 * N);
+            __builtin_amdgcn_sched_barrier(0);
+            add(c1);
+            __builtin_amdgcn_sched_barrier(0);
+            load(c1, k + 3 * N);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        add(c0);
+        add(c1);
+        k += 2 * N;
+    }
+    for (; k + N <= m; k += N) {
+        float4 q[B];
+        load(q, k);
+        add(q);
     }
     for (; k < m; ++k) p = p + r[k];
     return p;
