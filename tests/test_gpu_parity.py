@@ -227,6 +227,43 @@ def test_gemv_slab_within_bound(hl, oracle, dev, t, case):
     assert np.all(err <= tol)
 
 
+def extreme_x(n_vec: int, cols: int, seed: int) -> np.ndarray:
+    """x rows 2^-40, 1 and 2^40 times N(0, 1), each 256-column group scaled by its own 2^k
+    (|k| <= 20), one whole group and a few scattered elements exactly zero: the slab GEMV scales
+    each group's x by a power of two before its three-piece split, and rows of very different
+    magnitude share one launch."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n_vec, cols))
+    x *= np.ldexp(1.0, np.array([-40, 0, 40, -20][:n_vec]))[:, None]
+    ng = cols // 256
+    x *= np.repeat(np.ldexp(1.0, rng.integers(-20, 21, (n_vec, ng))), 256, axis=1)
+    x[:, 256 * (ng // 2): 256 * (ng // 2 + 1)] = 0.0
+    x[rng.random((n_vec, cols)) < 0.01] = 0.0
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+@pytest.mark.parametrize("rows,cols", [(576, 5120), (17408, 5120)])
+def test_gemv_slab_extreme_magnitudes(hl, oracle, dev, t, rows, cols):
+    """The slab GEMV (the chunked split at 576 rows, the even split at 17408 except Q6_K) with
+    extreme_x's rows: within the derived bound of cpu::matmul for every row, and every row of the
+    three-vector call bitwise its one-vector call."""
+    say("gemv_slab extreme x", NAMES[t], rows, cols)
+    buf, stride = make_weights(t, rows, cols, seed=2600 + t)
+    dense = dense_of(buf, t, rows, cols, stride, 0)
+    x = extreme_x(3, cols, 2700 + t)
+    slab = slab_of(hl, dev, t, dense, rows, cols)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMV)
+    ref = oracle.matmul(t, dense, rows, cols, x)
+    tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
+    err = np.abs(y.astype(np.float64) - ref)
+    print(f"    extreme x {NAMES[t]} {rows}x{cols} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    assert np.all(np.isfinite(y)) and np.all(err <= tol)
+    for v in range(3):
+        y1 = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[v:v + 1], rows, cols, hl.Variant.SLAB_GEMV)
+        assert isclose_bits(y1, y[v:v + 1]), f"row {v} depends on the batch"
+
+
 INVARIANT_VARIANTS = ("SLAB_GEMV", "SLAB_GEMM_EXACT_INVARIANT")
 
 
