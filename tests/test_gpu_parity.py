@@ -244,24 +244,27 @@ def extreme_x(n_vec: int, cols: int, seed: int) -> np.ndarray:
 
 @pytest.mark.parametrize("t", QUANT_TYPES)
 @pytest.mark.parametrize("rows,cols", [(576, 5120), (17408, 5120)])
-def test_gemv_slab_extreme_magnitudes(hl, oracle, dev, t, rows, cols):
-    """The slab GEMV (the chunked split at 576 rows, the even split at 17408 except Q6_K) with
-    extreme_x's rows: within the derived bound of cpu::matmul for every row, and every row of the
+@pytest.mark.parametrize("variant", ["SLAB_GEMV", "SLAB_GEMM_EXACT_INVARIANT"])
+def test_gemv_slab_extreme_magnitudes(hl, oracle, dev, t, rows, cols, variant):
+    """The two batch-invariant kernels (the slab GEMV: the chunked split at 576 rows, the even
+    split at 17408 except Q6_K; the exact GEMM with its fixed K split) with extreme_x's rows:
+    within the slab GEMV's derived bound of cpu::matmul for every row, and every row of the
     three-vector call bitwise its one-vector call."""
-    say("gemv_slab extreme x", NAMES[t], rows, cols)
+    v = getattr(hl.Variant, variant)
+    say("extreme x", variant, NAMES[t], rows, cols)
     buf, stride = make_weights(t, rows, cols, seed=2600 + t)
     dense = dense_of(buf, t, rows, cols, stride, 0)
     x = extreme_x(3, cols, 2700 + t)
     slab = slab_of(hl, dev, t, dense, rows, cols)
-    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, hl.Variant.SLAB_GEMV)
+    y = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x, rows, cols, v)
     ref = oracle.matmul(t, dense, rows, cols, x)
     tol = slab_gemv_tol(oracle, t, dense, rows, cols, x)
     err = np.abs(y.astype(np.float64) - ref)
-    print(f"    extreme x {NAMES[t]} {rows}x{cols} worst |d|/bound = {max_ratio(err, tol):.4f}")
+    print(f"    extreme x {variant} {NAMES[t]} {rows}x{cols} worst |d|/bound = {max_ratio(err, tol):.4f}")
     assert np.all(np.isfinite(y)) and np.all(err <= tol)
-    for v in range(3):
-        y1 = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[v:v + 1], rows, cols, hl.Variant.SLAB_GEMV)
-        assert isclose_bits(y1, y[v:v + 1]), f"row {v} depends on the batch"
+    for i in range(3):
+        y1 = run_gemv(hl, dev, t, slab, hl.Layout.SLAB, x[i:i + 1], rows, cols, v)
+        assert isclose_bits(y1, y[i:i + 1]), f"row {i} depends on the batch"
 
 
 INVARIANT_VARIANTS = ("SLAB_GEMV", "SLAB_GEMM_EXACT_INVARIANT")
