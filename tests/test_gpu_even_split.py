@@ -80,15 +80,18 @@ def test_even_split_bound_invariance_repeat(hl, oracle, dev, t, rows, cols, pair
 @pytest.mark.parametrize("rows,cols", [(32768, 2048), (26240, 2560), (17408, 5120)])
 def test_even_split_fused_norm_bitwise(hl, oracle, dev, t, rows, cols):
     """One vector: the norm inside the even kernel (the first workgroup publishes 1 / rms to one
-    word per workgroup) is bitwise RMS_NORM then the unfused GEMV; two calls in a row (the words
-    are cleared by their readers, the generations move on)."""
+    word per workgroup) is bitwise RMS_NORM then the unfused GEMV; three calls in a row (the words
+    are cleared by their readers, the generations move on), the last with a row of very large and
+    widely spread magnitudes."""
     say("even split norm", NAMES[t], rows, cols)
     dg = synth_matrix(hl, t, rows, cols, 710 + rows)
     wg = slab_of(hl, dev, t, dg, rows, cols)
     rng = np.random.default_rng(7100 + rows)
     w = rng.uniform(0.25, 1.75, cols).astype(np.float32)
-    for call in range(2):
+    for call in range(3):
         x = (rng.standard_normal((1, cols)) * 3.0).astype(np.float32)
+        if call == 2:  # a row of 2^30 N(0, 1), each 256-column group scaled by 2^k (|k| <= 20)
+            x *= np.float32(2.0 ** 30) * np.repeat(np.ldexp(1.0, rng.integers(-20, 21, cols // 256)), 256).astype(np.float32)
         xn = oracle.rms_norm(x, w, EPS)
         fused = _run(hl, dev, t, wg, None, x, rows, cols, norm_w=w)
         assert isclose_bits(fused, _run(hl, dev, t, wg, None, xn, rows, cols)), \
