@@ -138,7 +138,11 @@ __device__ __forceinline__ uint32_t ld_nt2(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
-template <uint32_t T>
+// SPLIT (Q6_K): the eight ql records, then the eight qh records (two sequential streams), instead
+// of each slot's pair in turn. Measured on MI355X for the one-group form (5120 x 17408: M = 1
+// 19.3 either way, M = 2 24.9 -> 24.2 us, M = 4 28.2 -> 26.2); the form with several groups per
+// wave (the 151936-row head 114.5 -> 115.5) and Q5_K's qh words (14.52 -> 14.83) keep the pairs.
+template <uint32_t T, bool SPLIT = false>
 __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __restrict__ slab, const SlabGeom& g,
                                            uint32_t lane, uint32_t grp, uint32_t S) {
     const uint32_t sb = grp * 8;
@@ -162,10 +166,17 @@ __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __res
     } else if constexpr (T == kQ6_K) {
         G.d = ld_nt2(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
         G.sc = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+        if constexpr (SPLIT) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
-            G.qh[j] = ld_nt8(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+            for (int j = 0; j < 8; ++j) G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) G.qh[j] = ld_nt8(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+                G.qh[j] = ld_nt8(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+            }
         }
     } else if constexpr (T == kQ4_0) {
         const uint32_t n = min(8u, S - sb);
@@ -1081,7 +1092,7 @@ __device__ __forceinline__ void gemv_mx_body(const GemvSlabArgs& a, uint32_t bid
             // for in issue order)
             mx_load_x<NV>(xr, a.x, a.x_stride, w0, S, lane);
             if constexpr (NORM) mx_load_nw(wr, a.norm_w, w0, S, lane);
-            load_group<T>(G, slab0, geo, lane, w0, S);
+            load_group<T, true>(G, slab0, geo, lane, w0, S);
             ticket = gemv_ticket(a, slab, nch);
             if constexpr (NORM) mx_norm_x(xr, wr, norm_inv(), w0, S, lane);
             s16x4 A[4 * M];
