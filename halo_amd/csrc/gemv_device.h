@@ -138,10 +138,12 @@ __device__ __forceinline__ uint32_t ld_nt2(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
-// SPLIT (Q6_K): the eight ql records, then the eight qh records (two sequential streams), instead
-// of each slot's pair in turn. Measured on MI355X for the one-group form (5120 x 17408: M = 1
-// 19.3 either way, M = 2 24.9 -> 24.2 us, M = 4 28.2 -> 26.2); the form with several groups per
-// wave (the 151936-row head 114.5 -> 115.5) and Q5_K's qh words (14.52 -> 14.83) keep the pairs.
+// SPLIT (Q6_K): the eight ql records, then the eight qh records (two sequential streams), then
+// the group's scales, instead of the scales first and each slot's pair in turn. Measured on
+// MI355X for the one-group form (5120 x 17408, against the pairs: M = 2 24.9 -> 24.2 us, M = 4
+// 28.2 -> 26.2; the scales last: M = 1 19.3 -> 19.05, M = 2 24.1 -> 24.8); the form with several
+// groups per wave (the 151936-row head 114.5 -> 115.5) and Q5_K's qh words (14.52 -> 14.83) keep
+// the pairs, and Q4_0 / Q8_0 measured slower with their scales first or last.
 template <uint32_t T, bool SPLIT = false>
 __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __restrict__ slab, const SlabGeom& g,
                                            uint32_t lane, uint32_t grp, uint32_t S) {
@@ -164,14 +166,16 @@ __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __res
 #pragma unroll
         for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
     } else if constexpr (T == kQ6_K) {
-        G.d = ld_nt2(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
-        G.sc = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
         if constexpr (SPLIT) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
 #pragma unroll
             for (int j = 0; j < 8; ++j) G.qh[j] = ld_nt8(slab + g.aux_off + ((uint64_t)(sb + j) * 64 + lane) * 8);
+            G.sc = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
+            G.d = ld_nt2(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
         } else {
+            G.d = ld_nt2(slab + g.d_off + ((uint64_t)grp * 64 + lane) * 2);
+            G.sc = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 G.ql[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
