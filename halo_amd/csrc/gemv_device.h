@@ -148,12 +148,13 @@ template <uint32_t T, bool SPLIT = false>
 __device__ __forceinline__ void load_group(SlotGroup<T>& G, const uint8_t* __restrict__ slab, const SlabGeom& g,
                                            uint32_t lane, uint32_t grp, uint32_t S) {
     const uint32_t sb = grp * 8;
-    // scales first, then the quants in slot order: loads complete in order, so slot j can be
-    // used as soon as its own record has arrived
+    // the quants in slot order with the scales first (loads complete in order, so slot j can be
+    // used as soon as its own record has arrived), except Q4_K's header after its quants (measured
+    // on MI355X, 17408 x 5120 M = 1: 11.95 -> 11.84 us; IQ4_XS's header last: 14.19 -> 14.69)
     if constexpr (T == kQ4_K) {
-        G.hdr = ld_nt16(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 16);
 #pragma unroll
         for (int j = 0; j < 8; ++j) G.q[j] = ld_nt16(slab + g.q_off + ((uint64_t)(sb + j) * 64 + lane) * 16);
+        G.hdr = ld_nt16(slab + g.aux_off + ((uint64_t)grp * 64 + lane) * 16);
     } else if constexpr (T == kQ5_K) {
         G.hdr = ld_nt16(slab + g.sc_off + ((uint64_t)grp * 64 + lane) * 16);
 #pragma unroll
