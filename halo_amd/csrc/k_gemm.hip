@@ -195,6 +195,25 @@ __device__ __forceinline__ uint32_t bld32(__amdgpu_buffer_rsrc_t r, uint32_t vof
 __device__ __forceinline__ uint32_t bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
+// The same with a cache policy (2: nontemporal) for weight records read once per launch
+template <int CP>
+__device__ __forceinline__ uint4 bld128p(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CP);
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+template <int CP>
+__device__ __forceinline__ uint2 bld64p(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, CP);
+    return uint2{v[0], v[1]};
+}
+template <int CP>
+__device__ __forceinline__ uint32_t bld32p(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CP);
+}
+template <int CP>
+__device__ __forceinline__ uint32_t bld16p(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, CP);
+}
 
 // Per-lane byte offsets of a producer thread's records inside one stage of a slab.
 struct PcOff {
@@ -231,43 +250,45 @@ struct SmH<kQ6_K> {
     uint32_t d;
 };
 
-// The per-slot fields of a weight record (codes; Q4_0 / Q8_0's d, Q5_K / Q6_K's high bits).
-template <uint32_t T>
+// The per-slot fields of a weight record (codes; Q4_0 / Q8_0's d, Q5_K / Q6_K's high bits). NT:
+// nontemporal loads (k_gemm_pc, measured on MI355X at gate/up M = 64: 49.9 -> 49.3 us; the
+// M = 512 and small-M kernels measured the same or slower with them)
+template <uint32_t T, bool NT = false>
 __device__ __forceinline__ void sm_load_q(PcW<T>& R, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
                                           uint32_t s, bool live) {
     auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
     if constexpr (T == kQ4_K || T == kIQ4_XS) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
+        R.q = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 1024));
     } else if constexpr (T == kQ4_0) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+        R.q = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 1024));
+        R.d = bld16p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + s * 128));
     } else if constexpr (T == kQ5_K) {
-        R.q = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 256));
+        R.q = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + s * 256));
     } else if constexpr (T == kQ8_0) {
-        R.qa = bld64(slab, o.q, so(g.q_off + s * 2048));
-        R.qb = bld64(slab, o.q, so(g.q_off + s * 2048 + 1024));
-        R.d = bld16(slab, o.aux, so(g.aux_off + s * 128));
+        R.qa = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 2048));
+        R.qb = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 2048 + 1024));
+        R.d = bld16p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + s * 128));
     } else {
-        R.ql = bld64(slab, o.q, so(g.q_off + s * 1024));
-        R.qh = bld32(slab, o.aux, so(g.aux_off + s * 512));
+        R.ql = bld64p<NT ? 2 : 0>(slab, o.q, so(g.q_off + s * 1024));
+        R.qh = bld32p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + s * 512));
     }
 }
 
-// The per-super-block fields of super-block sb.
-template <uint32_t T>
+// The per-super-block fields of super-block sb (NT as sm_load_q's).
+template <uint32_t T, bool NT = false>
 __device__ __forceinline__ void sm_load_h(SmH<T>& H, __amdgpu_buffer_rsrc_t slab, const SlabGeom& g, const PcOff& o,
                                           uint32_t sb, bool live) {
     auto so = [&](uint64_t x) { return live ? (uint32_t)x : kPcOob; };
     if constexpr (T == kQ4_K) {
-        H.hdr = bld128(slab, o.aux, so(g.aux_off + sb * 1024));
+        H.hdr = bld128p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + sb * 1024));
     } else if constexpr (T == kQ5_K) {
-        H.hdr = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
+        H.hdr = bld128p<NT ? 2 : 0>(slab, o.sc, so(g.sc_off + sb * 1024));
     } else if constexpr (T == kIQ4_XS) {
-        H.hdr = bld64(slab, o.aux, so(g.aux_off + sb * 512));
+        H.hdr = bld64p<NT ? 2 : 0>(slab, o.aux, so(g.aux_off + sb * 512));
     } else if constexpr (T == kQ6_K) {
-        H.sc = bld128(slab, o.sc, so(g.sc_off + sb * 1024));
-        H.d = bld16(slab, o.d, so(g.d_off + sb * 128));
+        H.sc = bld128p<NT ? 2 : 0>(slab, o.sc, so(g.sc_off + sb * 1024));
+        H.d = bld16p<NT ? 2 : 0>(slab, o.d, so(g.d_off + sb * 128));
     }
 }
 
@@ -635,8 +656,8 @@ __device__ __forceinline__ void gemm_pc_body(const GemmPcArgs& a, uint32_t bid, 
     SmH<T> H[NH];
     // first: s starts a super-block (known statically: s_begin is a multiple of 8)
     auto load = [&](int slot, uint32_t s, bool first, int hslot) {
-        if (first) sm_load_h<T>(H[hslot], slab, g, off, s / 8, s < s_end);
-        sm_load_q<T>(R[slot], slab, g, off, s, s < s_end);
+        if (first) sm_load_h<T, true>(H[hslot], slab, g, off, s / 8, s < s_end);
+        sm_load_q<T, true>(R[slot], slab, g, off, s, s < s_end);
     };
     // j: the stage's slot within its super-block (static in the unrolled loop)
     auto store = [&](int slot, uint32_t j, int buf) {

@@ -46,19 +46,21 @@ constexpr uint32_t kSxWgsPerCu = 1;        // workgroups per CU the K split aims
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sx_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
+// Weight records, read once per launch: nontemporal loads (cache policy 2; measured on MI355X
+// against the default: Q4_K gate/up M = 4 30.6 -> 28.6 us, 17408 x 5120 M = 4 18.5 -> 17.9)
 __device__ __forceinline__ uint4 sx_ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
     return uint4{v[0], v[1], v[2], v[3]};
 }
 __device__ __forceinline__ uint2 sx_ld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 2);
     return uint2{v[0], v[1]};
 }
 __device__ __forceinline__ uint32_t sx_ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 2);
 }
 __device__ __forceinline__ uint32_t sx_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 2);
 }
 
 template <int CTRL>
